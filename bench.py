@@ -1,0 +1,307 @@
+#!/usr/bin/env python3
+"""Benchmark of the ternary BitLinear hot path on one MI355X (BASELINE.json metric).
+
+Headline workload: batch-1 decode GEMV at BitNet-2B shapes (N x K) 2560x2560,
+3200x2560, 13824x2560, 2560x6912, each its own kernel.  One step = those four kernels, each on a
+weight copy not touched for the previous 63 steps (64 rotated copies, 1.1 GB, so neither the
+256 MB Infinity Cache nor L2 serves repeats).  value = aggregate algorithmic GB/s of a step:
+bytes per launch B = N*K/4 + M*K + 2*M*N + 4 + 4*M (packed W, int8 A, bf16 Y, scales).
+
+Timing: the launches of the timed region are queued behind a bounded device sleep, so the HIP
+events on the launch stream measure device time of back-to-back kernels (host launch latency is
+excluded); warmup steps run first.  Extra fields: per-shape GEMV numbers, the prefill GEMM at
+M=2048 in int8 TOP/s vs the 5.0 POP/s dense int8 peak, the fused RMSNorm+quant
+kernel, and the reference CPU kernel timed on this host (cpu_baseline).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode GEMV HBM GB/s (% peak) + prefill GEMM int8 TOPS (% MFMA peak), 2B shape"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+GEMV_SHAPES = [(2560, 2560), (3200, 2560), (13824, 2560), (2560, 6912)]  # (N, K)
+PREFILL_SHAPES = [(13824, 2560), (2560, 6912)]
+N_COPIES = 64
+
+
+def gemv_bytes(m: int, n: int, k: int) -> int:
+    return n * k // 4 + m * k + 2 * m * n + 4 + 4 * m
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--sweep", action="store_true", help="also run the batched M sweep (configs[2])")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    return p.parse_args()
+
+
+class Launcher:
+    """Pre-marshalled ctypes calls into libwfbitnet (one per kernel launch)."""
+
+    def __init__(self, pkg, torch):
+        self.torch = torch
+        self.lib = pkg._lib.load()
+        self.stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def linear_args(self, fn, qw, n, k, a, m, a_scale, ws_dev, out, acc=None):
+        vp = ctypes.c_void_p
+        args = (vp(qw.data_ptr()), n, k, vp(a.data_ptr()), m, a.stride(0) if m > 1 else k,
+                vp(a_scale.data_ptr()), vp(ws_dev.data_ptr()), ctypes.c_float(0.0), None, 0,
+                vp(out.data_ptr()), 1, n, None if acc is None else vp(acc.data_ptr()), self.stream)
+        f = getattr(self.lib, fn)
+
+        def call():
+            if f(*args) != 0:
+                raise RuntimeError(f"{fn}: {self.lib.wfb_last_error().decode()}")
+
+        return call
+
+
+def timed(torch, fns, steps, warmup):
+    """Device ms per step for `steps` repetitions of the launch list `fns` (step i uses fns[i % len])."""
+    for i in range(warmup):
+        for f in fns[i % len(fns)]:
+            f()
+    torch.cuda.synchronize()
+    # host enqueue cost, to size the device sleep that hides it
+    t0 = time.perf_counter()
+    for i in range(min(steps, 8)):
+        for f in fns[i % len(fns)]:
+            f()
+    torch.cuda.synchronize()
+    enqueue_s = (time.perf_counter() - t0) / min(steps, 8) * steps
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(_sleep_cycles(torch, 2.0 * enqueue_s + 0.005)))
+    start.record()
+    for i in range(steps):
+        for f in fns[i % len(fns)]:
+            f()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+_SLEEP_RATE = None
+
+
+def _sleep_cycles(torch, seconds):
+    """Cycles for torch.cuda._sleep to last about `seconds` (calibrated once)."""
+    global _SLEEP_RATE
+    if _SLEEP_RATE is None:
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
+        torch.cuda._sleep(10_000_000)
+        e.record()
+        torch.cuda.synchronize()
+        _SLEEP_RATE = 10_000_000 / max(s.elapsed_time(e) * 1e-3, 1e-6)
+    return min(max(seconds, 0.002), 2.0) * _SLEEP_RATE
+
+
+def cpu_baseline(seconds: float):
+    """The reference's own CPU GEMV op (oracle/_ref build of bitnet_gemv.cpp; OpenMP over rows as in
+    torch_extension_cpu.cpp:355-366) on the same four shapes; falls back to the C restatement."""
+    from oracle import bitnet_oracle as orc
+    from oracle import refbind
+
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
+    os.environ["OMP_NUM_THREADS"] = str(threads)
+    kind = "reference"
+    if refbind.RefLib.exists(refbind.REF_AVX2):
+        lib = refbind.RefLib(refbind.REF_AVX2)
+        run = lambda p, a, out: lib.gemv(p, a, 1.0, out)  # noqa: E731
+    else:
+        kind = "port"
+        c = refbind.OracleC()
+        run = lambda p, a, out: c.gemm(p, a, 1.0)  # noqa: E731
+    rng = np.random.default_rng(1001)
+    total_bytes, total_t, reps_done = 0, 0.0, []
+    for n, k in GEMV_SHAPES:
+        packed = orc.pack_i2s(orc.random_ternary(rng, n, k))
+        a = orc.random_int8(rng, 1, k)[0]
+        out = np.zeros(n, np.float32)
+        run(packed, a, out)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds / len(GEMV_SHAPES):
+            run(packed, a, out)
+            reps += 1
+        dt = time.perf_counter() - t0
+        total_bytes += gemv_bytes(1, n, k) * reps
+        total_t += dt
+        reps_done.append(reps)
+    cpu_model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(total_bytes / total_t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": f"reference I2_S GEMV op (AVX2, OpenMP {threads} threads) on the 4 BitNet-2B decode shapes, "
+                  f"{'/'.join(map(str, reps_done))} calls each over {seconds:.0f} s, same byte formula; "
+                  f"host CPU: {cpu_model}",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the hot path shards by output rows with no collective on the decode path, "
+              "so run one process per GPU.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    from oracle import bitnet_oracle as orc
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = Launcher(pkg, torch)
+    rng = np.random.default_rng(1000)
+
+    # ---- batch-1 decode GEMV at the four 2B shapes, rotated weights ----------------
+    shapes = []
+    for idx, (n, k) in enumerate(GEMV_SHAPES):
+        r = np.random.default_rng(1000 + idx)
+        packed = torch.from_numpy(orc.pack_i2s(orc.random_ternary(r, n, k))).to(dev)
+        copies = [packed.clone() for _ in range(N_COPIES)]
+        a = torch.from_numpy(orc.random_int8(r, 1, k)).to(dev)
+        a_scale = torch.from_numpy(orc.log_uniform(r, 1)).to(dev)
+        ws = torch.from_numpy(orc.log_uniform(r, 1)).to(dev)
+        out = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+        calls = [L.linear_args("wfb_linear_i2s", c, n, k, a, 1, a_scale, ws, out) for c in copies]
+        shapes.append(dict(n=n, k=k, calls=calls, bytes=gemv_bytes(1, n, k), copies=copies))
+    torch.cuda.synchronize()
+
+    per_shape = []
+    for s in shapes:
+        ms = timed(torch, [[c] for c in s["calls"]], args.steps, args.warmup)
+        gbs = s["bytes"] / (ms * 1e-3) / 1e9
+        per_shape.append({"N": s["n"], "K": s["k"], "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                          "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+    step_fns = [[s["calls"][i] for s in shapes] for i in range(N_COPIES)]
+    ms_step = timed(torch, step_fns, args.steps, args.warmup)
+    step_bytes = sum(s["bytes"] for s in shapes)
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    dom = max(range(len(shapes)), key=lambda i: per_shape[i]["us"])  # dominant kernel: longest launch
+    d = per_shape[dom]
+    roofline = {"bound": "hbm", "achieved": round(shapes[dom]["bytes"] / (d["us"] * 1e-6) / 1e9, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(d["frac_hbm_peak"], 4), "traffic": None,
+                "kernel": f"gemv_i2s M=1 N={d['N']} K={d['K']}",
+                "bytes_per_launch": shapes[dom]["bytes"]}
+
+    # ---- prefill GEMM at M=2048 ----------------------------------------------------
+    prefill = []
+    for n, k in PREFILL_SHAPES:
+        m = 2048
+        r = np.random.default_rng(3000 + n)
+        packed = torch.from_numpy(orc.pack_i2s(orc.random_ternary(r, n, k))).to(dev)
+        a = torch.from_numpy(orc.random_int8(r, m, k)).to(dev)
+        a_scale = torch.from_numpy(orc.log_uniform(r, m)).to(dev)
+        ws = torch.from_numpy(orc.log_uniform(r, 1)).to(dev)
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        call = L.linear_args("wfb_linear_i2s", packed, n, k, a, m, a_scale, ws, out)
+        ms = timed(torch, [[call]], max(10, args.steps // 10), 3)
+        tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        prefill.append({"M": m, "N": n, "K": k, "us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
+                        "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)})
+
+    # ---- fused RMSNorm + per-token quant (configs[2] input distribution) -----------------------
+    normq = []
+    for m, h in ((1, 2560), (2048, 2560), (16, 6912)):
+        r = np.random.default_rng(5000 + m + h)
+        x = torch.from_numpy(orc.outlier_hidden(r, m, h)).to(torch.bfloat16).to(dev)
+        g = torch.from_numpy((1 + 0.1 * r.standard_normal(h)).astype(np.float32)).to(torch.bfloat16).to(dev)
+        q = torch.empty((m, h), dtype=torch.int8, device=dev)
+        sc = torch.empty(m, dtype=torch.float32, device=dev)
+        vp = ctypes.c_void_p
+        nargs = (vp(x.data_ptr()), 1, h, vp(g.data_ptr()), 1, ctypes.c_float(1e-6), m, h, vp(q.data_ptr()), h, h,
+                 vp(sc.data_ptr()), L.stream)
+        f = L.lib.wfb_rmsnorm_quant_i8
+        ms = timed(torch, [[lambda: f(*nargs)]], max(20, args.steps // 4), 5)
+        nb = 2 * m * h + 2 * h + m * h + 4 * m
+        normq.append({"M": m, "H": h, "us": round(ms * 1e3, 3), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1)})
+
+    sweep = None
+    if args.sweep:
+        sweep = []
+        for n, k in ((2560, 2560), (2560, 6912), (13824, 2560)):
+            r = np.random.default_rng(6000 + n + k)
+            base = torch.from_numpy(orc.pack_i2s(orc.random_ternary(r, n, k))).to(dev)
+            copies = [base.clone() for _ in range(max(8, int(1.2e9 // (n * k // 4) // 4)))]
+            for m in (1, 2, 4, 8, 16, 32, 64):
+                a = torch.from_numpy(orc.random_int8(r, m, k)).to(dev)
+                a_scale = torch.ones(m, dtype=torch.float32, device=dev)
+                ws = torch.ones(1, dtype=torch.float32, device=dev)
+                out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+                calls = [[L.linear_args("wfb_linear_i2s", c, n, k, a, m, a_scale, ws, out)] for c in copies]
+                ms = timed(torch, calls, args.steps, 5)
+                gbs = gemv_bytes(m, n, k) / (ms * 1e-3) / 1e9
+                sweep.append({"M": m, "N": n, "K": k, "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                              "TOPS": round(2 * m * n * k / (ms * 1e-3) / 1e12, 2)})
+            del copies
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: BitLinear decode GEMV, BitNet-2B shapes 2560x2560, 3200x2560, "
+                               "13824x2560, 2560x6912 (N x K), batch 1, one kernel each, ternary P(0)=0.33 "
+                               "packed I2_S, int8 U[-127,127], 64 rotated weight copies (1.1 GB)",
+                   "global_batch": 1, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "gemv_per_shape": per_shape,
+        "prefill_gemm": prefill,
+        "rmsnorm_quant": normq,
+    }
+    if sweep is not None:
+        line["batched_sweep"] = sweep
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,142 @@
+/*
+ * wfbitnet.h - C ABI of the MI355X (gfx950) ternary BitLinear hot path.
+ *
+ * One shared library, libwfbitnet.so, built from wrinklefree-monorepo_amd/csrc.
+ * Every entry point:
+ *   - takes plain device pointers and sizes (no torch or HIP types in the signature);
+ *   - takes the HIP stream as `void* stream` (NULL = the default stream) and only enqueues
+ *     work on it: nothing synchronises the host, nothing allocates device memory;
+ *   - returns WFB_OK (0) or a negative status; the message of the last failure on the
+ *     calling thread is returned by wfb_last_error().
+ *
+ * Packed weight layout ("I2_S", 2 bits per ternary weight, per-tensor fp32 scale):
+ *   qweight is uint8 [N, K/4], row-major, K a multiple of 128.  Each row is split into
+ *   128-weight blocks of 32 bytes; byte j of block b holds
+ *       bits 7:6 -> k = 128b + j        bits 5:4 -> k = 128b + 32 + j
+ *       bits 3:2 -> k = 128b + 64 + j   bits 1:0 -> k = 128b + 96 + j
+ *   with code = w + 1 (00 -> -1, 01 -> 0, 10 -> +1; 11 never produced).
+ *   Reference: packages/inference/scripts/convert_to_sglkernel.py:55-61, 96-111 and
+ *   packages/inference/extern/sglang-bitnet/sgl-kernel/csrc/inference/bitnet_engine.cpp:51-81.
+ *
+ * Reference citations below use
+ *   SGB = packages/inference/extern/sglang-bitnet
+ *   WF  = packages/training/src/wrinklefree
+ */
+#ifndef WFBITNET_H
+#define WFBITNET_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WFB_QK_I2S 128          /* weights per I2_S block (SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.h:29) */
+#define WFB_ABSMEAN_WS_DOUBLES 1024 /* workspace size (in doubles) of wfb_weight_absmean */
+#define WFB_NORM_MAX_H 16384    /* largest row length of the per-token quantisers */
+
+/* status codes */
+#define WFB_OK 0
+#define WFB_EINVAL (-1)         /* bad argument (shape, dtype, alignment, null pointer) */
+#define WFB_EHIP (-2)           /* the HIP runtime reported an error */
+
+/* element types of floating-point buffers */
+#define WFB_F32 0
+#define WFB_BF16 1
+#define WFB_F16 2
+
+/* Message of the last failed call on this thread ("" if none).  Replaces the thread-local
+ * error of SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:86,167-169 (bitnet_get_error). */
+const char* wfb_last_error(void);
+
+/* Library ABI version (bumped on any signature change). */
+int wfb_version(void);
+
+/* ---- a1: offline pack -------------------------------------------------------------------- */
+
+/* scale_dev[0] = mean(|w|) over numel elements, summed in fp64 in a fixed order (deterministic),
+ * rounded to fp32; a mean below 1e-8 becomes 1.0.  workspace: >= WFB_ABSMEAN_WS_DOUBLES doubles
+ * of device memory.  Replaces the scale of pack_ternary_sglkernel
+ * (packages/inference/scripts/convert_to_sglkernel.py:81-85). */
+int wfb_weight_absmean(const void* w, int w_dtype, int64_t numel, float* scale_dev,
+                       double* workspace, void* stream);
+
+/* qweight[N, K/4] = I2_S pack of clamp(round_half_even(w / scale), -1, 1), w row-major [N, K]
+ * (row stride ldw elements).  scale is read from scale_dev[0].  Replaces the quantise + pack
+ * loop of pack_ternary_sglkernel (convert_to_sglkernel.py:87-111). */
+int wfb_pack_i2s(const void* w, int w_dtype, int64_t n, int64_t k, int64_t ldw,
+                 const float* scale_dev, uint8_t* qweight, void* stream);
+
+/* w_out[N, K] int8 in {-1, 0, +1} from qweight (inspection / format conversion).
+ * Same decode as the scalar reference dot, bitnet_engine.cpp:51-81. */
+int wfb_unpack_i2s(const uint8_t* qweight, int64_t n, int64_t k, int8_t* w_out, void* stream);
+
+/* ---- a2: activation quantisation ------------------------------------------------------- */
+
+/* Per-token absmax int8 quantisation of x [M, H] (row stride ldx elements) into q [M, k_pad]
+ * (row stride ldq bytes; columns H..k_pad-1 are written as 0) and a_scale[M]:
+ *   mx = max|x_row| (mx < 1e-6 -> 1), a_scale = mx / 127, q = sat_i8(rint(x * (127 / mx))).
+ * Row-wise restatement of quantize_activations_i8, SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:880-1135
+ * (vector path: round half to even, saturating pack).  H <= WFB_NORM_MAX_H. */
+int wfb_quantize_act_i8(const void* x, int x_dtype, int64_t m, int64_t h, int64_t ldx,
+                        int8_t* q, int64_t k_pad, int64_t ldq, float* a_scale, void* stream);
+
+/* Same quantiser with ONE scale for the whole buffer of numel elements (a_scale[0]), as the
+ * reference op bitnet_quantize_activations_cpu does (SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:409-426). */
+int wfb_quantize_act_i8_tensor(const void* x, int x_dtype, int64_t numel, int8_t* q,
+                               float* a_scale, void* stream);
+
+/* ---- a3: RMSNorm / SubLN fused with a2 --------------------------------------------------- */
+
+/* y = x * (1 / sqrt(sum(x^2) / H + eps)) * gamma in fp32, then the per-token quantiser of
+ * wfb_quantize_act_i8 on y.  Sum of squares in a fixed order: each of 256 threads accumulates
+ * the elements (it*256 + t)*8 + e, it ascending, e = 0..7, then a xor-butterfly over each wave
+ * (offsets 32,16,8,4,2,1) and the 4 wave sums added in wave order.  gamma may be NULL (no
+ * affine).  Replaces SubLN.forward / RMSNorm.forward (WF/models/subln.py:42-59, 64-97) followed
+ * by activation quantisation (WF/models/bitlinear.py:66-84).  H % 8 == 0, H <= WFB_NORM_MAX_H. */
+int wfb_rmsnorm_quant_i8(const void* x, int x_dtype, int64_t ldx, const void* gamma, int gamma_dtype,
+                         float eps, int64_t m, int64_t h, int8_t* q, int64_t k_pad, int64_t ldq,
+                         float* a_scale, void* stream);
+
+/* ---- a4 / a5 / a6: ternary BitLinear forward --------------------------------------------- */
+
+/* acc[m, n] = sum_k w[n, k] * act[m, k]        (int32, exact)
+ * y[m, n]   = ((float)acc * w_scale) * a_scale[m]  (+ bias[n]), stored as out_dtype
+ *
+ *   qweight : uint8 [N, K/4] I2_S, 16-byte aligned
+ *   act     : int8  [M, K] with row stride lda bytes (lda % 16 == 0, 16-byte aligned)
+ *   a_scale : fp32 [M] device, or NULL for 1.0
+ *   w_scale_dev : fp32 [1] device, or NULL to use the host value w_scale (no host sync either way)
+ *   bias    : [N] of bias_dtype, or NULL
+ *   out     : [M, N] of out_dtype (WFB_F32 or WFB_BF16) with row stride ldo elements, or NULL
+ *   acc_out : int32 [M, N] with row stride ldo, or NULL (parity / debugging)
+ *
+ * wfb_linear_i2s picks the kernel from (M, N, K).  wfb_gemv_i2s forces the VALU decode GEMV
+ * (M <= 8) and wfb_gemm_i2s forces the int8-MFMA GEMM (any M).  All three give identical acc.
+ * Replace bitnet_gemv_cpu / bitnet_gemm_cpu (SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:331-406,
+ * kernels SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:325-874) and the rescale of
+ * BitNetLinearMethod.apply (SGB/python/sglang/srt/layers/quantization/bitnet.py:232-253). */
+int wfb_linear_i2s(const uint8_t* qweight, int64_t n, int64_t k,
+                   const int8_t* act, int64_t m, int64_t lda,
+                   const float* a_scale, const float* w_scale_dev, float w_scale,
+                   const void* bias, int bias_dtype,
+                   void* out, int out_dtype, int64_t ldo, int32_t* acc_out, void* stream);
+
+int wfb_gemv_i2s(const uint8_t* qweight, int64_t n, int64_t k,
+                 const int8_t* act, int64_t m, int64_t lda,
+                 const float* a_scale, const float* w_scale_dev, float w_scale,
+                 const void* bias, int bias_dtype,
+                 void* out, int out_dtype, int64_t ldo, int32_t* acc_out, void* stream);
+
+int wfb_gemm_i2s(const uint8_t* qweight, int64_t n, int64_t k,
+                 const int8_t* act, int64_t m, int64_t lda,
+                 const float* a_scale, const float* w_scale_dev, float w_scale,
+                 const void* bias, int bias_dtype,
+                 void* out, int out_dtype, int64_t ldo, int32_t* acc_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WFBITNET_H */

@@ -1,0 +1,274 @@
+"""CPU oracle for the ternary BitLinear hot path -- TEST INFRASTRUCTURE ONLY.
+
+A numpy restatement of the reference algorithm.  Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg may use this module, and only as the checker; no product code imports it.
+
+Reference files (paths under the reference repository):
+  PACK = packages/inference/scripts/convert_to_sglkernel.py
+  GEMV = packages/inference/extern/sglang-bitnet/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp
+  ENG  = packages/inference/extern/sglang-bitnet/sgl-kernel/csrc/inference/bitnet_engine.cpp
+  OPS  = packages/inference/extern/sglang-bitnet/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp
+  METH = packages/inference/extern/sglang-bitnet/python/sglang/srt/layers/quantization/bitnet.py
+  SUBLN = packages/training/src/wrinklefree/models/subln.py
+
+How each function is pinned (see tests/test_oracle.py):
+  absmean_scale        KAT [1,-2,3,-4] -> 2.5; torch's own fp32 mean (the reference's library call).
+  ternarize / pack     byte KATs 0x00/0x55/0xAA and the single-weight KAT 0x95; the reference's
+                       compiled kernels (oracle/_ref) and its golden fixtures; round trips.
+  quantize_*           closed-form special cases (zero row, spike -> +-127, exact .5 ties) and the
+                       reference's compiled quantize_activations_i8 (golden fixtures).
+  rmsnorm_quant        float64 recomputation (codes may differ only at near-ties) and a brute
+                       force of the stated summation order on small rows.
+  accumulate           the reference's compiled bitnet_vec_dot_i2_i8 / bitnet_gemm_i2_i8 (golden
+                       fixtures and oracle/_ref), int64 brute force, and the identity
+                       sum(code*a) - sum(a) = sum(w*a).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+QK_I2_S = 128  # GEMV bitnet_gemv.h:29
+F32 = np.float32
+
+
+# ---- a1: weight scale, ternarisation, I2_S layout ----------------------------------------------
+
+
+def absmean_scale(w: np.ndarray) -> np.float32:
+    """mean(|W|) rounded to fp32 from an exact-enough float64 sum; < 1e-8 -> 1.0 (PACK:81-85)."""
+    s = F32(np.abs(w.astype(np.float64)).sum() / w.size) if w.size else F32(0.0)
+    return F32(1.0) if float(s) < 1e-8 else s
+
+
+def absmean_scale_device_order(w: np.ndarray, blocks: int = 1024) -> np.float32:
+    """The device kernel's deterministic fp64 summation order (stated in include/wfbitnet.h)."""
+    x = np.abs(w.astype(np.float32).ravel()).astype(np.float64)
+    n = x.size
+    stride = blocks * 256
+    pad = (-n) % stride
+    xp = np.concatenate([x, np.zeros(pad)]).reshape(-1, blocks, 256)
+    acc = np.zeros((blocks, 256))
+    for row in xp:  # thread-sequential over grid-stride iterations
+        acc = acc + row
+    part = acc
+    o = 128
+    while o >= 1:  # tree in shared memory
+        part = part[:, :o] + part[:, o:2 * o]
+        o //= 2
+    partial = part[:, 0]
+    fin = np.zeros(256)
+    for i in range(0, blocks, 256):
+        fin = fin + partial[i:i + 256]
+    o = 128
+    while o >= 1:
+        fin = fin[:o] + fin[o:2 * o]
+        o //= 2
+    s = F32(fin[0] / n) if n else F32(0.0)
+    return F32(1.0) if float(s) < 1e-8 else s
+
+
+def ternarize(w: np.ndarray, scale) -> np.ndarray:
+    """int8 q = clamp(round_half_even(W / s), -1, 1) in fp32 (PACK:87-88)."""
+    q = np.rint(w.astype(F32) / F32(scale))
+    return np.clip(q, -1, 1).astype(np.int8)
+
+
+def pack_i2s(q: np.ndarray) -> np.ndarray:
+    """I2_S layout of ternary q [N, K] -> uint8 [N, K/4] (PACK:96-111).
+
+    Byte j of 128-weight block b: code[128b+j]<<6 | code[128b+32+j]<<4 | code[128b+64+j]<<2 | code[128b+96+j],
+    code = q + 1.
+    """
+    n, k = q.shape
+    if k % QK_I2_S:
+        raise ValueError(f"K ({k}) must be multiple of {QK_I2_S}")
+    c = (q.astype(np.int16) + 1).astype(np.uint8).reshape(n, k // QK_I2_S, 4, 32)
+    b = (c[:, :, 0] << 6) | (c[:, :, 1] << 4) | (c[:, :, 2] << 2) | c[:, :, 3]
+    return b.reshape(n, k // 4).astype(np.uint8)
+
+
+def unpack_i2s(packed: np.ndarray) -> np.ndarray:
+    """int8 weights [N, K] from I2_S (the scalar reference decode, ENG:51-81)."""
+    n, kb = packed.shape
+    p = packed.reshape(n, kb // 32, 1, 32)
+    shifts = np.array([6, 4, 2, 0], dtype=np.uint8).reshape(1, 1, 4, 1)
+    codes = (p >> shifts) & 3
+    return (codes.astype(np.int8) - 1).reshape(n, kb * 4)
+
+
+def pack_ternary(w: np.ndarray, scale=None):
+    """(packed, scale): the whole of pack_ternary_sglkernel (PACK:51-123)."""
+    s = absmean_scale(w) if scale is None else F32(scale)
+    return pack_i2s(ternarize(w, s)), s
+
+
+# ---- a2: activation quantisation ---------------------------------------------------------------
+
+
+def quantize_row_params(mx: np.ndarray):
+    """(scale, inv) from the absmax, fp32: max < 1e-6 -> 1 (GEMV:909-915)."""
+    mx = np.where(mx < F32(1e-6), F32(1.0), mx).astype(F32)
+    return (mx / F32(127.0)).astype(F32), (F32(127.0) / mx).astype(F32)
+
+
+def quantize_with_inv(x: np.ndarray, inv) -> np.ndarray:
+    """sat_i8(round_half_even(x * inv)) in fp32 (GEMV:917-944, vector path)."""
+    return np.clip(np.rint(x.astype(F32) * inv), -128, 127).astype(np.int8)
+
+
+def quantize_per_token(x: np.ndarray, k_pad: int | None = None):
+    """Row-wise quantize_activations_i8: (q int8 [M, k_pad], scale fp32 [M])."""
+    x = np.asarray(x, dtype=F32).reshape(-1, x.shape[-1])
+    mx = np.abs(x).max(axis=1) if x.shape[1] else np.zeros(x.shape[0], F32)
+    scale, inv = quantize_row_params(mx.astype(F32))
+    q = quantize_with_inv(x, inv[:, None])
+    if k_pad is not None and k_pad > x.shape[1]:
+        q = np.concatenate([q, np.zeros((q.shape[0], k_pad - x.shape[1]), np.int8)], axis=1)
+    return q, scale
+
+
+def quantize_per_tensor(x: np.ndarray):
+    """bitnet_quantize_activations_cpu: ONE scale for the flattened buffer (OPS:409-426)."""
+    x = np.asarray(x, dtype=F32)
+    mx = F32(np.abs(x).max()) if x.size else F32(0.0)
+    scale, inv = quantize_row_params(np.array([mx], F32))
+    return quantize_with_inv(x, inv[0]), scale
+
+
+# ---- a3: RMSNorm / SubLN fused with the quantiser ----------------------------------------------
+
+
+def _sum_squares_device_order(x: np.ndarray, tpb: int = 256, vec: int = 8) -> np.ndarray:
+    """fp32 sum of squares per row in the kernel's stated order (thread-sequential over
+    (iteration, element), xor butterfly per wave, waves added in order)."""
+    m, h = x.shape
+    per_it = tpb * vec
+    its = (h + per_it - 1) // per_it
+    xp = np.zeros((m, its * per_it), F32)
+    xp[:, :h] = x
+    xp = xp.reshape(m, its, tpb, vec)
+    acc = np.zeros((m, tpb), F32)
+    for it in range(its):
+        for e in range(vec):
+            v = xp[:, it, :, e]
+            acc = (acc + (v * v).astype(F32)).astype(F32)
+    waves = acc.reshape(m, tpb // 64, 64)
+    lanes = np.arange(64)
+    o = 32
+    while o >= 1:
+        waves = (waves + waves[:, :, lanes ^ o]).astype(F32)
+        o //= 2
+    tot = waves[:, 0, 0]
+    for w in range(1, tpb // 64):
+        tot = (tot + waves[:, w, 0]).astype(F32)
+    return tot
+
+
+def rmsnorm(x: np.ndarray, gamma=None, eps: float = 1e-6, exact_order: bool = True) -> np.ndarray:
+    """y = x * (1 / sqrt(sum(x^2)/H + eps)) * gamma in fp32 (SUBLN:42-59; ENG:172-183 for fp32 form)."""
+    x = np.asarray(x, dtype=F32)
+    h = x.shape[1]
+    if exact_order:
+        ss = _sum_squares_device_order(x)
+    else:
+        ss = (x.astype(np.float64) ** 2).sum(axis=1).astype(F32)
+    r = (F32(1.0) / np.sqrt((ss / F32(h)).astype(F32) + F32(eps))).astype(F32)
+    y = (x * r[:, None]).astype(F32)
+    if gamma is not None:
+        y = (y * np.asarray(gamma, dtype=F32)[None, :]).astype(F32)
+    return y
+
+
+def rmsnorm_quant(x: np.ndarray, gamma=None, eps: float = 1e-6, k_pad: int | None = None, exact_order: bool = True):
+    """Fused SubLN + per-token int8 quantisation: (q int8 [M, k_pad], scale fp32 [M])."""
+    return quantize_per_token(rmsnorm(x, gamma, eps, exact_order), k_pad)
+
+
+# ---- a4 / a5 / a6: accumulators and rescale ---------------------------------------------------
+
+
+def accumulate(packed: np.ndarray, a: np.ndarray) -> np.ndarray:
+    """acc[m, n] = sum_k w[n, k] * a[m, k] as int64 (exact: float64 products/sums stay < 2^53)."""
+    w = unpack_i2s(packed).astype(np.float64)
+    a2 = np.atleast_2d(a).astype(np.float64)
+    return np.rint(a2 @ w.T).astype(np.int64)
+
+
+def accumulate_bruteforce(packed: np.ndarray, a: np.ndarray) -> np.ndarray:
+    """Integer-only brute force (small shapes): per row, per 128-block, the scalar loop of ENG:51-81."""
+    n, kb = packed.shape
+    a2 = np.atleast_2d(a).astype(np.int64)
+    out = np.zeros((a2.shape[0], n), np.int64)
+    for r in range(n):
+        for blk in range(kb // 32):
+            for j in range(32):
+                byte = int(packed[r, 32 * blk + j])
+                for f, shift in enumerate((6, 4, 2, 0)):
+                    w = ((byte >> shift) & 3) - 1
+                    out[:, r] += w * a2[:, 128 * blk + 32 * f + j]
+    return out
+
+
+def accumulate_code_identity(packed: np.ndarray, a: np.ndarray) -> np.ndarray:
+    """sum_k code * a - sum_k a, the form the SIMD kernel evaluates (GEMV:346-402, 685)."""
+    codes = (unpack_i2s(packed).astype(np.int64) + 1).astype(np.float64)
+    a2 = np.atleast_2d(a).astype(np.float64)
+    return np.rint(a2 @ codes.T).astype(np.int64) - a2.sum(axis=1, keepdims=True).astype(np.int64)
+
+
+def rescale(acc: np.ndarray, w_scale, a_scale=None, bias=None) -> np.ndarray:
+    """y = (float(acc) * w_scale) * a_scale[m] (+ bias) in fp32 (GEMV:846; METH:241, 253)."""
+    y = (acc.astype(F32) * F32(w_scale)).astype(F32)
+    if a_scale is not None:
+        y = (y * np.asarray(a_scale, F32).reshape(-1, 1)).astype(F32)
+    if bias is not None:
+        y = (y + np.asarray(bias, F32).reshape(1, -1)).astype(F32)
+    return y
+
+
+def f32_to_bf16_bits(y: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (uint16)."""
+    u = np.asarray(y, F32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7F800000) == 0x7F800000
+    nan &= (u & 0x007FFFFF) != 0
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(F32)
+
+
+def bitlinear_forward(x: np.ndarray, packed: np.ndarray, w_scale, bias=None):
+    """Quantised BitLinear forward (per-token activations): (y fp32 [M, N], acc int64, q, a_scale)."""
+    q, a_scale = quantize_per_token(x, k_pad=packed.shape[1] * 4)
+    acc = accumulate(packed, q)
+    return rescale(acc, w_scale, a_scale, bias), acc, q, a_scale
+
+
+# ---- synthetic inputs of the benchmark configurations -------------------------------------------
+
+
+def random_ternary(rng: np.random.Generator, n: int, k: int, p_zero: float = 0.33) -> np.ndarray:
+    """i.i.d. ternary with P(0) = p_zero and P(+1) = P(-1)."""
+    u = rng.random((n, k))
+    half = (1.0 - p_zero) / 2.0
+    return np.where(u < half, -1, np.where(u < half + p_zero, 0, 1)).astype(np.int8)
+
+
+def random_int8(rng: np.random.Generator, m: int, k: int) -> np.ndarray:
+    """int8 uniform on [-127, 127]."""
+    return rng.integers(-127, 128, size=(m, k), dtype=np.int16).astype(np.int8)
+
+
+def log_uniform(rng: np.random.Generator, size=None, lo: float = 1e-3, hi: float = 1.0):
+    return np.exp(rng.uniform(np.log(lo), np.log(hi), size=size)).astype(F32)
+
+
+def outlier_hidden(rng: np.random.Generator, m: int, h: int, frac: float = 0.01, mag: float = 20.0) -> np.ndarray:
+    """N(0,1) hidden states with a fraction replaced by +-mag (random sign)."""
+    x = rng.standard_normal((m, h)).astype(F32)
+    mask = rng.random((m, h)) < frac
+    x[mask] = np.where(rng.random(mask.sum()) < 0.5, -mag, mag).astype(F32)
+    return x

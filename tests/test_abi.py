@@ -1,0 +1,102 @@
+"""CPU checks of the C-ABI library: it loads, exports every declared symbol, and rejects bad
+arguments on the host (before any GPU work) with the reference's error conditions."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "wfbitnet.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+(wfb_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("wfb_linear_i2s", "wfb_gemv_i2s", "wfb_gemm_i2s", "wfb_pack_i2s", "wfb_rmsnorm_quant_i8",
+              "wfb_quantize_act_i8", "wfb_quantize_act_i8_tensor", "wfb_weight_absmean", "wfb_unpack_i2s",
+              "wfb_last_error", "wfb_version"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg._lib.load()
+    for s in declared_symbols():
+        assert hasattr(lib, s), f"{s} declared in include/wfbitnet.h but not exported"
+    assert set(pkg._lib.SIGNATURES) | {"wfb_last_error", "wfb_version"} == set(declared_symbols())
+    assert lib.wfb_version() == 1
+
+
+def _linear_status(pkg, fn="wfb_linear_i2s", n=256, k=256, m=1, lda=None, w=16, a=16, out=16, acc=0,
+                   out_dtype=1, ldo=None):
+    vp = ctypes.c_void_p
+    return pkg._lib.status(fn, vp(w) if w else None, n, k, vp(a) if a else None, m, k if lda is None else lda,
+                           None, None, 1.0, None, 0, vp(out) if out else None, out_dtype,
+                           n if ldo is None else ldo, vp(acc) if acc else None, None)
+
+
+def test_k_not_multiple_of_128_rejected(pkg):
+    assert _linear_status(pkg, k=200) == -1
+    assert "must be multiple of 128" in pkg._lib.last_error()
+
+
+def test_argument_errors(pkg):
+    assert _linear_status(pkg, w=0) == -1 and "null" in pkg._lib.last_error()
+    assert _linear_status(pkg, w=8) == -1 and "aligned" in pkg._lib.last_error()
+    assert _linear_status(pkg, lda=100) == -1 and "stride" in pkg._lib.last_error()
+    assert _linear_status(pkg, out=0, acc=0) == -1
+    assert _linear_status(pkg, out_dtype=2) == -1 and "dtype" in pkg._lib.last_error()
+    assert _linear_status(pkg, ldo=10) == -1
+    assert _linear_status(pkg, fn="wfb_gemv_i2s", m=4) == -1 and "GEMV" in pkg._lib.last_error()
+
+
+def test_empty_batch_is_a_noop(pkg):
+    # M == 0 returns before touching any pointer or the GPU
+    assert _linear_status(pkg, m=0, w=0, a=0) == 0
+    assert pkg._lib.last_error() == ""
+
+
+def test_other_entry_points_validate(pkg):
+    vp = ctypes.c_void_p
+    st = pkg._lib.status
+    assert st("wfb_pack_i2s", vp(16), 0, 4, 100, 100, vp(16), vp(16), None) == -1
+    assert st("wfb_pack_i2s", vp(16), 9, 4, 128, 128, vp(16), vp(16), None) == -1  # bad dtype
+    assert st("wfb_rmsnorm_quant_i8", vp(16), 1, 100, None, 0, 1e-6, 1, 100, vp(16), 100, 104, vp(16), None) == -1
+    assert "multiple of 8" in pkg._lib.last_error()
+    assert st("wfb_quantize_act_i8", vp(16), 0, 1, 20000, 20000, vp(16), 20000, 20000, vp(16), None) == -1
+    assert st("wfb_quantize_act_i8", vp(16), 0, 0, 64, 64, None, 64, 64, None, None) == 0
+    assert st("wfb_weight_absmean", vp(16), 0, 10, None, None, None) == -1
+    assert st("wfb_unpack_i2s", vp(16), 4, 130, vp(16), None) == -1
+
+
+def test_python_wrappers_keep_reference_errors(pkg):
+    # ValueError for the K % 128 / shape checks of the reference wrappers (bitnet.py:93-104, 131-135)
+    with pytest.raises(ValueError):
+        pkg.bitnet_gemv(torch.zeros((4, 25), dtype=torch.uint8), torch.zeros(100, dtype=torch.int8), 1.0)
+    with pytest.raises(ValueError):
+        pkg.bitnet_gemv(torch.zeros((4, 32), dtype=torch.uint8), torch.zeros(100, dtype=torch.int8), 1.0)
+    with pytest.raises(ValueError):
+        pkg.bitnet_gemm(torch.zeros((4, 25), dtype=torch.uint8), torch.zeros((2, 100), dtype=torch.int8), 1.0)
+
+
+def test_no_cpu_fallback(pkg):
+    # CPU tensors are refused loudly: the product path has no eager / CPU implementation
+    with pytest.raises(RuntimeError, match="HIP device"):
+        pkg.bitnet_gemv(torch.zeros((4, 32), dtype=torch.uint8), torch.zeros(128, dtype=torch.int8), 1.0)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        pkg.quantize_activations_i8_per_token(torch.zeros((2, 128)))
+    with pytest.raises(RuntimeError, match="HIP device"):
+        pkg.BitLinear(128, 64)(torch.zeros(2, 128))
+
+
+def test_product_does_not_import_oracle():
+    pkg_dir = ROOT / "wrinklefree-monorepo_amd"
+    for f in list(pkg_dir.rglob("*.py")) + list(pkg_dir.rglob("*.hip")) + list(pkg_dir.rglob("*.h")):
+        text = f.read_text()
+        assert "import oracle" not in text and "from oracle" not in text and "oracle/" not in text, f

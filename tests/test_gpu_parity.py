@@ -1,0 +1,320 @@
+"""GPU parity of every hot-path kernel against the CPU oracle, through the C ABI.
+
+Bars: int8 codes, packed bytes and int32 accumulators bit-exact; fp32 outputs bit-exact (same
+operation order as the oracle); bf16 outputs within 1e-2 relative (and here also bit-exact).
+Full BASELINE shapes are checked exactly for the GEMV/batched sweep; the large prefill GEMMs are
+checked exactly on sampled token rows plus a whole-output checksum identity.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bitnet_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+SHAPES_2B = [(2560, 2560), (3200, 2560), (13824, 2560), (2560, 6912)]  # (N, K)
+BF16_RTOL = 1e-2
+
+
+def _packed(rng, n, k):
+    q = orc.random_ternary(rng, n, k)
+    return orc.pack_i2s(q)
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _ref_acc(packed, a):
+    """Exact accumulators via an fp32 GEMM of the unpacked weights (partial sums < 2^24)."""
+    w = orc.unpack_i2s(packed).astype(np.float32)
+    return (np.atleast_2d(a).astype(np.float32) @ w.T).astype(np.int64)
+
+
+def _check_linear(pkg, dev, packed, a, w_scale, a_scale, kernel="auto", bias=None, check_fp32=True):
+    n, k = packed.shape[0], packed.shape[1] * 4
+    pw, pa, ps = _t(packed, dev), _t(a, dev), _t(a_scale, dev)
+    pb = None if bias is None else _t(bias, dev)
+    y, acc = pkg.bitnet_linear(pw, pa, float(w_scale), a_scale=ps, bias=pb, return_acc=True, kernel=kernel)
+    acc_ref = _ref_acc(packed, a)
+    acc_g = acc.cpu().numpy().astype(np.int64)
+    assert acc_g.shape == acc_ref.shape
+    bad = np.argwhere(acc_g != acc_ref)
+    assert bad.size == 0, f"{len(bad)} accumulator mismatches, first at {bad[:3].tolist()}"
+    y_ref = orc.rescale(acc_ref, w_scale, a_scale, bias)
+    yb = y.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(yb, orc.f32_to_bf16_bits(y_ref)), "bf16 output bits differ"
+    yg = orc.bf16_bits_to_f32(yb)
+    rel = np.abs(yg - y_ref) / np.maximum(np.abs(y_ref), 1e-30)
+    assert float(rel[np.abs(y_ref) > 0].max(initial=0)) <= BF16_RTOL
+    if check_fp32:
+        y32 = pkg.bitnet_linear(pw, pa, float(w_scale), a_scale=ps, bias=pb, out_dtype=torch.float32, kernel=kernel)
+        assert np.array_equal(y32.cpu().numpy(), y_ref)
+
+
+# ---- a1: pack -------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("n,k", SHAPES_2B + [(576, 576), (1536, 576)])
+def test_pack_matches_oracle(pkg, dev, n, k):
+    rng = np.random.default_rng(n * 7 + k)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    kp = (k + 127) // 128 * 128
+    qw, scale = pkg.pack_ternary_i2s(_t(w, dev), k_pad=kp)
+    s = np.float32(scale.item())
+    assert s == orc.absmean_scale_device_order(w)
+    t = np.float32(torch.from_numpy(w).abs().mean().item())  # the reference's own fp32 mean
+    assert abs(float(s) - float(t)) <= float(np.spacing(t))
+    wpad = np.zeros((n, kp), np.float32)
+    wpad[:, :k] = w
+    packed_ref = orc.pack_i2s(orc.ternarize(wpad, s))
+    assert np.array_equal(qw.cpu().numpy(), packed_ref)
+    assert np.array_equal(pkg.unpack_i2s(qw).cpu().numpy(), orc.unpack_i2s(packed_ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_pack_half_inputs(pkg, dev, dtype):
+    rng = np.random.default_rng(3)
+    w = torch.from_numpy((rng.standard_normal((300, 512)) * 0.05).astype(np.float32)).to(dtype)
+    qw, scale = pkg.pack_ternary_i2s(w.to(dev))
+    wf = w.float().numpy()
+    s = np.float32(scale.item())
+    assert s == orc.absmean_scale_device_order(wf)
+    assert np.array_equal(qw.cpu().numpy(), orc.pack_i2s(orc.ternarize(wf, s)))
+
+
+def test_pack_given_scale_and_ties(pkg, dev):
+    # exact .5 ties under a given scale round half to even, like torch.round
+    w = np.tile(np.array([0.5, -0.5, 1.5, -1.5, 0.25, 2.0, -0.75, 0.0], np.float32), (4, 16))
+    qw, _ = pkg.pack_ternary_i2s(_t(w, dev), scale=torch.ones(1, device=dev))
+    assert np.array_equal(qw.cpu().numpy(), orc.pack_i2s(orc.ternarize(w, 1.0)))
+
+
+def test_absmean_tiny_weights(pkg, dev):
+    w = torch.full((8, 128), 1e-9, device=dev)
+    assert pkg.absmean_scale(w).item() == 1.0
+
+
+# ---- a2 / a3: activation quantisers ------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,h,kp", [(1, 2560, 2560), (7, 576, 640), (64, 6912, 6912), (3, 14336, 14336), (2, 100, 128)])
+def test_quant_per_token(pkg, dev, dtype, m, h, kp):
+    rng = np.random.default_rng(m * 1000 + h)
+    x = torch.from_numpy(orc.outlier_hidden(rng, m, h)).to(dtype)
+    q, s = pkg.quantize_activations_i8_per_token(x.to(dev), k_pad=kp)
+    q_ref, s_ref = orc.quantize_per_token(x.float().numpy(), k_pad=kp)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_quant_special_rows(pkg, dev):
+    x = np.zeros((4, 256), np.float32)
+    x[1, :8] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5]  # exact ties
+    x[2, 100] = -3.25  # single spike
+    x[3, :] = 5e-7  # below the 1e-6 floor
+    q, s = pkg.quantize_activations_i8_per_token(_t(x, dev))
+    q_ref, s_ref = orc.quantize_per_token(x)
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+    assert q[1, :8].tolist() == [127, 0, 2, 2, 0, -2, -2, 126]
+
+
+@pytest.mark.parametrize("numel", [1, 1000, 2560 * 16, 3 * 1000003])
+def test_quant_per_tensor(pkg, dev, numel):
+    rng = np.random.default_rng(numel)
+    x = (rng.standard_normal(numel) * 3).astype(np.float32)
+    q, s = pkg.quantize_activations_i8(_t(x, dev))
+    q_ref, s_ref = orc.quantize_per_tensor(x)
+    assert np.array_equal(q.cpu().numpy(), q_ref) and s.item() == s_ref[0]
+
+
+@pytest.mark.parametrize("gdtype", [None, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("m,h,kp", [(1, 576, 640), (16, 2560, 2560), (5, 6912, 6912), (64, 4096, 4096), (2, 1536, 1536)])
+def test_rmsnorm_quant(pkg, dev, gdtype, m, h, kp):
+    rng = np.random.default_rng(h + m)
+    x = torch.from_numpy(orc.outlier_hidden(rng, m, h)).to(torch.bfloat16)
+    g = None if gdtype is None else torch.from_numpy((1 + 0.1 * rng.standard_normal(h)).astype(np.float32)).to(gdtype)
+    q, s = pkg.rmsnorm_quantize_i8(x.to(dev), None if g is None else g.to(dev), eps=1e-6, k_pad=kp)
+    q_ref, s_ref = orc.rmsnorm_quant(x.float().numpy(), None if g is None else g.float().numpy(), 1e-6, k_pad=kp)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_rmsnorm_quant_fp32_input_eps(pkg, dev):
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((9, 2560)).astype(np.float32)
+    x[3] = 0.0  # zero row: y = 0, codes 0
+    q, s = pkg.rmsnorm_quantize_i8(_t(x, dev), None, eps=1e-5)
+    q_ref, s_ref = orc.rmsnorm_quant(x, None, 1e-5)
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+
+
+# ---- a4 / a5 / a6: GEMV, batched sweep, prefill GEMM ---------------------------------------------
+
+
+@pytest.mark.parametrize("n,k", SHAPES_2B)
+@pytest.mark.parametrize("m", [1, 2])
+def test_decode_gemv_2b_shapes(pkg, dev, n, k, m):
+    rng = np.random.default_rng(1000 + n + k + m)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    _check_linear(pkg, dev, packed, a, orc.log_uniform(rng), orc.log_uniform(rng, m), kernel="gemv")
+
+
+@pytest.mark.parametrize("n,k", [(2560, 2560), (2560, 6912), (13824, 2560)])
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16, 32, 64])
+def test_batched_sweep_mfma(pkg, dev, n, k, m):
+    rng = np.random.default_rng(2000 + n + k + m)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    _check_linear(pkg, dev, packed, a, orc.log_uniform(rng), orc.log_uniform(rng, m), kernel="gemm")
+    if m <= 2:
+        _check_linear(pkg, dev, packed, a, 1.0, np.ones(m, np.float32), kernel="auto", check_fp32=False)
+
+
+@pytest.mark.parametrize("n,k", [(13824, 2560), (2560, 6912)])
+@pytest.mark.parametrize("m", [512, 2048])
+def test_prefill_gemm_exact(pkg, dev, n, k, m):
+    rng = np.random.default_rng(3000 + n + m)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    _check_linear(pkg, dev, packed, a, orc.log_uniform(rng), orc.log_uniform(rng, m), check_fp32=False)
+
+
+@pytest.mark.parametrize("n,k", [(13824, 2560), (2560, 6912)])
+def test_prefill_gemm_8192_sampled(pkg, dev, n, k):
+    m = 8192
+    rng = np.random.default_rng(4000 + n)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    _, acc = pkg.bitnet_linear(_t(packed, dev), _t(a, dev), 1.0, return_acc=True)
+    acc_g = acc.cpu().numpy().astype(np.int64)
+    rows = np.sort(rng.choice(m, 96, replace=False))
+    rows = np.concatenate([[0, m - 1], rows])
+    assert np.array_equal(acc_g[rows], _ref_acc(packed, a[rows]))
+    # checksum of the whole output: sum_{m,n} acc = sum_k (sum_m a[m,k]) * (sum_n w[n,k])
+    w_col = orc.unpack_i2s(packed).astype(np.int64).sum(axis=0)
+    a_col = a.astype(np.int64).sum(axis=0)
+    assert acc_g.sum() == int(a_col @ w_col)
+    # and per-row sums: sum_n acc[m, n] = a[m] . w_col
+    assert np.array_equal(acc_g.sum(axis=1), a.astype(np.int64) @ w_col)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 17, 33, 300])
+@pytest.mark.parametrize("n,k", [(100, 128), (17, 640), (1, 256), (77, 14336), (130, 16384)])
+def test_ragged_shapes(pkg, dev, m, n, k):
+    rng = np.random.default_rng(m * 31 + n + k)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    a[:, :3] = -128
+    _check_linear(pkg, dev, packed, a, 0.5, orc.log_uniform(rng, m))
+
+
+def test_strided_activations_bias_and_device_scale(pkg, dev):
+    rng = np.random.default_rng(5)
+    n, k, m = 257, 512, 6
+    packed = _packed(rng, n, k)
+    big = orc.random_int8(rng, m, k + 64)
+    a_view = _t(big, dev)[:, :k]  # row stride k + 64
+    bias = rng.standard_normal(n).astype(np.float32)
+    a_scale = orc.log_uniform(rng, m)
+    ws = torch.tensor([0.0123], dtype=torch.float32, device=dev)
+    for b in (torch.from_numpy(bias).to(dev), torch.from_numpy(bias).to(dev).to(torch.bfloat16)):
+        y, acc = pkg.bitnet_linear(_t(packed, dev), a_view, ws, a_scale=_t(a_scale, dev), bias=b,
+                                   out_dtype=torch.float32, return_acc=True)
+        acc_ref = _ref_acc(packed, big[:, :k])
+        assert np.array_equal(acc.cpu().numpy().astype(np.int64), acc_ref)
+        y_ref = orc.rescale(acc_ref, np.float32(0.0123), a_scale, b.float().cpu().numpy())
+        assert np.array_equal(y.cpu().numpy(), y_ref)
+
+
+def test_empty_batch(pkg, dev):
+    packed = torch.zeros((64, 32), dtype=torch.uint8, device=dev)
+    y = pkg.bitnet_linear(packed, torch.zeros((0, 128), dtype=torch.int8, device=dev), 1.0)
+    assert y.shape == (0, 64)
+
+
+def test_gemv_and_gemm_kernels_agree(pkg, dev):
+    rng = np.random.default_rng(8)
+    packed = _t(_packed(rng, 3200, 2560), dev)
+    for m in (1, 2):
+        a = _t(orc.random_int8(rng, m, 2560), dev)
+        _, acc1 = pkg.bitnet_linear(packed, a, 1.0, return_acc=True, out_dtype=None, kernel="gemv")
+        _, acc2 = pkg.bitnet_linear(packed, a, 1.0, return_acc=True, out_dtype=None, kernel="gemm")
+        assert torch.equal(acc1, acc2)
+
+
+# ---- reference op surface -----------------------------------------------------------------------
+
+
+def test_reference_op_surface(pkg, dev):
+    rng = np.random.default_rng(12)
+    n, k = 640, 2560
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, 3, k)
+    pw = _t(packed, dev)
+    acc = _ref_acc(packed, a)
+    y1 = pkg.bitnet_gemv(pw, _t(a[0], dev), 0.25)
+    assert np.array_equal(y1.cpu().numpy(), orc.rescale(acc[:1], 0.25)[0])
+    y2 = pkg.bitnet_gemm(pw, _t(a, dev), 0.25)
+    assert np.array_equal(y2.cpu().numpy(), orc.rescale(acc, 0.25))
+    y3 = torch.ops.wfbitnet.bitnet_gemm(pw, _t(a, dev), 0.25)
+    assert torch.equal(y2, y3)
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    q, s = torch.ops.wfbitnet.bitnet_quantize_activations(_t(x, dev))
+    q_ref, s_ref = orc.quantize_per_tensor(x)
+    assert np.array_equal(q.cpu().numpy(), q_ref) and s.item() == s_ref[0]
+
+
+def test_bitlinear_module(pkg, dev):
+    rng = np.random.default_rng(21)
+    for in_f, out_f in ((576, 1536), (2560, 3200)):
+        lin = pkg.BitLinear(in_f, out_f).to(dev)
+        with torch.no_grad():
+            lin.weight.normal_(0, 0.02, generator=torch.Generator(device=dev).manual_seed(in_f))
+        x = torch.from_numpy(orc.outlier_hidden(rng, 6, in_f)).to(torch.bfloat16).to(dev)
+        y = lin(x.view(2, 3, in_f))
+        assert y.shape == (2, 3, out_f) and y.dtype == torch.bfloat16
+        w = lin.weight.detach().cpu().numpy()
+        packed, s = orc.pack_ternary(np.pad(w, ((0, 0), (0, lin.k_pad - in_f))), scale=orc.absmean_scale_device_order(w))
+        assert np.array_equal(lin.qweight.cpu().numpy(), packed)
+        y_ref, acc, _, _ = orc.bitlinear_forward(x.float().cpu().numpy(), packed, s)
+        assert np.array_equal(y.view(6, out_f).view(torch.int16).cpu().numpy().view(np.uint16), orc.f32_to_bf16_bits(y_ref))
+
+
+def test_subln_bitlinear_fused(pkg, dev):
+    rng = np.random.default_rng(22)
+    mod = pkg.SubLNBitLinear(1536, 576).to(dev)
+    with torch.no_grad():
+        mod.norm_weight.copy_(torch.from_numpy((1 + 0.1 * rng.standard_normal(1536)).astype(np.float32)))
+        mod.linear.weight.normal_(0, 0.02)
+    x = torch.from_numpy(orc.outlier_hidden(rng, 4, 1536)).to(torch.bfloat16).to(dev)
+    y, acc = mod(x, return_acc=True)
+    w = mod.linear.weight.detach().cpu().numpy()
+    packed, s = orc.pack_ternary(w, scale=orc.absmean_scale_device_order(w))
+    q_ref, s_ref = orc.rmsnorm_quant(x.float().cpu().numpy(), mod.norm_weight.detach().cpu().numpy(), 1e-6)
+    acc_ref = orc.accumulate(packed, q_ref)
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), acc_ref)
+    y_ref = orc.rescale(acc_ref, s, s_ref)
+    assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), orc.f32_to_bf16_bits(y_ref))
+
+
+def test_serving_method_per_tensor_matches_reference_contract(pkg, dev):
+    rng = np.random.default_rng(23)
+    layer = torch.nn.Module()
+    meth = pkg.BitNetLinearMethod(per_token=False)
+    meth.create_weights(layer, 640, [320, 64], 640, 384, torch.bfloat16, device=dev)
+    packed = _packed(rng, 384, 640)
+    layer.qweight.data.copy_(_t(packed, dev))
+    layer.scale.data.fill_(0.031)
+    x = (rng.standard_normal((5, 640)) * 2).astype(np.float32)
+    y = meth.apply(layer, _t(x, dev))
+    # reference: quantize_activations_i8 (one scale) -> bitnet_gemm(scale) -> * act_scale
+    q_ref, s_ref = orc.quantize_per_tensor(x)
+    y_ref = orc.rescale(orc.accumulate(packed, q_ref), np.float32(0.031), np.repeat(s_ref, 5))
+    assert np.array_equal(y.cpu().numpy(), y_ref)
+    with pytest.raises(ValueError):
+        meth.create_weights(torch.nn.Module(), 600, [64], 600, 64, torch.bfloat16, device=dev)

@@ -1,0 +1,35 @@
+"""MI355X-native (gfx950) ternary BitLinear hot path: I2_S W2A8 pack, fused RMSNorm + int8 quant,
+decode GEMV and int8-MFMA prefill GEMM behind a C ABI (include/wfbitnet.h).
+
+The directory name is not a Python identifier; entry points load it under the module name
+``wrinklefree_monorepo_amd`` (see ``__graft_entry__.load_package``).
+"""
+
+from ._lib import LIB_PATH, available as library_available
+from .ops import (
+    QK_I2_S,
+    absmean_scale,
+    bitnet_gemm,
+    bitnet_gemv,
+    bitnet_linear,
+    check_kernel_available,
+    pack_ternary_i2s,
+    quantize_activations_i8,
+    quantize_activations_i8_per_token,
+    rmsnorm_quantize_i8,
+    unpack_i2s,
+)
+from .bitlinear import (
+    BitLinear,
+    BitNetLinearMethod,
+    SubLNBitLinear,
+    convert_linear_to_bitlinear,
+    patch_model_with_native_kernels,
+)
+
+__all__ = [
+    "LIB_PATH", "library_available", "QK_I2_S", "absmean_scale", "bitnet_gemm", "bitnet_gemv", "bitnet_linear",
+    "check_kernel_available", "pack_ternary_i2s", "quantize_activations_i8", "quantize_activations_i8_per_token",
+    "rmsnorm_quantize_i8", "unpack_i2s", "BitLinear", "BitNetLinearMethod", "SubLNBitLinear",
+    "convert_linear_to_bitlinear", "patch_model_with_native_kernels",
+]

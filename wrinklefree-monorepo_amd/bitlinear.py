@@ -1,0 +1,219 @@
+"""Drop-in BitLinear modules whose forward runs the MI355X kernels.
+
+Surfaces kept from the reference:
+  * ``BitLinear(in_features, out_features, bias=False, eps=1e-5)`` with ``forward(x[..., in]) -> [..., out]``
+    (packages/training/src/wrinklefree/models/bitlinear.py:36-113);
+  * ``convert_linear_to_bitlinear(module, exclude_names)`` (same file :154-192);
+  * ``BitNetLinearMethod.create_weights / apply`` with ``qweight`` uint8 [out, in/4] + ``scale`` fp32[1]
+    (packages/inference/extern/sglang-bitnet/python/sglang/srt/layers/quantization/bitnet.py:137-255);
+  * ``patch_model_with_native_kernels`` (packages/inference/src/wrinklefree_inference/kernels/bitnet_patch.py:165-210).
+
+The forward is the quantised serving forward of the reference CPU path (per-token absmax int8
+activations, I2_S ternary weights with a per-tensor absmean scale, exact int32 accumulation, then
+acc * w_scale * a_scale).  The float fake-quant QAT forward of the training module is not provided:
+this module is the inference hot path and has no CPU or eager-torch fallback.
+"""
+
+from __future__ import annotations
+
+from typing import Iterable, List, Optional
+
+import torch
+import torch.nn as nn
+
+from .ops import (
+    QK_I2_S,
+    bitnet_linear,
+    pack_ternary_i2s,
+    quantize_activations_i8,
+    quantize_activations_i8_per_token,
+    rmsnorm_quantize_i8,
+)
+
+
+def _pad_k(k: int) -> int:
+    return (k + QK_I2_S - 1) // QK_I2_S * QK_I2_S
+
+
+def _out_dtype(x: torch.Tensor) -> torch.dtype:
+    return torch.float32 if x.dtype == torch.float32 else torch.bfloat16
+
+
+class BitLinear(nn.Linear):
+    """Ternary-weight, int8-activation linear layer executed by libwfbitnet.
+
+    ``in_features`` need not be a multiple of 128: K is zero-padded to ``k_pad`` inside the packed
+    weight and the quantised activations (padded weights are 0, padded activations are 0, so the
+    accumulators are those of the unpadded product).  Call :meth:`pack` after changing ``weight``;
+    the first forward packs automatically.
+    """
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False, eps: float = 1e-5,
+                 device=None, dtype=None):
+        super().__init__(in_features, out_features, bias=bias, device=device, dtype=dtype)
+        self.eps = eps  # kept for signature parity; the int8 quantiser uses the kernel rule max < 1e-6 -> 1
+        self.k_pad = _pad_k(in_features)
+        self.register_buffer("qweight", None, persistent=True)
+        self.register_buffer("weight_scale", None, persistent=True)
+
+    @torch.no_grad()
+    def pack(self) -> "BitLinear":
+        self.qweight, self.weight_scale = pack_ternary_i2s(self.weight.detach().contiguous(), k_pad=self.k_pad)
+        return self
+
+    @classmethod
+    def from_packed(cls, qweight: torch.Tensor, weight_scale: torch.Tensor, in_features: int,
+                    bias: Optional[torch.Tensor] = None) -> "BitLinear":
+        """Module around an existing I2_S tensor (e.g. loaded from a converted checkpoint)."""
+        out_features = qweight.shape[0]
+        mod = cls.__new__(cls)
+        nn.Module.__init__(mod)
+        mod.in_features, mod.out_features = in_features, out_features
+        mod.eps = 1e-5
+        mod.k_pad = qweight.shape[1] * 4
+        if mod.k_pad < in_features or mod.k_pad % QK_I2_S:
+            raise ValueError(f"qweight K ({mod.k_pad}) does not cover in_features ({in_features})")
+        mod.register_parameter("weight", None)
+        mod.register_parameter("bias", None if bias is None else nn.Parameter(bias, requires_grad=False))
+        mod.register_buffer("qweight", qweight)
+        mod.register_buffer("weight_scale", weight_scale.reshape(1).to(torch.float32))
+        return mod
+
+    def forward_quantized(self, q: torch.Tensor, a_scale: torch.Tensor, out_dtype=torch.bfloat16,
+                          return_acc: bool = False):
+        """Linear on already-quantised activations q [M, k_pad] with per-token scales a_scale [M]."""
+        if self.qweight is None:
+            self.pack()
+        return bitnet_linear(self.qweight, q, self.weight_scale, a_scale=a_scale, bias=self.bias,
+                             out_dtype=out_dtype, return_acc=return_acc)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.qweight is None:
+            self.pack()
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.in_features)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        q, a_scale = quantize_activations_i8_per_token(x2, k_pad=self.k_pad)
+        y = bitnet_linear(self.qweight, q, self.weight_scale, a_scale=a_scale, bias=self.bias,
+                          out_dtype=_out_dtype(x))
+        y = y.view(*lead, self.out_features)
+        return y if y.dtype == x.dtype else y.to(x.dtype)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, k_pad={self.k_pad}, " \
+               f"bias={self.bias is not None}, packed={self.qweight is not None}"
+
+
+class SubLNBitLinear(nn.Module):
+    """SubLN followed by BitLinear, run as ONE fused RMSNorm + per-token quant kernel and the linear.
+
+    Same math as ``nn.Sequential(SubLN(in_features, eps=1e-6), BitLinear(...))``, the layout stage 1
+    gives o_proj and down_proj (packages/training/src/wrinklefree/training/stage1.py:93-113, 146-166).
+    """
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False, norm_eps: float = 1e-6,
+                 device=None, dtype=None):
+        super().__init__()
+        self.norm_weight = nn.Parameter(torch.ones(in_features, device=device, dtype=dtype))
+        self.norm_eps = norm_eps
+        self.linear = BitLinear(in_features, out_features, bias=bias, device=device, dtype=dtype)
+
+    def forward(self, x: torch.Tensor, return_acc: bool = False):
+        lin = self.linear
+        if lin.qweight is None:
+            lin.pack()
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, lin.in_features)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        q, a_scale = rmsnorm_quantize_i8(x2, self.norm_weight, eps=self.norm_eps, k_pad=lin.k_pad)
+        res = bitnet_linear(lin.qweight, q, lin.weight_scale, a_scale=a_scale, bias=lin.bias,
+                            out_dtype=_out_dtype(x), return_acc=return_acc)
+        y = res[0] if return_acc else res
+        y = y.view(*lead, lin.out_features)
+        y = y if y.dtype == x.dtype else y.to(x.dtype)
+        return (y, res[1]) if return_acc else y
+
+
+@torch.no_grad()
+def convert_linear_to_bitlinear(module: nn.Module, exclude_names: Optional[List[str]] = None) -> nn.Module:
+    """Replace every nn.Linear under ``module`` by a packed :class:`BitLinear` (weights copied)."""
+    exclude_names = exclude_names or []
+    for name, child in module.named_children():
+        if name in exclude_names:
+            continue
+        if isinstance(child, nn.Linear) and not isinstance(child, BitLinear):
+            new = BitLinear(child.in_features, child.out_features, bias=child.bias is not None,
+                            device=child.weight.device, dtype=child.weight.dtype)
+            new.weight.copy_(child.weight)
+            if child.bias is not None:
+                new.bias.copy_(child.bias)
+            new.pack()
+            setattr(module, name, new)
+        else:
+            convert_linear_to_bitlinear(child, exclude_names)
+    return module
+
+
+def patch_model_with_native_kernels(model: nn.Module, targets: Iterable[str] = (
+        "q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")) -> nn.Module:
+    """Swap the named projection Linears for packed BitLinear modules (in place); returns the model."""
+    targets = set(targets)
+    for parent in list(model.modules()):
+        for name, child in list(parent.named_children()):
+            if name in targets and isinstance(child, nn.Linear) and not isinstance(child, BitLinear):
+                with torch.no_grad():
+                    new = BitLinear(child.in_features, child.out_features, bias=child.bias is not None,
+                                    device=child.weight.device, dtype=child.weight.dtype)
+                    new.weight.copy_(child.weight)
+                    if child.bias is not None:
+                        new.bias.copy_(child.bias)
+                    new.pack()
+                setattr(parent, name, new)
+    return model
+
+
+class BitNetLinearMethod:
+    """Serving quant method with the reference's weight schema and ``apply`` signature.
+
+    ``per_token=True`` (default) quantises activations per token, as the BitLinear spec does;
+    ``per_token=False`` reproduces the reference op's single per-tensor scale
+    (torch_extension_cpu.cpp:409-426).  No fallback: failures raise RuntimeError.
+    """
+
+    block_size = QK_I2_S
+
+    def __init__(self, per_token: bool = True):
+        self.per_token = per_token
+
+    def create_weights(self, layer: nn.Module, input_size_per_partition: int, output_partition_sizes: List[int],
+                       input_size: int, output_size: int, params_dtype: torch.dtype, device=None, **_):
+        if input_size_per_partition % self.block_size != 0:
+            raise ValueError(
+                f"BitNet: input_size_per_partition ({input_size_per_partition}) "
+                f"must be divisible by block_size ({self.block_size})")
+        out = sum(output_partition_sizes)
+        layer.register_parameter("qweight", nn.Parameter(
+            torch.empty((out, input_size_per_partition // 4), dtype=torch.uint8, device=device), requires_grad=False))
+        layer.register_parameter("scale", nn.Parameter(
+            torch.ones(1, dtype=torch.float32, device=device), requires_grad=False))
+
+    def process_weights_after_loading(self, layer: nn.Module) -> None:
+        if layer.qweight.dtype != torch.uint8:
+            raise ValueError(f"BitNet: Expected qweight dtype uint8, got {layer.qweight.dtype}.")
+
+    def apply(self, layer: nn.Module, x: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        try:
+            x2 = x.reshape(-1, x.shape[-1]).contiguous()
+            if self.per_token:
+                q, a_scale = quantize_activations_i8_per_token(x2)
+            else:
+                q, s = quantize_activations_i8(x2)
+                a_scale = s.expand(x2.shape[0]).contiguous()
+            y = bitnet_linear(layer.qweight, q, layer.scale.data, a_scale=a_scale, bias=bias,
+                              out_dtype=_out_dtype(x))
+        except (ValueError, RuntimeError) as e:
+            raise RuntimeError(f"BitNet apply FAILED: {e}. Native BitNet kernels are required; NO FALLBACK.") from e
+        y = y.view(*x.shape[:-1], y.shape[-1])
+        return y if y.dtype == x.dtype else y.to(x.dtype)

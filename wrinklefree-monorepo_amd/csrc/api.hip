@@ -1,0 +1,186 @@
+// extern "C" entry points of libwfbitnet: argument validation, error reporting and kernel choice.
+//
+// Validation mirrors the reference op boundary (TORCH_CHECK on dtype/rank/shape in
+// SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:336-346, 375-386, 410 and the K % 128 check of
+// SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:331-336, 824-829) and adds the alignment the 128-bit
+// loads need.  Every check runs on the host before anything touches the GPU.
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "wfb_common.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return WFB_OK;
+}
+
+int hip_status(hipError_t e, const char* where) {
+  if (e != hipSuccess) return fail(WFB_EHIP, "%s: HIP error %d (%s)", where, (int)e, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+bool valid_dtype(int dt) { return dt == WFB_F32 || dt == WFB_BF16 || dt == WFB_F16; }
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+enum class Kernel { Auto, Gemv, Gemm };
+
+// Decode (M <= 2) runs the VALU GEMV while the MFMA kernel is slower; everything else runs MFMA.
+bool use_gemv(int64_t m, int64_t k) { return m <= 2 && k <= (m == 1 ? 32768 : 20480); }
+
+int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act,
+                int64_t m, int64_t lda, const float* a_scale, const float* w_scale_dev, float w_scale,
+                const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo, int32_t* acc_out,
+                void* stream) {
+  if (n <= 0 || k <= 0 || m < 0) return fail(WFB_EINVAL, "%s: bad sizes m=%lld n=%lld k=%lld", name, (long long)m, (long long)n, (long long)k);
+  if (k % WFB_QK_I2S != 0)
+    return fail(WFB_EINVAL, "%s: K (%lld) must be multiple of %d", name, (long long)k, WFB_QK_I2S);
+  if (n > INT32_MAX / 2 || m > INT32_MAX / 2 || k > (1 << 20))
+    return fail(WFB_EINVAL, "%s: sizes too large m=%lld n=%lld k=%lld", name, (long long)m, (long long)n, (long long)k);
+  if (m == 0) return ok();
+  if (!qweight || !act) return fail(WFB_EINVAL, "%s: null qweight or activations", name);
+  if (!out && !acc_out) return fail(WFB_EINVAL, "%s: out and acc_out are both null", name);
+  if (!aligned(qweight, 16) || !aligned(act, 16))
+    return fail(WFB_EINVAL, "%s: qweight and activations must be 16-byte aligned", name);
+  if (lda < k || lda % 16 != 0)
+    return fail(WFB_EINVAL, "%s: activation row stride (%lld) must be >= K and a multiple of 16", name, (long long)lda);
+  if (ldo < n) return fail(WFB_EINVAL, "%s: output row stride (%lld) < N (%lld)", name, (long long)ldo, (long long)n);
+  if (out && out_dtype != WFB_F32 && out_dtype != WFB_BF16)
+    return fail(WFB_EINVAL, "%s: out dtype must be WFB_F32 or WFB_BF16", name);
+  if (bias && !valid_dtype(bias_dtype)) return fail(WFB_EINVAL, "%s: bad bias dtype %d", name, bias_dtype);
+  if (kind == Kernel::Gemv && !use_gemv(m, k))
+    return fail(WFB_EINVAL, "%s: the GEMV kernel takes M <= 2 tokens and K <= 20480/32768 (got M=%lld K=%lld)", name,
+                (long long)m, (long long)k);
+
+  wfb::Epilogue e;
+  e.a_scale = a_scale;
+  e.ws_dev = w_scale_dev;
+  e.ws = w_scale;
+  e.bias = bias;
+  e.bias_dtype = bias_dtype;
+  e.out = out;
+  e.out_dtype = out_dtype;
+  e.ldo = ldo;
+  e.acc_out = acc_out;
+
+  const bool gemv = kind == Kernel::Gemv || (kind == Kernel::Auto && use_gemv(m, k));
+  hipError_t st = gemv ? wfb::launch_gemv_i2s(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream))
+                       : wfb::launch_gemm_i2s(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream));
+  return hip_status(st, name);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* wfb_last_error(void) { return g_err.c_str(); }
+
+int wfb_version(void) { return 1; }
+
+int wfb_weight_absmean(const void* w, int w_dtype, int64_t numel, float* scale_dev, double* workspace, void* stream) {
+  if (!valid_dtype(w_dtype)) return fail(WFB_EINVAL, "wfb_weight_absmean: bad dtype %d", w_dtype);
+  if (numel < 0) return fail(WFB_EINVAL, "wfb_weight_absmean: numel < 0");
+  if (!scale_dev || !workspace || (numel > 0 && !w)) return fail(WFB_EINVAL, "wfb_weight_absmean: null pointer");
+  return hip_status(wfb::launch_weight_absmean(w, w_dtype, numel, scale_dev, workspace, as_stream(stream)),
+                    "wfb_weight_absmean");
+}
+
+int wfb_pack_i2s(const void* w, int w_dtype, int64_t n, int64_t k, int64_t ldw, const float* scale_dev,
+                 uint8_t* qweight, void* stream) {
+  if (!valid_dtype(w_dtype)) return fail(WFB_EINVAL, "wfb_pack_i2s: bad dtype %d", w_dtype);
+  if (n < 0 || k <= 0 || k % WFB_QK_I2S != 0)
+    return fail(WFB_EINVAL, "wfb_pack_i2s: K (%lld) must be multiple of %d", (long long)k, WFB_QK_I2S);
+  if (ldw < k) return fail(WFB_EINVAL, "wfb_pack_i2s: row stride %lld < K %lld", (long long)ldw, (long long)k);
+  if (n > 0 && (!w || !qweight || !scale_dev)) return fail(WFB_EINVAL, "wfb_pack_i2s: null pointer");
+  if (!aligned(qweight, 4)) return fail(WFB_EINVAL, "wfb_pack_i2s: qweight must be 4-byte aligned");
+  return hip_status(wfb::launch_pack_i2s(w, w_dtype, n, k, ldw, scale_dev, qweight, as_stream(stream)), "wfb_pack_i2s");
+}
+
+int wfb_unpack_i2s(const uint8_t* qweight, int64_t n, int64_t k, int8_t* w_out, void* stream) {
+  if (n < 0 || k <= 0 || k % WFB_QK_I2S != 0)
+    return fail(WFB_EINVAL, "wfb_unpack_i2s: K (%lld) must be multiple of %d", (long long)k, WFB_QK_I2S);
+  if (n > 0 && (!qweight || !w_out)) return fail(WFB_EINVAL, "wfb_unpack_i2s: null pointer");
+  return hip_status(wfb::launch_unpack_i2s(qweight, n, k, w_out, as_stream(stream)), "wfb_unpack_i2s");
+}
+
+int wfb_quantize_act_i8(const void* x, int x_dtype, int64_t m, int64_t h, int64_t ldx, int8_t* q, int64_t k_pad,
+                        int64_t ldq, float* a_scale, void* stream) {
+  if (!valid_dtype(x_dtype)) return fail(WFB_EINVAL, "wfb_quantize_act_i8: bad dtype %d", x_dtype);
+  if (m < 0 || h <= 0 || h > WFB_NORM_MAX_H)
+    return fail(WFB_EINVAL, "wfb_quantize_act_i8: row length %lld outside 1..%d", (long long)h, WFB_NORM_MAX_H);
+  if (ldx < h || k_pad < h || ldq < k_pad)
+    return fail(WFB_EINVAL, "wfb_quantize_act_i8: strides must satisfy ldx >= H, ldq >= k_pad >= H");
+  if (m == 0) return ok();
+  if (!x || !q || !a_scale) return fail(WFB_EINVAL, "wfb_quantize_act_i8: null pointer");
+  if (!aligned(q, 8) || ldq % 8 != 0) return fail(WFB_EINVAL, "wfb_quantize_act_i8: q must be 8-byte aligned rows");
+  return hip_status(wfb::launch_quant_rows(x, x_dtype, ldx, nullptr, 0, false, 0.0f, m, h, q, k_pad, ldq, a_scale,
+                                           as_stream(stream)),
+                    "wfb_quantize_act_i8");
+}
+
+int wfb_quantize_act_i8_tensor(const void* x, int x_dtype, int64_t numel, int8_t* q, float* a_scale, void* stream) {
+  if (!valid_dtype(x_dtype)) return fail(WFB_EINVAL, "wfb_quantize_act_i8_tensor: bad dtype %d", x_dtype);
+  if (numel < 0) return fail(WFB_EINVAL, "wfb_quantize_act_i8_tensor: numel < 0");
+  if (!a_scale || (numel > 0 && (!x || !q))) return fail(WFB_EINVAL, "wfb_quantize_act_i8_tensor: null pointer");
+  if (!aligned(a_scale, 4)) return fail(WFB_EINVAL, "wfb_quantize_act_i8_tensor: a_scale misaligned");
+  return hip_status(wfb::launch_quant_tensor(x, x_dtype, numel, q, a_scale, as_stream(stream)),
+                    "wfb_quantize_act_i8_tensor");
+}
+
+int wfb_rmsnorm_quant_i8(const void* x, int x_dtype, int64_t ldx, const void* gamma, int gamma_dtype, float eps,
+                         int64_t m, int64_t h, int8_t* q, int64_t k_pad, int64_t ldq, float* a_scale, void* stream) {
+  if (!valid_dtype(x_dtype) || (gamma && !valid_dtype(gamma_dtype)))
+    return fail(WFB_EINVAL, "wfb_rmsnorm_quant_i8: bad dtype");
+  if (m < 0 || h <= 0 || h > WFB_NORM_MAX_H || h % 8 != 0)
+    return fail(WFB_EINVAL, "wfb_rmsnorm_quant_i8: H (%lld) must be a multiple of 8 in 8..%d", (long long)h,
+                WFB_NORM_MAX_H);
+  if (ldx < h || k_pad < h || ldq < k_pad)
+    return fail(WFB_EINVAL, "wfb_rmsnorm_quant_i8: strides must satisfy ldx >= H, ldq >= k_pad >= H");
+  if (!(eps >= 0.0f)) return fail(WFB_EINVAL, "wfb_rmsnorm_quant_i8: eps must be >= 0");
+  if (m == 0) return ok();
+  if (!x || !q || !a_scale) return fail(WFB_EINVAL, "wfb_rmsnorm_quant_i8: null pointer");
+  if (!aligned(q, 8) || ldq % 8 != 0) return fail(WFB_EINVAL, "wfb_rmsnorm_quant_i8: q must be 8-byte aligned rows");
+  return hip_status(wfb::launch_quant_rows(x, x_dtype, ldx, gamma, gamma_dtype, true, eps, m, h, q, k_pad, ldq,
+                                           a_scale, as_stream(stream)),
+                    "wfb_rmsnorm_quant_i8");
+}
+
+int wfb_linear_i2s(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m, int64_t lda,
+                   const float* a_scale, const float* w_scale_dev, float w_scale, const void* bias, int bias_dtype,
+                   void* out, int out_dtype, int64_t ldo, int32_t* acc_out, void* stream) {
+  return linear_impl(Kernel::Auto, "wfb_linear_i2s", qweight, n, k, act, m, lda, a_scale, w_scale_dev, w_scale, bias,
+                     bias_dtype, out, out_dtype, ldo, acc_out, stream);
+}
+
+int wfb_gemv_i2s(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m, int64_t lda,
+                 const float* a_scale, const float* w_scale_dev, float w_scale, const void* bias, int bias_dtype,
+                 void* out, int out_dtype, int64_t ldo, int32_t* acc_out, void* stream) {
+  return linear_impl(Kernel::Gemv, "wfb_gemv_i2s", qweight, n, k, act, m, lda, a_scale, w_scale_dev, w_scale, bias,
+                     bias_dtype, out, out_dtype, ldo, acc_out, stream);
+}
+
+int wfb_gemm_i2s(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m, int64_t lda,
+                 const float* a_scale, const float* w_scale_dev, float w_scale, const void* bias, int bias_dtype,
+                 void* out, int out_dtype, int64_t ldo, int32_t* acc_out, void* stream) {
+  return linear_impl(Kernel::Gemm, "wfb_gemm_i2s", qweight, n, k, act, m, lda, a_scale, w_scale_dev, w_scale, bias,
+                     bias_dtype, out, out_dtype, ldo, acc_out, stream);
+}
+
+}  // extern "C"

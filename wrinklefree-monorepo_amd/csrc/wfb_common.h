@@ -1,0 +1,124 @@
+// Shared device helpers and internal launcher declarations of libwfbitnet (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/wfbitnet.h"
+
+namespace wfb {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// ---- scalar conversions -------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t v) {
+  return (float)__builtin_bit_cast(_Float16, v);
+}
+
+// fp32 -> bf16 with round-to-nearest-even (NaN stays a quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* p, int64_t i) {
+  if constexpr (DT == WFB_F32) {
+    return reinterpret_cast<const float*>(p)[i];
+  } else if constexpr (DT == WFB_BF16) {
+    return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  } else {
+    return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  }
+}
+
+// Load 8 consecutive elements starting at element index i (16-byte aligned for 16-bit types,
+// 32-byte for fp32) and widen them to fp32.
+template <int DT>
+__device__ __forceinline__ void load8(const void* p, int64_t i, float (&v)[8]) {
+  if constexpr (DT == WFB_F32) {
+    const float4* q = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+    float4 a = q[0], b = q[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    uint4 r = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + i);
+    uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (DT == WFB_BF16) {
+        v[2 * e] = __uint_as_float(w[e] << 16);
+        v[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+      } else {
+        v[2 * e] = f16_bits_to_f32((uint16_t)(w[e] & 0xffffu));
+        v[2 * e + 1] = f16_bits_to_f32((uint16_t)(w[e] >> 16));
+      }
+    }
+  }
+}
+
+// Round half to even, then saturate to int8 (the vector path of the reference quantiser:
+// _mm256_round_ps(NEAREST_INT) + saturating packs).
+__device__ __forceinline__ int quant_i8(float v, float inv) {
+  float r = __builtin_rintf(__fmul_rn(v, inv));
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  return (int)r;
+}
+
+// ---- GEMV / GEMM epilogue -------------------------------------------------------------------
+
+struct Epilogue {
+  const float* a_scale;  // [M] or null
+  const float* ws_dev;   // [1] or null
+  float ws;              // used when ws_dev is null
+  const void* bias;      // [N] or null
+  int bias_dtype;
+  void* out;             // [M, N] or null
+  int out_dtype;
+  int64_t ldo;
+  int32_t* acc_out;      // [M, N] or null
+};
+
+__device__ __forceinline__ float epi_wscale(const Epilogue& e) { return e.ws_dev ? e.ws_dev[0] : e.ws; }
+
+// y = ((float)acc * ws) * as (+ bias): the two products in this order, each rounded to fp32
+// (SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:846 then SGB/python/sglang/srt/layers/quantization/bitnet.py:241).
+__device__ __forceinline__ void epi_store(const Epilogue& e, float ws, int m, int n, int32_t acc) {
+  const int64_t off = (int64_t)m * e.ldo + n;
+  if (e.acc_out) e.acc_out[off] = acc;
+  if (!e.out) return;
+  const float as = e.a_scale ? e.a_scale[m] : 1.0f;
+  float y = __fmul_rn(__fmul_rn((float)acc, ws), as);
+  if (e.bias) {
+    float b;
+    if (e.bias_dtype == WFB_F32) b = reinterpret_cast<const float*>(e.bias)[n];
+    else if (e.bias_dtype == WFB_BF16) b = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(e.bias)[n]);
+    else b = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(e.bias)[n]);
+    y = __fadd_rn(y, b);
+  }
+  if (e.out_dtype == WFB_F32) reinterpret_cast<float*>(e.out)[off] = y;
+  else reinterpret_cast<uint16_t*>(e.out)[off] = f32_to_bf16_rne(y);
+}
+
+// ---- internal launchers (return hipError_t of the launch) --------------------------------
+
+hipError_t launch_weight_absmean(const void* w, int dt, int64_t numel, float* scale, double* ws, hipStream_t s);
+hipError_t launch_pack_i2s(const void* w, int dt, int64_t n, int64_t k, int64_t ldw, const float* scale,
+                           uint8_t* qw, hipStream_t s);
+hipError_t launch_unpack_i2s(const uint8_t* qw, int64_t n, int64_t k, int8_t* out, hipStream_t s);
+hipError_t launch_quant_rows(const void* x, int dt, int64_t ldx, const void* gamma, int gdt, bool norm,
+                             float eps, int64_t m, int64_t h, int8_t* q, int64_t k_pad, int64_t ldq,
+                             float* a_scale, hipStream_t s);
+hipError_t launch_quant_tensor(const void* x, int dt, int64_t numel, int8_t* q, float* a_scale, hipStream_t s);
+hipError_t launch_gemv_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
+                           const Epilogue& e, hipStream_t s);
+hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
+                           const Epilogue& e, hipStream_t s);
+
+}  // namespace wfb

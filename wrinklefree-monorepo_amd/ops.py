@@ -1,0 +1,325 @@
+"""Torch-facing ops over the C ABI: the MI355X counterparts of the reference BitNet op wrappers.
+
+Names, argument meaning and error behaviour follow the reference wrappers
+(SGB/sgl-kernel/python/sgl_kernel/quantization/bitnet.py:73-179) and the torch ops they call
+(SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:331-426); SGB = packages/inference/extern/sglang-bitnet.
+Differences, all deliberate:
+  * tensors live on the GPU and work is enqueued on the current HIP stream (no host sync);
+  * ``scale`` may be a Python float or a 1-element fp32 device tensor (no ``.item()`` sync);
+  * ``bitnet_gemm`` returns [batch, out] directly (the reference op fills [out, batch] and its
+    wrapper transposes, bitnet.py:139-145);
+  * non-contiguous inputs are rejected instead of being read through ``data_ptr`` as if contiguous.
+The ops are also registered as ``torch.ops.wfbitnet.*`` with the reference schemas.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _lib
+from ._lib import WFB_ABSMEAN_WS_DOUBLES, WFB_BF16, WFB_F16, WFB_F32, WFB_QK_I2S
+
+QK_I2_S = WFB_QK_I2S
+
+_DT = {torch.float32: WFB_F32, torch.bfloat16: WFB_BF16, torch.float16: WFB_F16}
+
+Scale = Union[float, torch.Tensor]
+
+
+def check_kernel_available() -> bool:
+    """True when libwfbitnet loads and a HIP device is visible (reference: bitnet.py:38-44)."""
+    return _lib.available() and torch.cuda.is_available()
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _require_gpu(name: str, *ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(f"{name}: tensors must be on a HIP device (got {t.device})")
+        if not t.is_contiguous():
+            raise RuntimeError(f"{name}: tensors must be contiguous")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{name}: tensors are on different devices ({dev}, {t.device})")
+    assert dev is not None
+    return dev
+
+
+def _float_dtype(name: str, t: torch.Tensor) -> int:
+    if t.dtype not in _DT:
+        raise RuntimeError(f"{name}: expected float32, bfloat16 or float16, got {t.dtype}")
+    return _DT[t.dtype]
+
+
+def _scale_args(name: str, scale: Scale, dev: torch.device):
+    """(device pointer or None, host float) for the C ABI's w_scale_dev / w_scale pair."""
+    if isinstance(scale, torch.Tensor):
+        if scale.dtype != torch.float32 or scale.numel() != 1 or scale.device != dev:
+            raise RuntimeError(f"{name}: scale tensor must be one fp32 element on {dev}")
+        return _p(scale.contiguous()), 0.0
+    return None, float(scale)
+
+
+# ---- a1: offline pack -------------------------------------------------------------------------
+
+
+def absmean_scale(weights: torch.Tensor) -> torch.Tensor:
+    """fp32[1] device tensor holding mean(|W|) (< 1e-8 -> 1.0), as convert_to_sglkernel.py:81-85."""
+    name = "absmean_scale"
+    dev = _require_gpu(name, weights)
+    dt = _float_dtype(name, weights)
+    scale = torch.empty(1, dtype=torch.float32, device=dev)
+    ws = torch.empty(WFB_ABSMEAN_WS_DOUBLES, dtype=torch.float64, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("wfb_weight_absmean", _p(weights), dt, weights.numel(), _p(scale), _p(ws), _stream(dev))
+    return scale
+
+
+def pack_ternary_i2s(
+    weights: torch.Tensor, scale: Optional[torch.Tensor] = None, k_pad: Optional[int] = None
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Ternarise and pack W [out, in] to I2_S: (qweight uint8 [out, k_pad/4], scale fp32[1]).
+
+    Device counterpart of pack_ternary_sglkernel (packages/inference/scripts/convert_to_sglkernel.py:51-123).
+    ``scale`` defaults to absmean(W) over the real columns.  ``k_pad`` (a multiple of 128, >= in)
+    zero-pads K: padded weights are 0 (code 01), so accumulators are unchanged.
+    """
+    name = "pack_ternary_i2s"
+    if weights.dim() != 2:
+        raise RuntimeError(f"{name}: weights must be 2D [out_features, in_features]")
+    dev = _require_gpu(name, weights)
+    _float_dtype(name, weights)
+    n, k = weights.shape
+    kp = k if k_pad is None else int(k_pad)
+    if kp % QK_I2_S != 0 or kp < k:
+        raise ValueError(f"K ({kp}) must be multiple of {QK_I2_S}")
+    if scale is None:
+        scale = absmean_scale(weights)
+    elif scale.dtype != torch.float32 or scale.numel() != 1 or scale.device != dev:
+        raise RuntimeError(f"{name}: scale must be one fp32 element on {dev}")
+    w = weights
+    if kp != k:
+        w = torch.zeros((n, kp), dtype=weights.dtype, device=dev)
+        w[:, :k] = weights
+    packed = torch.empty((n, kp // 4), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("wfb_pack_i2s", _p(w), _DT[w.dtype], n, kp, kp, _p(scale.contiguous()), _p(packed), _stream(dev))
+    return packed, scale
+
+
+def unpack_i2s(packed_weights: torch.Tensor) -> torch.Tensor:
+    """int8 [out, in] in {-1, 0, +1} from an I2_S tensor (decode of bitnet_engine.cpp:51-81)."""
+    name = "unpack_i2s"
+    if packed_weights.dtype != torch.uint8 or packed_weights.dim() != 2:
+        raise RuntimeError(f"{name}: packed_weights must be 2D uint8")
+    dev = _require_gpu(name, packed_weights)
+    n, kb = packed_weights.shape
+    out = torch.empty((n, kb * 4), dtype=torch.int8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("wfb_unpack_i2s", _p(packed_weights), n, kb * 4, _p(out), _stream(dev))
+    return out
+
+
+# ---- a2 / a3: activation quantisation ----------------------------------------------------------
+
+
+def quantize_activations_i8(activations: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-TENSOR absmax int8 quantisation: (int8 same shape, fp32[1] scale).
+
+    Same contract as the reference wrapper / op (bitnet.py:155-179, torch_extension_cpu.cpp:409-426):
+    one scale for the whole buffer.  The BitLinear path uses the per-token variant below.
+    """
+    name = "quantize_activations_i8"
+    dev = _require_gpu(name, activations)
+    dt = _float_dtype(name, activations)
+    q = torch.empty(activations.shape, dtype=torch.int8, device=dev)
+    scale = torch.empty(1, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("wfb_quantize_act_i8_tensor", _p(activations), dt, activations.numel(), _p(q), _p(scale), _stream(dev))
+    return q, scale
+
+
+def _rows(name: str, x: torch.Tensor, k_pad: Optional[int]):
+    if x.dim() < 1:
+        raise RuntimeError(f"{name}: input must have a feature dimension")
+    h = x.shape[-1]
+    kp = h if k_pad is None else int(k_pad)
+    if kp < h:
+        raise ValueError(f"{name}: k_pad ({kp}) < features ({h})")
+    kp_alloc = (kp + 15) // 16 * 16  # rows of q are 16-byte aligned for the 128-bit loads
+    m = x.numel() // h if h else 0
+    return h, kp, kp_alloc, m
+
+
+def quantize_activations_i8_per_token(
+    x: torch.Tensor, k_pad: Optional[int] = None
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-token absmax int8: (q int8 [..., k_pad], a_scale fp32 [...]).
+
+    The quantiser of bitnet_gemv.cpp:880-1135 applied row by row (the per-token form of
+    WF/models/bitlinear.py:66-84 used by the decode engine, bitnet_engine.cpp:268).
+    """
+    name = "quantize_activations_i8_per_token"
+    dev = _require_gpu(name, x)
+    dt = _float_dtype(name, x)
+    h, kp, kpa, m = _rows(name, x, k_pad)
+    q = torch.empty((*x.shape[:-1], kpa), dtype=torch.int8, device=dev)
+    a_scale = torch.empty(x.shape[:-1], dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("wfb_quantize_act_i8", _p(x), dt, m, h, h, _p(q), kpa, kpa, _p(a_scale), _stream(dev))
+    return (q if kpa == kp else q[..., :kp]), a_scale
+
+
+def rmsnorm_quantize_i8(
+    x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float = 1e-6, k_pad: Optional[int] = None
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Fused RMSNorm/SubLN + per-token int8 quantisation: (q int8 [..., k_pad], a_scale fp32 [...]).
+
+    y = x / sqrt(mean(x^2) + eps) * weight (WF/models/subln.py:42-59) in fp32, then the quantiser.
+    """
+    name = "rmsnorm_quantize_i8"
+    dev = _require_gpu(name, x, weight)
+    dt = _float_dtype(name, x)
+    gdt = _float_dtype(name, weight) if weight is not None else WFB_F32
+    h, kp, kpa, m = _rows(name, x, k_pad)
+    if weight is not None and weight.numel() != h:
+        raise RuntimeError(f"{name}: weight has {weight.numel()} elements, expected {h}")
+    q = torch.empty((*x.shape[:-1], kpa), dtype=torch.int8, device=dev)
+    a_scale = torch.empty(x.shape[:-1], dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "wfb_rmsnorm_quant_i8", _p(x), dt, h, _p(weight), gdt, float(eps), m, h, _p(q), kpa, kpa, _p(a_scale), _stream(dev)
+        )
+    return (q if kpa == kp else q[..., :kp]), a_scale
+
+
+# ---- a4 / a5 / a6: ternary linear ----------------------------------------------------------------
+
+_KERNELS = {"auto": "wfb_linear_i2s", "gemv": "wfb_gemv_i2s", "gemm": "wfb_gemm_i2s"}
+
+
+def bitnet_linear(
+    packed_weights: torch.Tensor,
+    activations: torch.Tensor,
+    scale: Scale,
+    a_scale: Optional[torch.Tensor] = None,
+    bias: Optional[torch.Tensor] = None,
+    out_dtype: Optional[torch.dtype] = torch.bfloat16,
+    return_acc: bool = False,
+    kernel: str = "auto",
+):
+    """y[m, n] = acc[m, n] * scale * a_scale[m] (+ bias[n]) for int8 activations [M, K] (or [K]).
+
+    Returns y ([M, N] or [N], ``out_dtype`` bf16/fp32), or (y, acc int32) with ``return_acc``;
+    ``out_dtype=None`` computes only acc.  ``kernel`` forces "gemv" (M <= 2) or "gemm" (MFMA).
+    """
+    name = "bitnet_linear"
+    if packed_weights.dtype != torch.uint8 or packed_weights.dim() != 2:
+        raise RuntimeError(f"{name}: packed_weights must be uint8 2D [out_features, in_features/4]")
+    if activations.dtype != torch.int8 or activations.dim() not in (1, 2):
+        raise RuntimeError(f"{name}: activations must be int8 [in_features] or [batch, in_features]")
+    n, kb = packed_weights.shape
+    k = kb * 4
+    if k % QK_I2_S != 0:
+        raise ValueError(f"{name}: in_features ({k}) must be multiple of {QK_I2_S}")
+    a2 = activations.view(1, -1) if activations.dim() == 1 else activations
+    if a2.shape[1] != k:
+        raise ValueError(f"{name}: activations have {a2.shape[1]} features, packed weights {k}")
+    m = a2.shape[0]
+    dev = _require_gpu(name, packed_weights, a_scale, bias)
+    if a2.device != dev:
+        raise RuntimeError(f"{name}: activations are on {a2.device}, weights on {dev}")
+    if a2.stride(1) != 1 or (m > 1 and a2.stride(0) % 16 != 0) or a2.data_ptr() % 16 != 0:
+        a2 = a2.contiguous()
+    if a_scale is not None and (a_scale.dtype != torch.float32 or a_scale.numel() != m):
+        raise RuntimeError(f"{name}: a_scale must be fp32 with one element per token ({m})")
+    ws_dev, ws = _scale_args(name, scale, dev)
+    if out_dtype is None and not return_acc:
+        raise RuntimeError(f"{name}: nothing to compute (out_dtype=None and return_acc=False)")
+    out = None
+    odt = 0
+    if out_dtype is not None:
+        if out_dtype not in (torch.float32, torch.bfloat16):
+            raise RuntimeError(f"{name}: out_dtype must be float32 or bfloat16")
+        out = torch.empty((m, n), dtype=out_dtype, device=dev)
+        odt = _DT[out_dtype]
+    acc = torch.empty((m, n), dtype=torch.int32, device=dev) if return_acc else None
+    bdt = _float_dtype(name, bias) if bias is not None else 0
+    if bias is not None and bias.numel() != n:
+        raise RuntimeError(f"{name}: bias has {bias.numel()} elements, expected {n}")
+    lda = a2.stride(0) if m > 1 else k
+    if kernel not in _KERNELS:
+        raise ValueError(f"{name}: kernel must be one of {sorted(_KERNELS)}")
+    with torch.cuda.device(dev):
+        _lib.call(
+            _KERNELS[kernel], _p(packed_weights), n, k, _p(a2), m, lda, _p(a_scale), ws_dev, ws,
+            _p(bias), bdt, _p(out), odt, n, _p(acc), _stream(dev),
+        )
+    if activations.dim() == 1:
+        out = None if out is None else out.view(n)
+        acc = None if acc is None else acc.view(n)
+    return (out, acc) if return_acc else out
+
+
+def bitnet_gemv(packed_weights: torch.Tensor, activations: torch.Tensor, scale: Scale) -> torch.Tensor:
+    """fp32 [out] = acc * scale for one int8 token [in] (reference: bitnet.py:73-111)."""
+    if activations.dim() != 1:
+        raise RuntimeError("bitnet_gemv: activations must be 1D [in_features]")
+    if packed_weights.shape[1] * 4 % QK_I2_S != 0:
+        raise ValueError(f"bitnet_gemv: in_features ({packed_weights.shape[1] * 4}) must be multiple of {QK_I2_S}")
+    if activations.shape[0] != packed_weights.shape[1] * 4:
+        raise ValueError(
+            f"bitnet_gemv: activations.shape[0] ({activations.shape[0]}) != in_features ({packed_weights.shape[1] * 4})"
+        )
+    return bitnet_linear(packed_weights, activations, scale, out_dtype=torch.float32)
+
+
+def bitnet_gemm(packed_weights: torch.Tensor, activations: torch.Tensor, scale: Scale) -> torch.Tensor:
+    """fp32 [batch, out] = acc * scale for int8 tokens [batch, in] (reference: bitnet.py:114-152)."""
+    if activations.dim() != 2:
+        raise RuntimeError("bitnet_gemm: activations must be 2D [batch, in_features]")
+    if packed_weights.shape[1] * 4 % QK_I2_S != 0:
+        raise ValueError(f"bitnet_gemm: in_features ({packed_weights.shape[1] * 4}) must be multiple of {QK_I2_S}")
+    return bitnet_linear(packed_weights, activations, scale, out_dtype=torch.float32)
+
+
+# ---- torch.ops.wfbitnet registrations (reference schemas, torch_extension_cpu.cpp:913-920) ------
+
+_LIB_DEF = torch.library.Library("wfbitnet", "DEF")
+_LIB_DEF.define("bitnet_gemv(Tensor packed_weights, Tensor activations, float scale) -> Tensor")
+_LIB_DEF.define("bitnet_gemm(Tensor packed_weights, Tensor activations, float scale) -> Tensor")
+_LIB_DEF.define("bitnet_quantize_activations(Tensor input) -> (Tensor, Tensor)")
+_LIB_DEF.impl("bitnet_gemv", bitnet_gemv, "CUDA")
+_LIB_DEF.impl("bitnet_gemm", bitnet_gemm, "CUDA")
+_LIB_DEF.impl("bitnet_quantize_activations", quantize_activations_i8, "CUDA")
+
+
+def _gemv_meta(packed_weights, activations, scale):
+    return packed_weights.new_empty((packed_weights.shape[0],), dtype=torch.float32)
+
+
+def _gemm_meta(packed_weights, activations, scale):
+    return packed_weights.new_empty((activations.shape[0], packed_weights.shape[0]), dtype=torch.float32)
+
+
+def _quant_meta(x):
+    return x.new_empty(x.shape, dtype=torch.int8), x.new_empty((1,), dtype=torch.float32)
+
+
+_LIB_DEF.impl("bitnet_gemv", _gemv_meta, "Meta")
+_LIB_DEF.impl("bitnet_gemm", _gemm_meta, "Meta")
+_LIB_DEF.impl("bitnet_quantize_activations", _quant_meta, "Meta")
