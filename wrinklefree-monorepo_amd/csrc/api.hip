@@ -42,8 +42,11 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 enum class Kernel { Auto, Gemv, Gemm };
 
-// Decode (M <= 2) runs the VALU GEMV while the MFMA kernel is slower; everything else runs MFMA.
-bool use_gemv(int64_t m, int64_t k) { return m <= 2 && k <= (m == 1 ? 32768 : 20480); }
+// Decode (M <= 2) runs the VALU GEMV; everything else runs MFMA.  The GEMV addresses weights and
+// activations through 32-bit buffer offsets.
+bool use_gemv(int64_t m, int64_t n, int64_t k, int64_t lda) {
+  return m >= 1 && m <= 2 && k <= 32768 && n * (k / 4) <= INT32_MAX && (m - 1) * lda + k <= INT32_MAX;
+}
 
 int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act,
                 int64_t m, int64_t lda, const float* a_scale, const float* w_scale_dev, float w_scale,
@@ -65,9 +68,9 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
   if (out && out_dtype != WFB_F32 && out_dtype != WFB_BF16)
     return fail(WFB_EINVAL, "%s: out dtype must be WFB_F32 or WFB_BF16", name);
   if (bias && !valid_dtype(bias_dtype)) return fail(WFB_EINVAL, "%s: bad bias dtype %d", name, bias_dtype);
-  if (kind == Kernel::Gemv && !use_gemv(m, k))
-    return fail(WFB_EINVAL, "%s: the GEMV kernel takes M <= 2 tokens and K <= 20480/32768 (got M=%lld K=%lld)", name,
-                (long long)m, (long long)k);
+  if (kind == Kernel::Gemv && !use_gemv(m, n, k, lda))
+    return fail(WFB_EINVAL, "%s: the GEMV kernel takes M <= 2 tokens, K <= 32768 and N*K/4 < 2^31 (got M=%lld N=%lld K=%lld)",
+                name, (long long)m, (long long)n, (long long)k);
 
   wfb::Epilogue e;
   e.a_scale = a_scale;
@@ -80,7 +83,7 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
   e.ldo = ldo;
   e.acc_out = acc_out;
 
-  const bool gemv = kind == Kernel::Gemv || (kind == Kernel::Auto && use_gemv(m, k));
+  const bool gemv = kind == Kernel::Gemv || (kind == Kernel::Auto && use_gemv(m, n, k, lda));
   hipError_t st = gemv ? wfb::launch_gemv_i2s(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream))
                        : wfb::launch_gemm_i2s(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream));
   return hip_status(st, name);

@@ -75,8 +75,87 @@ __global__ __launch_bounds__(64 * WPB) void gemm_i2s_mfma16_kernel(const uint8_t
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int tok = m0 + mt * 16 + 4 * g + j;
-        if (tok < M) epi_store(ep, ws, tok, n, acc[mt][j]);
+        if (tok < M) epi_store(ep, ws, epi_ascale(ep, tok), epi_bias(ep, n), tok, n, acc[mt][j]);
       }
+  }
+}
+
+// Skinny GEMM for M <= 16 tokens (decode batches): one 16-row weight tile per workgroup, K split
+// over the S waves of the workgroup (SPW K-steps of 256 weights each), partial tiles summed in LDS.
+// Fields enter the MFMA masked but not shifted -- bits 1:0 (x1), 3:2 (x4), 5:4 and 7:6>>2 (x16) --
+// into three accumulators, so a packed dword costs 4 AND + 1 shift; the code offset (+1) is removed
+// with sum(a) per token: acc = acc1 + acc4/4 + acc16/16 - sum(a).
+template <int SPW, int S>
+__global__ __launch_bounds__(64 * S) void gemv_mfma16_kernel(const uint8_t* __restrict__ W,
+                                                             const int8_t* __restrict__ A, int64_t lda, int M,
+                                                             int N, int C, Epilogue ep) {
+  __shared__ int red[S][4][64];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * 16;
+  const int nl = lane & 15, g = lane >> 4;
+  const int n = n0 + nl;
+  const int64_t row_bytes = (int64_t)C * 16;
+  const uint8_t* wr = W + (int64_t)(n < N ? n : N - 1) * row_bytes;
+  const bool tok_ok = nl < M;
+  const int8_t* ar = A + (int64_t)(tok_ok ? nl : 0) * lda;
+  const int t0 = w * SPW;
+
+  // issue every load first
+  v4i wv[SPW];
+  v4i av[SPW][4];
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    const int c = 4 * (t0 + i) + g;
+    const bool ok = c < C;
+    wv[i] = ok ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wr + 16 * c)) : v4i{0, 0, 0, 0};
+    const int aoff = 128 * (c >> 1) + 16 * (c & 1);
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+      av[i][f] = (ok && tok_ok) ? *reinterpret_cast<const v4i*>(ar + aoff + 32 * f) : v4i{0, 0, 0, 0};
+  }
+
+  v4i acc1 = {0, 0, 0, 0}, acc4 = {0, 0, 0, 0}, acc16 = {0, 0, 0, 0};
+  int sa = 0;
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    v4i b0, b1, b2, b3;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = wv[i][e];
+      b0[e] = (d >> 2) & 0x30303030;
+      b1[e] = d & 0x30303030;
+      b2[e] = d & 0x0C0C0C0C;
+      b3[e] = d & 0x03030303;
+    }
+    acc16 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][0], b0, acc16, 0, 0, 0);
+    acc16 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][1], b1, acc16, 0, 0, 0);
+    acc4 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][2], b2, acc4, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][3], b3, acc1, 0, 0, 0);
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sa = __builtin_amdgcn_sdot4(av[i][f][e], 0x01010101, sa, false);
+  }
+  // sum(a) of token nl over this wave's K range: add the 4 lane groups
+  sa += __shfl_xor(sa, 16, 64);
+  sa += __shfl_xor(sa, 32, 64);
+  // this lane holds tokens 4g + j of column nl
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int saj = __shfl(sa, 4 * g + j, 64);
+    red[w][j][lane] = acc1[j] + (acc4[j] >> 2) + (acc16[j] >> 4) - saj;
+  }
+  __syncthreads();
+  if (w != 0) return;
+  const float ws = epi_wscale(ep);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tok = 4 * g + j;
+    int tot = red[0][j][lane];
+#pragma unroll
+    for (int k = 1; k < S; ++k) tot += red[k][j][lane];
+    if (tok < M && n < N) epi_store(ep, ws, epi_ascale(ep, tok), epi_bias(ep, n), tok, n, tot);
   }
 }
 

@@ -1,14 +1,11 @@
-// Decode GEMV for the I2_S ternary BitLinear (M <= 2 tokens): VALU sdot4, no MFMA.
+// Decode GEMV for the I2_S ternary BitLinear (M <= 2 tokens): VALU sdot4 + DPP reductions, no MFMA.
 //
 // Replaces bitnet_vec_dot_i2_i8 / bitnet_gemv_cpu
 // (SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:325-808, SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:331-367):
 //   acc[n] = sum_k code(W[n,k]) * a[k] - sum_k a[k] = sum_k w[n,k] * a[k].
 //
-// Work mapping (wave64).  A row of K weights is C = K/64 chunks of 16 packed bytes.  L lanes share
-// a row ("row group" = 64/L rows per wave pass); lane s of a group owns chunks s, s+L, ..., s+L*(CPL-1).
-// One 128-bit load per chunk per row, so each wave instruction reads 64/L rows x 16L contiguous bytes.
-// The activations a lane needs for its chunks (4 fields x 16 bytes per chunk) are loaded once into
-// registers and reused for every row group the wave visits.
+// Work mapping (wave64).  A row of K weights is C = K/64 chunks of 16 packed bytes; each chunk is
+// read with one 128-bit load and pairs with 4 x 16 activation bytes (one per 2-bit field).
 //
 // Inner product of one packed dword d (16 weights) with the 4 activation dwords it pairs with uses
 // the fields in place instead of shifting each down:
@@ -36,65 +33,98 @@ __device__ __forceinline__ int group_sum(int v) {
   return v;
 }
 
-template <int M, int L, int CPL>
-__global__ __launch_bounds__(64) void gemv_i2s_kernel(const uint8_t* __restrict__ W, const int8_t* __restrict__ A,
-                                                      int64_t lda, int N, int C, int n_groups, int rg,
-                                                      Epilogue ep) {
-  constexpr int RPG = 64 / L;
-  const int lane = threadIdx.x;
-  const int r_in = lane / L, s = lane % L;
-  const int64_t row_bytes = (int64_t)C * 16;
+// Split-K GEMV.  A workgroup owns RB = RP * (64/L) consecutive weight rows and all of K; its S waves
+// split K into S ranges of L*CPL chunks.  In a wave, L lanes share a row: lane s of a row group owns
+// chunks kc0 + s + L*i (i < CPL) and keeps the activations of those chunks in registers for all RP
+// row passes, so each activation byte is fetched once per wave and reused for 64/L * RP rows.
+// Loads go through raw buffer descriptors: rows past N read as zeros, so nothing is masked when the
+// chunk ranges tile K exactly (EXACT); otherwise chunks past K are zeroed explicitly.
+// All weight loads of the wave (RP*CPL x 16 B per lane) are issued before the first wait.
+// The code offset is removed with the wave's sum(a), computed once from a separate small load.
+// Per pass, each row's partial is reduced over its L lanes with DPP and parked in LDS; after one
+// barrier the first RB threads add the S partials of their row and store it (one coalesced store
+// per token).
+__device__ __forceinline__ int wave_sum(int v) {
+  v = group_sum<16>(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
 
-  // Activations for this lane's chunks, all tokens: a[m][i][q] = a_m[128b + 32q + j0 .. +15].
-  v4i a[M][CPL][4];
-  int suma[M];
+template <int M, int L, int CPL, int RP, int S, bool EXACT>
+__global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restrict__ W,
+                                                          const int8_t* __restrict__ A, int64_t lda, int N,
+                                                          int C, Epilogue ep) {
+  constexpr int RPG = 64 / L;  // rows per pass
+  constexpr int RB = RP * RPG; // rows per workgroup
+  static_assert(RB <= 64 * S, "one thread per row in the epilogue");
+  __shared__ int red[S][M][RB];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int r_in = lane / L, s = lane % L;
+  const uint32_t row_bytes = (uint32_t)C * 16;
+  const int row0 = blockIdx.x * RB;
+  const int kc0 = w * (L * CPL);
+  const buf_t wb = make_buf(W, (uint32_t)N * row_bytes);
+  const buf_t ab = make_buf(A, (uint32_t)((M - 1) * lda + (int64_t)C * 64));
+
+  // weights of every pass first
+  v4i wv[RP][CPL];
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    suma[m] = 0;
+  for (int p = 0; p < RP; ++p) {
+    const uint32_t rowoff = (uint32_t)(row0 + p * RPG + r_in) * row_bytes;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const int c = s + L * i;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (c < C) {
-          a[m][i][q] = *reinterpret_cast<const v4i*>(A + m * lda + 128 * (c >> 1) + 32 * q + 16 * (c & 1));
-        } else {
-          a[m][i][q] = v4i{0, 0, 0, 0};
-        }
-      }
+      const int c = kc0 + s + L * i;
+      wv[p][i] = buf_load16<kLoadNT>(wb, rowoff + 16 * c);
+      if (!EXACT && c >= C) wv[p][i] = v4i{0, 0, 0, 0};
     }
   }
+  // a[m][i][q] = a_m[128b + 32q + j0 .. +15] for chunk c (b = c/2, j0 = 16*(c%2))
+  v4i a[M][CPL][4];
 #pragma unroll
   for (int m = 0; m < M; ++m)
 #pragma unroll
-    for (int i = 0; i < CPL; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) suma[m] = __builtin_amdgcn_sdot4(a[m][i][q][t], 0x01010101, suma[m], false);
-
-  const float ws = epi_wscale(ep);
-  const int g0 = blockIdx.x * rg;
-
-  v4i cur[CPL], nxt[CPL];
-  auto load_group = [&](v4i (&w)[CPL], int g) {
-    const int n = g * RPG + r_in;
-    const bool row_ok = (g < n_groups) && (n < N);
-    const uint8_t* wr = W + (int64_t)n * row_bytes;
-#pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const int c = s + L * i;
-      if (row_ok && c < C) w[i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wr + 16 * c));
-      else w[i] = v4i{0, 0, 0, 0};
+      const int c = kc0 + s + L * i;
+      const uint32_t off = (uint32_t)(m * lda) + 128 * (c >> 1) + 16 * (c & 1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        a[m][i][q] = buf_load16(ab, off + 32 * q);
+        if (!EXACT && c >= C) a[m][i][q] = v4i{0, 0, 0, 0};
+      }
     }
-  };
 
-  load_group(cur, g0);
-  for (int r = 0; r < rg; ++r) {
-    const int g = g0 + r;
-    if (g >= n_groups) break;
-    if (r + 1 < rg) load_group(nxt, g + 1);
-    const int n = g * RPG + r_in;
+  // sum(a) over the wave's K range (contiguous activation bytes [64*kc0, 64*(kc0 + L*CPL))):
+  // each lane adds L*CPL of those bytes, then a wave reduction.  Subtracted once per row.
+  int suma[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const uint32_t boff = (uint32_t)(64 * kc0 + lane * (L * CPL));
+    int part = 0;
+    if (EXACT || boff < (uint32_t)(64 * C)) {
+      const uint32_t off = (uint32_t)(m * lda) + boff;
+      if constexpr (L * CPL == 4) {
+        part = __builtin_amdgcn_sdot4(__builtin_amdgcn_raw_buffer_load_b32(ab, (int)off, 0, 0), 0x01010101, 0, false);
+      } else if constexpr (L * CPL == 8) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(ab, (int)off, 0, 0);
+        part = __builtin_amdgcn_sdot4(v[0], 0x01010101, 0, false);
+        part = __builtin_amdgcn_sdot4(v[1], 0x01010101, part, false);
+      } else {
+        static_assert((L * CPL) % 16 == 0, "sum(a) slice must be 4, 8 or a multiple of 16 bytes");
+#pragma unroll
+        for (int b = 0; b < (L * CPL) / 16; ++b) {
+          const v4i v = buf_load16(ab, off + 16 * b);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) part = __builtin_amdgcn_sdot4(v[e], 0x01010101, part, false);
+        }
+      }
+    }
+    suma[m] = wave_sum(part);
+  }
+
+#pragma unroll
+  for (int p = 0; p < RP; ++p) {
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       int acc_a = 0, acc_b = 0, acc_c = 0;
@@ -102,52 +132,60 @@ __global__ __launch_bounds__(64) void gemv_i2s_kernel(const uint8_t* __restrict_
       for (int i = 0; i < CPL; ++i) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const int d = cur[i][t];
+          const int d = wv[p][i][t];
           acc_c = __builtin_amdgcn_sdot4((d >> 2) & 0x30303030, a[m][i][0][t], acc_c, false);
           acc_c = __builtin_amdgcn_sdot4(d & 0x30303030, a[m][i][1][t], acc_c, false);
           acc_b = __builtin_amdgcn_sdot4(d & 0x0C0C0C0C, a[m][i][2][t], acc_b, false);
           acc_a = __builtin_amdgcn_sdot4(d & 0x03030303, a[m][i][3][t], acc_a, false);
         }
       }
-      int tot = acc_a + (acc_b >> 2) + (acc_c >> 4) - suma[m];
-      tot = group_sum<L>(tot);
-      if (s == 0 && n < N) epi_store(ep, ws, m, n, tot);
+      int tot = group_sum<L>(acc_a + (acc_b >> 2) + (acc_c >> 4));
+      if (s == 0) red[w][m][p * RPG + r_in] = tot - suma[m];
     }
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t >= RB) return;
+  const int n = row0 + t;
+  if (n >= N) return;
+  const float ws = epi_wscale(ep);
+  const float bias = epi_bias(ep, n);
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) cur[i] = nxt[i];
+  for (int m = 0; m < M; ++m) {
+    int tot = red[0][m][t];
+#pragma unroll
+    for (int k = 1; k < S; ++k) tot += red[k][m][t];
+    epi_store(ep, ws, epi_ascale(ep, m), bias, m, n, tot);
   }
 }
 
-template <int M, int L, int CPL>
+template <int M, int L, int CPL, int RP, int S>
 hipError_t launch_cfg(const uint8_t* W, int n, int C, const int8_t* A, int64_t lda, const Epilogue& e,
-                      hipStream_t s) {
-  constexpr int RPG = 64 / L;
-  const int n_groups = (n + RPG - 1) / RPG;
-  // Aim for >= 4 waves per CU on 256 CUs before a wave takes a second row group.
-  int rg = n_groups / 2048;
-  if (rg < 1) rg = 1;
-  if (rg > 8) rg = 8;
-  const int blocks = (n_groups + rg - 1) / rg;
-  hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL>), dim3(blocks), dim3(64), 0, s, W, A, lda, n, C, n_groups, rg, e);
+                      hipStream_t st) {
+  constexpr int RB = RP * (64 / L);
+  const dim3 grid((n + RB - 1) / RB), block(64 * S);
+  if (C == L * CPL * S)
+    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true>), grid, block, 0, st, W, A, lda, n, C, e);
+  else
+    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, false>), grid, block, 0, st, W, A, lda, n, C, e);
   return hipGetLastError();
 }
 
-// Pick (L, CPL) with L * CPL >= C, at most 10 token-chunks of activations per lane (160 VGPRs),
-// L as small as possible (more rows share each wave instruction's activation addresses).
+// Launch shape by K (C = K/64 chunks) and N, from cold-HBM sweeps on MI355X at the BitNet-2B
+// shapes: 8 lanes x 1 chunk per row for K <= 4096, 16 lanes for longer rows, 4 row passes per wave
+// when there are enough rows to keep every CU busy.  Other K take the nearest shape with masking.
 template <int M>
 hipError_t launch_m(const uint8_t* W, int n, int C, const int8_t* A, int64_t lda, const Epilogue& e, hipStream_t s) {
-#define WFB_TRY(LL, CC) \
-  if constexpr (M * (CC) <= 10) {                                   \
-    if (C <= (LL) * (CC)) return launch_cfg<M, LL, CC>(W, n, C, A, lda, e, s); \
-  }
-  WFB_TRY(1, 4) WFB_TRY(1, 8)
-  WFB_TRY(2, 4) WFB_TRY(2, 5) WFB_TRY(2, 8)
-  WFB_TRY(4, 4) WFB_TRY(4, 5) WFB_TRY(4, 7) WFB_TRY(4, 8)
-  WFB_TRY(8, 4) WFB_TRY(8, 5) WFB_TRY(8, 7) WFB_TRY(8, 8)
-  WFB_TRY(16, 4) WFB_TRY(16, 5) WFB_TRY(16, 7) WFB_TRY(16, 8)
-  WFB_TRY(32, 4) WFB_TRY(32, 5) WFB_TRY(32, 7) WFB_TRY(32, 8)
-  WFB_TRY(64, 4) WFB_TRY(64, 5) WFB_TRY(64, 7) WFB_TRY(64, 8)
-#undef WFB_TRY
+  const bool tall = n >= 8192;
+  if (C <= 8) return launch_cfg<M, 8, 1, 2, 1>(W, n, C, A, lda, e, s);
+  if (C <= 16) return launch_cfg<M, 8, 1, 2, 2>(W, n, C, A, lda, e, s);
+  if (C <= 24) return launch_cfg<M, 8, 1, 2, 3>(W, n, C, A, lda, e, s);
+  if (C <= 40) return tall ? launch_cfg<M, 8, 1, 4, 5>(W, n, C, A, lda, e, s) : launch_cfg<M, 8, 1, 2, 5>(W, n, C, A, lda, e, s);
+  if (C <= 64) return tall ? launch_cfg<M, 8, 1, 4, 8>(W, n, C, A, lda, e, s) : launch_cfg<M, 8, 1, 2, 8>(W, n, C, A, lda, e, s);
+  if (C <= 112) return launch_cfg<M, 16, 1, 4, 7>(W, n, C, A, lda, e, s);
+  if (C <= 224) return launch_cfg<M, 16, 1, 4, 14>(W, n, C, A, lda, e, s);
+  if (C <= 256) return launch_cfg<M, 16, 1, 4, 16>(W, n, C, A, lda, e, s);
+  if (C <= 512) return launch_cfg<M, 16, 2, 4, 16>(W, n, C, A, lda, e, s);
   return hipErrorInvalidValue;  // K > 32768: callers route these to the MFMA kernel
 }
 

@@ -67,7 +67,7 @@ __global__ __launch_bounds__(kTPB) void quant_rows_kernel(const void* __restrict
 #pragma unroll
     for (int w = 1; w < kTPB / 64; ++w) tot = __fadd_rn(tot, red[w]);
     __syncthreads();
-    const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, (float)h), eps)));
+    const float r = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)h), eps)));
 #pragma unroll
     for (int it = 0; it < kMaxIt; ++it) {
       const int e0 = (it * kTPB + t) * kVec;

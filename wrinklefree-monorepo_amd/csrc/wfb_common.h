@@ -71,6 +71,20 @@ __device__ __forceinline__ int quant_i8(float v, float inv) {
   return (int)r;
 }
 
+// ---- raw buffer access (out-of-range reads return 0) --------------------------------------
+
+typedef __amdgpu_buffer_rsrc_t buf_t;
+constexpr int kBufDword3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+constexpr int kLoadNT = 2;              // non-temporal: streamed once, do not keep in cache
+
+__device__ __forceinline__ buf_t make_buf(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufDword3);
+}
+template <int AUX = 0>
+__device__ __forceinline__ v4i buf_load16(buf_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX);
+}
+
 // ---- GEMV / GEMM epilogue -------------------------------------------------------------------
 
 struct Epilogue {
@@ -86,22 +100,24 @@ struct Epilogue {
 };
 
 __device__ __forceinline__ float epi_wscale(const Epilogue& e) { return e.ws_dev ? e.ws_dev[0] : e.ws; }
+__device__ __forceinline__ float epi_ascale(const Epilogue& e, int m) { return e.a_scale ? e.a_scale[m] : 1.0f; }
+__device__ __forceinline__ float epi_bias(const Epilogue& e, int n) {
+  if (!e.bias) return 0.0f;
+  if (e.bias_dtype == WFB_F32) return reinterpret_cast<const float*>(e.bias)[n];
+  if (e.bias_dtype == WFB_BF16) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(e.bias)[n]);
+  return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(e.bias)[n]);
+}
 
 // y = ((float)acc * ws) * as (+ bias): the two products in this order, each rounded to fp32
 // (SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:846 then SGB/python/sglang/srt/layers/quantization/bitnet.py:241).
-__device__ __forceinline__ void epi_store(const Epilogue& e, float ws, int m, int n, int32_t acc) {
+// ws, as and bias are loaded by the caller (ahead of the main loop, to keep them off the critical path).
+__device__ __forceinline__ void epi_store(const Epilogue& e, float ws, float as, float bias, int m, int n,
+                                          int32_t acc) {
   const int64_t off = (int64_t)m * e.ldo + n;
   if (e.acc_out) e.acc_out[off] = acc;
   if (!e.out) return;
-  const float as = e.a_scale ? e.a_scale[m] : 1.0f;
   float y = __fmul_rn(__fmul_rn((float)acc, ws), as);
-  if (e.bias) {
-    float b;
-    if (e.bias_dtype == WFB_F32) b = reinterpret_cast<const float*>(e.bias)[n];
-    else if (e.bias_dtype == WFB_BF16) b = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(e.bias)[n]);
-    else b = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(e.bias)[n]);
-    y = __fadd_rn(y, b);
-  }
+  if (e.bias) y = __fadd_rn(y, bias);
   if (e.out_dtype == WFB_F32) reinterpret_cast<float*>(e.out)[off] = y;
   else reinterpret_cast<uint16_t*>(e.out)[off] = f32_to_bf16_rne(y);
 }
