@@ -90,7 +90,7 @@ def timed(torch, fns, steps, warmup):
     torch.cuda.synchronize()
     enqueue_s = (time.perf_counter() - t0) / min(steps, 8) * steps
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(int(_sleep_cycles(torch, 2.0 * enqueue_s + 0.005)))
+    torch.cuda._sleep(int(_sleep_cycles(torch, 3.0 * enqueue_s + 0.01)))
     start.record()
     for i in range(steps):
         for f in fns[i % len(fns)]:
@@ -115,6 +115,20 @@ def _sleep_cycles(torch, seconds):
         torch.cuda.synchronize()
         _SLEEP_RATE = 10_000_000 / max(s.elapsed_time(e) * 1e-3, 1e-6)
     return min(max(seconds, 0.002), 2.0) * _SLEEP_RATE
+
+
+def measured_traffic(n: int, k: int):
+    """HBM bytes per launch of the M=1 GEMV at (n, k) from the committed FETCH_SIZE / WRITE_SIZE
+    profile (profiles/gemv_i2s_decode_bitnet2b.txt, calibrated against a plain copy kernel), or None."""
+    path = ROOT / "profiles" / "gemv_i2s_decode_bitnet2b.txt"
+    key = f"traffic_bytes_per_launch gemv_i2s M=1 N={n} K={k}:"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith(key):
+                return int(line[len(key):].split()[0])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def cpu_baseline(seconds: float):
@@ -214,10 +228,11 @@ def main():
     ms_step = timed(torch, step_fns, args.steps, args.warmup)
     step_bytes = sum(s["bytes"] for s in shapes)
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    dom = max(range(len(shapes)), key=lambda i: per_shape[i]["us"])  # dominant kernel: longest launch
+    dom = max(range(len(shapes)), key=lambda i: shapes[i]["bytes"])  # dominant kernel: most bytes per launch
     d = per_shape[dom]
     roofline = {"bound": "hbm", "achieved": round(shapes[dom]["bytes"] / (d["us"] * 1e-6) / 1e9, 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(d["frac_hbm_peak"], 4), "traffic": None,
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(d["frac_hbm_peak"], 4),
+                "traffic": measured_traffic(d["N"], d["K"]),
                 "kernel": f"gemv_i2s M=1 N={d['N']} K={d['K']}",
                 "bytes_per_launch": shapes[dom]["bytes"]}
 

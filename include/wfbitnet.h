@@ -90,10 +90,11 @@ int wfb_quantize_act_i8_tensor(const void* x, int x_dtype, int64_t numel, int8_t
 /* ---- a3: RMSNorm / SubLN fused with a2 --------------------------------------------------- */
 
 /* y = x * (1 / sqrt(sum(x^2) / H + eps)) * gamma in fp32, then the per-token quantiser of
- * wfb_quantize_act_i8 on y.  Sum of squares in a fixed order: each of 256 threads accumulates
- * the elements (it*256 + t)*8 + e, it ascending, e = 0..7, then a xor-butterfly over each wave
- * (offsets 32,16,8,4,2,1) and the 4 wave sums added in wave order.  gamma may be NULL (no
- * affine).  Replaces SubLN.forward / RMSNorm.forward (WF/models/subln.py:42-59, 64-97) followed
+ * wfb_quantize_act_i8 on y.  Sum of squares in a fixed order.  H <= 4096: one wave per row, lane l
+ * accumulates elements (l + 64*j)*8 + e, j ascending, e = 0..7, then a xor butterfly over the wave
+ * (offsets 32,16,8,4,2,1).  H > 4096: each of 256 threads accumulates elements (it*256 + t)*8 + e,
+ * it ascending, e = 0..7, then the butterfly per wave and the 4 wave sums added in wave order.
+ * gamma may be NULL (no affine).  Replaces SubLN.forward / RMSNorm.forward (WF/models/subln.py:42-59, 64-97) followed
  * by activation quantisation (WF/models/bitlinear.py:66-84).  H % 8 == 0, H <= WFB_NORM_MAX_H. */
 int wfb_rmsnorm_quant_i8(const void* x, int x_dtype, int64_t ldx, const void* gamma, int gamma_dtype,
                          float eps, int64_t m, int64_t h, int8_t* q, int64_t k_pad, int64_t ldq,
@@ -113,7 +114,7 @@ int wfb_rmsnorm_quant_i8(const void* x, int x_dtype, int64_t ldx, const void* ga
  *   acc_out : int32 [M, N] with row stride ldo, or NULL (parity / debugging)
  *
  * wfb_linear_i2s picks the kernel from (M, N, K).  wfb_gemv_i2s forces the VALU decode GEMV
- * (M <= 8) and wfb_gemm_i2s forces the int8-MFMA GEMM (any M).  All three give identical acc.
+ * (M <= 2, K <= 32768, N*K/4 < 2^31) and wfb_gemm_i2s forces the int8-MFMA GEMM (any M).  All three give identical acc.
  * Replace bitnet_gemv_cpu / bitnet_gemm_cpu (SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:331-406,
  * kernels SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:325-874) and the rescale of
  * BitNetLinearMethod.apply (SGB/python/sglang/srt/layers/quantization/bitnet.py:232-253). */

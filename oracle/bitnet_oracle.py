@@ -139,10 +139,43 @@ def quantize_per_tensor(x: np.ndarray):
 # ---- a3: RMSNorm / SubLN fused with the quantiser ----------------------------------------------
 
 
-def _sum_squares_device_order(x: np.ndarray, tpb: int = 256, vec: int = 8) -> np.ndarray:
-    """fp32 sum of squares per row in the kernel's stated order (thread-sequential over
-    (iteration, element), xor butterfly per wave, waves added in order)."""
+WAVE_MAX_H = 4096  # rows up to this length use the one-wave-per-row order
+
+
+def _butterfly64(acc: np.ndarray) -> np.ndarray:
+    """Fixed xor butterfly over the last axis (64 lanes, offsets 32..1); returns lane 0."""
+    lanes = np.arange(64)
+    o = 32
+    while o >= 1:
+        acc = (acc + acc[..., lanes ^ o]).astype(F32)
+        o //= 2
+    return acc[..., 0]
+
+
+def _sum_squares_wave_order(x: np.ndarray, vec: int = 8) -> np.ndarray:
+    """One wave per row: lane l adds the squares of elements (l + 64*j)*8 + e sequentially over
+    (j, e), then the xor butterfly."""
     m, h = x.shape
+    per = 64 * vec
+    vpl = (h + per - 1) // per
+    xp = np.zeros((m, vpl * per), F32)
+    xp[:, :h] = x
+    xp = xp.reshape(m, vpl, 64, vec)
+    acc = np.zeros((m, 64), F32)
+    for j in range(vpl):
+        for e in range(vec):
+            v = xp[:, j, :, e]
+            acc = (acc + (v * v).astype(F32)).astype(F32)
+    return _butterfly64(acc)
+
+
+def _sum_squares_device_order(x: np.ndarray, tpb: int = 256, vec: int = 8) -> np.ndarray:
+    """fp32 sum of squares per row in the kernel's stated order: the one-wave order for rows up to
+    WAVE_MAX_H, else 256 threads per row (thread-sequential over (iteration, element), xor
+    butterfly per wave, waves added in order)."""
+    m, h = x.shape
+    if h <= WAVE_MAX_H:
+        return _sum_squares_wave_order(x, vec)
     per_it = tpb * vec
     its = (h + per_it - 1) // per_it
     xp = np.zeros((m, its * per_it), F32)

@@ -132,11 +132,8 @@ def test_rmsnorm_order_matches_float64_except_near_ties():
         assert (diff != 0).mean() < 1e-3
 
 
-def test_rmsnorm_sum_order_bruteforce():
-    # pure-python loops of the stated order on a small row
-    rng = np.random.default_rng(9)
-    h = 4096 + 256
-    x = rng.standard_normal((1, h)).astype(np.float32)
+def _bruteforce_block_order(x):
+    h = x.shape[1]
     acc = [np.float32(0.0)] * 256
     for it in range((h + 2047) // 2048):
         for t in range(256):
@@ -150,6 +147,29 @@ def test_rmsnorm_sum_order_bruteforce():
     tot = waves[0][0]
     for w in range(1, 4):
         tot = np.float32(tot + waves[w][0])
+    return tot
+
+
+def _bruteforce_wave_order(x):
+    h = x.shape[1]
+    acc = [np.float32(0.0)] * 64
+    for j in range((h + 511) // 512):
+        for lane in range(64):
+            for e in range(8):
+                i = (lane + 64 * j) * 8 + e
+                if i < h:
+                    acc[lane] = np.float32(acc[lane] + np.float32(x[0, i] * x[0, i]))
+    for o in (32, 16, 8, 4, 2, 1):
+        acc = [np.float32(acc[i] + acc[i ^ o]) for i in range(64)]
+    return acc[0]
+
+
+@pytest.mark.parametrize("h", [576, 2560, 4096, 4352, 6912])
+def test_rmsnorm_sum_order_bruteforce(h):
+    # pure-python loops of the stated orders (one wave per row up to 4096, else 256 threads per row)
+    rng = np.random.default_rng(h)
+    x = rng.standard_normal((1, h)).astype(np.float32)
+    tot = _bruteforce_wave_order(x) if h <= orc.WAVE_MAX_H else _bruteforce_block_order(x)
     assert orc._sum_squares_device_order(x)[0] == tot
     assert abs(float(tot) - float((x.astype(np.float64) ** 2).sum())) < 1e-4 * float(tot)
 
