@@ -1,0 +1,61 @@
+"""End-to-end parity: random-init SmolLM2-135M-shape BitNet, greedy decode of 128
+tokens from a 32-token random prompt.  The same model runs twice: every quantised BitLinear group
+(RMSNorm/SubLN -> per-token int8 -> ternary linear -> rescale) once on libwfbitnet and once on the
+CPU oracle; the float glue (embedding, RoPE, attention, SiLU, residuals, tied LM head) is the same
+code on the same device in both runs.  Token ids and every per-layer int32 accumulator must be equal.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bitnet_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+class OracleBackend:
+    """Quantised BitLinear groups computed by the numpy oracle on the host."""
+
+    def __init__(self, model, dev):
+        self.dev = dev
+        self.acc_log = []
+        self.w = {}
+        for lin in model.backend_linears:
+            packed = lin.qweight.cpu().numpy()
+            self.w[id(lin)] = (orc.unpack_i2s(packed).astype(np.float32), np.float32(lin.scale.item()))
+
+    def norm_linears(self, x, norm_weight, eps, linears):
+        xn = x.float().cpu().numpy()
+        g = None if norm_weight is None else norm_weight.float().cpu().numpy()
+        q, s = orc.rmsnorm_quant(xn, g, eps, k_pad=linears[0].k_pad)
+        outs = []
+        for lin in linears:
+            w, ws = self.w[id(lin)]
+            acc = (q.astype(np.float32) @ w.T).astype(np.int64)  # exact: |partial sums| < 2^24
+            self.acc_log.append(acc)
+            outs.append(torch.from_numpy(orc.rescale(acc, ws, s)).to(self.dev))
+        return outs
+
+
+def test_greedy_decode_tokens_and_accumulators_match_oracle(pkg, dev):
+    M = pkg.model
+    model = M.BitNetDecoder(M.SMOLLM2_135M, seed=0, device=dev)
+    model.backend_linears = list(M.quantised_linears(model).values())
+    prompt = torch.randint(0, M.SMOLLM2_135M.vocab_size, (1, 32), generator=torch.Generator().manual_seed(1))
+
+    hip = M.HipBackend(out_dtype=torch.float32, keep_acc=True)
+    model.backend = hip
+    toks_hip = model.generate(prompt, 128).cpu()
+
+    ref = OracleBackend(model, dev)
+    model.backend = ref
+    toks_ref = model.generate(prompt, 128).cpu()
+
+    assert toks_hip.shape == (1, 128)
+    assert torch.equal(toks_hip, toks_ref), f"first divergence at {int((toks_hip != toks_ref).nonzero()[0, 1])}"
+    assert len(hip.acc_log) == len(ref.acc_log) == 128 * 30 * 7
+    for i, (a, b) in enumerate(zip(hip.acc_log, ref.acc_log)):
+        assert np.array_equal(a.cpu().numpy().astype(np.int64), b), f"accumulator mismatch at call {i}"
+    # the generated text is not degenerate (random weights still give varied tokens)
+    assert len(set(toks_hip[0].tolist())) > 4

@@ -19,6 +19,7 @@ from .ops import (
     rmsnorm_quantize_i8,
     unpack_i2s,
 )
+from . import model
 from .bitlinear import (
     BitLinear,
     BitNetLinearMethod,
@@ -31,5 +32,5 @@ __all__ = [
     "LIB_PATH", "library_available", "QK_I2_S", "absmean_scale", "bitnet_gemm", "bitnet_gemv", "bitnet_linear",
     "check_kernel_available", "pack_ternary_i2s", "quantize_activations_i8", "quantize_activations_i8_per_token",
     "rmsnorm_quantize_i8", "unpack_i2s", "BitLinear", "BitNetLinearMethod", "SubLNBitLinear",
-    "convert_linear_to_bitlinear", "patch_model_with_native_kernels",
+    "convert_linear_to_bitlinear", "patch_model_with_native_kernels", "model",
 ]

@@ -1,0 +1,228 @@
+"""Minimal BitNet b1.58 decoder (stage-1 layout) running its BitLinears on the MI355X kernels.
+
+Layout follows the stage-1 conversion (packages/training/src/wrinklefree/training/stage1.py:63-214):
+HF Llama attention/MLP with q/k/v/gate/up as BitLinear and o_proj/down_proj as SubLN + BitLinear,
+SiLU SwiGLU, RMSNorm before attention and MLP, HF rotary embeddings (rotate-half form), GQA.
+Random init is normal(0, 0.02) for every weight and ones for every norm (BitNetLlama._init_weights,
+packages/training/src/wrinklefree/models/llama.py:58-65).
+
+Every quantised op goes through a *BitLinear backend*: one call per (norm -> quantise -> linear)
+group, so the norm before q/k/v (and before gate/up) is fused with the activation quantiser and
+shared by the projections that read it.  ``HipBackend`` runs libwfbitnet; a test can substitute
+another backend with the same two methods to compare the quantised path while the float code
+(embedding, RoPE, attention, SiLU, residuals, LM head) stays identical.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Sequence
+
+import torch
+
+from .ops import QK_I2_S, bitnet_linear, pack_ternary_i2s, rmsnorm_quantize_i8
+
+
+@dataclass(frozen=True)
+class BitNetConfig:
+    vocab_size: int
+    hidden_size: int
+    intermediate_size: int
+    num_layers: int
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    rope_theta: float
+    rms_eps: float = 1e-5   # input / post-attention / final RMSNorm
+    subln_eps: float = 1e-6  # SubLN before o_proj and down_proj (stage1.py:98, 151)
+    tie_embeddings: bool = True
+    ternary_lm_head: bool = False
+
+
+# SmolLM2-135M architecture (packages/training/configs/model/smollm2_135m.yaml)
+SMOLLM2_135M = BitNetConfig(vocab_size=49152, hidden_size=576, intermediate_size=1536, num_layers=30, num_heads=9,
+                            num_kv_heads=3, head_dim=64, rope_theta=100000.0)
+# Llama-3-8B architecture, every linear ternary (incl. the LM head)
+LLAMA3_8B = BitNetConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_layers=32, num_heads=32,
+                         num_kv_heads=8, head_dim=128, rope_theta=500000.0, tie_embeddings=False,
+                         ternary_lm_head=True)
+
+
+def _pad_k(k: int) -> int:
+    return (k + QK_I2_S - 1) // QK_I2_S * QK_I2_S
+
+
+class PackedLinear:
+    """I2_S weight of one projection: qweight uint8 [out, k_pad/4], scale fp32 [1] (device)."""
+
+    def __init__(self, weight: torch.Tensor):
+        self.out_features, self.in_features = weight.shape
+        self.k_pad = _pad_k(self.in_features)
+        self.qweight, self.scale = pack_ternary_i2s(weight.contiguous(), k_pad=self.k_pad)
+
+
+class HipBackend:
+    """Quantised BitLinear groups on libwfbitnet: fused RMSNorm/SubLN + per-token int8 quantisation,
+    then one GEMV/GEMM per projection with the rescale fused in its epilogue."""
+
+    def __init__(self, out_dtype: torch.dtype = torch.float32, keep_acc: bool = False):
+        self.out_dtype = out_dtype
+        self.keep_acc = keep_acc
+        self.acc_log: List[torch.Tensor] = []
+
+    def norm_linears(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], eps: float,
+                     linears: Sequence[PackedLinear]) -> List[torch.Tensor]:
+        k_pad = linears[0].k_pad
+        q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=k_pad)
+        outs = []
+        for lin in linears:
+            if self.keep_acc:
+                y, acc = bitnet_linear(lin.qweight, q, lin.scale, a_scale=a_scale, out_dtype=self.out_dtype,
+                                       return_acc=True)
+                self.acc_log.append(acc)
+            else:
+                y = bitnet_linear(lin.qweight, q, lin.scale, a_scale=a_scale, out_dtype=self.out_dtype)
+            outs.append(y)
+        return outs
+
+
+class _Layer:
+    def __init__(self, cfg: BitNetConfig, gen: torch.Generator, device: torch.device, dtype: torch.dtype):
+        h, f = cfg.hidden_size, cfg.intermediate_size
+        qd, kvd = cfg.num_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+
+        def w(o, i):
+            return (torch.randn((o, i), generator=gen, dtype=torch.float32) * 0.02).to(device)
+
+        self.q, self.k, self.v = PackedLinear(w(qd, h)), PackedLinear(w(kvd, h)), PackedLinear(w(kvd, h))
+        self.o = PackedLinear(w(h, qd))
+        self.gate, self.up = PackedLinear(w(f, h)), PackedLinear(w(f, h))
+        self.down = PackedLinear(w(h, f))
+        ones = lambda n: torch.ones(n, device=device, dtype=dtype)  # noqa: E731
+        self.input_norm, self.attn_sub_norm = ones(h), ones(qd)
+        self.post_attn_norm, self.ffn_sub_norm = ones(h), ones(f)
+
+
+class BitNetDecoder:
+    """Decoder-only BitNet model with a per-layer KV cache; float glue in ``dtype``."""
+
+    def __init__(self, cfg: BitNetConfig, seed: int = 0, device: str = "cuda", dtype: torch.dtype = torch.float32,
+                 backend=None):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.backend = backend if backend is not None else HipBackend(out_dtype=dtype if dtype == torch.float32
+                                                                       else torch.bfloat16)
+        gen = torch.Generator().manual_seed(seed)
+        self.embed = (torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen) * 0.02).to(self.device, dtype)
+        self.layers = [_Layer(cfg, gen, self.device, dtype) for _ in range(cfg.num_layers)]
+        self.final_norm = torch.ones(cfg.hidden_size, device=self.device, dtype=dtype)
+        if cfg.ternary_lm_head:
+            self.lm_head = PackedLinear((torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen) * 0.02)
+                                        .to(self.device))
+        else:
+            self.lm_head = None  # tied to the embedding
+        inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, dtype=torch.float32) / cfg.head_dim))
+        self.inv_freq = inv.to(self.device)
+        self.kv: List[Optional[List[torch.Tensor]]] = []
+
+    # ---- float glue --------------------------------------------------------------------------
+
+    def _rope(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """HF rotate-half rotary embedding; x [B, T, H, D], pos [T]."""
+        freqs = pos.to(torch.float32)[:, None] * self.inv_freq[None, :]
+        emb = torch.cat([freqs, freqs], dim=-1)
+        cos, sin = emb.cos()[None, :, None, :], emb.sin()[None, :, None, :]
+        x32 = x.to(torch.float32)
+        half = x32.shape[-1] // 2
+        rot = torch.cat([-x32[..., half:], x32[..., :half]], dim=-1)
+        return (x32 * cos + rot * sin).to(x.dtype)
+
+    def _rmsnorm(self, x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+        x32 = x.to(torch.float32)
+        return (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps) * w.to(torch.float32)).to(x.dtype)
+
+    def _attention(self, li: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start: int) -> torch.Tensor:
+        cfg = self.cfg
+        b, t = q.shape[0], q.shape[1]
+        cache = self.kv[li]
+        if cache is None:
+            cache = [torch.zeros((b, cfg.num_kv_heads, self._max_len, cfg.head_dim), device=self.device,
+                                 dtype=torch.float32) for _ in range(2)]
+            self.kv[li] = cache
+        cache[0][:, :, start:start + t] = k.transpose(1, 2).to(torch.float32)
+        cache[1][:, :, start:start + t] = v.transpose(1, 2).to(torch.float32)
+        kk = cache[0][:, :, :start + t]
+        vv = cache[1][:, :, :start + t]
+        rep = cfg.num_heads // cfg.num_kv_heads
+        kk = kk.repeat_interleave(rep, dim=1).contiguous()
+        vv = vv.repeat_interleave(rep, dim=1).contiguous()
+        qq = q.transpose(1, 2).to(torch.float32).contiguous()                 # [B, H, T, D]
+        scores = torch.matmul(qq, kk.transpose(-1, -2).contiguous()) / math.sqrt(cfg.head_dim)
+        if t > 1:
+            mask = torch.ones((t, start + t), device=self.device, dtype=torch.bool).tril(diagonal=start)
+            scores = scores.masked_fill(~mask, float("-inf"))
+        probs = torch.softmax(scores, dim=-1)
+        out = torch.matmul(probs, vv)                                          # [B, H, T, D]
+        return out.transpose(1, 2).reshape(b, t, cfg.num_heads * cfg.head_dim).to(self.dtype)
+
+    # ---- forward -------------------------------------------------------------------------------
+
+    def reset(self, batch: int, max_len: int) -> None:
+        self._max_len = max_len
+        self.kv = [None] * self.cfg.num_layers
+
+    def forward(self, ids: torch.Tensor, start: int) -> torch.Tensor:
+        """ids [B, T] at positions start..start+T-1; returns fp32 logits of the last position [B, vocab]."""
+        cfg, be = self.cfg, self.backend
+        b, t = ids.shape
+        x = self.embed[ids]                                                     # [B, T, H]
+        pos = torch.arange(start, start + t, device=self.device)
+        for li, L in enumerate(self.layers):
+            h2 = x.reshape(b * t, cfg.hidden_size)
+            q, k, v = be.norm_linears(h2, L.input_norm, cfg.rms_eps, [L.q, L.k, L.v])
+            q = self._rope(q.reshape(b, t, cfg.num_heads, cfg.head_dim).to(self.dtype), pos)
+            k = self._rope(k.reshape(b, t, cfg.num_kv_heads, cfg.head_dim).to(self.dtype), pos)
+            v = v.reshape(b, t, cfg.num_kv_heads, cfg.head_dim).to(self.dtype)
+            attn = self._attention(li, q, k, v, start).reshape(b * t, -1)
+            (o,) = be.norm_linears(attn, L.attn_sub_norm, cfg.subln_eps, [L.o])
+            x = x + o.reshape(b, t, -1).to(self.dtype)
+            h2 = x.reshape(b * t, cfg.hidden_size)
+            gate, up = be.norm_linears(h2, L.post_attn_norm, cfg.rms_eps, [L.gate, L.up])
+            act = (torch.nn.functional.silu(gate.to(torch.float32)) * up.to(torch.float32)).to(self.dtype)
+            (down,) = be.norm_linears(act, L.ffn_sub_norm, cfg.subln_eps, [L.down])
+            x = x + down.reshape(b, t, -1).to(self.dtype)
+        last = x[:, -1, :]
+        if self.lm_head is not None:
+            (logits,) = be.norm_linears(last.contiguous(), self.final_norm, cfg.rms_eps, [self.lm_head])
+            return logits.to(torch.float32)
+        hn = self._rmsnorm(last, self.final_norm, cfg.rms_eps).to(torch.float32)
+        return torch.matmul(hn, self.embed.to(torch.float32).t().contiguous())
+
+    @torch.no_grad()
+    def generate(self, prompt: torch.Tensor, new_tokens: int) -> torch.Tensor:
+        """Greedy decoding: prompt [B, T0] -> generated ids [B, new_tokens]."""
+        b, t0 = prompt.shape
+        self.reset(b, t0 + new_tokens)
+        logits = self.forward(prompt.to(self.device), 0)
+        out = []
+        nxt = torch.argmax(logits, dim=-1)
+        for i in range(new_tokens):
+            out.append(nxt)
+            if i + 1 == new_tokens:
+                break
+            logits = self.forward(nxt[:, None], t0 + i)
+            nxt = torch.argmax(logits, dim=-1)
+        return torch.stack(out, dim=1)
+
+
+def quantised_linears(model: BitNetDecoder) -> Dict[str, PackedLinear]:
+    """name -> PackedLinear for every ternary projection of the model."""
+    out = {}
+    for i, L in enumerate(model.layers):
+        for n in ("q", "k", "v", "o", "gate", "up", "down"):
+            out[f"layers.{i}.{n}"] = getattr(L, n)
+    if model.lm_head is not None:
+        out["lm_head"] = model.lm_head
+    return out
