@@ -80,353 +80,211 @@ __global__ __launch_bounds__(64 * WPB) void gemm_i2s_mfma16_kernel(const uint8_t
   }
 }
 
-// Skinny GEMM for M <= 16 tokens (decode batches): one 16-row weight tile per workgroup, K split
-// over the S waves of the workgroup (SPW K-steps of 256 weights each), partial tiles summed in LDS.
-// Fields enter the MFMA masked but not shifted -- bits 1:0 (x1), 3:2 (x4), 5:4 and 7:6>>2 (x16) --
-// into three accumulators, so a packed dword costs 4 AND + 1 shift; the code offset (+1) is removed
-// with sum(a) per token: acc = acc1 + acc4/4 + acc16/16 - sum(a).
-template <int SPW, int S>
-__global__ __launch_bounds__(64 * S) void gemv_mfma16_kernel(const uint8_t* __restrict__ W,
-                                                             const int8_t* __restrict__ A, int64_t lda, int M,
-                                                             int N, int C, Epilogue ep) {
-  __shared__ int red[S][4][64];
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * 16;
-  const int nl = lane & 15, g = lane >> 4;
-  const int n = n0 + nl;
-  const int64_t row_bytes = (int64_t)C * 16;
-  const uint8_t* wr = W + (int64_t)(n < N ? n : N - 1) * row_bytes;
-  const bool tok_ok = nl < M;
-  const int8_t* ar = A + (int64_t)(tok_ok ? nl : 0) * lda;
-  const int t0 = w * SPW;
+// Prefill GEMM (M > 64): v_mfma_i32_32x32x32_i8, workgroup tile BM x BN, four waves side by side in
+// N (wave tile BM x BN/4 = TM x TN sub-tiles of 32 x 32), K advancing one I2_S block (128 weights)
+// per step.
+//  * Operands: weights are src0 and activations src1, so an accumulator tile is C^T: lane (i, g)
+//    register r holds token row i and weight column 8*(r/4) + 4*g + r%4, and the epilogue writes 4
+//    consecutive outputs of one token row per store.
+//  * Weights go from global memory straight into registers (each wave owns its BN/4 columns): lane
+//    (i, g) of a 32-column sub-tile loads the 16 packed bytes of chunk 2*kt + g of its weight row,
+//    the src0 operands of 4 MFMAs, one per 2-bit field f, which pair with activation bytes
+//    [128*kt + 32f + 16g, +16).  A field enters the MFMA as its raw code {0,1,2} (shift + AND per
+//    dword); the +1 offset is removed at the end with each token's sum of activations, accumulated
+//    while the activations are staged: acc = sum(code * a) - sum(a).
+//  * Activations stream through LDS, double buffered (rows padded to 144 bytes so the 32 rows read
+//    by one MFMA operand fall on distinct banks).
+//  * Software pipeline: activation loads run three steps ahead and weight loads two steps ahead, in
+//    two register sets each (the K loop is unrolled by two so every register index is static); a
+//    step's activations are written to LDS one step before they are used; one barrier per step.
+//    The MFMA operands of field f + 1 are read from LDS while field f is multiplied.
+//  * Tile order: workgroup ids are remapped so that each XCD takes a contiguous range of tiles, and
+//    tiles are numbered in groups of kGroupM tile rows (column-major inside a group), so the
+//    workgroups resident on one XCD share activation rows and weight columns in its L2.
+//  * EPI = 1: bf16 output without bias or accumulator copy (the prefill case), vector stores only;
+//    EPI = 0: any output type, bias, accumulator copy.
+constexpr int kGroupM = 8;
 
-  // issue every load first
-  v4i wv[SPW];
-  v4i av[SPW][4];
-#pragma unroll
-  for (int i = 0; i < SPW; ++i) {
-    const int c = 4 * (t0 + i) + g;
-    const bool ok = c < C;
-    wv[i] = ok ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wr + 16 * c)) : v4i{0, 0, 0, 0};
-    const int aoff = 128 * (c >> 1) + 16 * (c & 1);
-#pragma unroll
-    for (int f = 0; f < 4; ++f)
-      av[i][f] = (ok && tok_ok) ? *reinterpret_cast<const v4i*>(ar + aoff + 32 * f) : v4i{0, 0, 0, 0};
-  }
-
-  v4i acc1 = {0, 0, 0, 0}, acc4 = {0, 0, 0, 0}, acc16 = {0, 0, 0, 0};
-  int sa = 0;
-#pragma unroll
-  for (int i = 0; i < SPW; ++i) {
-    v4i b0, b1, b2, b3;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int d = wv[i][e];
-      b0[e] = (d >> 2) & 0x30303030;
-      b1[e] = d & 0x30303030;
-      b2[e] = d & 0x0C0C0C0C;
-      b3[e] = d & 0x03030303;
-    }
-    acc16 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][0], b0, acc16, 0, 0, 0);
-    acc16 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][1], b1, acc16, 0, 0, 0);
-    acc4 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][2], b2, acc4, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][3], b3, acc1, 0, 0, 0);
-#pragma unroll
-    for (int f = 0; f < 4; ++f)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sa = __builtin_amdgcn_sdot4(av[i][f][e], 0x01010101, sa, false);
-  }
-  // sum(a) of token nl over this wave's K range: add the 4 lane groups
-  sa += __shfl_xor(sa, 16, 64);
-  sa += __shfl_xor(sa, 32, 64);
-  // this lane holds tokens 4g + j of column nl
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int saj = __shfl(sa, 4 * g + j, 64);
-    red[w][j][lane] = acc1[j] + (acc4[j] >> 2) + (acc16[j] >> 4) - saj;
-  }
-  __syncthreads();
-  if (w != 0) return;
-  const float ws = epi_wscale(ep);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tok = 4 * g + j;
-    int tot = red[0][j][lane];
-#pragma unroll
-    for (int k = 1; k < S; ++k) tot += red[k][j][lane];
-    if (tok < M && n < N) epi_store(ep, ws, epi_ascale(ep, tok), epi_bias(ep, n), tok, n, tot);
-  }
-}
-
-// Prefill GEMM (large M): v_mfma_i32_32x32x32_i8, workgroup tile BM x BN computed by 4 waves in a
-// WM x WN grid (wave tile TM x TN sub-tiles of 32 x 32), K advancing one I2_S block (128 weights) per
-// step.
-//  * A (int8 activations) streams through LDS, double buffered; rows are padded to 144 bytes so the
-//    32 lanes reading one MFMA fragment (16 B each, row stride 144) hit distinct banks.
-//  * W goes from global memory straight into registers: lane (j, g) of a 32-row weight sub-tile
-//    loads the 16 packed bytes of chunk 2*kt + g of row j, which are the B operands of 4 MFMAs, one
-//    per 2-bit field f; field f pairs with activation bytes [128*kt + 32f + 16g, +16) of each row.
-//  * Codes become signed int8 with one v_perm_b32 byte lookup per dword.
-//  * Workgroup ids are remapped so that the 8 XCDs each take a contiguous range of tiles (tiles in
-//    one range share activation rows in that XCD's L2).
-template <int BM, int BN, int WM, int WN, int KB = 1, int OCC = 1>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) void gemm_i2s_mfma32_kernel(
-    const uint8_t* __restrict__ W, const int8_t* __restrict__ A, int64_t lda, int M, int N, int C, int tiles_n,
-    int ntiles, Epilogue ep) {
-  static_assert(WM * WN == 4, "4 waves");
-  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-  constexpr int PITCH = 128 * KB + 16;
-  constexpr int AS = BM * KB / 32;  // 16-byte A segments per thread per K-step
+template <int BM, int BN, int OCC, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) void gemm_i2s_tile_kernel(
+    const uint8_t* __restrict__ W, const int8_t* __restrict__ A, int64_t lda, int M, int N, int C, int tiles_m,
+    int tiles_n, int ntiles, bool vec_out, Epilogue ep) {
+  constexpr int WN = 4;
+  constexpr int TM = BM / 32, TN = BN / WN / 32;
+  constexpr int PITCH = 144;
+  constexpr int AS = BM / 32;  // 16-byte activation segments per thread and step (8 threads per row)
+  static_assert(TN >= 1 && BN % (32 * WN) == 0 && BM % 32 == 0, "tile shape");
   __shared__ __attribute__((aligned(16))) int8_t lds[2][BM * PITCH];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int i = lane & 31, g = lane >> 5;
-
-  // XCD-aware tile order: hardware hands consecutive workgroup ids to the 8 XCDs in turn.
-  const int per = gridDim.x / 8;  // the grid is a multiple of 8
-  const int b = blockIdx.x;
-  const int t = (b % 8) * per + b / 8;
-  if (t >= ntiles) return;  // padding workgroups (whole workgroup leaves before any barrier)
-  const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
-
-  const int KT = C / (2 * KB);  // K-steps of 128*KB weights (callers guarantee C % (2*KB) == 0)
-  const uint32_t row_bytes = (uint32_t)C * 16;
-  const buf_t wb = make_buf(W, (uint32_t)N * row_bytes);
-  const buf_t ab = make_buf(A, (uint32_t)((int64_t)(M - 1) * lda + (int64_t)C * 64));
-
-  // A staging: thread covers rows arow + (256/(8*KB))*s, 16-byte segment aseg of the step's 128*KB bytes
-  constexpr int RPS = 256 / (8 * KB);  // rows covered per pass of the 256 threads
-  v4i areg[AS];
-  v4i breg[TN][KB];
-  const int arow = tid / (8 * KB), aseg = (tid % (8 * KB)) * 16;
-  auto load_a = [&](int kt) {
-#pragma unroll
-    for (int s = 0; s < AS; ++s)
-      areg[s] = buf_load16(ab, (uint32_t)((int64_t)(m0 + arow + RPS * s) * lda) + 128 * KB * kt + aseg);
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int s = 0; s < AS; ++s) *reinterpret_cast<v4i*>(&lds[buf][(arow + RPS * s) * PITCH + aseg]) = areg[s];
-  };
-  auto load_b = [&](int kt) {
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn) {
-      const int n = n0 + (wn * TN + tn) * 32 + i;
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) breg[tn][kb] = buf_load16(wb, (uint32_t)n * row_bytes + (2 * (KB * kt + kb) + g) * 16);
-    }
-  };
-
-  v16i acc[TM][TN];
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[tm][tn][r] = 0;
-
-  load_a(0);
-  load_b(0);
-  store_a(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    v4i bcur[TN][KB];
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) bcur[tn][kb] = breg[tn][kb];
-    if (kt + 1 < KT) {
-      load_a(kt + 1);
-      load_b(kt + 1);
-    }
-    const int8_t* la = &lds[cur][(wm * TM * 32 + i) * PITCH + 16 * g];
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        v4i bf[TN];
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) bf[tn][e] = codes_to_i8(((uint32_t)bcur[tn][kb][e] >> (6 - 2 * f)) & 0x03030303u);
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm) {
-          const v4i a = *reinterpret_cast<const v4i*>(la + tm * 32 * PITCH + 128 * kb + 32 * f);
-#pragma unroll
-          for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bf[tn], acc[tm][tn], 0, 0, 0);
-        }
-      }
-    if (kt + 1 < KT) store_a(cur ^ 1);
-    __syncthreads();
-  }
-
-  // 32x32 accumulator layout: lane (i, g), register r -> row 8*(r/4) + 4*g + r%4, column i.
-  const float ws = epi_wscale(ep);
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) {
-    const int n = n0 + (wn * TN + tn) * 32 + i;
-    if (n >= N) continue;
-    const float bias = epi_bias(ep, n);
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + (wm * TM + tm) * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (m < M) epi_store(ep, ws, epi_ascale(ep, m), bias, m, n, acc[tm][tn][r]);
-      }
-  }
-}
-
-template <int BM, int BN, int WM, int WN, int KB = 1, int OCC = 1>
-hipError_t launch_tile(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
-                       hipStream_t s) {
-  const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
-  const int nwg = tiles_n * tiles_m;
-  const int grid = ((nwg + 7) / 8) * 8;
-  hipLaunchKernelGGL((gemm_i2s_mfma32_kernel<BM, BN, WM, WN, KB, OCC>), dim3(grid), dim3(256), 0, s, W, A, lda, m,
-                     n, C, tiles_n, nwg, e);
-  return hipGetLastError();
-}
-
-// Prefill GEMM, pipelined: workgroup tile BM x BN, WM x WN waves (wave tile TM x TN sub-tiles of 32x32,
-// v_mfma_i32_32x32x32_i8), K advancing one I2_S block (128 weights) per step.
-//  * Both operands are staged through LDS, double buffered: A (int8, 128 B per row and step, rows
-//    padded to 144 B) and W (packed, 32 B per row and step, rows padded to 48 B); both pitches keep
-//    the 8 lanes of a 128-bit LDS read phase on distinct banks.
-//  * Global loads run two steps ahead through two register stage sets (the K loop is unrolled by two
-//    so every register index is static); a step's data is written to LDS one iteration after it was
-//    requested, and one barrier per step orders the buffers.
-//  * Lane (j, g) of a 32-row weight sub-tile reads the 16 packed bytes of chunk 2*kt + g of its row:
-//    the B operands of 4 MFMAs, one per 2-bit field f, which pair with activation bytes
-//    [32f + 16g, +16) of the step.  Codes become signed int8 with one v_perm_b32 per dword.
-//  * Workgroup ids are remapped so that each XCD takes a contiguous range of tiles.
-template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_i2s_pipe_kernel(const uint8_t* __restrict__ W,
-                                                                     const int8_t* __restrict__ A, int64_t lda,
-                                                                     int M, int N, int C, int tiles_n, int ntiles,
-                                                                     Epilogue ep) {
-  constexpr int NT = 64 * WM * WN;
-  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-  constexpr int AP = 144, BP = 48;             // LDS row pitches
-  constexpr int AS = BM * 8 / NT;              // 16-byte A segments per thread per step
-  constexpr int BS = BN * 2 / NT;              // 16-byte W segments per thread per step
-  static_assert(AS >= 1 && BS >= 1 && BM * 8 % NT == 0 && BN * 2 % NT == 0, "tile / thread mismatch");
-  __shared__ __attribute__((aligned(16))) int8_t la[2][BM * AP];
-  __shared__ __attribute__((aligned(16))) uint8_t lb[2][BN * BP];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
+  __shared__ int rowsum[BM];
+  const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
   const int i = lane & 31, g = lane >> 5;
 
   const int per = gridDim.x / 8;  // the grid is a multiple of 8
   const int t = (blockIdx.x % 8) * per + blockIdx.x / 8;
   if (t >= ntiles) return;
-  const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
+  const int gsz = kGroupM * tiles_n;
+  const int grp = t / gsz, r = t - grp * gsz;
+  const int gm = min(kGroupM, tiles_m - grp * kGroupM);
+  const int m0 = (grp * kGroupM + r % gm) * BM, n0 = (r / gm) * BN;
 
   const int KT = C / 2;
   const uint32_t row_bytes = (uint32_t)C * 16;
-  const buf_t wb = make_buf(W, (uint32_t)N * row_bytes);
-  const buf_t ab = make_buf(A, (uint32_t)((int64_t)(M - 1) * lda + (int64_t)C * 64));
-
-  // per-thread global source / LDS destination of its segments
+  const uint32_t a_end = (uint32_t)((int64_t)(M - 1) * lda + (int64_t)C * 64), b_end = (uint32_t)N * row_bytes;
+  const buf_t wb = make_buf(W, b_end);
+  const buf_t ab = make_buf(A, a_end);
+  // rows past the end of A or W are clamped to the last one (their results are never stored)
   const int arow = tid >> 3, aseg = (tid & 7) * 16;
-  const int brow = tid >> 1, bseg = (tid & 1) * 16;
-  uint32_t aoff[AS], boff[BS];
+  uint32_t aoff[AS], boff[TN];
 #pragma unroll
-  for (int s = 0; s < AS; ++s) aoff[s] = (uint32_t)((int64_t)(m0 + arow + s * (NT / 8)) * lda) + aseg;
+  for (int s = 0; s < AS; ++s) aoff[s] = (uint32_t)((int64_t)min(m0 + arow + 32 * s, M - 1) * lda) + aseg;
 #pragma unroll
-  for (int s = 0; s < BS; ++s) boff[s] = (uint32_t)(n0 + brow + s * (NT / 2)) * row_bytes + bseg;
+  for (int tn = 0; tn < TN; ++tn) boff[tn] = (uint32_t)min(n0 + (wn * TN + tn) * 32 + i, N - 1) * row_bytes + g * 16;
 
-  v4i ra0[AS], rb0[BS], ra1[AS], rb1[BS];
-  auto gload = [&](v4i (&ra)[AS], v4i (&rb)[BS], int kt) {
+  // Loads past the last step get an offset beyond the buffer: they return zeros without touching
+  // memory, so every load in the loop is unconditional (a fixed count of loads in flight).
+  v4i areg[2][AS], breg[2][TN];
+  int sa[AS];
 #pragma unroll
-    for (int s = 0; s < AS; ++s) ra[s] = buf_load16(ab, aoff[s] + 128 * kt);
+  for (int s = 0; s < AS; ++s) sa[s] = 0;
+  auto load_a = [&](int p, int kt) {
 #pragma unroll
-    for (int s = 0; s < BS; ++s) rb[s] = buf_load16(wb, boff[s] + 32 * kt);
+    for (int s = 0; s < AS; ++s) areg[p][s] = buf_load16(ab, kt < KT ? aoff[s] + 128 * kt : a_end);
   };
-  auto lstore = [&](const v4i (&ra)[AS], const v4i (&rb)[BS], int buf) {
+  auto load_b = [&](int p, int kt) {
 #pragma unroll
-    for (int s = 0; s < AS; ++s) *reinterpret_cast<v4i*>(&la[buf][(arow + s * (NT / 8)) * AP + aseg]) = ra[s];
+    for (int tn = 0; tn < TN; ++tn) breg[p][tn] = buf_load16(wb, kt < KT ? boff[tn] + 32 * kt : b_end);
+  };
+  auto stage_a = [&](int p) {
 #pragma unroll
-    for (int s = 0; s < BS; ++s) *reinterpret_cast<v4i*>(&lb[buf][(brow + s * (NT / 2)) * BP + bseg]) = rb[s];
+    for (int s = 0; s < AS; ++s) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sa[s] = __builtin_amdgcn_sdot4(areg[p][s][e], 0x01010101, sa[s], false);
+      *reinterpret_cast<v4i*>(&lds[p][(arow + 32 * s) * PITCH + aseg]) = areg[p][s];
+    }
   };
 
-  v16i acc[TM][TN];
+  v16i acc[TN][TM];
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
+  for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn)
+    for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[tm][tn][r] = 0;
+      for (int q = 0; q < 16; ++q) acc[tn][tm][q] = 0;
 
-  auto compute = [&](int buf) {
-    const int8_t* pa = &la[buf][(wm * TM * 32 + i) * AP + 16 * g];
-    const uint8_t* pb = &lb[buf][(wn * TN * 32 + i) * BP + 16 * g];
-    v4i bp[TN];
+  auto compute = [&](int p) {
+    const int8_t* la = &lds[p][i * PITCH + 16 * g];
+    v4i af[2][TM];
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) bp[tn] = *reinterpret_cast<const v4i*>(pb + tn * 32 * BP);
+    for (int tm = 0; tm < TM; ++tm) af[0][tm] = *reinterpret_cast<const v4i*>(la + tm * 32 * PITCH);
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
+      if (f < 3) {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+          af[(f + 1) & 1][tm] = *reinterpret_cast<const v4i*>(la + tm * 32 * PITCH + 32 * (f + 1));
+      }
+      __builtin_amdgcn_sched_barrier(0);
       v4i bf[TN];
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bf[tn][e] = codes_to_i8(((uint32_t)bp[tn][e] >> (6 - 2 * f)) & 0x03030303u);
+        for (int e = 0; e < 4; ++e) bf[tn][e] = (int)(((uint32_t)breg[p][tn][e] >> (6 - 2 * f)) & 0x03030303u);
 #pragma unroll
-      for (int tm = 0; tm < TM; ++tm) {
-        const v4i a = *reinterpret_cast<const v4i*>(pa + tm * 32 * AP + 32 * f);
+      for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bf[tn], acc[tm][tn], 0, 0, 0);
-      }
+        for (int tn = 0; tn < TN; ++tn)
+          acc[tn][tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[tn], af[f & 1][tm], acc[tn][tm], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // prologue: steps 0 and 1 in flight, step 0 in LDS
-  gload(ra0, rb0, 0);
-  if (KT > 1) gload(ra1, rb1, 1);
-  lstore(ra0, rb0, 0);
+  // A(j) lives in areg[j & 1] and lds[j & 1], B(j) in breg[j & 1].  Step kt: stage A(kt + 1), load
+  // A(kt + 3), multiply step kt, load B(kt + 2), barrier.
+  load_a(0, 0);
+  load_b(0, 0);
+  load_a(1, 1);
+  load_b(1, 1);
+  stage_a(0);
+  load_a(0, 2);
   __syncthreads();
-  for (int kt = 0; kt < KT; kt += 2) {
-    // even step kt: compute buffer 0; registers 0 take step kt+2; registers 1 (step kt+1) -> buffer 1
-    if (kt + 2 < KT) gload(ra0, rb0, kt + 2);
-    compute(0);
-    if (kt + 1 < KT) lstore(ra1, rb1, 1);
-    __syncthreads();
-    if (kt + 1 >= KT) break;
-    // odd step kt+1: compute buffer 1; registers 1 take step kt+3; registers 0 (step kt+2) -> buffer 0
-    if (kt + 3 < KT) gload(ra1, rb1, kt + 3);
-    compute(1);
-    if (kt + 2 < KT) lstore(ra0, rb0, 0);
-    __syncthreads();
+  const int KT2 = KT & ~1;
+  for (int kb = 0; kb < KT2; kb += 2) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int kt = kb + p;
+      if (kt + 1 < KT) stage_a(p ^ 1);
+      load_a(p ^ 1, kt + 3);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(p);
+      load_b(p, kt + 2);
+      __syncthreads();
+    }
   }
+  if (KT & 1) compute(0);  // last step (even index), staged in lds[0] by the previous step
 
-  // 32x32 accumulator layout: lane (i, g), register r -> row 8*(r/4) + 4*g + r%4, column i.
+  // the 8 threads of a row (consecutive lanes) hold partial sums of its 16-byte segments
+#pragma unroll
+  for (int s = 0; s < AS; ++s) {
+    int v = sa[s];
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    if ((tid & 7) == 0) rowsum[arow + 32 * s] = v;
+  }
+  __syncthreads();
+
   const float ws = epi_wscale(ep);
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn) {
-    const int n = n0 + (wn * TN + tn) * 32 + i;
-    if (n >= N) continue;
-    const float bias = epi_bias(ep, n);
+  for (int tm = 0; tm < TM; ++tm) {
+    const int ml = tm * 32 + i;
+    const int m = m0 + ml;
+    if (m >= M) continue;
+    const float as = epi_ascale(ep, m);
+    const int rs = rowsum[ml];
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
+    for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + (wm * TM + tm) * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (m < M) epi_store(ep, ws, epi_ascale(ep, m), bias, m, n, acc[tm][tn][r]);
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + (wn * TN + tn) * 32 + 8 * q + 4 * g;
+        if (n >= N) continue;
+        const int32_t v[4] = {acc[tn][tm][4 * q] - rs, acc[tn][tm][4 * q + 1] - rs, acc[tn][tm][4 * q + 2] - rs,
+                              acc[tn][tm][4 * q + 3] - rs};
+        if constexpr (EPI == 1) {
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = __fmul_rn(__fmul_rn((float)v[e], ws), as);
+          uint16_t* o = reinterpret_cast<uint16_t*>(ep.out) + (int64_t)m * ep.ldo + n;
+          if (n + 3 < N) {
+            const bf16x2_t lo = __builtin_convertvector((f32x2_t){y[0], y[1]}, bf16x2_t);
+            const bf16x2_t hi = __builtin_convertvector((f32x2_t){y[2], y[3]}, bf16x2_t);
+            *reinterpret_cast<uint2*>(o) =
+                make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < N) o[e] = f32_to_bf16_rne(y[e]);
+          }
+        } else {
+          epi_store4(ep, ws, as, m, n, v, vec_out && n + 3 < N, N);
+        }
       }
   }
 }
 
-template <int BM, int BN, int WM, int WN>
-hipError_t launch_pipe(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
+template <int BM, int BN, int OCC>
+hipError_t launch_tile(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
                        hipStream_t s) {
   const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
   const int nwg = tiles_n * tiles_m;
   const int grid = ((nwg + 7) / 8) * 8;
-  hipLaunchKernelGGL((gemm_i2s_pipe_kernel<BM, BN, WM, WN>), dim3(grid), dim3(64 * WM * WN), 0, s, W, A, lda, m,
-                     n, C, tiles_n, nwg, e);
+  const bool vec_out = e.ldo % 4 == 0 && (uintptr_t)e.out % 16 == 0 && (uintptr_t)e.acc_out % 16 == 0;
+  const bool bf16_only = e.out && e.out_dtype == WFB_BF16 && !e.bias && !e.acc_out && vec_out;
+  if (bf16_only)
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<BM, BN, OCC, 1>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, C,
+                       tiles_m, tiles_n, nwg, vec_out, e);
+  else
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<BM, BN, OCC, 0>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, C,
+                       tiles_m, tiles_n, nwg, vec_out, e);
   return hipGetLastError();
 }
 
@@ -448,7 +306,7 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   if (m <= 16) return launch_mt<1>(W, n, C, A, m, lda, e, s);
   if (m <= 32) return launch_mt<2>(W, n, C, A, m, lda, e, s);
   if (m <= 64) return launch_mt<4>(W, n, C, A, m, lda, e, s);
-  return launch_tile<64, 256, 1, 4, 1, 3>(W, n, C, A, m, lda, e, s);
+  return launch_tile<64, 256, 3>(W, n, C, A, m, lda, e, s);
 }
 
 }  // namespace wfb

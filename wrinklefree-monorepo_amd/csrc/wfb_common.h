@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
 #include <stdint.h>
 
 #include "../../include/wfbitnet.h"
@@ -120,6 +121,54 @@ __device__ __forceinline__ void epi_store(const Epilogue& e, float ws, float as,
   if (e.bias) y = __fadd_rn(y, bias);
   if (e.out_dtype == WFB_F32) reinterpret_cast<float*>(e.out)[off] = y;
   else reinterpret_cast<uint16_t*>(e.out)[off] = f32_to_bf16_rne(y);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Four consecutive outputs of one token row: y[m, n..n+3] from int32 accumulators v[0..3].
+// Same arithmetic as epi_store; bf16 conversion by v_cvt_pk_bf16_f32 (round to nearest even).
+// vec: the 4 outputs are in range and their address is 4-element aligned (one wide store).
+__device__ __forceinline__ void epi_store4(const Epilogue& e, float ws, float as, int m, int n, const int32_t (&v)[4],
+                                           bool vec, int N) {
+  const int64_t off = (int64_t)m * e.ldo + n;
+  if (e.acc_out) {
+    if (vec) {
+      *reinterpret_cast<v4i*>(e.acc_out + off) = v4i{v[0], v[1], v[2], v[3]};
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (n + j < N) e.acc_out[off + j] = v[j];
+    }
+  }
+  if (!e.out) return;
+  float y[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    y[j] = __fmul_rn(__fmul_rn((float)v[j], ws), as);
+    if (e.bias && n + j < N) y[j] = __fadd_rn(y[j], epi_bias(e, n + j));
+  }
+  if (e.out_dtype == WFB_F32) {
+    float* o = reinterpret_cast<float*>(e.out) + off;
+    if (vec) {
+      *reinterpret_cast<float4*>(o) = make_float4(y[0], y[1], y[2], y[3]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (n + j < N) o[j] = y[j];
+    }
+  } else {
+    uint16_t* o = reinterpret_cast<uint16_t*>(e.out) + off;
+    if (vec) {
+      const bf16x2_t lo = __builtin_convertvector((f32x2_t){y[0], y[1]}, bf16x2_t);
+      const bf16x2_t hi = __builtin_convertvector((f32x2_t){y[2], y[3]}, bf16x2_t);
+      *reinterpret_cast<uint2*>(o) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (n + j < N) o[j] = f32_to_bf16_rne(y[j]);
+    }
+  }
 }
 
 // ---- internal launchers (return hipError_t of the launch) --------------------------------
