@@ -80,88 +80,124 @@ __global__ __launch_bounds__(64 * WPB) void gemm_i2s_mfma16_kernel(const uint8_t
   }
 }
 
-// Prefill GEMM (M > 64): v_mfma_i32_32x32x32_i8, workgroup tile BM x BN, four waves side by side in
-// N (wave tile BM x BN/4 = TM x TN sub-tiles of 32 x 32), K advancing one I2_S block (128 weights)
-// per step.
-//  * Operands: weights are src0 and activations src1, so an accumulator tile is C^T: lane (i, g)
-//    register r holds token row i and weight column 8*(r/4) + 4*g + r%4, and the epilogue writes 4
-//    consecutive outputs of one token row per store.
-//  * Weights go from global memory straight into registers (each wave owns its BN/4 columns): lane
-//    (i, g) of a 32-column sub-tile loads the 16 packed bytes of chunk 2*kt + g of its weight row,
-//    the src0 operands of 4 MFMAs, one per 2-bit field f, which pair with activation bytes
-//    [128*kt + 32f + 16g, +16).  A field enters the MFMA as its raw code {0,1,2} (shift + AND per
-//    dword); the +1 offset is removed at the end with each token's sum of activations, accumulated
-//    while the activations are staged: acc = sum(code * a) - sum(a).
-//  * Activations stream through LDS, double buffered (rows padded to 144 bytes so the 32 rows read
-//    by one MFMA operand fall on distinct banks).
-//  * Software pipeline: activation loads run three steps ahead and weight loads two steps ahead, in
-//    two register sets each (the K loop is unrolled by two so every register index is static); a
-//    step's activations are written to LDS one step before they are used; one barrier per step.
-//    The MFMA operands of field f + 1 are read from LDS while field f is multiplied.
-//  * Tile order: workgroup ids are remapped so that each XCD takes a contiguous range of tiles, and
-//    tiles are numbered in groups of kGroupM tile rows (column-major inside a group), so the
-//    workgroups resident on one XCD share activation rows and weight columns in its L2.
-//  * EPI = 1: bf16 output without bias or accumulator copy (the prefill case), vector stores only;
-//    EPI = 0: any output type, bias, accumulator copy.
+// Prefill GEMM (M > 64): v_mfma_i32_32x32x32_i8.  Workgroup tile BM x 256 (BM = 32 TM), four waves
+// side by side in N, each owning 64 weight columns (wave tile BM x 64 = TM x 2 MFMA tiles).  K advances
+// in stages of KB I2_S blocks (128 KB weights).
+//  * Operand roles: weights are src0 and activations src1, so an accumulator tile is C^T: lane (i, g)
+//    register r holds token row i and weight column 8*(r/4) + 4*g + r%4.
+//  * k-slot pairing: lane (i, g) feeds the 16 packed bytes of half g of an I2_S block of its weight
+//    row -- field f of them covers k = 128*b + 32f + 16g + 0..15 -- so the activation operand of
+//    the same lane is the 16 contiguous bytes at that k.  A field enters the MFMA as its raw code
+//    {0,1,2} (shift + AND per dword); the +1 offset is removed at the end with each token's sum of
+//    activations: acc = sum(code * a) - sum(a).
+//  * Both operands go from global memory straight into LDS (buffer_load_dwordx4 ... lds, 16 bytes per
+//    lane at LDS base + 16 * lane), double buffered per stage.  Each load instruction covers whole
+//    128-byte lines (activations: 8 or 4 rows) or 16-32 rows x 32-64 bytes (weights), against 32 rows
+//    per instruction when weights are loaded into registers in MFMA layout.  The global source of
+//    each lane is chosen so the LDS rows come out XOR-swizzled in 16-byte chunks, which makes the
+//    MFMA-operand reads conflict-free.
+//  * Per stage: one vmcnt(0) + barrier, the next stage's loads issued, then the stage multiplied.
+//    All operand fragments of the stage are read up front (double-buffered MFMA tiles per field for
+//    TM = 4); the unpack of field f + 1 is interleaved with the MFMAs of field f.
+//  * sum(a): each wave sums a quarter of the tile rows from the staged activations.
+//  * Tile order: XCD-aware (each XCD takes a contiguous range of tiles) and grouped by kGroupM tile
+//    rows, so the workgroups resident on one XCD share activation rows and weight columns in its L2.
+//  * EPI = 1 (bf16 output, no bias, no accumulator copy): the tile is converted in registers, staged
+//    through LDS and written with 16-byte stores that fill whole output lines.  EPI = 0: any output
+//    type, bias, accumulator copy, stored from registers.
 constexpr int kGroupM = 8;
 
-template <int BM, int BN, int OCC, int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) void gemm_i2s_tile_kernel(
-    const uint8_t* __restrict__ W, const int8_t* __restrict__ A, int64_t lda, int M, int N, int C, int tiles_m,
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void lds_load16(buf_t r, void* lds_base, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_base, 16, voff, 0, 0, 0);
+}
+
+template <int TM, int KB, int OCC, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_i2s_tile_kernel(
+    const uint8_t* __restrict__ W, const int8_t* __restrict__ A, int64_t lda, int M, int N, int K, int tiles_m,
     int tiles_n, int ntiles, bool vec_out, Epilogue ep) {
-  constexpr int WN = 4;
-  constexpr int TM = BM / 32, TN = BN / WN / 32;
-  constexpr int PITCH = 144;
-  constexpr int AS = BM / 32;  // 16-byte activation segments per thread and step (8 threads per row)
-  static_assert(TN >= 1 && BN % (32 * WN) == 0 && BM % 32 == 0, "tile shape");
-  __shared__ __attribute__((aligned(16))) int8_t lds[2][BM * PITCH];
+  constexpr int BM = 32 * TM, BN = 256, TN = 2;
+  constexpr int AROW = 128 * KB;  // bytes of an activation row per stage
+  constexpr int CH = 8 * KB;      // 16-byte chunks per activation row
+  constexpr int BROW = 32 * KB;   // bytes of a weight row per stage
+  constexpr int ASZ = BM * AROW, BSZ = BN * BROW;
+  constexpr int AI = ASZ / 4096, BI = BSZ / 4096;  // 1 KB load instructions per wave and stage
+  constexpr int ARPI = 64 / CH;                    // activation rows per load instruction
+  constexpr int BLPR = BROW / 16;                  // lanes per weight row in a load instruction
+  constexpr int X = 4 * KB;                        // (block, field) MFMA steps per stage
+  constexpr int LPR = 256 / BM, SCH = CH / LPR;    // sum(a): lanes per row, chunks per lane
+  static_assert(AI >= 1 && BI >= 1 && ASZ >= 8192 && BSZ >= 8192 && SCH >= 1 && SCH <= X, "tile shape");
+  __shared__ __attribute__((aligned(16))) int8_t lds_a0[ASZ];
+  __shared__ __attribute__((aligned(16))) int8_t lds_a1[ASZ];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b0[BSZ];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b1[BSZ];
   __shared__ int rowsum[BM];
-  const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
-  const int i = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, l = tid & 63, wn = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = l & 31, g = l >> 5;
 
   const int per = gridDim.x / 8;  // the grid is a multiple of 8
   const int t = (blockIdx.x % 8) * per + blockIdx.x / 8;
   if (t >= ntiles) return;
   const int gsz = kGroupM * tiles_n;
-  const int grp = t / gsz, r = t - grp * gsz;
+  const int grp = t / gsz, rr = t - grp * gsz;
   const int gm = min(kGroupM, tiles_m - grp * kGroupM);
-  const int m0 = (grp * kGroupM + r % gm) * BM, n0 = (r / gm) * BN;
+  const int m0 = (grp * kGroupM + rr % gm) * BM, n0 = (rr / gm) * BN;
 
-  const int KT = C / 2;
-  const uint32_t row_bytes = (uint32_t)C * 16;
-  const uint32_t a_end = (uint32_t)((int64_t)(M - 1) * lda + (int64_t)C * 64), b_end = (uint32_t)N * row_bytes;
-  const buf_t wb = make_buf(W, b_end);
+  const int KS = (K + AROW - 1) / AROW;
+  const uint32_t row_bytes = (uint32_t)K / 4;
+  const uint32_t a_end = (uint32_t)((int64_t)(M - 1) * lda + K), b_end = (uint32_t)N * row_bytes;
   const buf_t ab = make_buf(A, a_end);
-  // rows past the end of A or W are clamped to the last one (their results are never stored)
-  const int arow = tid >> 3, aseg = (tid & 7) * 16;
-  uint32_t aoff[AS], boff[TN];
-#pragma unroll
-  for (int s = 0; s < AS; ++s) aoff[s] = (uint32_t)((int64_t)min(m0 + arow + 32 * s, M - 1) * lda) + aseg;
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) boff[tn] = (uint32_t)min(n0 + (wn * TN + tn) * 32 + i, N - 1) * row_bytes + g * 16;
+  const buf_t wb = make_buf(W, b_end);
 
-  // Loads past the last step get an offset beyond the buffer: they return zeros without touching
-  // memory, so every load in the loop is unconditional (a fixed count of loads in flight).
-  v4i areg[2][AS], breg[2][TN];
-  int sa[AS];
+  // LDS position p of activation row r holds chunk p ^ aswz(r); position q of weight row R holds
+  // 16-byte piece q ^ bswz(R).  (16 consecutive rows then fall on 16 distinct 16-byte bank groups.)
+  auto aswz = [](int r) { return KB == 2 ? (r & 15) : ((r >> 1) & 7); };
+  auto bswz = [](int R) { return KB == 2 ? ((R >> 2) & 3) : ((R >> 3) & 1); };
+
+  // Load descriptors: wave wn issues instructions AI*wn.. and BI*wn.. of each stage.  Rows past the
+  // end of A or W are clamped to the last one (their results are never stored); bytes past K get an
+  // offset beyond the buffer and load as zeros without touching memory.
+  uint32_t a_row[AI], a_col[AI], b_row[BI], b_col[BI];
 #pragma unroll
-  for (int s = 0; s < AS; ++s) sa[s] = 0;
-  auto load_a = [&](int p, int kt) {
+  for (int jj = 0; jj < AI; ++jj) {
+    const int r = ARPI * (AI * wn + jj) + l / CH;
+    a_row[jj] = (uint32_t)((int64_t)min(m0 + r, M - 1) * lda);
+    a_col[jj] = 16 * ((l % CH) ^ aswz(r));
+  }
 #pragma unroll
-    for (int s = 0; s < AS; ++s) areg[p][s] = buf_load16(ab, kt < KT ? aoff[s] + 128 * kt : a_end);
-  };
-  auto load_b = [&](int p, int kt) {
+  for (int jj = 0; jj < BI; ++jj) {
+    const int R = (64 / BLPR) * (BI * wn + jj) + l / BLPR;
+    b_row[jj] = (uint32_t)min(n0 + R, N - 1) * row_bytes;
+    b_col[jj] = 16 * ((l % BLPR) ^ bswz(R));
+  }
+  auto issue = [&](int kt, int8_t* la, uint8_t* lb) {
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) breg[p][tn] = buf_load16(wb, kt < KT ? boff[tn] + 32 * kt : b_end);
-  };
-  auto stage_a = [&](int p) {
+    for (int jj = 0; jj < AI; ++jj) {
+      const uint32_t ka = (uint32_t)AROW * kt + a_col[jj];
+      lds_load16(ab, la + (AI * wn + jj) * 1024, ka < (uint32_t)K ? a_row[jj] + ka : a_end);
+    }
 #pragma unroll
-    for (int s = 0; s < AS; ++s) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sa[s] = __builtin_amdgcn_sdot4(areg[p][s][e], 0x01010101, sa[s], false);
-      *reinterpret_cast<v4i*>(&lds[p][(arow + 32 * s) * PITCH + aseg]) = areg[p][s];
+    for (int jj = 0; jj < BI; ++jj) {
+      const uint32_t kb = (uint32_t)BROW * kt + b_col[jj];
+      lds_load16(wb, lb + (BI * wn + jj) * 1024, kb < row_bytes ? b_row[jj] + kb : b_end);
     }
   };
+
+  // per-lane LDS offsets of the MFMA operands and of the sum(a) chunks (the same every stage)
+  uint32_t aoffs[X], boffs[KB][TN], soffs[SCH];
+#pragma unroll
+  for (int x = 0; x < X; ++x) aoffs[x] = i * AROW + (((8 * (x >> 2) + 2 * (x & 3) + g) ^ aswz(i)) * 16);
+#pragma unroll
+  for (int u = 0; u < KB; ++u)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int R = (wn * TN + tn) * 32 + i;
+      boffs[u][tn] = R * BROW + (((2 * u + g) ^ bswz(R)) * 16);
+    }
+  const int srow = wn * (BM / 4) + l / LPR;  // wave wn sums rows [wn BM/4, (wn + 1) BM/4)
+#pragma unroll
+  for (int j = 0; j < SCH; ++j) soffs[j] = srow * AROW + ((l % LPR) * SCH + j) * 16;
+  int ssum = 0;
 
   v16i acc[TN][TM];
 #pragma unroll
@@ -171,119 +207,148 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) v
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[tn][tm][q] = 0;
 
-  auto compute = [&](int p) {
-    const int8_t* la = &lds[p][i * PITCH + 16 * g];
-    v4i af[2][TM];
+  auto compute = [&](const int8_t* la, const uint8_t* lb) {
+    constexpr int AF = TM >= 4 ? 2 : X;  // A fragments held: all of the stage, or a two-step ring
+    v4i af[AF][TM], bw[KB][TN], bf[2][TN], sv[SCH];
+    auto read_a = [&](v4i(&dst)[TM], int x) {
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) af[0][tm] = *reinterpret_cast<const v4i*>(la + tm * 32 * PITCH);
+      for (int tm = 0; tm < TM; ++tm) dst[tm] = *reinterpret_cast<const v4i*>(la + aoffs[x] + tm * 32 * AROW);
+    };
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      if (f < 3) {
+    for (int u = 0; u < KB; ++u)
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-          af[(f + 1) & 1][tm] = *reinterpret_cast<const v4i*>(la + tm * 32 * PITCH + 32 * (f + 1));
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      v4i bf[TN];
+      for (int tn = 0; tn < TN; ++tn) bw[u][tn] = *reinterpret_cast<const v4i*>(lb + boffs[u][tn]);
+#pragma unroll
+    for (int x = 0; x < (AF == X ? X : 1); ++x) read_a(af[x], x);
+#pragma unroll
+    for (int j = 0; j < SCH; ++j) sv[j] = *reinterpret_cast<const v4i*>(la + soffs[j]);
+    __builtin_amdgcn_sched_barrier(0);
+    auto unpack = [&](v4i(&dst)[TN], const v4i(&src)[TN], int f) {
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bf[tn][e] = (int)(((uint32_t)breg[p][tn][e] >> (6 - 2 * f)) & 0x03030303u);
+        for (int e = 0; e < 4; ++e) dst[tn][e] = (int)(((uint32_t)src[tn][e] >> (6 - 2 * f)) & 0x03030303u);
+    };
+    unpack(bf[0], bw[0], 0);
+#pragma unroll
+    for (int x = 0; x < X; ++x) {
+      if (AF != X && x + 1 < X) read_a(af[(x + 1) % AF], x + 1);
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn)
-          acc[tn][tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[tn], af[f & 1][tm], acc[tn][tm], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
+          acc[tn][tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[x & 1][tn], af[x % AF][tm], acc[tn][tm], 0, 0, 0);
+      if (x + 1 < X) unpack(bf[(x + 1) & 1], bw[(x + 1) >> 2], (x + 1) & 3);
+      if (x < SCH) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ssum = __builtin_amdgcn_sdot4(sv[x][e], 0x01010101, ssum, false);
+      }
+      // interleave: one MFMA, then a share of the unpack / sum VALU work (and the next A reads)
+#pragma unroll
+      for (int k = 0; k < TM * TN; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        if (AF != X && k < TM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
     }
   };
 
-  // A(j) lives in areg[j & 1] and lds[j & 1], B(j) in breg[j & 1].  Step kt: stage A(kt + 1), load
-  // A(kt + 3), multiply step kt, load B(kt + 2), barrier.
-  load_a(0, 0);
-  load_b(0, 0);
-  load_a(1, 1);
-  load_b(1, 1);
-  stage_a(0);
-  load_a(0, 2);
-  __syncthreads();
-  const int KT2 = KT & ~1;
-  for (int kb = 0; kb < KT2; kb += 2) {
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int kt = kb + p;
-      if (kt + 1 < KT) stage_a(p ^ 1);
-      load_a(p ^ 1, kt + 3);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(p);
-      load_b(p, kt + 2);
+  issue(0, lds_a0, lds_b0);
+  for (int kb = 0; kb < KS; kb += 2) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of stage kb are in LDS
+    __syncthreads();                      // everyone's; and everyone is done with stage kb - 1
+    if (kb + 1 < KS) issue(kb + 1, lds_a1, lds_b1);
+    compute(lds_a0, lds_b0);
+    if (kb + 1 < KS) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
+      if (kb + 2 < KS) issue(kb + 2, lds_a0, lds_b0);
+      compute(lds_a1, lds_b1);
     }
   }
-  if (KT & 1) compute(0);  // last step (even index), staged in lds[0] by the previous step
 
-  // the 8 threads of a row (consecutive lanes) hold partial sums of its 16-byte segments
-#pragma unroll
-  for (int s = 0; s < AS; ++s) {
-    int v = sa[s];
-    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
-    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
-    v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
-    if ((tid & 7) == 0) rowsum[arow + 32 * s] = v;
-  }
-  __syncthreads();
+  // sum(a) per row: the LPR lanes of a row (consecutive) hold partial sums of its chunks
+  ssum += __builtin_amdgcn_update_dpp(0, ssum, 0xB1, 0xF, 0xF, false);    // quad_perm 1,0,3,2
+  if constexpr (LPR == 4) ssum += __builtin_amdgcn_update_dpp(0, ssum, 0x4E, 0xF, 0xF, false);  // 2,3,0,1
+  if ((l % LPR) == 0) rowsum[srow] = ssum;
+  __syncthreads();  // also: every wave is done reading the operand buffers
 
   const float ws = epi_wscale(ep);
+  if constexpr (EPI == 1) {
+    // per 32-row MFMA tile: convert in registers, stage 32 rows x 64 bf16 (128-byte rows, 16-byte
+    // chunks XOR-swizzled by row) in this wave's own LDS buffer, store 8 rows x 128 B per instruction
+    uint8_t* st = wn == 0 ? reinterpret_cast<uint8_t*>(lds_a0)
+                : wn == 1 ? reinterpret_cast<uint8_t*>(lds_a1)
+                : wn == 2 ? lds_b0 : lds_b1;
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) {
-    const int ml = tm * 32 + i;
-    const int m = m0 + ml;
-    if (m >= M) continue;
-    const float as = epi_ascale(ep, m);
-    const int rs = rowsum[ml];
+    for (int tm = 0; tm < TM; ++tm) {
+      const int rs = rowsum[tm * 32 + i];
+      const float as = epi_ascale(ep, min(m0 + tm * 32 + i, M - 1));
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn)
+      for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + (wn * TN + tn) * 32 + 8 * q + 4 * g;
-        if (n >= N) continue;
-        const int32_t v[4] = {acc[tn][tm][4 * q] - rs, acc[tn][tm][4 * q + 1] - rs, acc[tn][tm][4 * q + 2] - rs,
-                              acc[tn][tm][4 * q + 3] - rs};
-        if constexpr (EPI == 1) {
+        for (int q = 0; q < 4; ++q) {
           float y[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = __fmul_rn(__fmul_rn((float)v[e], ws), as);
+          for (int e = 0; e < 4; ++e) y[e] = __fmul_rn(__fmul_rn((float)(acc[tn][tm][4 * q + e] - rs), ws), as);
+          const bf16x2_t lo = __builtin_convertvector((f32x2_t){y[0], y[1]}, bf16x2_t);
+          const bf16x2_t hi = __builtin_convertvector((f32x2_t){y[2], y[3]}, bf16x2_t);
+          const int c = tn * 4 + q;
+          *reinterpret_cast<uint2*>(st + i * 128 + ((c ^ (i & 7)) * 16) + 8 * g) =
+              make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+        }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 8 * j + (l >> 3), c = l & 7;
+        const v4i v = *reinterpret_cast<const v4i*>(st + r * 128 + ((c ^ (r & 7)) * 16));
+        const int m = m0 + tm * 32 + r, n = n0 + wn * 64 + c * 8;
+        if (m < M) {
           uint16_t* o = reinterpret_cast<uint16_t*>(ep.out) + (int64_t)m * ep.ldo + n;
-          if (n + 3 < N) {
-            const bf16x2_t lo = __builtin_convertvector((f32x2_t){y[0], y[1]}, bf16x2_t);
-            const bf16x2_t hi = __builtin_convertvector((f32x2_t){y[2], y[3]}, bf16x2_t);
-            *reinterpret_cast<uint2*>(o) =
-                make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+          if (n + 7 < N) {
+            *reinterpret_cast<v4i*>(o) = v;
           } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (n + e < N) o[e] = f32_to_bf16_rne(y[e]);
+            for (int e = 0; e < 8; ++e)
+              if (n + e < N) o[e] = (uint16_t)((uint32_t)v[e / 2] >> (16 * (e & 1)));
           }
-        } else {
-          epi_store4(ep, ws, as, m, n, v, vec_out && n + 3 < N, N);
         }
       }
+    }
+  } else {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      const int m = m0 + tm * 32 + i;
+      if (m >= M) continue;
+      const float as = epi_ascale(ep, m);
+      const int rs = rowsum[tm * 32 + i];
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + (wn * TN + tn) * 32 + 8 * q + 4 * g;
+          if (n >= N) continue;
+          const int32_t v[4] = {acc[tn][tm][4 * q] - rs, acc[tn][tm][4 * q + 1] - rs, acc[tn][tm][4 * q + 2] - rs,
+                                acc[tn][tm][4 * q + 3] - rs};
+          epi_store4(ep, ws, as, m, n, v, vec_out && n + 3 < N, N);
+        }
+    }
   }
 }
 
-template <int BM, int BN, int OCC>
-hipError_t launch_tile(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
+template <int TM, int KB, int OCC>
+hipError_t launch_tile(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, const Epilogue& e,
                        hipStream_t s) {
-  const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
+  const int tiles_n = (n + 255) / 256, tiles_m = (m + 32 * TM - 1) / (32 * TM);
   const int nwg = tiles_n * tiles_m;
   const int grid = ((nwg + 7) / 8) * 8;
   const bool vec_out = e.ldo % 4 == 0 && (uintptr_t)e.out % 16 == 0 && (uintptr_t)e.acc_out % 16 == 0;
-  const bool bf16_only = e.out && e.out_dtype == WFB_BF16 && !e.bias && !e.acc_out && vec_out;
+  const bool bf16_only = e.out && e.out_dtype == WFB_BF16 && !e.bias && !e.acc_out && e.ldo % 8 == 0 &&
+                         (uintptr_t)e.out % 16 == 0;
   if (bf16_only)
-    hipLaunchKernelGGL((gemm_i2s_tile_kernel<BM, BN, OCC, 1>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, C,
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 1>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
                        tiles_m, tiles_n, nwg, vec_out, e);
   else
-    hipLaunchKernelGGL((gemm_i2s_tile_kernel<BM, BN, OCC, 0>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, C,
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 0>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
                        tiles_m, tiles_n, nwg, vec_out, e);
   return hipGetLastError();
 }
@@ -306,7 +371,10 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   if (m <= 16) return launch_mt<1>(W, n, C, A, m, lda, e, s);
   if (m <= 32) return launch_mt<2>(W, n, C, A, m, lda, e, s);
   if (m <= 64) return launch_mt<4>(W, n, C, A, m, lda, e, s);
-  return launch_tile<64, 256, 3>(W, n, C, A, m, lda, e, s);
+  // measured on MI355X: 128-row tiles (half the weight unpack per MFMA) pay off for wide N; for
+  // narrow N (few column tiles) 64-row tiles with 256-weight stages keep more workgroups busy
+  if (n >= 4096) return launch_tile<4, 1, 2>(W, n, k, A, m, lda, e, s);
+  return launch_tile<2, 2, 2>(W, n, k, A, m, lda, e, s);
 }
 
 }  // namespace wfb
