@@ -10,8 +10,9 @@ bytes per launch B = N*K/4 + M*K + 2*M*N + 4 + 4*M (packed W, int8 A, bf16 Y, sc
 Timing: the launches of the timed region are queued behind a bounded device sleep, so the HIP
 events on the launch stream measure device time of back-to-back kernels (host launch latency is
 excluded); warmup steps run first.  Extra fields: per-shape GEMV numbers, the prefill GEMM at
-M=2048 in int8 TOP/s vs the 5.0 POP/s dense int8 peak, the fused RMSNorm+quant
-kernel, and the reference CPU kernel timed on this host (cpu_baseline).
+M = 512, 2048, 8192 in int8 TOP/s vs the 5.0 POP/s dense int8 peak, the fused
+RMSNorm+quant kernel, one BitNet-2B decode layer's quantised path with separate vs fused launches
+(decode_layer_2b), and the reference CPU kernel timed on this host (cpu_baseline).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
 """
@@ -76,6 +77,38 @@ class Launcher:
         return call
 
 
+    def rmsnorm_quant_args(self, x, gamma, eps, m, h, q, a_scale):
+        vp = ctypes.c_void_p
+        args = (vp(x.data_ptr()), 1, h, vp(gamma.data_ptr()), 1, ctypes.c_float(eps), m, h, vp(q.data_ptr()), h, h,
+                vp(a_scale.data_ptr()), self.stream)
+        return self._wrap("wfb_rmsnorm_quant_i8", args)
+
+    def glu_args(self, gate, up, ldx, act, gamma, eps, m, h, q, a_scale):
+        vp = ctypes.c_void_p
+        args = (vp(gate.data_ptr()), vp(up.data_ptr()), 1, ldx, act, vp(gamma.data_ptr()), 1, ctypes.c_float(eps), m, h,
+                vp(q.data_ptr()), h, h, vp(a_scale.data_ptr()), self.stream)
+        return self._wrap("wfb_glu_rmsnorm_quant_i8", args)
+
+    def segmented_args(self, qw, rows, scales, k, a, m, a_scale, out):
+        vp = ctypes.c_void_p
+        seg = (ctypes.c_int64 * len(rows))(*rows)
+        args = (vp(qw.data_ptr()), sum(rows), k, len(rows), ctypes.cast(seg, vp), vp(scales.data_ptr()),
+                vp(a.data_ptr()), m, k, vp(a_scale.data_ptr()), None, 0, vp(out.data_ptr()), 1, sum(rows), None,
+                self.stream)
+        call = self._wrap("wfb_linear_i2s_segmented", args)
+        call.keep = seg  # the host array must outlive the call object
+        return call
+
+    def _wrap(self, fn, args):
+        f = getattr(self.lib, fn)
+
+        def call():
+            if f(*args) != 0:
+                raise RuntimeError(f"{fn}: {self.lib.wfb_last_error().decode()}")
+
+        return call
+
+
 def timed(torch, fns, steps, warmup):
     """Device ms per step for `steps` repetitions of the launch list `fns` (step i uses fns[i % len])."""
     for i in range(warmup):
@@ -115,6 +148,79 @@ def _sleep_cycles(torch, seconds):
         torch.cuda.synchronize()
         _SLEEP_RATE = 10_000_000 / max(s.elapsed_time(e) * 1e-3, 1e-6)
     return min(max(seconds, 0.002), 2.0) * _SLEEP_RATE
+
+
+# BitNet-2B decoder layer: hidden 2560, QKV 2560 + 2 x 320 (the configs[1] shapes), FFN 6912
+LAYER_2B = dict(h=2560, q=2560, kv=320, f=6912)
+
+
+def decode_layer_bench(torch, L, orc, dev, steps, warmup, n_layers=30):
+    """Device time of the quantised part of one BitNet-2B decode layer at batch 1 (attention math
+    excluded), weights rotated over n_layers copies (0.77 GB, past the 256 MB Infinity Cache):
+      separate: norm+quant, q, k, v, SubLN+quant, o, norm+quant, gate, up, relu2*up+SubLN+quant, down
+      fused:    norm+quant, q|k|v, SubLN+quant, o, norm+quant, gate|up, relu2*up+SubLN+quant, down"""
+    h, qd, kv, f = LAYER_2B["h"], LAYER_2B["q"], LAYER_2B["kv"], LAYER_2B["f"]
+    rng = np.random.default_rng(4000)
+    shapes = {"q": (qd, h), "k": (kv, h), "v": (kv, h), "o": (h, qd), "gate": (f, h), "up": (f, h), "down": (h, f)}
+    base = {nm: torch.from_numpy(orc.pack_i2s(orc.random_ternary(rng, n, k))).to(dev) for nm, (n, k) in shapes.items()}
+    scales = {nm: torch.from_numpy(orc.log_uniform(rng, 1)).to(dev) for nm in shapes}
+    wbytes = sum(t.numel() for t in base.values())
+    layers = []
+    for _ in range(n_layers):
+        w = {nm: t.clone() for nm, t in base.items()}
+        w["qkv"] = torch.cat([w["q"], w["k"], w["v"]]).contiguous()
+        w["gu"] = torch.cat([w["gate"], w["up"]]).contiguous()
+        layers.append(w)
+    s_qkv = torch.cat([scales["q"], scales["k"], scales["v"]]).contiguous()
+    s_gu = torch.cat([scales["gate"], scales["up"]]).contiguous()
+    bf = torch.bfloat16
+    x = torch.randn((1, h), device=dev).to(bf)
+    attn = torch.randn((1, qd), device=dev).to(bf)
+    g_h, g_q, g_f = (torch.ones(n, device=dev, dtype=bf) for n in (h, qd, f))
+    q8 = {n: torch.empty((1, n), dtype=torch.int8, device=dev) for n in (h, qd, f)}
+    sc = {n: torch.empty(1, dtype=torch.float32, device=dev) for n in (h, qd, f)}
+    out = {nm: torch.empty((1, n), dtype=bf, device=dev) for nm, (n, _) in shapes.items()}
+    qkv_out = torch.empty((1, qd + 2 * kv), dtype=bf, device=dev)
+    gu_out = torch.empty((1, 2 * f), dtype=bf, device=dev)
+
+    def lin(w, nm, a, a_s, o):
+        n, k = shapes[nm]
+        return L.linear_args("wfb_linear_i2s", w[nm], n, k, a, 1, a_s, scales[nm], o)
+
+    sep, fus = [], []
+    for w in layers:
+        sep.append([
+            L.rmsnorm_quant_args(x, g_h, 1e-5, 1, h, q8[h], sc[h]),
+            lin(w, "q", q8[h], sc[h], out["q"]), lin(w, "k", q8[h], sc[h], out["k"]), lin(w, "v", q8[h], sc[h], out["v"]),
+            L.rmsnorm_quant_args(attn, g_q, 1e-6, 1, qd, q8[qd], sc[qd]),
+            lin(w, "o", q8[qd], sc[qd], out["o"]),
+            L.rmsnorm_quant_args(x, g_h, 1e-5, 1, h, q8[h], sc[h]),
+            lin(w, "gate", q8[h], sc[h], out["gate"]), lin(w, "up", q8[h], sc[h], out["up"]),
+            L.glu_args(out["gate"], out["up"], f, 2, g_f, 1e-6, 1, f, q8[f], sc[f]),
+            lin(w, "down", q8[f], sc[f], out["down"]),
+        ])
+        fus.append([
+            L.rmsnorm_quant_args(x, g_h, 1e-5, 1, h, q8[h], sc[h]),
+            L.segmented_args(w["qkv"], [qd, kv, kv], s_qkv, h, q8[h], 1, sc[h], qkv_out),
+            L.rmsnorm_quant_args(attn, g_q, 1e-6, 1, qd, q8[qd], sc[qd]),
+            lin(w, "o", q8[qd], sc[qd], out["o"]),
+            L.rmsnorm_quant_args(x, g_h, 1e-5, 1, h, q8[h], sc[h]),
+            L.segmented_args(w["gu"], [f, f], s_gu, h, q8[h], 1, sc[h], gu_out),
+            L.glu_args(gu_out, gu_out[:, f:], 2 * f, 2, g_f, 1e-6, 1, f, q8[f], sc[f]),
+            lin(w, "down", q8[f], sc[f], out["down"]),
+        ])
+    torch.cuda.synchronize()
+    ms_sep = timed(torch, sep, steps, warmup)
+    ms_fus = timed(torch, fus, steps, warmup)
+    return {
+        "workload": "BitNet-2B decode layer, batch 1, quantised path (attention math excluded), relu2 MLP, "
+                    f"{n_layers} rotated weight copies",
+        "weight_bytes": int(wbytes),
+        "separate": {"launches": len(sep[0]), "us": round(ms_sep * 1e3, 2),
+                     "GB/s": round(wbytes / (ms_sep * 1e-3) / 1e9, 1)},
+        "fused": {"launches": len(fus[0]), "us": round(ms_fus * 1e3, 2),
+                  "GB/s": round(wbytes / (ms_fus * 1e-3) / 1e9, 1)},
+    }
 
 
 def measured_traffic(n: int, k: int):
@@ -236,21 +342,22 @@ def main():
                 "kernel": f"gemv_i2s M=1 N={d['N']} K={d['K']}",
                 "bytes_per_launch": shapes[dom]["bytes"]}
 
-    # ---- prefill GEMM at M=2048 ----------------------------------------------------
+    # ---- prefill GEMM, M in {512, 2048, 8192} ---------------------------------------
     prefill = []
     for n, k in PREFILL_SHAPES:
-        m = 2048
         r = np.random.default_rng(3000 + n)
         packed = torch.from_numpy(orc.pack_i2s(orc.random_ternary(r, n, k))).to(dev)
-        a = torch.from_numpy(orc.random_int8(r, m, k)).to(dev)
-        a_scale = torch.from_numpy(orc.log_uniform(r, m)).to(dev)
         ws = torch.from_numpy(orc.log_uniform(r, 1)).to(dev)
-        out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-        call = L.linear_args("wfb_linear_i2s", packed, n, k, a, m, a_scale, ws, out)
-        ms = timed(torch, [[call]], max(10, args.steps // 10), 3)
-        tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        prefill.append({"M": m, "N": n, "K": k, "us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
-                        "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)})
+        for m in (512, 2048, 8192):
+            a = torch.from_numpy(orc.random_int8(r, m, k)).to(dev)
+            a_scale = torch.from_numpy(orc.log_uniform(r, m)).to(dev)
+            out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+            call = L.linear_args("wfb_linear_i2s", packed, n, k, a, m, a_scale, ws, out)
+            ms = timed(torch, [[call]], max(10, args.steps // 10), 3)
+            tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            prefill.append({"M": m, "N": n, "K": k, "us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
+                            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)})
+            del a, out
 
     # ---- fused RMSNorm + per-token quant (configs[2] input distribution) -----------------------
     normq = []
@@ -267,6 +374,9 @@ def main():
         ms = timed(torch, [[lambda: f(*nargs)]], max(20, args.steps // 4), 5)
         nb = 2 * m * h + 2 * h + m * h + 4 * m
         normq.append({"M": m, "H": h, "us": round(ms * 1e3, 3), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1)})
+
+    # ---- fused decode layer (configs[1] shapes as one BitNet-2B layer) -------------------------
+    layer = decode_layer_bench(torch, L, orc, dev, max(50, args.steps // 2), 5)
 
     sweep = None
     if args.sweep:
@@ -312,6 +422,7 @@ def main():
         "gemv_per_shape": per_shape,
         "prefill_gemm": prefill,
         "rmsnorm_quant": normq,
+        "decode_layer_2b": layer,
     }
     if sweep is not None:
         line["batched_sweep"] = sweep

@@ -20,6 +20,7 @@
  *
  * Reference citations below use
  *   SGB = packages/inference/extern/sglang-bitnet
+ *   MSB = packages/inference/extern/BitNet
  *   WF  = packages/training/src/wrinklefree
  */
 #ifndef WFBITNET_H
@@ -35,11 +36,16 @@ extern "C" {
 #define WFB_QK_I2S 128          /* weights per I2_S block (SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.h:29) */
 #define WFB_ABSMEAN_WS_DOUBLES 1024 /* workspace size (in doubles) of wfb_weight_absmean */
 #define WFB_NORM_MAX_H 16384    /* largest row length of the per-token quantisers */
+#define WFB_MAX_SEGMENTS 8      /* weight segments of one wfb_linear_i2s_segmented call */
 
 /* status codes */
 #define WFB_OK 0
 #define WFB_EINVAL (-1)         /* bad argument (shape, dtype, alignment, null pointer) */
 #define WFB_EHIP (-2)           /* the HIP runtime reported an error */
+
+/* gated activations of wfb_glu_rmsnorm_quant_i8 */
+#define WFB_ACT_SILU 1          /* silu(gate) * up (SwiGLU) */
+#define WFB_ACT_RELU2 2         /* relu(gate)^2 * up */
 
 /* element types of floating-point buffers */
 #define WFB_F32 0
@@ -135,6 +141,41 @@ int wfb_gemm_i2s(const uint8_t* qweight, int64_t n, int64_t k,
                  const float* a_scale, const float* w_scale_dev, float w_scale,
                  const void* bias, int bias_dtype,
                  void* out, int out_dtype, int64_t ldo, int32_t* acc_out, void* stream);
+
+/* ---- fused decode layer pieces ------------------------------------------------------------ */
+
+/* One wfb_linear_i2s over weights that are the row-wise concatenation of n_seg projections sharing
+ * the same input (fused QKV: q|k|v; gate+up: gate|up), each with its own per-tensor scale:
+ *   qweight  : uint8 [N, K/4], rows of segment s are [sum(seg_rows[:s]), sum(seg_rows[:s+1]))
+ *   seg_rows : host array of n_seg row counts, each a multiple of 8, summing to N (1 <= n_seg <= 8)
+ *   w_scales_dev : fp32 [n_seg] device
+ *   out[m, n] = ((float)acc[m, n] * w_scales_dev[seg(n)]) * a_scale[m] (+ bias[n])
+ * Accumulators and outputs equal those of n_seg separate wfb_linear_i2s calls on the segments.
+ * Intent of the fused QKV / gate-up GEMVs of SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:150-231,
+ * 289-375 (each projection scaled by its own weight scale; the reference's double sum(a) subtraction
+ * and missing weight scales are not reproduced) and the segment scale lookup of the MS CUDA kernel
+ * (MSB/gpu/bitnet_kernels/bitnet_kernels.h:80-82). */
+int wfb_linear_i2s_segmented(const uint8_t* qweight, int64_t n, int64_t k, int n_seg, const int64_t* seg_rows,
+                             const float* w_scales_dev, const int8_t* act, int64_t m, int64_t lda,
+                             const float* a_scale, const void* bias, int bias_dtype,
+                             void* out, int out_dtype, int64_t ldo, int32_t* acc_out, void* stream);
+
+/* Gated activation fused with SubLN and the per-token quantiser, the middle of the BitNet MLP
+ * (gate|up GEMV -> this -> down GEMV):
+ *   v = act(gate[m, :H]) * up[m, :H]  (fp32; gate and up rows share the row stride ldx)
+ *   then exactly wfb_rmsnorm_quant_i8 on v (same reduction order, gamma = the FFN SubLN weight).
+ * act = WFB_ACT_SILU: silu(g) = g / (1 + 2^(-g*log2(e))) with 2^x evaluated as 2^n * p(x - n)
+ * (n = rint(x) clamped to [-125, 125], p a degree-7 Taylor polynomial of 2^f in Horner form), every
+ * step one correctly rounded fp32 operation, so a float32 CPU restatement reproduces it bit for bit;
+ * against exact silu: relative error below 1e-6 for |g| <= 16, absolute error below 2e-6 everywhere
+ * (finite inputs).  act = WFB_ACT_RELU2: max(g, 0)^2 * u.
+ * Replaces the relu^2 * up -> rms_norm -> quantize steps of bitnet_mlp_fused
+ * (SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:200-216) and SiLU-gated MLP + SubLN of the
+ * stage-1 model (WF/models/subln.py:42-59; WF/training/stage1.py:63-214).
+ * H % 8 == 0, H <= WFB_NORM_MAX_H. */
+int wfb_glu_rmsnorm_quant_i8(const void* gate, const void* up, int x_dtype, int64_t ldx, int act,
+                             const void* gamma, int gamma_dtype, float eps, int64_t m, int64_t h,
+                             int8_t* q, int64_t k_pad, int64_t ldq, float* a_scale, void* stream);
 
 #ifdef __cplusplus
 }

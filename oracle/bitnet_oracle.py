@@ -10,6 +10,8 @@ Reference files (paths under the reference repository):
   OPS  = packages/inference/extern/sglang-bitnet/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp
   METH = packages/inference/extern/sglang-bitnet/python/sglang/srt/layers/quantization/bitnet.py
   SUBLN = packages/training/src/wrinklefree/models/subln.py
+  FUSED = packages/inference/extern/sglang-bitnet/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp
+  MSK  = packages/inference/extern/BitNet/gpu/bitnet_kernels/bitnet_kernels.h
 
 How each function is pinned (see tests/test_oracle.py):
   absmean_scale        KAT [1,-2,3,-4] -> 2.5; torch's own fp32 mean (the reference's library call).
@@ -22,6 +24,10 @@ How each function is pinned (see tests/test_oracle.py):
   accumulate           the reference's compiled bitnet_vec_dot_i2_i8 / bitnet_gemm_i2_i8 (golden
                        fixtures and oracle/_ref), int64 brute force, and the identity
                        sum(code*a) - sum(a) = sum(w*a).
+  exp2_fixed / silu_fixed / glu
+                       float64 exp2 / silu (relative error bound), exact powers of two, the
+                       relu^2 closed form; the composition glu_rmsnorm_quant = rmsnorm_quant(glu).
+  rescale_segmented    equals rescale of each segment with its own scale (the separate-call form).
 """
 
 from __future__ import annotations
@@ -218,6 +224,53 @@ def rmsnorm_quant(x: np.ndarray, gamma=None, eps: float = 1e-6, k_pad: int | Non
     return quantize_per_token(rmsnorm(x, gamma, eps, exact_order), k_pad)
 
 
+# ---- gated activation before the MLP SubLN (FUSED:200-216, SiLU form of the stage-1 MLP) ------
+
+ACT_SILU, ACT_RELU2 = 1, 2  # codes of include/wfbitnet.h
+
+# ln(2)^k / k!, k = 7 .. 1, as fp32 (Horner coefficients of 2^f on |f| <= 1/2)
+_EXP2_C = [F32(1.525273380405984e-05), F32(1.5403530393381606e-04), F32(1.3333558146428443e-03),
+           F32(9.618129107628477e-03), F32(5.550410866482158e-02), F32(2.402265069591007e-01),
+           F32(6.931471805599453e-01), F32(1.0)]
+_LOG2E = F32(1.4426950408889634)
+
+
+def exp2_fixed(t: np.ndarray) -> np.ndarray:
+    """2^t as the kernels evaluate it: t clamped to [-125, 125], n = rint(t), f = t - n,
+    p = Horner(_EXP2_C, f) with one rounding per multiply and per add, result p * 2^n (exact)."""
+    t = np.minimum(np.maximum(np.asarray(t, F32), F32(-125.0)), F32(125.0))
+    n = np.rint(t).astype(F32)
+    f = (t - n).astype(F32)
+    p = np.full_like(f, _EXP2_C[0])
+    for c in _EXP2_C[1:]:
+        p = (p * f).astype(F32)
+        p = (p + c).astype(F32)
+    return np.ldexp(p, n.astype(np.int32)).astype(F32)
+
+
+def silu_fixed(g: np.ndarray) -> np.ndarray:
+    """silu(g) = g / (1 + exp(-g)), exp(-g) = exp2_fixed(-g * log2(e)), fp32 step by step."""
+    g = np.asarray(g, F32)
+    e = exp2_fixed(((-g).astype(F32) * _LOG2E).astype(F32))
+    return (g / (F32(1.0) + e).astype(F32)).astype(F32)
+
+
+def glu(gate: np.ndarray, up: np.ndarray, act: int) -> np.ndarray:
+    """act(gate) * up in fp32: silu (ACT_SILU) or relu^2 (ACT_RELU2, max(g,0)*max(g,0) then * up)."""
+    gate, up = np.asarray(gate, F32), np.asarray(up, F32)
+    if act == ACT_SILU:
+        return (silu_fixed(gate) * up).astype(F32)
+    if act == ACT_RELU2:
+        r = np.maximum(gate, F32(0.0))
+        return ((r * r).astype(F32) * up).astype(F32)
+    raise ValueError(f"unknown activation {act}")
+
+
+def glu_rmsnorm_quant(gate, up, act: int, gamma=None, eps: float = 1e-6, k_pad: int | None = None):
+    """wfb_glu_rmsnorm_quant_i8: rmsnorm_quant of glu(gate, up) (same reduction order)."""
+    return rmsnorm_quant(glu(gate, up, act), gamma, eps, k_pad)
+
+
 # ---- a4 / a5 / a6: accumulators and rescale ---------------------------------------------------
 
 
@@ -253,6 +306,20 @@ def accumulate_code_identity(packed: np.ndarray, a: np.ndarray) -> np.ndarray:
 def rescale(acc: np.ndarray, w_scale, a_scale=None, bias=None) -> np.ndarray:
     """y = (float(acc) * w_scale) * a_scale[m] (+ bias) in fp32 (GEMV:846; METH:241, 253)."""
     y = (acc.astype(F32) * F32(w_scale)).astype(F32)
+    if a_scale is not None:
+        y = (y * np.asarray(a_scale, F32).reshape(-1, 1)).astype(F32)
+    if bias is not None:
+        y = (y + np.asarray(bias, F32).reshape(1, -1)).astype(F32)
+    return y
+
+
+def rescale_segmented(acc: np.ndarray, seg_rows, w_scales, a_scale=None, bias=None) -> np.ndarray:
+    """wfb_linear_i2s_segmented: output column n takes the scale of its weight segment (MSK:80-82
+    with explicit segment sizes); equal to rescale() of each segment with its own scale."""
+    ends = np.cumsum(np.asarray(seg_rows, np.int64))
+    seg = np.searchsorted(ends, np.arange(acc.shape[-1]), side="right")
+    ws = np.asarray(w_scales, F32)[seg]
+    y = (acc.astype(F32) * ws.reshape(1, -1)).astype(F32)
     if a_scale is not None:
         y = (y * np.asarray(a_scale, F32).reshape(-1, 1)).astype(F32)
     if bias is not None:

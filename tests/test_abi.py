@@ -100,3 +100,20 @@ def test_product_does_not_import_oracle():
     for f in list(pkg_dir.rglob("*.py")) + list(pkg_dir.rglob("*.hip")) + list(pkg_dir.rglob("*.h")):
         text = f.read_text()
         assert "import oracle" not in text and "from oracle" not in text and "oracle/" not in text, f
+
+
+def test_segmented_and_glu_argument_errors(pkg):
+    vp = ctypes.c_void_p
+    rows = (ctypes.c_int64 * 2)(32, 32)
+    st = pkg._lib.status("wfb_linear_i2s_segmented", vp(16), 64, 128, 0, ctypes.cast(rows, vp), vp(16), vp(16), 1, 128,
+                         None, None, 0, vp(16), 1, 64, None, None)
+    assert st == -1 and "n_seg" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_linear_i2s_segmented", vp(16), 96, 128, 2, ctypes.cast(rows, vp), vp(16), vp(16), 1, 128,
+                         None, None, 0, vp(16), 1, 96, None, None)
+    assert st == -1 and "sum to 64" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_glu_rmsnorm_quant_i8", vp(16), vp(16), 0, 256, 5, None, 0, 1e-6, 1, 256, vp(16), 256,
+                         256, vp(16), None)
+    assert st == -1 and "activation" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_glu_rmsnorm_quant_i8", vp(16), vp(16), 0, 250, 1, None, 0, 1e-6, 1, 250, vp(16), 256,
+                         256, vp(16), None)
+    assert st == -1 and "multiple of 8" in pkg._lib.last_error()

@@ -1,8 +1,9 @@
 """End-to-end parity: random-init SmolLM2-135M-shape BitNet, greedy decode of 128
 tokens from a 32-token random prompt.  The same model runs twice: every quantised BitLinear group
-(RMSNorm/SubLN -> per-token int8 -> ternary linear -> rescale) once on libwfbitnet and once on the
-CPU oracle; the float glue (embedding, RoPE, attention, SiLU, residuals, tied LM head) is the same
-code on the same device in both runs.  Token ids and every per-layer int32 accumulator must be equal.
+(RMSNorm/SubLN -> per-token int8 -> ternary linear -> rescale, and the MLP middle act(gate) * up ->
+SubLN -> int8 -> down) once on libwfbitnet (separate or fused launches) and once on the CPU oracle;
+the float glue (embedding, RoPE, attention, residuals, tied LM head) is the same code on the same
+device in both runs.  Token ids and every per-layer int32 accumulator must be equal.
 """
 
 import numpy as np
@@ -37,14 +38,28 @@ class OracleBackend:
             outs.append(torch.from_numpy(orc.rescale(acc, ws, s)).to(self.dev))
         return outs
 
+    def glu_norm_linears(self, gate, up, act, norm_weight, eps, linears):
+        g = None if norm_weight is None else norm_weight.float().cpu().numpy()
+        code = orc.ACT_SILU if act == "silu" else orc.ACT_RELU2
+        q, s = orc.glu_rmsnorm_quant(gate.float().cpu().numpy(), up.float().cpu().numpy(), code, g, eps,
+                                     k_pad=linears[0].k_pad)
+        outs = []
+        for lin in linears:
+            w, ws = self.w[id(lin)]
+            acc = (q.astype(np.float32) @ w.T).astype(np.int64)
+            self.acc_log.append(acc)
+            outs.append(torch.from_numpy(orc.rescale(acc, ws, s)).to(self.dev))
+        return outs
 
-def test_greedy_decode_tokens_and_accumulators_match_oracle(pkg, dev):
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_greedy_decode_tokens_and_accumulators_match_oracle(pkg, dev, fused):
     M = pkg.model
     model = M.BitNetDecoder(M.SMOLLM2_135M, seed=0, device=dev)
     model.backend_linears = list(M.quantised_linears(model).values())
     prompt = torch.randint(0, M.SMOLLM2_135M.vocab_size, (1, 32), generator=torch.Generator().manual_seed(1))
 
-    hip = M.HipBackend(out_dtype=torch.float32, keep_acc=True)
+    hip = M.HipBackend(out_dtype=torch.float32, keep_acc=True, fused=fused)
     model.backend = hip
     toks_hip = model.generate(prompt, 128).cpu()
 
@@ -59,3 +74,24 @@ def test_greedy_decode_tokens_and_accumulators_match_oracle(pkg, dev):
         assert np.array_equal(a.cpu().numpy().astype(np.int64), b), f"accumulator mismatch at call {i}"
     # the generated text is not degenerate (random weights still give varied tokens)
     assert len(set(toks_hip[0].tolist())) > 4
+
+
+def test_relu2_model_fused_matches_oracle(pkg, dev):
+    """The relu(gate)^2 * up MLP of the BitNet b1.58 2B form (bitnet_fused_layer.cpp:200-204), small
+    model, fused launches, prefill of 8 tokens as a batch of 2 plus 24 decode steps."""
+    M = pkg.model
+    cfg = M.BitNetConfig(vocab_size=2048, hidden_size=256, intermediate_size=640, num_layers=3, num_heads=4,
+                         num_kv_heads=2, head_dim=64, rope_theta=10000.0, hidden_act="relu2")
+    model = M.BitNetDecoder(cfg, seed=3, device=dev)
+    model.backend_linears = list(M.quantised_linears(model).values())
+    prompt = torch.randint(0, cfg.vocab_size, (2, 8), generator=torch.Generator().manual_seed(4))
+    hip = M.HipBackend(out_dtype=torch.float32, keep_acc=True, fused=True)
+    model.backend = hip
+    toks_hip = model.generate(prompt, 24).cpu()
+    ref = OracleBackend(model, dev)
+    model.backend = ref
+    toks_ref = model.generate(prompt, 24).cpu()
+    assert torch.equal(toks_hip, toks_ref)
+    assert len(hip.acc_log) == len(ref.acc_log)
+    for a, b in zip(hip.acc_log, ref.acc_log):
+        assert np.array_equal(a.cpu().numpy().astype(np.int64), b)

@@ -1,0 +1,126 @@
+"""GPU parity of the fused decode-layer pieces against the CPU oracle, through the C ABI.
+
+* wfb_linear_i2s_segmented: accumulators and outputs equal to separate wfb_linear_i2s calls on the
+  segments (bit-exact, every kernel path: GEMV M <= 2, skinny MFMA, tiled MFMA).
+* wfb_glu_rmsnorm_quant_i8: int8 codes and scales bit-exact against the oracle's step-by-step fp32
+  restatement (the SiLU is evaluated with the same fixed sequence of correctly rounded operations).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bitnet_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+SEGMENTS = {
+    "qkv_2b": ([2560, 320, 320], 2560),
+    "gate_up_smollm2": ([1536, 1536], 640),
+    "qkv_smollm2": ([576, 192, 192], 640),
+    "three_odd": ([8, 24, 104], 256),
+}
+
+
+@pytest.mark.parametrize("case", sorted(SEGMENTS))
+@pytest.mark.parametrize("m", [1, 2, 5, 64, 130])
+def test_segmented_linear_equals_separate_calls(pkg, dev, case, m):
+    rows, k = SEGMENTS[case]
+    rng = np.random.default_rng(7000 + m + sum(rows))
+    packs = [orc.pack_i2s(orc.random_ternary(rng, r, k)) for r in rows]
+    scales = orc.log_uniform(rng, len(rows))
+    a = orc.random_int8(rng, m, k)
+    a_scale = orc.log_uniform(rng, m)
+    packed = np.concatenate(packs, axis=0)
+    pw, pa, ps = _t(packed, dev), _t(a, dev), _t(a_scale, dev)
+    y, acc = pkg.bitnet_linear_segmented(pw, rows, _t(scales, dev), pa, a_scale=ps, out_dtype=torch.float32,
+                                         return_acc=True)
+    acc_ref = orc.accumulate(packed, a)
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), acc_ref)
+    y_ref = orc.rescale_segmented(acc_ref, rows, scales, a_scale)
+    assert np.array_equal(y.cpu().numpy(), y_ref)
+    # the separate-call form, segment by segment
+    r0 = 0
+    for p, r, s in zip(packs, rows, scales):
+        ys = pkg.bitnet_linear(_t(p, dev), pa, float(s), a_scale=ps, out_dtype=torch.float32)
+        assert np.array_equal(ys.cpu().numpy(), y.cpu().numpy()[:, r0:r0 + r])
+        r0 += r
+    yb = pkg.bitnet_linear_segmented(pw, rows, _t(scales, dev), pa, a_scale=ps)
+    assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), orc.f32_to_bf16_bits(y_ref))
+
+
+def test_segmented_rejects_bad_segments(pkg, dev):
+    from wrinklefree_monorepo_amd import _lib
+    rng = np.random.default_rng(1)
+    packed = _t(orc.pack_i2s(orc.random_ternary(rng, 64, 128)), dev)
+    a = _t(orc.random_int8(rng, 1, 128), dev)
+    sc = torch.ones(2, dtype=torch.float32, device=dev)
+    with pytest.raises(ValueError):
+        pkg.bitnet_linear_segmented(packed, [32, 16], sc, a)       # rows do not sum to N
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        pkg.bitnet_linear_segmented(packed, [36, 28], sc, a)       # not multiples of 8
+    assert "multiple of 8" in _lib.last_error()
+
+
+GLU_CASES = [(1, 1536), (4, 1536), (1, 6912), (16, 6912), (3, 14336), (64, 2560), (5, 4104)]
+
+
+@pytest.mark.parametrize("act", ["silu", "relu2"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("m,h", GLU_CASES)
+def test_glu_rmsnorm_quant_matches_oracle(pkg, dev, act, dtype, m, h):
+    rng = np.random.default_rng(8000 + m + h)
+    gu = (rng.standard_normal((m, 2 * h)) * 2.0).astype(np.float32)
+    gu[:, ::97] *= 12.0  # a few large gates (silu tails, relu^2 growth)
+    gamma = (1 + 0.1 * rng.standard_normal(h)).astype(np.float32)
+    x = _t(gu, dev).to(dtype)
+    gate, up = x[:, :h], x[:, h:]  # halves of one gate|up output: common row stride 2H
+    g = _t(gamma, dev).to(torch.bfloat16)
+    kp = (h + 127) // 128 * 128
+    q, s = pkg.glu_rmsnorm_quantize_i8(gate, up, act, g, eps=1e-6, k_pad=kp)
+    xin = x.to(torch.float32).cpu().numpy()
+    gref = g.to(torch.float32).cpu().numpy()
+    code = orc.ACT_SILU if act == "silu" else orc.ACT_RELU2
+    q_ref, s_ref = orc.glu_rmsnorm_quant(xin[:, :h], xin[:, h:], code, gref, 1e-6, kp)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+def test_glu_separate_gate_and_up_buffers(pkg, dev):
+    rng = np.random.default_rng(9)
+    m, h = 3, 2560
+    gate = (rng.standard_normal((m, h)) * 3).astype(np.float32)
+    up = rng.standard_normal((m, h)).astype(np.float32)
+    q, s = pkg.glu_rmsnorm_quantize_i8(_t(gate, dev), _t(up, dev), "silu", None, eps=1e-5)
+    q_ref, s_ref = orc.glu_rmsnorm_quant(gate, up, orc.ACT_SILU, None, 1e-5)
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_glu_rejects_mismatched_inputs(pkg, dev):
+    g = torch.zeros((2, 64), device=dev)
+    with pytest.raises(RuntimeError):
+        pkg.glu_rmsnorm_quantize_i8(g, torch.zeros((2, 72), device=dev))
+    with pytest.raises(ValueError):
+        pkg.glu_rmsnorm_quantize_i8(g, g, "gelu")
+
+
+def test_bitnet_linear_native_module(pkg, dev):
+    """BitNetLinearNative (reference bitnet_patch.py:28-78): per-tensor activation scale, fp32 out."""
+    rng = np.random.default_rng(11)
+    n, k = 256, 640
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    packed, ws = orc.pack_ternary(w)
+    bias = rng.standard_normal(n).astype(np.float32)
+    mod = pkg.BitNetLinearNative(k, n, _t(packed, dev), torch.tensor([ws], device=dev), _t(bias, dev))
+    for m in (1, 5):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y = mod(_t(x, dev)).cpu().numpy()
+        q, a_s = orc.quantize_per_tensor(x)
+        acc = orc.accumulate(packed, q.reshape(m, k))
+        y_ref = orc.rescale(acc, ws, np.full(m, a_s, np.float32), bias)
+        assert np.array_equal(y, y_ref)

@@ -296,3 +296,69 @@ def test_reference_avx512_anomaly_documented():
         a = orc.random_int8(rng, 1, k)[0]
         got = ref.gemv(packed, a, 1.0).astype(np.int64)
         assert np.array_equal(got, orc.accumulate(packed, a)[0]) == agree
+
+
+# ---- gated activation (fixed-sequence SiLU, relu^2) and segmented rescale ------------------------
+
+
+def test_exp2_fixed_exact_powers_and_accuracy():
+    n = np.arange(-125, 126).astype(np.float32)
+    assert np.array_equal(orc.exp2_fixed(n), np.exp2(n.astype(np.float64)).astype(np.float32))
+    t = np.linspace(-125, 125, 200001).astype(np.float32)
+    ref = np.exp2(t.astype(np.float64))
+    assert float((np.abs(orc.exp2_fixed(t) - ref) / ref).max()) < 1e-7
+    # clamping keeps 2^n a normal number
+    assert orc.exp2_fixed(np.float32(200.0)) == np.float32(2.0 ** 125)
+    assert orc.exp2_fixed(np.float32(-200.0)) == np.float32(2.0 ** -125)
+
+
+def test_silu_fixed_against_float64():
+    x = np.linspace(-16, 16, 400001).astype(np.float32)
+    ref = x.astype(np.float64) / (1.0 + np.exp(-x.astype(np.float64)))
+    got = orc.silu_fixed(x).astype(np.float64)
+    nz = np.abs(ref) > 0
+    assert float((np.abs(got - ref)[nz] / np.abs(ref)[nz]).max()) < 1e-6
+    wide = np.linspace(-1e4, 1e4, 200001).astype(np.float32)
+    refw = wide.astype(np.float64) * 0.5 * (1.0 + np.tanh(wide.astype(np.float64) / 2.0))
+    assert float(np.abs(orc.silu_fixed(wide) - refw).max()) < 2e-6
+    assert orc.silu_fixed(np.float32(0.0)) == 0.0
+    assert orc.silu_fixed(np.float32(100.0)) == np.float32(100.0)
+
+
+def test_relu2_gate_closed_form():
+    rng = np.random.default_rng(5)
+    g = (rng.standard_normal(10000) * 4).astype(np.float32)
+    u = rng.standard_normal(10000).astype(np.float32)
+    v = orc.glu(g, u, orc.ACT_RELU2)
+    assert np.all(v[g <= 0] == 0)
+    pos = g > 0
+    ref = (np.float64(1) * g[pos] * g[pos] * u[pos])
+    assert float((np.abs(v[pos] - ref) / np.maximum(np.abs(ref), 1e-30)).max()) < 2.5e-7  # two fp32 roundings
+    with pytest.raises(ValueError):
+        orc.glu(g, u, 7)
+
+
+def test_glu_silu_gate_product_and_norm_quant_composition():
+    rng = np.random.default_rng(6)
+    g = rng.standard_normal((3, 1536)).astype(np.float32)
+    u = rng.standard_normal((3, 1536)).astype(np.float32)
+    v = orc.glu(g, u, orc.ACT_SILU)
+    ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    assert float(np.abs(v - ref).max()) < 1e-5
+    q, s = orc.glu_rmsnorm_quant(g, u, orc.ACT_SILU, None, 1e-6, 1536)
+    q2, s2 = orc.rmsnorm_quant(v, None, 1e-6, 1536)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+def test_rescale_segmented_equals_per_segment_rescale():
+    rng = np.random.default_rng(8)
+    rows = [16, 8, 40]
+    acc = rng.integers(-10000, 10000, size=(3, sum(rows)))
+    ws = orc.log_uniform(rng, 3)
+    a_s = orc.log_uniform(rng, 3)
+    y = orc.rescale_segmented(acc, rows, ws, a_s)
+    parts, r0 = [], 0
+    for r, w in zip(rows, ws):
+        parts.append(orc.rescale(acc[:, r0:r0 + r], w, a_s))
+        r0 += r
+    assert np.array_equal(y, np.concatenate(parts, axis=1))

@@ -21,6 +21,9 @@ WFB_OK = 0
 WFB_QK_I2S = 128
 WFB_ABSMEAN_WS_DOUBLES = 1024
 WFB_NORM_MAX_H = 16384
+WFB_MAX_SEGMENTS = 8
+WFB_ACT_SILU = 1
+WFB_ACT_RELU2 = 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -38,6 +41,9 @@ SIGNATURES = {
     "wfb_linear_i2s": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _int, _vp, _int, _i64, _vp, _vp],
     "wfb_gemv_i2s": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _int, _vp, _int, _i64, _vp, _vp],
     "wfb_gemm_i2s": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _int, _vp, _int, _i64, _vp, _vp],
+    "wfb_linear_i2s_segmented": [_vp, _i64, _i64, _int, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _int, _vp, _int, _i64,
+                                 _vp, _vp],
+    "wfb_glu_rmsnorm_quant_i8": [_vp, _vp, _int, _i64, _int, _vp, _int, _f32, _i64, _i64, _vp, _i64, _i64, _vp, _vp],
 }
 
 _lib = None

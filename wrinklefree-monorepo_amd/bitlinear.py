@@ -105,6 +105,38 @@ class BitLinear(nn.Linear):
                f"bias={self.bias is not None}, packed={self.qweight is not None}"
 
 
+class BitNetLinearNative(nn.Module):
+    """The reference's native-kernel linear (WFI/kernels/bitnet_patch.py:28-78), same constructor and
+    forward: per-tensor int8 activation quantisation, y = acc * weight_scale * act_scale (+ bias) in
+    fp32.  The scales stay on the device (the reference calls ``weight_scale.item()``); M == 1 runs the
+    decode GEMV, larger batches the MFMA GEMM, as there.
+    """
+
+    def __init__(self, in_features: int, out_features: int, packed_weight: torch.Tensor,
+                 weight_scale: torch.Tensor, bias: Optional[torch.Tensor] = None):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        if packed_weight.shape[0] != out_features or packed_weight.shape[1] * 4 != in_features:
+            raise ValueError(f"packed_weight {tuple(packed_weight.shape)} does not match "
+                             f"[{out_features}, {in_features}/4]")
+        self.register_buffer("packed_weight", packed_weight)
+        self.register_buffer("weight_scale", weight_scale.reshape(1).to(torch.float32))
+        if bias is not None:
+            self.register_buffer("bias", bias)
+        else:
+            self.bias = None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        batch_shape = x.shape[:-1]
+        x_flat = x.reshape(-1, self.in_features).contiguous()
+        m = x_flat.shape[0]
+        x_int8, act_scale = quantize_activations_i8(x_flat)
+        out = bitnet_linear(self.packed_weight, x_int8, self.weight_scale, a_scale=act_scale.expand(m).contiguous(),
+                            bias=self.bias, out_dtype=torch.float32)
+        return out.view(*batch_shape, self.out_features)
+
+
 class SubLNBitLinear(nn.Module):
     """SubLN followed by BitLinear, run as ONE fused RMSNorm + per-token quant kernel and the linear.
 

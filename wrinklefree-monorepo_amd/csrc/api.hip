@@ -51,7 +51,7 @@ bool use_gemv(int64_t m, int64_t n, int64_t k, int64_t lda) {
 int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act,
                 int64_t m, int64_t lda, const float* a_scale, const float* w_scale_dev, float w_scale,
                 const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo, int32_t* acc_out,
-                void* stream) {
+                void* stream, int n_seg = 1, const int64_t* seg_rows = nullptr) {
   if (n <= 0 || k <= 0 || m < 0) return fail(WFB_EINVAL, "%s: bad sizes m=%lld n=%lld k=%lld", name, (long long)m, (long long)n, (long long)k);
   if (k % WFB_QK_I2S != 0)
     return fail(WFB_EINVAL, "%s: K (%lld) must be multiple of %d", name, (long long)k, WFB_QK_I2S);
@@ -73,6 +73,12 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
                 name, (long long)m, (long long)n, (long long)k);
 
   wfb::Epilogue e;
+  e.nseg = n_seg;
+  for (int j = 0; j < WFB_MAX_SEGMENTS - 1; ++j) e.seg_end[j] = 0;
+  if (n_seg > 1) {
+    int64_t end = 0;
+    for (int j = 0; j + 1 < n_seg; ++j) e.seg_end[j] = (int)(end += seg_rows[j]);
+  }
   e.a_scale = a_scale;
   e.ws_dev = w_scale_dev;
   e.ws = w_scale;
@@ -184,6 +190,45 @@ int wfb_gemm_i2s(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act
                  void* out, int out_dtype, int64_t ldo, int32_t* acc_out, void* stream) {
   return linear_impl(Kernel::Gemm, "wfb_gemm_i2s", qweight, n, k, act, m, lda, a_scale, w_scale_dev, w_scale, bias,
                      bias_dtype, out, out_dtype, ldo, acc_out, stream);
+}
+
+int wfb_linear_i2s_segmented(const uint8_t* qweight, int64_t n, int64_t k, int n_seg, const int64_t* seg_rows,
+                             const float* w_scales_dev, const int8_t* act, int64_t m, int64_t lda,
+                             const float* a_scale, const void* bias, int bias_dtype, void* out, int out_dtype,
+                             int64_t ldo, int32_t* acc_out, void* stream) {
+  const char* name = "wfb_linear_i2s_segmented";
+  if (n_seg < 1 || n_seg > WFB_MAX_SEGMENTS)
+    return fail(WFB_EINVAL, "%s: n_seg (%d) must be in 1..%d", name, n_seg, WFB_MAX_SEGMENTS);
+  if (!seg_rows || !w_scales_dev) return fail(WFB_EINVAL, "%s: null seg_rows or w_scales_dev", name);
+  int64_t total = 0;
+  for (int j = 0; j < n_seg; ++j) {
+    if (seg_rows[j] <= 0 || seg_rows[j] % 8 != 0)
+      return fail(WFB_EINVAL, "%s: segment %d has %lld rows (must be a positive multiple of 8)", name, j,
+                  (long long)seg_rows[j]);
+    total += seg_rows[j];
+  }
+  if (total != n) return fail(WFB_EINVAL, "%s: segment rows sum to %lld, N is %lld", name, (long long)total, (long long)n);
+  return linear_impl(Kernel::Auto, name, qweight, n, k, act, m, lda, a_scale, w_scales_dev, 0.0f, bias, bias_dtype,
+                     out, out_dtype, ldo, acc_out, stream, n_seg, seg_rows);
+}
+
+int wfb_glu_rmsnorm_quant_i8(const void* gate, const void* up, int x_dtype, int64_t ldx, int act,
+                             const void* gamma, int gamma_dtype, float eps, int64_t m, int64_t h, int8_t* q,
+                             int64_t k_pad, int64_t ldq, float* a_scale, void* stream) {
+  const char* name = "wfb_glu_rmsnorm_quant_i8";
+  if (!valid_dtype(x_dtype) || (gamma && !valid_dtype(gamma_dtype))) return fail(WFB_EINVAL, "%s: bad dtype", name);
+  if (act != WFB_ACT_SILU && act != WFB_ACT_RELU2) return fail(WFB_EINVAL, "%s: bad activation %d", name, act);
+  if (m < 0 || h <= 0 || h > WFB_NORM_MAX_H || h % 8 != 0)
+    return fail(WFB_EINVAL, "%s: H (%lld) must be a multiple of 8 in 8..%d", name, (long long)h, WFB_NORM_MAX_H);
+  if (ldx < h || k_pad < h || ldq < k_pad)
+    return fail(WFB_EINVAL, "%s: strides must satisfy ldx >= H, ldq >= k_pad >= H", name);
+  if (!(eps >= 0.0f)) return fail(WFB_EINVAL, "%s: eps must be >= 0", name);
+  if (m == 0) return ok();
+  if (!gate || !up || !q || !a_scale) return fail(WFB_EINVAL, "%s: null pointer", name);
+  if (!aligned(q, 8) || ldq % 8 != 0) return fail(WFB_EINVAL, "%s: q must be 8-byte aligned rows", name);
+  return hip_status(wfb::launch_glu_quant_rows(gate, up, x_dtype, ldx, act, gamma, gamma_dtype, eps, m, h, q, k_pad,
+                                               ldq, a_scale, as_stream(stream)),
+                    name);
 }
 
 }  // extern "C"

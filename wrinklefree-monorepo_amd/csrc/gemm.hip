@@ -68,7 +68,7 @@ __global__ __launch_bounds__(64 * WPB) void gemm_i2s_mfma16_kernel(const uint8_t
   }
 
   // C layout of a 16x16 MFMA tile: lane holds rows 4*(lane/16) + j (tokens), column lane % 16 (weight row).
-  const float ws = epi_wscale(ep);
+  const float ws = epi_wscale(ep, n);
   if (n < N) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -273,7 +273,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
   if ((l % LPR) == 0) rowsum[srow] = ssum;
   __syncthreads();  // also: every wave is done reading the operand buffers
 
-  const float ws = epi_wscale(ep);
+  // weight scale per 4-column output group (segments are multiples of 8 rows, so a group has one)
+  float wsg[TN][4];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wsg[tn][q] = epi_wscale(ep, n0 + (wn * TN + tn) * 32 + 8 * q + 4 * g);
   if constexpr (EPI == 1) {
     // per 32-row MFMA tile: convert in registers, stage 32 rows x 64 bf16 (128-byte rows, 16-byte
     // chunks XOR-swizzled by row) in this wave's own LDS buffer, store 8 rows x 128 B per instruction
@@ -290,7 +295,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
         for (int q = 0; q < 4; ++q) {
           float y[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = __fmul_rn(__fmul_rn((float)(acc[tn][tm][4 * q + e] - rs), ws), as);
+          for (int e = 0; e < 4; ++e) y[e] = __fmul_rn(__fmul_rn((float)(acc[tn][tm][4 * q + e] - rs), wsg[tn][q]), as);
           const bf16x2_t lo = __builtin_convertvector((f32x2_t){y[0], y[1]}, bf16x2_t);
           const bf16x2_t hi = __builtin_convertvector((f32x2_t){y[2], y[3]}, bf16x2_t);
           const int c = tn * 4 + q;
@@ -329,7 +334,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
           if (n >= N) continue;
           const int32_t v[4] = {acc[tn][tm][4 * q] - rs, acc[tn][tm][4 * q + 1] - rs, acc[tn][tm][4 * q + 2] - rs,
                                 acc[tn][tm][4 * q + 3] - rs};
-          epi_store4(ep, ws, as, m, n, v, vec_out && n + 3 < N, N);
+          epi_store4(ep, wsg[tn][q], as, m, n, v, vec_out && n + 3 < N, N);
         }
     }
   }

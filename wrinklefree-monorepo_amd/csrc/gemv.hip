@@ -148,7 +148,7 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   if (t >= RB) return;
   const int n = row0 + t;
   if (n >= N) return;
-  const float ws = epi_wscale(ep);
+  const float ws = epi_wscale(ep, n);
   const float bias = epi_bias(ep, n);
 #pragma unroll
   for (int m = 0; m < M; ++m) {

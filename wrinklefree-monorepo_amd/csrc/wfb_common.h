@@ -90,7 +90,7 @@ __device__ __forceinline__ v4i buf_load16(buf_t r, uint32_t off) {
 
 struct Epilogue {
   const float* a_scale;  // [M] or null
-  const float* ws_dev;   // [1] or null
+  const float* ws_dev;   // [nseg] or null
   float ws;              // used when ws_dev is null
   const void* bias;      // [N] or null
   int bias_dtype;
@@ -98,9 +98,20 @@ struct Epilogue {
   int out_dtype;
   int64_t ldo;
   int32_t* acc_out;      // [M, N] or null
+  // Output rows (weight rows) split in nseg consecutive segments, each with its own weight scale
+  // ws_dev[s]; segment s ends at row seg_end[s] (s < nseg - 1).  nseg = 1: one per-tensor scale.
+  int nseg;
+  int seg_end[WFB_MAX_SEGMENTS - 1];
 };
 
-__device__ __forceinline__ float epi_wscale(const Epilogue& e) { return e.ws_dev ? e.ws_dev[0] : e.ws; }
+// Weight scale of output column n (segment lookup without branches).
+__device__ __forceinline__ float epi_wscale(const Epilogue& e, int n) {
+  if (!e.ws_dev) return e.ws;
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < WFB_MAX_SEGMENTS - 1; ++j) s += (j + 1 < e.nseg && n >= e.seg_end[j]) ? 1 : 0;
+  return e.ws_dev[s];
+}
 __device__ __forceinline__ float epi_ascale(const Epilogue& e, int m) { return e.a_scale ? e.a_scale[m] : 1.0f; }
 __device__ __forceinline__ float epi_bias(const Epilogue& e, int n) {
   if (!e.bias) return 0.0f;
@@ -180,6 +191,9 @@ hipError_t launch_unpack_i2s(const uint8_t* qw, int64_t n, int64_t k, int8_t* ou
 hipError_t launch_quant_rows(const void* x, int dt, int64_t ldx, const void* gamma, int gdt, bool norm,
                              float eps, int64_t m, int64_t h, int8_t* q, int64_t k_pad, int64_t ldq,
                              float* a_scale, hipStream_t s);
+hipError_t launch_glu_quant_rows(const void* gate, const void* up, int dt, int64_t ldx, int act, const void* gamma,
+                                 int gdt, float eps, int64_t m, int64_t h, int8_t* q, int64_t k_pad, int64_t ldq,
+                                 float* a_scale, hipStream_t s);
 hipError_t launch_quant_tensor(const void* x, int dt, int64_t numel, int8_t* q, float* a_scale, hipStream_t s);
 hipError_t launch_gemv_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                            const Epilogue& e, hipStream_t s);

@@ -2,15 +2,17 @@
 
 Layout follows the stage-1 conversion (packages/training/src/wrinklefree/training/stage1.py:63-214):
 HF Llama attention/MLP with q/k/v/gate/up as BitLinear and o_proj/down_proj as SubLN + BitLinear,
-SiLU SwiGLU, RMSNorm before attention and MLP, HF rotary embeddings (rotate-half form), GQA.
+gated MLP (SiLU SwiGLU, or relu^2 for the BitNet b1.58 2B form), RMSNorm before attention and MLP, HF rotary embeddings (rotate-half form), GQA.
 Random init is normal(0, 0.02) for every weight and ones for every norm (BitNetLlama._init_weights,
 packages/training/src/wrinklefree/models/llama.py:58-65).
 
 Every quantised op goes through a *BitLinear backend*: one call per (norm -> quantise -> linear)
 group, so the norm before q/k/v (and before gate/up) is fused with the activation quantiser and
-shared by the projections that read it.  ``HipBackend`` runs libwfbitnet; a test can substitute
-another backend with the same two methods to compare the quantised path while the float code
-(embedding, RoPE, attention, SiLU, residuals, LM head) stays identical.
+shared by the projections that read it, and one call for the MLP middle (act(gate) * up -> SubLN ->
+quantise -> down).  ``HipBackend`` runs libwfbitnet -- with ``fused=True`` the projections of a group
+run as one segmented launch (q|k|v, gate|up) and the gated activation, SubLN and quantiser as one
+kernel; a test can substitute another backend with the same two methods to compare the quantised
+path while the float code (embedding, RoPE, attention, residuals, LM head) stays identical.
 """
 
 from __future__ import annotations
@@ -21,7 +23,8 @@ from typing import Dict, List, Optional, Sequence
 
 import torch
 
-from .ops import QK_I2_S, bitnet_linear, pack_ternary_i2s, rmsnorm_quantize_i8
+from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_segmented, glu_rmsnorm_quantize_i8, pack_ternary_i2s,
+                  rmsnorm_quantize_i8)
 
 
 @dataclass(frozen=True)
@@ -38,6 +41,7 @@ class BitNetConfig:
     subln_eps: float = 1e-6  # SubLN before o_proj and down_proj (stage1.py:98, 151)
     tie_embeddings: bool = True
     ternary_lm_head: bool = False
+    hidden_act: str = "silu"  # gated MLP activation: "silu" (SwiGLU) or "relu2" (BitNet b1.58 2B)
 
 
 # SmolLM2-135M architecture (packages/training/configs/model/smollm2_135m.yaml)
@@ -64,17 +68,39 @@ class PackedLinear:
 
 class HipBackend:
     """Quantised BitLinear groups on libwfbitnet: fused RMSNorm/SubLN + per-token int8 quantisation,
-    then one GEMV/GEMM per projection with the rescale fused in its epilogue."""
+    then the projections with the rescale fused in their epilogue.
 
-    def __init__(self, out_dtype: torch.dtype = torch.float32, keep_acc: bool = False):
+    ``fused=True``: the projections of a group (q|k|v, gate|up) run as one segmented launch on their
+    concatenated weights, so a decode layer takes 8 library launches (norm+quant, q|k|v, SubLN+quant,
+    o, norm+quant, gate|up, act+SubLN+quant, down) instead of 11."""
+
+    def __init__(self, out_dtype: torch.dtype = torch.float32, keep_acc: bool = False, fused: bool = False):
         self.out_dtype = out_dtype
         self.keep_acc = keep_acc
+        self.fused = fused
         self.acc_log: List[torch.Tensor] = []
+        self._groups: Dict[tuple, tuple] = {}
 
-    def norm_linears(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], eps: float,
-                     linears: Sequence[PackedLinear]) -> List[torch.Tensor]:
-        k_pad = linears[0].k_pad
-        q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=k_pad)
+    def _group(self, linears: Sequence[PackedLinear]):
+        key = tuple(id(l) for l in linears)
+        g = self._groups.get(key)
+        if g is None:
+            qw = torch.cat([l.qweight for l in linears], dim=0).contiguous()
+            sc = torch.cat([l.scale.reshape(1) for l in linears]).contiguous()
+            g = (qw, sc, [l.out_features for l in linears])
+            self._groups[key] = g
+        return g
+
+    def _linears(self, q: torch.Tensor, a_scale: torch.Tensor, linears: Sequence[PackedLinear]) -> List[torch.Tensor]:
+        if self.fused and len(linears) > 1:
+            qw, sc, rows = self._group(linears)
+            if self.keep_acc:
+                y, acc = bitnet_linear_segmented(qw, rows, sc, q, a_scale=a_scale, out_dtype=self.out_dtype,
+                                                 return_acc=True)
+                self.acc_log.extend(torch.split(acc, rows, dim=1))
+            else:
+                y = bitnet_linear_segmented(qw, rows, sc, q, a_scale=a_scale, out_dtype=self.out_dtype)
+            return list(torch.split(y, rows, dim=1))
         outs = []
         for lin in linears:
             if self.keep_acc:
@@ -85,6 +111,19 @@ class HipBackend:
                 y = bitnet_linear(lin.qweight, q, lin.scale, a_scale=a_scale, out_dtype=self.out_dtype)
             outs.append(y)
         return outs
+
+    def norm_linears(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], eps: float,
+                     linears: Sequence[PackedLinear]) -> List[torch.Tensor]:
+        q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=linears[0].k_pad)
+        return self._linears(q, a_scale, linears)
+
+    def glu_norm_linears(self, gate: torch.Tensor, up: torch.Tensor, act: str, norm_weight: Optional[torch.Tensor],
+                         eps: float, linears: Sequence[PackedLinear]) -> List[torch.Tensor]:
+        """act(gate) * up -> SubLN -> per-token int8 -> linears (one kernel before the projections)."""
+        if gate.stride(-1) != 1 or up.stride(-1) != 1 or gate.stride(0) != up.stride(0):
+            gate, up = gate.contiguous(), up.contiguous()
+        q, a_scale = glu_rmsnorm_quantize_i8(gate, up, act, norm_weight, eps=eps, k_pad=linears[0].k_pad)
+        return self._linears(q, a_scale, linears)
 
 
 class _Layer:
@@ -190,8 +229,7 @@ class BitNetDecoder:
             x = x + o.reshape(b, t, -1).to(self.dtype)
             h2 = x.reshape(b * t, cfg.hidden_size)
             gate, up = be.norm_linears(h2, L.post_attn_norm, cfg.rms_eps, [L.gate, L.up])
-            act = (torch.nn.functional.silu(gate.to(torch.float32)) * up.to(torch.float32)).to(self.dtype)
-            (down,) = be.norm_linears(act, L.ffn_sub_norm, cfg.subln_eps, [L.down])
+            (down,) = be.glu_norm_linears(gate, up, cfg.hidden_act, L.ffn_sub_norm, cfg.subln_eps, [L.down])
             x = x + down.reshape(b, t, -1).to(self.dtype)
         last = x[:, -1, :]
         if self.lm_head is not None:

@@ -20,7 +20,8 @@ from typing import Optional, Tuple, Union
 import torch
 
 from . import _lib
-from ._lib import WFB_ABSMEAN_WS_DOUBLES, WFB_BF16, WFB_F16, WFB_F32, WFB_QK_I2S
+from ._lib import (WFB_ABSMEAN_WS_DOUBLES, WFB_ACT_RELU2, WFB_ACT_SILU, WFB_BF16, WFB_F16, WFB_F32,
+                   WFB_MAX_SEGMENTS, WFB_QK_I2S)
 
 QK_I2_S = WFB_QK_I2S
 
@@ -273,6 +274,116 @@ def bitnet_linear(
         out = None if out is None else out.view(n)
         acc = None if acc is None else acc.view(n)
     return (out, acc) if return_acc else out
+
+
+def bitnet_linear_segmented(
+    packed_weights: torch.Tensor,
+    seg_rows,
+    scales: torch.Tensor,
+    activations: torch.Tensor,
+    a_scale: Optional[torch.Tensor] = None,
+    bias: Optional[torch.Tensor] = None,
+    out_dtype: Optional[torch.dtype] = torch.bfloat16,
+    return_acc: bool = False,
+):
+    """One launch for several projections that read the same activations (fused QKV, gate|up).
+
+    ``packed_weights`` is the row concatenation of the projections' I2_S weights, ``seg_rows`` their
+    row counts (multiples of 8), ``scales`` fp32 [n_seg] on the device: output column n is scaled by
+    the scale of its segment.  Equal to separate ``bitnet_linear`` calls on the segments.
+    """
+    name = "bitnet_linear_segmented"
+    rows = [int(r) for r in seg_rows]
+    if not 1 <= len(rows) <= WFB_MAX_SEGMENTS:
+        raise ValueError(f"{name}: 1..{WFB_MAX_SEGMENTS} segments, got {len(rows)}")
+    if packed_weights.dtype != torch.uint8 or packed_weights.dim() != 2:
+        raise RuntimeError(f"{name}: packed_weights must be uint8 2D [out_features, in_features/4]")
+    if sum(rows) != packed_weights.shape[0]:
+        raise ValueError(f"{name}: segment rows sum to {sum(rows)}, packed_weights has {packed_weights.shape[0]}")
+    if scales.dtype != torch.float32 or scales.numel() != len(rows):
+        raise RuntimeError(f"{name}: scales must be fp32 with one element per segment")
+    if activations.dtype != torch.int8 or activations.dim() not in (1, 2):
+        raise RuntimeError(f"{name}: activations must be int8 [in_features] or [batch, in_features]")
+    n, kb = packed_weights.shape
+    k = kb * 4
+    a2 = activations.view(1, -1) if activations.dim() == 1 else activations
+    if a2.shape[1] != k:
+        raise ValueError(f"{name}: activations have {a2.shape[1]} features, packed weights {k}")
+    m = a2.shape[0]
+    dev = _require_gpu(name, packed_weights, scales, a_scale, bias)
+    if a2.device != dev:
+        raise RuntimeError(f"{name}: activations are on {a2.device}, weights on {dev}")
+    if a2.stride(1) != 1 or (m > 1 and a2.stride(0) % 16 != 0) or a2.data_ptr() % 16 != 0:
+        a2 = a2.contiguous()
+    if a_scale is not None and (a_scale.dtype != torch.float32 or a_scale.numel() != m):
+        raise RuntimeError(f"{name}: a_scale must be fp32 with one element per token ({m})")
+    if out_dtype is None and not return_acc:
+        raise RuntimeError(f"{name}: nothing to compute (out_dtype=None and return_acc=False)")
+    out, odt = None, 0
+    if out_dtype is not None:
+        if out_dtype not in (torch.float32, torch.bfloat16):
+            raise RuntimeError(f"{name}: out_dtype must be float32 or bfloat16")
+        out = torch.empty((m, n), dtype=out_dtype, device=dev)
+        odt = _DT[out_dtype]
+    acc = torch.empty((m, n), dtype=torch.int32, device=dev) if return_acc else None
+    bdt = _float_dtype(name, bias) if bias is not None else 0
+    if bias is not None and bias.numel() != n:
+        raise RuntimeError(f"{name}: bias has {bias.numel()} elements, expected {n}")
+    seg = (ctypes.c_int64 * len(rows))(*rows)
+    lda = a2.stride(0) if m > 1 else k
+    with torch.cuda.device(dev):
+        _lib.call(
+            "wfb_linear_i2s_segmented", _p(packed_weights), n, k, len(rows), ctypes.cast(seg, ctypes.c_void_p),
+            _p(scales), _p(a2), m, lda, _p(a_scale), _p(bias), bdt, _p(out), odt, n, _p(acc), _stream(dev),
+        )
+    if activations.dim() == 1:
+        out = None if out is None else out.view(n)
+        acc = None if acc is None else acc.view(n)
+    return (out, acc) if return_acc else out
+
+
+_ACTS = {"silu": WFB_ACT_SILU, "relu2": WFB_ACT_RELU2}
+
+
+def glu_rmsnorm_quantize_i8(
+    gate: torch.Tensor, up: torch.Tensor, act: str = "silu", weight: Optional[torch.Tensor] = None,
+    eps: float = 1e-6, k_pad: Optional[int] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """act(gate) * up -> SubLN (weight) -> per-token int8: (q int8 [..., k_pad], a_scale fp32 [...]).
+
+    ``act`` is "silu" (SwiGLU) or "relu2" (relu(gate)^2, the reference fused MLP,
+    bitnet_fused_layer.cpp:200-216).  gate and up must have the same shape and row stride with
+    contiguous rows (e.g. the two halves of one gate|up output).
+    """
+    name = "glu_rmsnorm_quantize_i8"
+    if act not in _ACTS:
+        raise ValueError(f"{name}: act must be one of {sorted(_ACTS)}")
+    if weight is not None:
+        _require_gpu(name, weight)
+    if gate.device.type != "cuda" or up.device != gate.device or (weight is not None and weight.device != gate.device):
+        raise RuntimeError(f"{name}: gate, up and weight must be on one HIP device")
+    dev = gate.device
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise RuntimeError(f"{name}: gate and up must have the same shape and dtype")
+    dt = _float_dtype(name, gate)
+    h = gate.shape[-1]
+    g2, u2 = gate.reshape(-1, h), up.reshape(-1, h)
+    if g2.stride(-1) != 1 or u2.stride(-1) != 1 or g2.stride(0) != u2.stride(0):
+        raise RuntimeError(f"{name}: gate and up need contiguous rows with one common row stride")
+    m = g2.shape[0]
+    ldx = g2.stride(0) if m > 1 else h
+    gdt = _float_dtype(name, weight) if weight is not None else WFB_F32
+    if weight is not None and weight.numel() != h:
+        raise RuntimeError(f"{name}: weight has {weight.numel()} elements, expected {h}")
+    _, kp, kpa, _ = _rows(name, gate, k_pad)
+    q = torch.empty((*gate.shape[:-1], kpa), dtype=torch.int8, device=dev)
+    a_scale = torch.empty(gate.shape[:-1], dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "wfb_glu_rmsnorm_quant_i8", _p(g2), _p(u2), dt, ldx, _ACTS[act], _p(weight), gdt, float(eps), m, h,
+            _p(q), kpa, kpa, _p(a_scale), _stream(dev),
+        )
+    return (q if kpa == kp else q[..., :kp]), a_scale
 
 
 def bitnet_gemv(packed_weights: torch.Tensor, activations: torch.Tensor, scale: Scale) -> torch.Tensor:
