@@ -14,7 +14,7 @@ M = 512, 2048, 8192 in int8 TOP/s vs the 5.0 POP/s dense int8 peak,
 RMSNorm+quant kernel, one BitNet-2B decode layer's quantised path with separate vs fused launches
 (decode_layer_2b), and the reference CPU kernel timed on this host (cpu_baseline).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--e2e] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -52,6 +52,8 @@ def parse():
     p.add_argument("--sweep", action="store_true", help="also run the batched M sweep (configs[2])")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--e2e", action="store_true",
+                   help="also run the end-to-end models (configs[4] Llama-3-8B shape, configs[0] SmolLM2 shape)")
     return p.parse_args()
 
 
@@ -221,6 +223,61 @@ def decode_layer_bench(torch, L, orc, dev, steps, warmup, n_layers=30):
         "fused": {"launches": len(fus[0]), "us": round(ms_fus * 1e3, 2),
                   "GB/s": round(wbytes / (ms_fus * 1e-3) / 1e9, 1)},
     }
+
+
+def e2e_bench(pkg, torch, dev):
+    """Greedy decoding on the fused HIP backend (BitLinears on libwfbitnet, float glue in torch).
+    Llama-3-8B shape, every linear ternary, random init on the device; prefill of 8
+    prompts x 256 tokens (2048 tokens, one M = 2048 GEMM per projection), then 256 decode steps at
+    batch 8.  configs[0]: SmolLM2-135M shape, 32-token prompt, 128 new tokens at batch 1.
+    Wall-clock times around synchronised regions (host launch overhead included); decode is timed
+    both with eager launches and replayed from one HIP graph capture of the decode step."""
+    M = pkg.model
+    res = {}
+
+    def run(cfg, batch, t0, new, dtype, name):
+        print(f"[e2e] {name}: building", file=sys.stderr, flush=True)
+        model = M.BitNetDecoder(cfg, seed=0, device=dev, dtype=dtype, init_on_device=True,
+                                backend=M.HipBackend(out_dtype=torch.bfloat16 if dtype == torch.bfloat16
+                                                     else torch.float32, fused=True))
+        wbytes = sum(l.qweight.numel() for l in M.quantised_linears(model).values())
+        prompt = torch.randint(0, cfg.vocab_size, (batch, t0), generator=torch.Generator().manual_seed(5)).to(dev)
+        with torch.no_grad():
+            model.generate(prompt[:, :8], 4, graph=True)       # warm-up (kernels, allocator, graph path)
+            torch.cuda.synchronize()
+            model.reset(batch, t0 + new)
+            ta = time.perf_counter()
+            torch.argmax(model.forward(prompt, 0), dim=-1)
+            torch.cuda.synchronize()
+            prefill_s = time.perf_counter() - ta
+            timings = {}
+            for mode in ("eager", "graph"):
+                tb = time.perf_counter()
+                out = model.generate(prompt, new, graph=(mode == "graph"))
+                torch.cuda.synchronize()
+                timings[mode] = time.perf_counter() - tb - prefill_s
+        print(f"[e2e] {name}: prefill {prefill_s:.3f} s, decode eager {timings['eager']:.3f} s, "
+              f"graph {timings['graph']:.3f} s", file=sys.stderr, flush=True)
+        steps = new - 1
+        res[name] = {
+            "config": f"{cfg.num_layers} layers, hidden {cfg.hidden_size}, heads {cfg.num_heads}/{cfg.num_kv_heads}, "
+                      f"FFN {cfg.intermediate_size}, vocab {cfg.vocab_size}, ternary lm_head {cfg.ternary_lm_head}",
+            "packed_weight_bytes": int(wbytes),
+            "prefill_tokens": batch * t0, "prefill_s": round(prefill_s, 4),
+            "prefill_tok_s": round(batch * t0 / prefill_s, 1),
+            "decode_batch": batch, "decode_steps": steps,
+            "decode_graph_ms_per_step": round(timings["graph"] / steps * 1e3, 3),
+            "decode_graph_tok_s": round(batch * steps / timings["graph"], 1),
+            "decode_eager_ms_per_step": round(timings["eager"] / steps * 1e3, 3),
+            "decode_eager_tok_s": round(batch * steps / timings["eager"], 1),
+            "distinct_tokens": int(out.unique().numel()),
+        }
+        del model
+        torch.cuda.empty_cache()
+
+    run(M.LLAMA3_8B, 8, 256, 256, torch.bfloat16, "llama3_8b")
+    run(M.SMOLLM2_135M, 1, 32, 128, torch.float32, "smollm2_135m")
+    return res
 
 
 def measured_traffic(n: int, k: int):
@@ -397,6 +454,8 @@ def main():
                               "TOPS": round(2 * m * n * k / (ms * 1e-3) / 1e12, 2)})
             del copies
 
+    e2e = e2e_bench(__graft_entry__.load_package(), torch, dev) if args.e2e else None
+
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     line = {
@@ -426,6 +485,8 @@ def main():
     }
     if sweep is not None:
         line["batched_sweep"] = sweep
+    if e2e is not None:
+        line["e2e"] = e2e
     print(json.dumps(line), flush=True)
 
 

@@ -175,6 +175,16 @@ def test_batched_sweep_mfma(pkg, dev, n, k, m):
         _check_linear(pkg, dev, packed, a, 1.0, np.ones(m, np.float32), kernel="auto", check_fp32=False)
 
 
+@pytest.mark.parametrize("m,n,k", [(12, 32800, 128), (24, 16400, 256), (64, 8200, 384), (9, 40, 8192)])
+def test_batched_kernel_choice_boundaries(pkg, dev, m, n, k):
+    # 3 <= M <= 64 runs the split-K skinny kernel while N * ceil(M/16) <= 32768 (always for M <= 8) and
+    # the whole-K wave-per-rows kernel beyond; these shapes sit just past that boundary
+    rng = np.random.default_rng(2500 + m + n + k)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    _check_linear(pkg, dev, packed, a, orc.log_uniform(rng), orc.log_uniform(rng, m), kernel="gemm")
+
+
 @pytest.mark.parametrize("n,k", [(13824, 2560), (2560, 6912)])
 @pytest.mark.parametrize("m", [512, 2048])
 def test_prefill_gemm_exact(pkg, dev, n, k, m):

@@ -20,6 +20,9 @@ namespace {
 // byte-wise code -> weight: 0 -> 0xFF (-1), 1 -> 0x00, 2 -> 0x01
 __device__ __forceinline__ int codes_to_i8(uint32_t x) { return (int)__builtin_amdgcn_perm(0u, 0x000100FFu, x); }
 
+// Wave-per-16-rows batched kernel (whole K per wave, tokens split over grid.y): kept for the M <= 64
+// shapes where the split-K skinny kernel below re-reads too many activation rows (large N at M > 8) or
+// where offsets exceed 32 bits.
 template <int MT, int WPB>
 __global__ __launch_bounds__(64 * WPB) void gemm_i2s_mfma16_kernel(const uint8_t* __restrict__ W,
                                                                    const int8_t* __restrict__ A, int64_t lda,
@@ -78,6 +81,118 @@ __global__ __launch_bounds__(64 * WPB) void gemm_i2s_mfma16_kernel(const uint8_t
         if (tok < M) epi_store(ep, ws, epi_ascale(ep, tok), epi_bias(ep, n), tok, n, acc[mt][j]);
       }
   }
+}
+
+// Batched decode (3 <= M <= 64 tokens): v_mfma_i32_16x16x64_i8 over MT tiles of 16 tokens.  A
+// workgroup owns 16 weight rows and splits K over its S waves: wave w takes the 256-weight K-steps
+// w, w + S, w + 2S, ..., so the waves of a workgroup read adjacent 64-byte chunks of the same rows.
+// Lane (nl, g) loads 16 packed bytes of row n0 + nl, chunk 4t + g (64 weights; field f covers
+// k = 128*(c/2) + 32f + 16*(c%2) + 0..15), the B operands of four MFMAs.  Fields enter masked but not
+// shifted -- bits 1:0 (x1), 3:2 (x4), 5:4 and (7:6 >> 2) (x16) -- into three accumulators (5 VALU per
+// packed dword); the code offset is removed with each token's sum(a): acc = acc1 + acc4/4 + acc16/16 -
+// sum(a).  Partial 16 x 16 tiles of the S waves are summed through LDS.  Loads go through raw buffer
+// descriptors: rows past N or M and chunks past K read as zeros.
+template <int MT, int S>
+__global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* __restrict__ W,
+                                                                 const int8_t* __restrict__ A, int64_t lda,
+                                                                 int M, int N, int C, Epilogue ep) {
+  __shared__ int red[S][MT][4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * 16;
+  const int nl = lane & 15, g = lane >> 4;
+  const int n = n0 + nl;
+  const uint32_t row_bytes = (uint32_t)C * 16;
+  const uint32_t w_end = (uint32_t)N * row_bytes, a_end = (uint32_t)((int64_t)(M - 1) * lda + (int64_t)C * 64);
+  const buf_t wb = make_buf(W, w_end);
+  const buf_t ab = make_buf(A, a_end);
+  const uint32_t woff = (uint32_t)n * row_bytes + 16 * g;
+  uint32_t aoff[MT];
+  bool tok_ok[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    tok_ok[mt] = mt * 16 + nl < M;
+    aoff[mt] = (uint32_t)((int64_t)(mt * 16 + nl) * lda);
+  }
+
+  v4i acc1[MT], acc4[MT], acc16[MT];
+  int sa[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc1[mt] = acc4[mt] = acc16[mt] = v4i{0, 0, 0, 0};
+    sa[mt] = 0;
+  }
+  const int T = (C + 3) >> 2;
+#pragma unroll 2
+  for (int t = w; t < T; t += S) {
+    const int c = 4 * t + g;
+    const bool ok = c < C;
+    const v4i wv = buf_load16(wb, ok ? woff + 64u * t : w_end);
+    const uint32_t ab0 = 128u * (c >> 1) + 16u * (c & 1);
+    v4i av[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int f = 0; f < 4; ++f) av[mt][f] = buf_load16(ab, (ok && tok_ok[mt]) ? aoff[mt] + ab0 + 32 * f : a_end);
+    v4i b0, b1, b2, b3;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = wv[e];
+      b0[e] = (d >> 2) & 0x30303030;
+      b1[e] = d & 0x30303030;
+      b2[e] = d & 0x0C0C0C0C;
+      b3[e] = d & 0x03030303;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      acc16[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][0], b0, acc16[mt], 0, 0, 0);
+      acc16[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][1], b1, acc16[mt], 0, 0, 0);
+      acc4[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][2], b2, acc4[mt], 0, 0, 0);
+      acc1[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][3], b3, acc1[mt], 0, 0, 0);
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sa[mt] = __builtin_amdgcn_sdot4(av[mt][f][e], 0x01010101, sa[mt], false);
+    }
+  }
+  // C layout of a 16x16 tile: lane (nl, g) holds tokens 4g + j (j < 4) of weight row nl.  sum(a) of
+  // token nl over this wave's K range: add the 4 lane groups, then fetch token 4g + j's from lane 4g + j.
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    int s = sa[mt];
+    s += __shfl_xor(s, 16, 64);
+    s += __shfl_xor(s, 32, 64);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int sj = __shfl(s, 4 * g + j, 64);
+      red[w][mt][j][lane] = acc1[mt][j] + (acc4[mt][j] >> 2) + (acc16[mt][j] >> 4) - sj;
+    }
+  }
+  __syncthreads();
+  if (w != 0 || n >= N) return;
+  const float ws = epi_wscale(ep, n);
+  const float bias = epi_bias(ep, n);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tok = mt * 16 + 4 * g + j;
+      int tot = red[0][mt][j][lane];
+#pragma unroll
+      for (int k = 1; k < S; ++k) tot += red[k][mt][j][lane];
+      if (tok < M) epi_store(ep, ws, epi_ascale(ep, tok), bias, tok, n, tot);
+    }
+}
+
+template <int MT>
+hipError_t launch_skinny(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
+                         hipStream_t s) {
+  const int T = (C + 3) / 4;
+  const dim3 grid((n + 15) / 16);
+  if (T >= 8)
+    hipLaunchKernelGGL((gemm_i2s_skinny_kernel<MT, 8>), grid, dim3(512), 0, s, W, A, lda, m, n, C, e);
+  else
+    hipLaunchKernelGGL((gemm_i2s_skinny_kernel<MT, 4>), grid, dim3(256), 0, s, W, A, lda, m, n, C, e);
+  return hipGetLastError();
 }
 
 // Prefill GEMM (M > 64): v_mfma_i32_32x32x32_i8.  Workgroup tile BM x 256 (BM = 32 TM), four waves
@@ -373,6 +488,16 @@ hipError_t launch_mt(const uint8_t* W, int n, int C, const int8_t* A, int m, int
 hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, const Epilogue& e,
                            hipStream_t s) {
   const int C = k / 64;
+  // Split-K skinny kernel while its per-workgroup re-read of all M activation rows stays cheap against
+  // the weight stream (measured on MI355X over the Llama-3-8B / BitNet-2B decode shapes: always for
+  // M <= 8, for larger M while N * (16-token tiles) <= 32768); it addresses through 32-bit offsets.
+  const int mt = (m + 15) / 16;
+  const bool small_offsets = (int64_t)n * (k / 4) <= INT32_MAX && (int64_t)(m - 1) * lda + k <= INT32_MAX;
+  if (m <= 64 && small_offsets && (m <= 8 || (int64_t)n * (mt == 3 ? 4 : mt) <= 32768)) {
+    if (m <= 16) return launch_skinny<1>(W, n, C, A, m, lda, e, s);
+    if (m <= 32) return launch_skinny<2>(W, n, C, A, m, lda, e, s);
+    return launch_skinny<4>(W, n, C, A, m, lda, e, s);
+  }
   if (m <= 16) return launch_mt<1>(W, n, C, A, m, lda, e, s);
   if (m <= 32) return launch_mt<2>(W, n, C, A, m, lda, e, s);
   if (m <= 64) return launch_mt<4>(W, n, C, A, m, lda, e, s);

@@ -132,7 +132,7 @@ class _Layer:
         qd, kvd = cfg.num_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
 
         def w(o, i):
-            return (torch.randn((o, i), generator=gen, dtype=torch.float32) * 0.02).to(device)
+            return (torch.randn((o, i), generator=gen, dtype=torch.float32, device=gen.device) * 0.02).to(device)
 
         self.q, self.k, self.v = PackedLinear(w(qd, h)), PackedLinear(w(kvd, h)), PackedLinear(w(kvd, h))
         self.o = PackedLinear(w(h, qd))
@@ -147,18 +147,22 @@ class BitNetDecoder:
     """Decoder-only BitNet model with a per-layer KV cache; float glue in ``dtype``."""
 
     def __init__(self, cfg: BitNetConfig, seed: int = 0, device: str = "cuda", dtype: torch.dtype = torch.float32,
-                 backend=None):
+                 backend=None, init_on_device: bool = False):
+        """``init_on_device``: draw the random weights with a generator on ``device`` (fast for 8B-scale
+        models) instead of the host generator (the default, reproducible across devices)."""
         self.cfg = cfg
         self.device = torch.device(device)
         self.dtype = dtype
         self.backend = backend if backend is not None else HipBackend(out_dtype=dtype if dtype == torch.float32
                                                                        else torch.bfloat16)
-        gen = torch.Generator().manual_seed(seed)
-        self.embed = (torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen) * 0.02).to(self.device, dtype)
+        gen = torch.Generator(device=self.device if init_on_device else "cpu").manual_seed(seed)
+        self.embed = (torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen, device=gen.device) * 0.02).to(
+            self.device, dtype)
         self.layers = [_Layer(cfg, gen, self.device, dtype) for _ in range(cfg.num_layers)]
         self.final_norm = torch.ones(cfg.hidden_size, device=self.device, dtype=dtype)
         if cfg.ternary_lm_head:
-            self.lm_head = PackedLinear((torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen) * 0.02)
+            self.lm_head = PackedLinear((torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen,
+                                                     device=gen.device) * 0.02)
                                         .to(self.device))
         else:
             self.lm_head = None  # tied to the embedding
@@ -182,77 +186,144 @@ class BitNetDecoder:
         x32 = x.to(torch.float32)
         return (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps) * w.to(torch.float32)).to(x.dtype)
 
-    def _attention(self, li: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start: int) -> torch.Tensor:
-        cfg = self.cfg
-        b, t = q.shape[0], q.shape[1]
+    def _cache(self, li: int, b: int):
+        """Layer li's fp32 KV cache: K transposed [B, kv, D, L_max] (scores = q @ K without a transpose
+        copy), V [B, kv, L_max, D]."""
         cache = self.kv[li]
         if cache is None:
-            cache = [torch.zeros((b, cfg.num_kv_heads, self._max_len, cfg.head_dim), device=self.device,
-                                 dtype=torch.float32) for _ in range(2)]
+            cfg = self.cfg
+            cache = [torch.zeros((b, cfg.num_kv_heads, cfg.head_dim, self._max_len), device=self.device,
+                                 dtype=torch.float32),
+                     torch.zeros((b, cfg.num_kv_heads, self._max_len, cfg.head_dim), device=self.device,
+                                 dtype=torch.float32)]
             self.kv[li] = cache
-        cache[0][:, :, start:start + t] = k.transpose(1, 2).to(torch.float32)
-        cache[1][:, :, start:start + t] = v.transpose(1, 2).to(torch.float32)
-        kk = cache[0][:, :, :start + t]
-        vv = cache[1][:, :, :start + t]
-        rep = cfg.num_heads // cfg.num_kv_heads
-        kk = kk.repeat_interleave(rep, dim=1).contiguous()
-        vv = vv.repeat_interleave(rep, dim=1).contiguous()
-        qq = q.transpose(1, 2).to(torch.float32).contiguous()                 # [B, H, T, D]
-        scores = torch.matmul(qq, kk.transpose(-1, -2).contiguous()) / math.sqrt(cfg.head_dim)
+        return cache
+
+    def _attention(self, li: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start: int) -> torch.Tensor:
+        """Causal GQA attention of T new tokens at positions start.. over the KV cache.  The rep =
+        heads / kv_heads query heads that share a kv head are stacked as rows of one matrix
+        ([B, kv, rep*T, D]), so no kv repeat is materialised."""
+        cfg = self.cfg
+        b, t = q.shape[0], q.shape[1]
+        kvh, rep, hd = cfg.num_kv_heads, cfg.num_heads // cfg.num_kv_heads, cfg.head_dim
+        kt, vc = self._cache(li, b)
+        kt[:, :, :, start:start + t] = k.permute(0, 2, 3, 1).to(torch.float32)
+        vc[:, :, start:start + t] = v.transpose(1, 2).to(torch.float32)
+        # head h = g*rep + r reads kv head g (repeat_interleave order)
+        qq = q.to(torch.float32).reshape(b, t, kvh, rep, hd).permute(0, 2, 3, 1, 4).reshape(b, kvh, rep * t, hd)
+        scores = torch.matmul(qq.contiguous(), kt[:, :, :, :start + t]) / math.sqrt(hd)
         if t > 1:
             mask = torch.ones((t, start + t), device=self.device, dtype=torch.bool).tril(diagonal=start)
-            scores = scores.masked_fill(~mask, float("-inf"))
+            scores = scores.masked_fill(~mask.repeat(rep, 1), float("-inf"))
         probs = torch.softmax(scores, dim=-1)
-        out = torch.matmul(probs, vv)                                          # [B, H, T, D]
-        return out.transpose(1, 2).reshape(b, t, cfg.num_heads * cfg.head_dim).to(self.dtype)
+        out = torch.matmul(probs, vc[:, :, :start + t])                         # [B, kv, rep*T, D]
+        out = out.reshape(b, kvh, rep, t, hd).permute(0, 3, 1, 2, 4)           # [B, T, kv, rep, D]
+        return out.reshape(b, t, cfg.num_heads * hd).to(self.dtype)
+
+    def _attention_step(self, li: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                        pos: torch.Tensor) -> torch.Tensor:
+        """One decode token at the device position pos [1] (fixed shapes, so it can be captured in a
+        HIP graph): the cache write indexes by pos and the scores span the whole cache, keys past pos
+        masked."""
+        cfg = self.cfg
+        b = q.shape[0]
+        kvh, rep, hd = cfg.num_kv_heads, cfg.num_heads // cfg.num_kv_heads, cfg.head_dim
+        kt, vc = self._cache(li, b)
+        kt.index_copy_(3, pos, k.permute(0, 2, 3, 1).to(torch.float32))
+        vc.index_copy_(2, pos, v.transpose(1, 2).to(torch.float32))
+        qq = q.to(torch.float32).reshape(b, kvh, rep, hd)
+        scores = torch.matmul(qq, kt) / math.sqrt(hd)                          # [B, kv, rep, L_max]
+        scores = scores.masked_fill(self._key_pos > pos, float("-inf"))
+        probs = torch.softmax(scores, dim=-1)
+        out = torch.matmul(probs, vc)                                          # [B, kv, rep, D]
+        return out.reshape(b, 1, cfg.num_heads * hd).to(self.dtype)
 
     # ---- forward -------------------------------------------------------------------------------
 
     def reset(self, batch: int, max_len: int) -> None:
         self._max_len = max_len
         self.kv = [None] * self.cfg.num_layers
+        self._key_pos = torch.arange(max_len, device=self.device)
+        if self.lm_head is None and getattr(self, "_lm_t", None) is None:
+            self._lm_t = self.embed.to(torch.float32).t().contiguous()  # tied LM head, [H, vocab]
 
-    def forward(self, ids: torch.Tensor, start: int) -> torch.Tensor:
-        """ids [B, T] at positions start..start+T-1; returns fp32 logits of the last position [B, vocab]."""
+    def _layers(self, x: torch.Tensor, attend) -> torch.Tensor:
         cfg, be = self.cfg, self.backend
-        b, t = ids.shape
-        x = self.embed[ids]                                                     # [B, T, H]
-        pos = torch.arange(start, start + t, device=self.device)
+        b, t = x.shape[0], x.shape[1]
         for li, L in enumerate(self.layers):
             h2 = x.reshape(b * t, cfg.hidden_size)
             q, k, v = be.norm_linears(h2, L.input_norm, cfg.rms_eps, [L.q, L.k, L.v])
-            q = self._rope(q.reshape(b, t, cfg.num_heads, cfg.head_dim).to(self.dtype), pos)
-            k = self._rope(k.reshape(b, t, cfg.num_kv_heads, cfg.head_dim).to(self.dtype), pos)
-            v = v.reshape(b, t, cfg.num_kv_heads, cfg.head_dim).to(self.dtype)
-            attn = self._attention(li, q, k, v, start).reshape(b * t, -1)
+            attn = attend(li, q.reshape(b, t, cfg.num_heads, cfg.head_dim).to(self.dtype),
+                          k.reshape(b, t, cfg.num_kv_heads, cfg.head_dim).to(self.dtype),
+                          v.reshape(b, t, cfg.num_kv_heads, cfg.head_dim).to(self.dtype)).reshape(b * t, -1)
             (o,) = be.norm_linears(attn, L.attn_sub_norm, cfg.subln_eps, [L.o])
             x = x + o.reshape(b, t, -1).to(self.dtype)
             h2 = x.reshape(b * t, cfg.hidden_size)
             gate, up = be.norm_linears(h2, L.post_attn_norm, cfg.rms_eps, [L.gate, L.up])
             (down,) = be.glu_norm_linears(gate, up, cfg.hidden_act, L.ffn_sub_norm, cfg.subln_eps, [L.down])
             x = x + down.reshape(b, t, -1).to(self.dtype)
-        last = x[:, -1, :]
+        return x
+
+    def _logits(self, last: torch.Tensor) -> torch.Tensor:
+        cfg = self.cfg
         if self.lm_head is not None:
-            (logits,) = be.norm_linears(last.contiguous(), self.final_norm, cfg.rms_eps, [self.lm_head])
+            (logits,) = self.backend.norm_linears(last.contiguous(), self.final_norm, cfg.rms_eps, [self.lm_head])
             return logits.to(torch.float32)
         hn = self._rmsnorm(last, self.final_norm, cfg.rms_eps).to(torch.float32)
-        return torch.matmul(hn, self.embed.to(torch.float32).t().contiguous())
+        return torch.matmul(hn, self._lm_t)
+
+    def forward(self, ids: torch.Tensor, start: int) -> torch.Tensor:
+        """ids [B, T] at positions start..start+T-1; returns fp32 logits of the last position [B, vocab]."""
+        t = ids.shape[1]
+        pos = torch.arange(start, start + t, device=self.device)
+        x = self._layers(self.embed[ids],
+                         lambda li, q, k, v: self._attention(li, self._rope(q, pos), self._rope(k, pos), v, start))
+        return self._logits(x[:, -1, :])
+
+    def decode_step(self, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """One token per sequence, ids [B, 1] at the device position pos [1]; fixed shapes and no host
+        values, so the step can be captured once and replayed.  Returns fp32 logits [B, vocab]."""
+        x = self._layers(self.embed[ids],
+                         lambda li, q, k, v: self._attention_step(li, self._rope(q, pos), self._rope(k, pos), v, pos))
+        return self._logits(x[:, -1, :])
 
     @torch.no_grad()
-    def generate(self, prompt: torch.Tensor, new_tokens: int) -> torch.Tensor:
-        """Greedy decoding: prompt [B, T0] -> generated ids [B, new_tokens]."""
+    def generate(self, prompt: torch.Tensor, new_tokens: int, graph: bool = False) -> torch.Tensor:
+        """Greedy decoding: prompt [B, T0] -> generated ids [B, new_tokens].  The prompt is one
+        forward; every further token is decode_step, run directly or (graph=True) replayed from one
+        HIP graph capture, the next ids, position and output column updated on the device."""
         b, t0 = prompt.shape
         self.reset(b, t0 + new_tokens)
-        logits = self.forward(prompt.to(self.device), 0)
-        out = []
-        nxt = torch.argmax(logits, dim=-1)
-        for i in range(new_tokens):
-            out.append(nxt)
-            if i + 1 == new_tokens:
-                break
-            logits = self.forward(nxt[:, None], t0 + i)
-            nxt = torch.argmax(logits, dim=-1)
-        return torch.stack(out, dim=1)
+        nxt = torch.argmax(self.forward(prompt.to(self.device), 0), dim=-1)
+        out = torch.empty((b, new_tokens), dtype=torch.long, device=self.device)
+        out[:, 0] = nxt
+        ids = nxt[:, None].clone()
+        pos = torch.full((1,), t0, dtype=torch.long, device=self.device)
+        col = torch.ones(1, dtype=torch.long, device=self.device)
+
+        def step():
+            n = torch.argmax(self.decode_step(ids, pos), dim=-1)
+            out.index_copy_(1, col, n[:, None])
+            ids.copy_(n[:, None])
+            pos.add_(1)
+            col.add_(1)
+
+        steps = new_tokens - 1
+        if not graph or steps < 2:
+            for _ in range(steps):
+                step()
+            return out
+        step()  # also the warm-up before capture
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                step()
+        torch.cuda.current_stream().wait_stream(s)
+        for _ in range(steps - 1):
+            g.replay()
+        return out
 
 
 def quantised_linears(model: BitNetDecoder) -> Dict[str, PackedLinear]:
