@@ -177,6 +177,31 @@ int wfb_glu_rmsnorm_quant_i8(const void* gate, const void* up, int x_dtype, int6
                              const void* gamma, int gamma_dtype, float eps, int64_t m, int64_t h,
                              int8_t* q, int64_t k_pad, int64_t ldq, float* a_scale, void* stream);
 
+/* ---- GQA decode attention over a KV cache (one new token per sequence) --------------------- */
+
+/* For each sequence b < batch at position p = pos[b] (device int64 [batch]):
+ *   1. rotary embedding (HF rotate-half form) of the new query heads q[b] and key k_new[b] with
+ *      rope_cos/rope_sin [max_len, head_dim/2] fp32 (row p), each product and sum an fp32 operation,
+ *      the result rounded to dtype; both tables NULL = no rotary embedding (the C engine's form);
+ *   2. k_cache[b, kvh, p, :] = rotated key, v_cache[b, kvh, p, :] = v_new[b, kvh, :]
+ *      (caches [batch, num_kv_heads, max_len, head_dim] of dtype, 16-byte aligned);
+ *   3. out[b, h*D:(h+1)*D] = softmax_j(q_h . K[b, h/G, j] * scale) @ V[b, h/G, j], j = 0..p,
+ *      G = num_heads / num_kv_heads (query head h reads kv head h / G), fp32 math, stored as dtype.
+ * q [batch, num_heads*head_dim] (row stride ldq), k_new/v_new [batch, num_kv_heads*head_dim] (ldk,
+ * ldv), out row stride ldo, all in elements.  dtype WFB_F32 or WFB_BF16 for every buffer;
+ * head_dim 64 or 128; G <= 8.  A position outside [0, max_len) writes NaN to that sequence's output
+ * and leaves the cache untouched (positions live on the device and are not checked on the host).
+ * Replaces attention_forward (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:381-441) with the
+ * cache writes of kv_cache_update_key / kv_cache_update_value
+ * (SGB/sgl-kernel/csrc/inference/kv_cache.h:81-101) and the rotary embedding of the stage-1 HF model
+ * (WF/training/stage1.py:169-214). */
+int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int64_t ldk,
+                             const void* v_new, int64_t ldv, int dtype,
+                             const float* rope_cos, const float* rope_sin,
+                             void* k_cache, void* v_cache, int64_t max_len, const int64_t* pos,
+                             int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                             float scale, void* out, int64_t ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

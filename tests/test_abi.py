@@ -117,3 +117,25 @@ def test_segmented_and_glu_argument_errors(pkg):
     st = pkg._lib.status("wfb_glu_rmsnorm_quant_i8", vp(16), vp(16), 0, 250, 1, None, 0, 1e-6, 1, 250, vp(16), 256,
                          256, vp(16), None)
     assert st == -1 and "multiple of 8" in pkg._lib.last_error()
+
+
+def test_attention_argument_errors(pkg):
+    vp = ctypes.c_void_p
+
+    def st(**kw):
+        a = dict(q=vp(16), ldq=512, k=vp(16), ldk=128, v=vp(16), ldv=128, dtype=1, rc=None, rs=None, kc=vp(16),
+                 vc=vp(16), max_len=64, pos=vp(16), b=1, hq=8, hkv=2, d=64, scale=0.125, out=vp(16), ldo=512)
+        a.update(kw)
+        return pkg._lib.status("wfb_gqa_decode_attention", *a.values(), None)
+
+    assert st(d=96) == -1 and "head_dim" in pkg._lib.last_error()
+    assert st(hq=18, ldq=18 * 64, ldo=18 * 64) == -1 and "num_heads" in pkg._lib.last_error()
+    assert st(hq=6, hkv=4, ldk=256, ldv=256) == -1 and "num_heads" in pkg._lib.last_error()
+    assert st(dtype=2) == -1 and "dtype" in pkg._lib.last_error()
+    assert st(ldq=256) == -1 and "strides" in pkg._lib.last_error()
+    assert st(rc=vp(16)) == -1 and "rope" in pkg._lib.last_error()
+    assert st(max_len=1 << 30) == -1 and "max_len" in pkg._lib.last_error()
+    assert st(kc=vp(8)) == -1 and "aligned" in pkg._lib.last_error()
+    assert st(pos=None) == -1 and "null" in pkg._lib.last_error()
+    assert st(scale=float("inf")) == -1 and "finite" in pkg._lib.last_error()
+    assert st(b=0) == 0

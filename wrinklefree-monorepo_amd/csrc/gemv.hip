@@ -22,17 +22,6 @@ namespace wfb {
 
 namespace {
 
-template <int L>
-__device__ __forceinline__ int group_sum(int v) {
-  if constexpr (L >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
-  if constexpr (L >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
-  if constexpr (L >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
-  if constexpr (L >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false); // row_mirror
-  if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
-  return v;
-}
-
 // Split-K GEMV.  A workgroup owns RB = RP * (64/L) consecutive weight rows and all of K; its S waves
 // split K into S ranges of L*CPL chunks.  In a wave, L lanes share a row: lane s of a row group owns
 // chunks kc0 + s + L*i (i < CPL) and keeps the activations of those chunks in registers for all RP

@@ -64,6 +64,37 @@ __device__ __forceinline__ void load8(const void* p, int64_t i, float (&v)[8]) {
   }
 }
 
+// ---- lane-group reductions ------------------------------------------------------------------
+
+// Sum over aligned groups of L consecutive lanes (L = 2..64, a power of two); every lane of a group
+// ends with the group total.  DPP quad_perm / row_half_mirror / row_mirror below 32 lanes.
+template <int L>
+__device__ __forceinline__ int group_sum(int v) {
+  if constexpr (L >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+  if constexpr (L >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+  if constexpr (L >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  if constexpr (L >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false); // row_mirror
+  if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int L>
+__device__ __forceinline__ float group_sum_f32(float v) {
+  if constexpr (L >= 2) v += dpp_f32<0xB1>(v);
+  if constexpr (L >= 4) v += dpp_f32<0x4E>(v);
+  if constexpr (L >= 8) v += dpp_f32<0x141>(v);
+  if constexpr (L >= 16) v += dpp_f32<0x140>(v);
+  if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 // Round half to even, then saturate to int8 (the vector path of the reference quantiser:
 // _mm256_round_ps(NEAREST_INT) + saturating packs).
 __device__ __forceinline__ int quant_i8(float v, float inv) {
@@ -197,6 +228,10 @@ hipError_t launch_glu_quant_rows(const void* gate, const void* up, int dt, int64
 hipError_t launch_quant_tensor(const void* x, int dt, int64_t numel, int8_t* q, float* a_scale, hipStream_t s);
 hipError_t launch_gemv_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                            const Epilogue& e, hipStream_t s);
+hipError_t launch_gqa_decode(int dt, int d, int g, const void* q, int64_t ldq, const void* kn, int64_t ldk,
+                             const void* vn, int64_t ldv, const float* rc, const float* rs, void* kc, void* vc,
+                             int64_t max_len, const int64_t* pos, int b, int hkv, float scale, void* out, int64_t ldo,
+                             hipStream_t s);
 hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                            const Epilogue& e, hipStream_t s);
 

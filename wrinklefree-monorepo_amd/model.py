@@ -23,8 +23,8 @@ from typing import Dict, List, Optional, Sequence
 
 import torch
 
-from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_segmented, glu_rmsnorm_quantize_i8, pack_ternary_i2s,
-                  rmsnorm_quantize_i8)
+from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_segmented, glu_rmsnorm_quantize_i8, gqa_decode_attention,
+                  pack_ternary_i2s, rmsnorm_quantize_i8)
 
 
 @dataclass(frozen=True)
@@ -147,9 +147,14 @@ class BitNetDecoder:
     """Decoder-only BitNet model with a per-layer KV cache; float glue in ``dtype``."""
 
     def __init__(self, cfg: BitNetConfig, seed: int = 0, device: str = "cuda", dtype: torch.dtype = torch.float32,
-                 backend=None, init_on_device: bool = False):
+                 backend=None, init_on_device: bool = False, decode_attention: str = "hip"):
         """``init_on_device``: draw the random weights with a generator on ``device`` (fast for 8B-scale
-        models) instead of the host generator (the default, reproducible across devices)."""
+        models) instead of the host generator (the default, reproducible across devices).
+        ``decode_attention``: "hip" runs each decode step's rotary embedding, cache append and GQA attention
+        as one libwfbitnet kernel; "torch" runs them as torch ops (prefill always uses torch)."""
+        if decode_attention not in ("hip", "torch"):
+            raise ValueError("decode_attention must be 'hip' or 'torch'")
+        self.decode_attention = decode_attention
         self.cfg = cfg
         self.device = torch.device(device)
         self.dtype = dtype
@@ -187,15 +192,14 @@ class BitNetDecoder:
         return (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps) * w.to(torch.float32)).to(x.dtype)
 
     def _cache(self, li: int, b: int):
-        """Layer li's fp32 KV cache: K transposed [B, kv, D, L_max] (scores = q @ K without a transpose
-        copy), V [B, kv, L_max, D]."""
+        """Layer li's KV cache in the model dtype: K and V [B, kv, L_max, D] (one key = D contiguous
+        elements, the layout of the decode attention kernel)."""
         cache = self.kv[li]
         if cache is None:
             cfg = self.cfg
-            cache = [torch.zeros((b, cfg.num_kv_heads, cfg.head_dim, self._max_len), device=self.device,
-                                 dtype=torch.float32),
-                     torch.zeros((b, cfg.num_kv_heads, self._max_len, cfg.head_dim), device=self.device,
-                                 dtype=torch.float32)]
+            shape = (b, cfg.num_kv_heads, self._max_len, cfg.head_dim)
+            cache = [torch.zeros(shape, device=self.device, dtype=self.dtype),
+                     torch.zeros(shape, device=self.device, dtype=self.dtype)]
             self.kv[li] = cache
         return cache
 
@@ -206,37 +210,50 @@ class BitNetDecoder:
         cfg = self.cfg
         b, t = q.shape[0], q.shape[1]
         kvh, rep, hd = cfg.num_kv_heads, cfg.num_heads // cfg.num_kv_heads, cfg.head_dim
-        kt, vc = self._cache(li, b)
-        kt[:, :, :, start:start + t] = k.permute(0, 2, 3, 1).to(torch.float32)
-        vc[:, :, start:start + t] = v.transpose(1, 2).to(torch.float32)
+        kc, vc = self._cache(li, b)
+        kc[:, :, start:start + t] = k.transpose(1, 2)
+        vc[:, :, start:start + t] = v.transpose(1, 2)
         # head h = g*rep + r reads kv head g (repeat_interleave order)
         qq = q.to(torch.float32).reshape(b, t, kvh, rep, hd).permute(0, 2, 3, 1, 4).reshape(b, kvh, rep * t, hd)
-        scores = torch.matmul(qq.contiguous(), kt[:, :, :, :start + t]) / math.sqrt(hd)
+        kt = kc[:, :, :start + t].to(torch.float32).transpose(2, 3).contiguous()
+        scores = torch.matmul(qq.contiguous(), kt) / math.sqrt(hd)
         if t > 1:
             mask = torch.ones((t, start + t), device=self.device, dtype=torch.bool).tril(diagonal=start)
             scores = scores.masked_fill(~mask.repeat(rep, 1), float("-inf"))
         probs = torch.softmax(scores, dim=-1)
-        out = torch.matmul(probs, vc[:, :, :start + t])                         # [B, kv, rep*T, D]
+        out = torch.matmul(probs, vc[:, :, :start + t].to(torch.float32))      # [B, kv, rep*T, D]
         out = out.reshape(b, kvh, rep, t, hd).permute(0, 3, 1, 2, 4)           # [B, T, kv, rep, D]
         return out.reshape(b, t, cfg.num_heads * hd).to(self.dtype)
 
-    def _attention_step(self, li: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                        pos: torch.Tensor) -> torch.Tensor:
-        """One decode token at the device position pos [1] (fixed shapes, so it can be captured in a
-        HIP graph): the cache write indexes by pos and the scores span the whole cache, keys past pos
-        masked."""
+    def _attention_step_torch(self, li: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              pos: torch.Tensor) -> torch.Tensor:
+        """One decode token per sequence as torch ops, at the device position pos[0] shared by the batch
+        (fixed shapes, so it can be captured in a HIP graph): rotary embedding, the cache write indexed
+        by pos, scores over the whole cache with keys past pos masked.  q/k/v are [B, heads*D] rows."""
         cfg = self.cfg
         b = q.shape[0]
         kvh, rep, hd = cfg.num_kv_heads, cfg.num_heads // cfg.num_kv_heads, cfg.head_dim
-        kt, vc = self._cache(li, b)
-        kt.index_copy_(3, pos, k.permute(0, 2, 3, 1).to(torch.float32))
-        vc.index_copy_(2, pos, v.transpose(1, 2).to(torch.float32))
+        p1 = pos[:1]
+        q = self._rope(q.reshape(b, 1, cfg.num_heads, hd), p1)
+        k = self._rope(k.reshape(b, 1, kvh, hd), p1)
+        kc, vc = self._cache(li, b)
+        kc.index_copy_(2, p1, k.transpose(1, 2))
+        vc.index_copy_(2, p1, v.reshape(b, 1, kvh, hd).transpose(1, 2))
         qq = q.to(torch.float32).reshape(b, kvh, rep, hd)
-        scores = torch.matmul(qq, kt) / math.sqrt(hd)                          # [B, kv, rep, L_max]
-        scores = scores.masked_fill(self._key_pos > pos, float("-inf"))
+        scores = torch.matmul(qq, kc.to(torch.float32).transpose(2, 3).contiguous()) / math.sqrt(hd)
+        scores = scores.masked_fill(self._key_pos > p1, float("-inf"))          # [B, kv, rep, L_max]
         probs = torch.softmax(scores, dim=-1)
-        out = torch.matmul(probs, vc)                                          # [B, kv, rep, D]
-        return out.reshape(b, 1, cfg.num_heads * hd).to(self.dtype)
+        out = torch.matmul(probs, vc.to(torch.float32))                         # [B, kv, rep, D]
+        return out.reshape(b, cfg.num_heads * hd).to(self.dtype)
+
+    def _attention_step_hip(self, li: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                            pos: torch.Tensor) -> torch.Tensor:
+        """One decode token per sequence in one kernel: rotary embedding of q and k, cache append at pos[b],
+        GQA attention over positions 0..pos[b].  q/k/v are [B, heads*D] rows (possibly column slices of
+        one q|k|v output)."""
+        kc, vc = self._cache(li, q.shape[0])
+        return gqa_decode_attention(q, k, v, kc, vc, pos, self._rope_cos, self._rope_sin,
+                                    scale=1.0 / math.sqrt(self.cfg.head_dim))
 
     # ---- forward -------------------------------------------------------------------------------
 
@@ -244,6 +261,9 @@ class BitNetDecoder:
         self._max_len = max_len
         self.kv = [None] * self.cfg.num_layers
         self._key_pos = torch.arange(max_len, device=self.device)
+        # cos/sin of pos * inv_freq for every cache position (the values _rope computes per call)
+        freqs = self._key_pos.to(torch.float32)[:, None] * self.inv_freq[None, :]
+        self._rope_cos, self._rope_sin = freqs.cos().contiguous(), freqs.sin().contiguous()
         if self.lm_head is None and getattr(self, "_lm_t", None) is None:
             self._lm_t = self.embed.to(torch.float32).t().contiguous()  # tied LM head, [H, vocab]
 
@@ -253,9 +273,7 @@ class BitNetDecoder:
         for li, L in enumerate(self.layers):
             h2 = x.reshape(b * t, cfg.hidden_size)
             q, k, v = be.norm_linears(h2, L.input_norm, cfg.rms_eps, [L.q, L.k, L.v])
-            attn = attend(li, q.reshape(b, t, cfg.num_heads, cfg.head_dim).to(self.dtype),
-                          k.reshape(b, t, cfg.num_kv_heads, cfg.head_dim).to(self.dtype),
-                          v.reshape(b, t, cfg.num_kv_heads, cfg.head_dim).to(self.dtype)).reshape(b * t, -1)
+            attn = attend(li, q.to(self.dtype), k.to(self.dtype), v.to(self.dtype)).reshape(b * t, -1)
             (o,) = be.norm_linears(attn, L.attn_sub_norm, cfg.subln_eps, [L.o])
             x = x + o.reshape(b, t, -1).to(self.dtype)
             h2 = x.reshape(b * t, cfg.hidden_size)
@@ -274,17 +292,23 @@ class BitNetDecoder:
 
     def forward(self, ids: torch.Tensor, start: int) -> torch.Tensor:
         """ids [B, T] at positions start..start+T-1; returns fp32 logits of the last position [B, vocab]."""
-        t = ids.shape[1]
+        b, t = ids.shape
+        cfg = self.cfg
         pos = torch.arange(start, start + t, device=self.device)
-        x = self._layers(self.embed[ids],
-                         lambda li, q, k, v: self._attention(li, self._rope(q, pos), self._rope(k, pos), v, start))
+
+        def attend(li, q, k, v):
+            q = self._rope(q.reshape(b, t, cfg.num_heads, cfg.head_dim), pos)
+            k = self._rope(k.reshape(b, t, cfg.num_kv_heads, cfg.head_dim), pos)
+            return self._attention(li, q, k, v.reshape(b, t, cfg.num_kv_heads, cfg.head_dim), start)
+
+        x = self._layers(self.embed[ids], attend)
         return self._logits(x[:, -1, :])
 
     def decode_step(self, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-        """One token per sequence, ids [B, 1] at the device position pos [1]; fixed shapes and no host
-        values, so the step can be captured once and replayed.  Returns fp32 logits [B, vocab]."""
-        x = self._layers(self.embed[ids],
-                         lambda li, q, k, v: self._attention_step(li, self._rope(q, pos), self._rope(k, pos), v, pos))
+        """One token per sequence, ids [B, 1] at the device positions pos int64 [B]; fixed shapes and no
+        host values, so the step can be captured once and replayed.  Returns fp32 logits [B, vocab]."""
+        attend = self._attention_step_hip if self.decode_attention == "hip" else self._attention_step_torch
+        x = self._layers(self.embed[ids], lambda li, q, k, v: attend(li, q, k, v, pos))
         return self._logits(x[:, -1, :])
 
     @torch.no_grad()
@@ -298,7 +322,7 @@ class BitNetDecoder:
         out = torch.empty((b, new_tokens), dtype=torch.long, device=self.device)
         out[:, 0] = nxt
         ids = nxt[:, None].clone()
-        pos = torch.full((1,), t0, dtype=torch.long, device=self.device)
+        pos = torch.full((b,), t0, dtype=torch.long, device=self.device)
         col = torch.ones(1, dtype=torch.long, device=self.device)
 
         def step():

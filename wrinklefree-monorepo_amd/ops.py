@@ -386,6 +386,74 @@ def glu_rmsnorm_quantize_i8(
     return (q if kpa == kp else q[..., :kp]), a_scale
 
 
+# ---- GQA decode attention over a KV cache -------------------------------------------------------
+
+
+def _rows2d(name: str, t: torch.Tensor, b: int, width: int) -> Tuple[torch.Tensor, int]:
+    """View t as [b, width] rows with unit inner stride; returns (view, row stride)."""
+    t2 = t.reshape(b, width) if t.dim() != 2 or t.shape != (b, width) else t
+    if t2.stride(-1) != 1:
+        raise RuntimeError(f"{name}: rows must be contiguous")
+    return t2, (t2.stride(0) if b > 1 else width)
+
+
+def gqa_decode_attention(
+    q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+    pos: torch.Tensor, rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """One decode token per sequence: rotary embedding of q / k_new, append k/v at pos[b] to the caches,
+    attention over positions 0..pos[b].  Returns out [batch, num_heads * head_dim].
+
+    q [batch, num_heads*head_dim] (or [batch, 1, num_heads, head_dim]); k_new / v_new
+    [batch, num_kv_heads*head_dim]; caches [batch, num_kv_heads, max_len, head_dim] (contiguous, same
+    dtype as q: float32 or bfloat16); pos int64 [batch] on the device; rope tables fp32
+    [max_len, head_dim/2] (cos and sin of pos * inv_freq) or None.  2-D inputs may be column slices of
+    one q|k|v projection output (row strides are passed through).  Counterpart of the C engine's
+    attention_forward (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:381-441).
+    """
+    name = "gqa_decode_attention"
+    _require_gpu(name, k_cache, v_cache, pos, rope_cos, rope_sin)
+    dev = k_cache.device
+    for t in (q, k_new, v_new) + ((out,) if out is not None else ()):
+        if t.device != dev:
+            raise RuntimeError(f"{name}: tensors must be on {dev}")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise RuntimeError(f"{name}: caches must be [batch, kv_heads, max_len, head_dim] of one shape")
+    b, hkv, max_len, d = k_cache.shape
+    if q.dtype != k_cache.dtype or k_new.dtype != q.dtype or v_new.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise RuntimeError(f"{name}: q, k_new, v_new and the caches must share one dtype")
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError(f"{name}: dtype must be float32 or bfloat16, got {q.dtype}")
+    if pos.dtype != torch.int64 or pos.numel() != b:
+        raise RuntimeError(f"{name}: pos must be int64 [{b}]")
+    if q.numel() % (b * d) != 0:
+        raise RuntimeError(f"{name}: q has {q.numel()} elements, not a multiple of batch*head_dim")
+    hq = q.numel() // (b * d)
+    q2, ldq = _rows2d(name, q, b, hq * d)
+    k2, ldk = _rows2d(name, k_new, b, hkv * d)
+    v2, ldv = _rows2d(name, v_new, b, hkv * d)
+    if (rope_cos is None) != (rope_sin is None):
+        raise RuntimeError(f"{name}: give both rope tables or neither")
+    if rope_cos is not None:
+        for t in (rope_cos, rope_sin):
+            if t.dtype != torch.float32 or t.shape != (max_len, d // 2):
+                raise RuntimeError(f"{name}: rope tables must be fp32 [{max_len}, {d // 2}]")
+    if out is None:
+        out = torch.empty((b, hq * d), dtype=q.dtype, device=dev)
+    elif out.dtype != q.dtype or out.shape != (b, hq * d) or out.stride(-1) != 1:
+        raise RuntimeError(f"{name}: out must be [{b}, {hq * d}] {q.dtype} with contiguous rows")
+    ldo = out.stride(0) if b > 1 else hq * d
+    sc = 1.0 / float(d) ** 0.5 if scale is None else float(scale)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "wfb_gqa_decode_attention", _p(q2), ldq, _p(k2), ldk, _p(v2), ldv, _DT[q.dtype], _p(rope_cos),
+            _p(rope_sin), _p(k_cache), _p(v_cache), max_len, _p(pos), b, hq, hkv, d, sc, _p(out), ldo,
+            _stream(dev),
+        )
+    return out
+
+
 def bitnet_gemv(packed_weights: torch.Tensor, activations: torch.Tensor, scale: Scale) -> torch.Tensor:
     """fp32 [out] = acc * scale for one int8 token [in] (reference: bitnet.py:73-111)."""
     if activations.dim() != 1:
