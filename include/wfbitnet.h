@@ -177,6 +177,38 @@ int wfb_glu_rmsnorm_quant_i8(const void* gate, const void* up, int x_dtype, int6
                              const void* gamma, int gamma_dtype, float eps, int64_t m, int64_t h,
                              int8_t* q, int64_t k_pad, int64_t ldq, float* a_scale, void* stream);
 
+/* ---- greedy decoding: LM head + argmax ------------------------------------------------------ */
+
+/* uint64 elements of the workspace of the argmax entry points for M tokens and N vocabulary rows
+ * (one slot per 16 rows and token; every call writes all slots it reads, no initialisation needed). */
+#define WFB_ARGMAX_WS(m, n) ((((n) + 15) / 16) * (m))
+
+/* Ternary LM head with the greedy pick fused in: the logits of wfb_linear_i2s (no bias), rounded to
+ * logits_dtype (WFB_F32 or WFB_BF16), are stored to logits [M, N] (row stride ldo) unless logits is
+ * NULL, and token_out[m] (int64, device) = the first index of the maximal logit of token m.
+ * M <= 64; N*K/4 and (M-1)*lda + K below 2^31.  workspace: WFB_ARGMAX_WS(M, N) uint64 of device memory.
+ * Replaces the packed lm_head of the engine (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:544-549;
+ * packed by packages/inference/scripts/convert_to_sglkernel.py:264-286) and its greedy
+ * std::max_element (bitnet_engine.cpp:774-779). */
+int wfb_linear_i2s_argmax(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m,
+                          int64_t lda, const float* a_scale, const float* w_scale_dev, float w_scale,
+                          void* logits, int logits_dtype, int64_t ldo, uint64_t* workspace,
+                          int64_t* token_out, void* stream);
+
+/* Dense LM head (e.g. a tied embedding) with the final RMSNorm and the greedy pick fused in:
+ *   y[m, :] = x[m, :] * (1 / sqrt(sum(x[m, :]^2) / H + eps)) * gamma   (fp32, rounded to x_dtype)
+ *   logits[m, v] = sum_k y[m, k] * weight[v, k]                        (fp32 accumulation)
+ *   token_out[m] = first index of the maximal logits[m, :]
+ * x [M, H] of x_dtype (row stride ldx), gamma [H] or NULL, weight [N, H] of w_dtype (row stride ldw,
+ * a multiple of 8, 16-byte aligned); x_dtype and w_dtype WFB_F32 or WFB_BF16; logits fp32 [M, N]
+ * (row stride ldo) or NULL.  M <= 16, H % 8 == 0, M*H <= 16384, N*ldw*elem_size < 2^31.
+ * Replaces the final rms_norm + fp32_linear + greedy pick of the engine
+ * (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:539-553, 774-779). */
+int wfb_lm_head_argmax(const void* x, int x_dtype, int64_t ldx, const void* gamma, int gamma_dtype,
+                       float eps, const void* weight, int w_dtype, int64_t ldw, int64_t m, int64_t n,
+                       int64_t h, float* logits, int64_t ldo, uint64_t* workspace, int64_t* token_out,
+                       void* stream);
+
 /* ---- GQA decode attention over a KV cache (one new token per sequence) --------------------- */
 
 /* For each sequence b < batch at position p = pos[b] (device int64 [batch]):

@@ -139,3 +139,28 @@ def test_attention_argument_errors(pkg):
     assert st(pos=None) == -1 and "null" in pkg._lib.last_error()
     assert st(scale=float("inf")) == -1 and "finite" in pkg._lib.last_error()
     assert st(b=0) == 0
+
+
+def test_argmax_argument_errors(pkg):
+    vp = ctypes.c_void_p
+    st = pkg._lib.status("wfb_linear_i2s_argmax", vp(16), 64, 128, vp(16), 65, 128, None, None, 1.0, None, 0, 64,
+                         vp(16), vp(16), None)
+    assert st == -1 and "M (65)" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_linear_i2s_argmax", vp(16), 64, 128, vp(16), 2, 128, None, None, 1.0, None, 2, 64,
+                         vp(16), vp(16), None)
+    assert st == -1 and "logits dtype" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_linear_i2s_argmax", vp(16), 64, 128, vp(16), 2, 128, None, None, 1.0, None, 0, 64,
+                         None, vp(16), None)
+    assert st == -1 and "workspace" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_lm_head_argmax", vp(16), 0, 64, None, 0, 1e-5, vp(16), 0, 64, 17, 100, 64, None, 100,
+                         vp(16), vp(16), None)
+    assert st == -1 and "M (17)" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_lm_head_argmax", vp(16), 0, 4096, None, 0, 1e-5, vp(16), 0, 4096, 8, 100, 4096, None,
+                         100, vp(16), vp(16), None)
+    assert st == -1 and "M*H" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_lm_head_argmax", vp(16), 0, 60, None, 0, 1e-5, vp(16), 0, 60, 1, 100, 60, None, 100,
+                         vp(16), vp(16), None)
+    assert st == -1 and "multiple of 8" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_lm_head_argmax", vp(16), 0, 64, None, 0, 1e-5, vp(8), 0, 64, 1, 100, 64, None, 100,
+                         vp(16), vp(16), None)
+    assert st == -1 and "aligned" in pkg._lib.last_error()

@@ -38,6 +38,10 @@ class OracleBackend:
             outs.append(torch.from_numpy(orc.rescale(acc, ws, s)).to(self.dev))
         return outs
 
+    def norm_linear_argmax(self, x, norm_weight, eps, linear):
+        (logits,) = self.norm_linears(x, norm_weight, eps, [linear])
+        return torch.argmax(logits, dim=-1)  # first maximum, like the fused kernel
+
     def glu_norm_linears(self, gate, up, act, norm_weight, eps, linears):
         g = None if norm_weight is None else norm_weight.float().cpu().numpy()
         code = orc.ACT_SILU if act == "silu" else orc.ACT_RELU2
@@ -95,6 +99,28 @@ def test_relu2_model_fused_matches_oracle(pkg, dev):
     assert len(hip.acc_log) == len(ref.acc_log)
     for a, b in zip(hip.acc_log, ref.acc_log):
         assert np.array_equal(a.cpu().numpy().astype(np.int64), b)
+
+
+def test_ternary_lm_head_model_matches_oracle(pkg, dev):
+    """An untied ternary LM head (the configs[4] form): greedy tokens from the fused linear+argmax kernel
+    equal the oracle's argmax over exact logits, batch 3, 20 decode steps; every accumulator equal."""
+    M = pkg.model
+    cfg = M.BitNetConfig(vocab_size=3000, hidden_size=256, intermediate_size=512, num_layers=2, num_heads=4,
+                         num_kv_heads=1, head_dim=64, rope_theta=500000.0, tie_embeddings=False, ternary_lm_head=True)
+    model = M.BitNetDecoder(cfg, seed=9, device=dev)
+    model.backend_linears = list(M.quantised_linears(model).values())
+    prompt = torch.randint(0, cfg.vocab_size, (3, 6), generator=torch.Generator().manual_seed(10))
+    hip = M.HipBackend(out_dtype=torch.float32, keep_acc=True, fused=True)
+    model.backend = hip
+    toks_hip = model.generate(prompt, 20).cpu()
+    ref = OracleBackend(model, dev)
+    model.backend = ref
+    toks_ref = model.generate(prompt, 20).cpu()
+    assert torch.equal(toks_hip, toks_ref)
+    assert len(hip.acc_log) == len(ref.acc_log)
+    for a, b in zip(hip.acc_log, ref.acc_log):
+        assert np.array_equal(a.cpu().numpy().astype(np.int64), b)
+    assert len(set(toks_hip.flatten().tolist())) > 4
 
 
 def test_decode_graph_replays_match_eager(pkg, dev):

@@ -12,10 +12,12 @@ from .ops import (
     bitnet_gemm,
     bitnet_gemv,
     bitnet_linear,
+    bitnet_linear_argmax,
     bitnet_linear_segmented,
     check_kernel_available,
     glu_rmsnorm_quantize_i8,
     gqa_decode_attention,
+    lm_head_argmax,
     pack_ternary_i2s,
     quantize_activations_i8,
     quantize_activations_i8_per_token,
@@ -34,8 +36,8 @@ from .bitlinear import (
 
 __all__ = [
     "LIB_PATH", "library_available", "QK_I2_S", "absmean_scale", "bitnet_gemm", "bitnet_gemv", "bitnet_linear",
-    "bitnet_linear_segmented", "check_kernel_available", "glu_rmsnorm_quantize_i8", "gqa_decode_attention",
-    "pack_ternary_i2s",
+    "bitnet_linear_argmax", "bitnet_linear_segmented", "check_kernel_available", "glu_rmsnorm_quantize_i8", "gqa_decode_attention",
+    "lm_head_argmax", "pack_ternary_i2s",
     "quantize_activations_i8", "quantize_activations_i8_per_token", "rmsnorm_quantize_i8", "unpack_i2s",
     "BitLinear", "BitNetLinearMethod", "BitNetLinearNative", "SubLNBitLinear", "convert_linear_to_bitlinear",
     "patch_model_with_native_kernels", "model",

@@ -44,6 +44,9 @@ SIGNATURES = {
     "wfb_linear_i2s_segmented": [_vp, _i64, _i64, _int, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _int, _vp, _int, _i64,
                                  _vp, _vp],
     "wfb_glu_rmsnorm_quant_i8": [_vp, _vp, _int, _i64, _int, _vp, _int, _f32, _i64, _i64, _vp, _i64, _i64, _vp, _vp],
+    "wfb_linear_i2s_argmax": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _int, _i64, _vp, _vp, _vp],
+    "wfb_lm_head_argmax": [_vp, _int, _i64, _vp, _int, _f32, _vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp,
+                           _vp],
     "wfb_gqa_decode_attention": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
                                  _i64, _i64, _f32, _vp, _i64, _vp],
 }

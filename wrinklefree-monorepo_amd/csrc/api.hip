@@ -51,7 +51,8 @@ bool use_gemv(int64_t m, int64_t n, int64_t k, int64_t lda) {
 int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act,
                 int64_t m, int64_t lda, const float* a_scale, const float* w_scale_dev, float w_scale,
                 const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo, int32_t* acc_out,
-                void* stream, int n_seg = 1, const int64_t* seg_rows = nullptr) {
+                void* stream, int n_seg = 1, const int64_t* seg_rows = nullptr, uint64_t* amax = nullptr,
+                int amax_dt = WFB_F32, int64_t* tokens = nullptr) {
   if (n <= 0 || k <= 0 || m < 0) return fail(WFB_EINVAL, "%s: bad sizes m=%lld n=%lld k=%lld", name, (long long)m, (long long)n, (long long)k);
   if (k % WFB_QK_I2S != 0)
     return fail(WFB_EINVAL, "%s: K (%lld) must be multiple of %d", name, (long long)k, WFB_QK_I2S);
@@ -59,7 +60,7 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
     return fail(WFB_EINVAL, "%s: sizes too large m=%lld n=%lld k=%lld", name, (long long)m, (long long)n, (long long)k);
   if (m == 0) return ok();
   if (!qweight || !act) return fail(WFB_EINVAL, "%s: null qweight or activations", name);
-  if (!out && !acc_out) return fail(WFB_EINVAL, "%s: out and acc_out are both null", name);
+  if (!out && !acc_out && !amax) return fail(WFB_EINVAL, "%s: out and acc_out are both null", name);
   if (!aligned(qweight, 16) || !aligned(act, 16))
     return fail(WFB_EINVAL, "%s: qweight and activations must be 16-byte aligned", name);
   if (lda < k || lda % 16 != 0)
@@ -88,8 +89,16 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
   e.out_dtype = out_dtype;
   e.ldo = ldo;
   e.acc_out = acc_out;
+  e.amax = amax;
+  e.amax_dt = amax_dt;
 
   const bool gemv = kind == Kernel::Gemv || (kind == Kernel::Auto && use_gemv(m, n, k, lda));
+  if (amax) {  // greedy argmax: GEMV (M <= 2) or the skinny MFMA kernel, then the cross-workgroup maximum
+    hipError_t st = gemv ? wfb::launch_gemv_i2s(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream))
+                         : wfb::launch_gemm_i2s_skinny(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream));
+    if (st == hipSuccess) st = wfb::launch_argmax_finalize(amax, (n + 15) / 16, m, tokens, as_stream(stream));
+    return hip_status(st, name);
+  }
   hipError_t st = gemv ? wfb::launch_gemv_i2s(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream))
                        : wfb::launch_gemm_i2s(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream));
   return hip_status(st, name);
@@ -229,6 +238,47 @@ int wfb_glu_rmsnorm_quant_i8(const void* gate, const void* up, int x_dtype, int6
   return hip_status(wfb::launch_glu_quant_rows(gate, up, x_dtype, ldx, act, gamma, gamma_dtype, eps, m, h, q, k_pad,
                                                ldq, a_scale, as_stream(stream)),
                     name);
+}
+
+int wfb_linear_i2s_argmax(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m, int64_t lda,
+                          const float* a_scale, const float* w_scale_dev, float w_scale, void* logits,
+                          int logits_dtype, int64_t ldo, uint64_t* workspace, int64_t* token_out, void* stream) {
+  const char* name = "wfb_linear_i2s_argmax";
+  if (logits_dtype != WFB_F32 && logits_dtype != WFB_BF16)
+    return fail(WFB_EINVAL, "%s: logits dtype must be WFB_F32 or WFB_BF16", name);
+  if (m > 64) return fail(WFB_EINVAL, "%s: M (%lld) must be <= 64", name, (long long)m);
+  if (m > 0 && (!workspace || !token_out)) return fail(WFB_EINVAL, "%s: null workspace or token_out", name);
+  if (n > 0 && k > 0 && m > 0 && (n * (k / 4) > INT32_MAX || (m - 1) * lda + k > INT32_MAX))
+    return fail(WFB_EINVAL, "%s: N*K/4 and (M-1)*lda + K must stay below 2^31", name);
+  if (ldo < n) return fail(WFB_EINVAL, "%s: logits row stride (%lld) < N (%lld)", name, (long long)ldo, (long long)n);
+  return linear_impl(Kernel::Auto, name, qweight, n, k, act, m, lda, a_scale, w_scale_dev, w_scale, nullptr, 0,
+                     logits, logits_dtype, ldo, nullptr, stream, 1, nullptr, workspace, logits_dtype, token_out);
+}
+
+int wfb_lm_head_argmax(const void* x, int x_dtype, int64_t ldx, const void* gamma, int gamma_dtype, float eps,
+                       const void* weight, int w_dtype, int64_t ldw, int64_t m, int64_t n, int64_t h, float* logits,
+                       int64_t ldo, uint64_t* workspace, int64_t* token_out, void* stream) {
+  const char* name = "wfb_lm_head_argmax";
+  if ((x_dtype != WFB_F32 && x_dtype != WFB_BF16) || (w_dtype != WFB_F32 && w_dtype != WFB_BF16) ||
+      (gamma && !valid_dtype(gamma_dtype)))
+    return fail(WFB_EINVAL, "%s: x and weight must be WFB_F32 or WFB_BF16", name);
+  if (m < 0 || m > 16) return fail(WFB_EINVAL, "%s: M (%lld) must be in 0..16", name, (long long)m);
+  if (n <= 0 || n > INT32_MAX / 2 || h <= 0 || h % 8 != 0)
+    return fail(WFB_EINVAL, "%s: need N > 0 and H a positive multiple of 8 (N=%lld H=%lld)", name, (long long)n,
+                (long long)h);
+  if (m * h > 16384) return fail(WFB_EINVAL, "%s: M*H (%lld) must be <= 16384", name, (long long)(m * h));
+  const int64_t wsz = w_dtype == WFB_F32 ? 4 : 2;
+  if (ldx < h || ldw < h || (logits && ldo < n) || ldw % 8 != 0)
+    return fail(WFB_EINVAL, "%s: strides must satisfy ldx >= H, ldw >= H (multiple of 8), ldo >= N", name);
+  if (n * ldw * wsz > INT32_MAX) return fail(WFB_EINVAL, "%s: weight larger than 2^31 bytes", name);
+  if (!(eps >= 0.0f)) return fail(WFB_EINVAL, "%s: eps must be >= 0", name);
+  if (m == 0) return ok();
+  if (!x || !weight || !workspace || !token_out) return fail(WFB_EINVAL, "%s: null pointer", name);
+  if (!aligned(weight, 16)) return fail(WFB_EINVAL, "%s: weight must be 16-byte aligned", name);
+  hipError_t st = wfb::launch_lm_head_argmax(x, x_dtype, ldx, gamma, gamma_dtype, eps, weight, w_dtype, ldw, m, n, h,
+                                             logits, ldo, workspace, as_stream(stream));
+  if (st == hipSuccess) st = wfb::launch_argmax_finalize(workspace, (n + 15) / 16, m, token_out, as_stream(stream));
+  return hip_status(st, name);
 }
 
 int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int64_t ldk, const void* v_new,

@@ -1,0 +1,177 @@
+// Greedy decoding on the device: the LM head with the next-token argmax fused in.
+//
+// Replaces the engine's final steps (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:539-553: final
+// rms_norm, then the LM head as a packed BitLinear or an fp32 linear over the vocabulary) and its greedy
+// pick (bitnet_engine.cpp:774-779, std::max_element: the first maximal logit).
+//
+// Every producer writes, per 16 vocabulary rows and token, the largest 64-bit key of
+// (logit, row) (amax_key: orderable float bits above the inverted row index, so ties go to the smaller
+// row) into a workspace of ceil(N/16) x M slots; argmax_finalize_kernel reduces the slots of each
+// token and writes the row index.  No atomics, so the result does not depend on workgroup order, and
+// no workspace initialisation is needed (every slot is written).
+//
+// lm_head_kernel is the dense head (tied bf16/fp32 embedding): each workgroup recomputes the final
+// RMSNorm of the M token rows (y = x * (1/sqrt(mean(x^2) + eps)) * gamma, rounded to the x dtype as the
+// torch glue does) into LDS, then streams 64 vocabulary rows: 8 lanes per row, each lane a 16-byte
+// (bf16) or 32-byte (fp32) piece of the row per step against the normalised rows in LDS, fp32
+// accumulation, a DPP sum over the 8 lanes; each wave covers 16 rows = one workspace slot.
+#include "wfb_common.h"
+
+namespace wfb {
+
+namespace {
+
+__device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
+  if (dt == WFB_F32) return load_elem<WFB_F32>(p, i);
+  if (dt == WFB_BF16) return load_elem<WFB_BF16>(p, i);
+  return load_elem<WFB_F16>(p, i);
+}
+
+__global__ __launch_bounds__(256) void argmax_finalize_kernel(const uint64_t* __restrict__ parts, int64_t np, int m,
+                                                              int64_t* __restrict__ tokens) {
+  __shared__ uint64_t sb[4];
+  const int mm = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  uint64_t best = 0;
+  for (int64_t p = t; p < np; p += 256) {
+    const uint64_t v = parts[p * m + mm];
+    best = v > best ? v : best;
+  }
+  best = group_max_u64<64>(best);
+  if (lane == 0) sb[w] = best;
+  __syncthreads();
+  if (t == 0) {
+    uint64_t b = sb[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) b = sb[i] > b ? sb[i] : b;
+    tokens[mm] = b ? (int64_t)(0xFFFFFFFFu - (uint32_t)b) : -1;
+  }
+}
+
+template <int XT, int WT, int MM>
+__global__ __launch_bounds__(256) void lm_head_kernel(const void* __restrict__ x, int64_t ldx,
+                                                      const void* __restrict__ gamma, int gdt, float eps,
+                                                      const void* __restrict__ W, int64_t ldw, int m, int n, int h,
+                                                      float* __restrict__ logits, int64_t ldo,
+                                                      uint64_t* __restrict__ parts) {
+  extern __shared__ float xn[];  // [m][h]
+  __shared__ float rs[16];
+  constexpr int ESZ = WT == WFB_F32 ? 4 : 2;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+
+  for (int mm = w; mm < m; mm += 4) {
+    float ss = 0.0f;
+    for (int k = lane; k < h; k += 64) {
+      const float v = load_elem<XT>(x, (int64_t)mm * ldx + k);
+      ss += v * v;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) rs[mm] = 1.0f / sqrtf(ss / (float)h + eps);
+  }
+  __syncthreads();
+  for (int i = t; i < m * h; i += 256) {
+    const int mm = i / h, k = i - mm * h;
+    float v = load_elem<XT>(x, (int64_t)mm * ldx + k) * rs[mm];
+    if (gamma) v = v * load_any(gamma, gdt, k);
+    if constexpr (XT == WFB_BF16) v = bf16_bits_to_f32(f32_to_bf16_rne(v));
+    xn[i] = v;
+  }
+  __syncthreads();
+
+  const int s = lane & 7, rsub = lane >> 3, C = h >> 3;
+  const buf_t wb = make_buf(W, (uint32_t)((int64_t)n * ldw * ESZ));
+  uint64_t best[MM];
+#pragma unroll
+  for (int mm = 0; mm < MM; ++mm) best[mm] = 0;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int row = blockIdx.x * 64 + w * 16 + p * 8 + rsub;
+    const uint32_t roff = (uint32_t)((int64_t)row * ldw * ESZ);
+    float acc[MM];
+#pragma unroll
+    for (int mm = 0; mm < MM; ++mm) acc[mm] = 0.0f;
+#pragma unroll 4
+    for (int c = s; c < C; c += 8) {
+      float wv[8];
+      const v4i r0 = buf_load16(wb, roff + (uint32_t)(8 * c * ESZ));
+      if constexpr (WT == WFB_F32) {
+        const v4i r1 = buf_load16(wb, roff + (uint32_t)(8 * c * ESZ) + 16);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          wv[e] = __int_as_float(r0[e]);
+          wv[4 + e] = __int_as_float(r1[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          wv[2 * e] = __uint_as_float((uint32_t)r0[e] << 16);
+          wv[2 * e + 1] = __uint_as_float((uint32_t)r0[e] & 0xffff0000u);
+        }
+      }
+#pragma unroll
+      for (int mm = 0; mm < MM; ++mm) {
+        if (mm < m) {
+          const float4* xp = reinterpret_cast<const float4*>(xn + mm * h + 8 * c);
+          const float4 a = xp[0], b = xp[1];
+          acc[mm] += wv[0] * a.x + wv[1] * a.y + wv[2] * a.z + wv[3] * a.w + wv[4] * b.x + wv[5] * b.y +
+                     wv[6] * b.z + wv[7] * b.w;
+        }
+      }
+    }
+    const bool valid = row < n && s == 0;
+#pragma unroll
+    for (int mm = 0; mm < MM; ++mm) {
+      if (mm < m) {
+        const float y = group_sum_f32<8>(acc[mm]);
+        if (valid && logits) logits[(int64_t)mm * ldo + row] = y;
+        const uint64_t key = group_max_u64<64>(valid ? amax_key(y, row) : 0);
+        best[mm] = key > best[mm] ? key : best[mm];
+      }
+    }
+  }
+  const int slot = blockIdx.x * 4 + w;
+  if (lane == 0 && slot < (n + 15) / 16) {
+#pragma unroll
+    for (int mm = 0; mm < MM; ++mm)
+      if (mm < m) parts[(int64_t)slot * m + mm] = best[mm];
+  }
+}
+
+template <int XT, int WT>
+hipError_t launch_head_t(const void* x, int64_t ldx, const void* gamma, int gdt, float eps, const void* w, int64_t ldw,
+                         int m, int n, int h, float* logits, int64_t ldo, uint64_t* parts, hipStream_t s) {
+  const dim3 grid((n + 63) / 64);
+  const size_t lds = (size_t)m * h * sizeof(float);
+#define WFB_HEAD(MMV) \
+  hipLaunchKernelGGL((lm_head_kernel<XT, WT, MMV>), grid, dim3(256), lds, s, x, ldx, gamma, gdt, eps, w, ldw, m, n, h, \
+                     logits, ldo, parts)
+  if (m <= 1) WFB_HEAD(1);
+  else if (m <= 2) WFB_HEAD(2);
+  else if (m <= 4) WFB_HEAD(4);
+  else if (m <= 8) WFB_HEAD(8);
+  else WFB_HEAD(16);
+#undef WFB_HEAD
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_argmax_finalize(const uint64_t* parts, int64_t n_parts, int64_t m, int64_t* tokens, hipStream_t s) {
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)m), dim3(256), 0, s, parts, n_parts, (int)m, tokens);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_head_argmax(const void* x, int xdt, int64_t ldx, const void* gamma, int gdt, float eps,
+                                 const void* w, int wdt, int64_t ldw, int64_t m, int64_t n, int64_t h, float* logits,
+                                 int64_t ldo, uint64_t* parts, hipStream_t s) {
+  if (xdt == WFB_F32 && wdt == WFB_F32)
+    return launch_head_t<WFB_F32, WFB_F32>(x, ldx, gamma, gdt, eps, w, ldw, (int)m, (int)n, (int)h, logits, ldo, parts, s);
+  if (xdt == WFB_F32 && wdt == WFB_BF16)
+    return launch_head_t<WFB_F32, WFB_BF16>(x, ldx, gamma, gdt, eps, w, ldw, (int)m, (int)n, (int)h, logits, ldo, parts, s);
+  if (xdt == WFB_BF16 && wdt == WFB_F32)
+    return launch_head_t<WFB_BF16, WFB_F32>(x, ldx, gamma, gdt, eps, w, ldw, (int)m, (int)n, (int)h, logits, ldo, parts, s);
+  return launch_head_t<WFB_BF16, WFB_BF16>(x, ldx, gamma, gdt, eps, w, ldw, (int)m, (int)n, (int)h, logits, ldo, parts, s);
+}
+
+}  // namespace wfb

@@ -168,7 +168,26 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
     }
   }
   __syncthreads();
-  if (w != 0 || n >= N) return;
+  if (w != 0) return;
+  if (ep.amax) {  // argmax epilogue: max over the 16 rows (lanes 16g .. 16g + 15) of each token
+    const float ws = n < N ? epi_wscale(ep, n) : 0.0f;
+    const float bias = n < N ? epi_bias(ep, n) : 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tok = mt * 16 + 4 * g + j;
+        int tot = red[0][mt][j][lane];
+#pragma unroll
+        for (int k = 1; k < S; ++k) tot += red[k][mt][j][lane];
+        const bool valid = tok < M && n < N;
+        const uint64_t key = group_max_u64<16>(epi_store_key(ep, ws, valid ? epi_ascale(ep, tok) : 0.0f, bias, tok, n,
+                                                             tot, valid));
+        if (nl == 0 && tok < M) ep.amax[(int64_t)blockIdx.x * M + tok] = key;
+      }
+    return;
+  }
+  if (n >= N) return;
   const float ws = epi_wscale(ep, n);
   const float bias = epi_bias(ep, n);
 #pragma unroll
@@ -484,6 +503,15 @@ hipError_t launch_mt(const uint8_t* W, int n, int C, const int8_t* A, int m, int
 }
 
 }  // namespace
+
+hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
+                                  const Epilogue& e, hipStream_t s) {
+  const int C = k / 64;
+  if (m <= 16) return launch_skinny<1>(W, n, C, A, m, lda, e, s);
+  if (m <= 32) return launch_skinny<2>(W, n, C, A, m, lda, e, s);
+  if (m <= 64) return launch_skinny<4>(W, n, C, A, m, lda, e, s);
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, const Epilogue& e,
                            hipStream_t s) {

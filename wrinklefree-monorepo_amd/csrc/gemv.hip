@@ -134,8 +134,28 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   }
   __syncthreads();
   const int t = threadIdx.x;
-  if (t >= RB) return;
   const int n = row0 + t;
+  if (ep.amax) {  // argmax epilogue: the RB <= 64 rows sit in wave 0
+    if (t >= 64) return;
+    const bool valid = t < RB && n < N;
+    const float ws = valid ? epi_wscale(ep, n) : 0.0f;
+    const float bias = valid ? epi_bias(ep, n) : 0.0f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      int tot = 0;
+      if (valid) {
+        tot = red[0][m][t];
+#pragma unroll
+        for (int k = 1; k < S; ++k) tot += red[k][m][t];
+      }
+      const uint64_t key = group_max_u64<64>(epi_store_key(ep, ws, epi_ascale(ep, m), bias, m, n, tot, valid));
+      // slots are per 16 rows: the workgroup's first slot takes its maximum, the others key 0
+      const int slot = row0 / 16 + t;
+      if (t < RB / 16 && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + m] = t == 0 ? key : 0;
+    }
+    return;
+  }
+  if (t >= RB) return;
   if (n >= N) return;
   const float ws = epi_wscale(ep, n);
   const float bias = epi_bias(ep, n);

@@ -133,7 +133,37 @@ struct Epilogue {
   // ws_dev[s]; segment s ends at row seg_end[s] (s < nseg - 1).  nseg = 1: one per-tensor scale.
   int nseg;
   int seg_end[WFB_MAX_SEGMENTS - 1];
+  // Greedy-argmax epilogue (GEMV and skinny kernels only): when set, workgroup b writes, for each
+  // token m, the largest argmax key of its rows to amax[b * M + m] (see amax_key); the value compared
+  // is y rounded to amax_dt (WFB_F32 or WFB_BF16), i.e. the logit as stored.
+  uint64_t* amax;
+  int amax_dt;
 };
+
+// Orderable 64-bit key of (value y, row n): larger y wins, and among equal values the smaller row
+// (the first maximum, as std::max_element and torch.argmax pick).  Never 0 for n < 2^32 - 1.
+__device__ __forceinline__ uint64_t amax_key(float y, int n) {
+  const uint32_t u = __float_as_uint(y);
+  const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)k << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)n);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// max over aligned groups of L lanes (xor butterfly); every lane of a group ends with the maximum
+template <int L>
+__device__ __forceinline__ uint64_t group_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 1; o < L; o <<= 1) {
+    const uint64_t x = shfl_xor_u64(v, o);
+    v = x > v ? x : v;
+  }
+  return v;
+}
 
 // Weight scale of output column n (segment lookup without branches).
 __device__ __forceinline__ float epi_wscale(const Epilogue& e, int n) {
@@ -154,15 +184,30 @@ __device__ __forceinline__ float epi_bias(const Epilogue& e, int n) {
 // y = ((float)acc * ws) * as (+ bias): the two products in this order, each rounded to fp32
 // (SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:846 then SGB/python/sglang/srt/layers/quantization/bitnet.py:241).
 // ws, as and bias are loaded by the caller (ahead of the main loop, to keep them off the critical path).
+__device__ __forceinline__ float epi_y(const Epilogue& e, float ws, float as, float bias, int32_t acc) {
+  float y = __fmul_rn(__fmul_rn((float)acc, ws), as);
+  if (e.bias) y = __fadd_rn(y, bias);
+  return y;
+}
+
 __device__ __forceinline__ void epi_store(const Epilogue& e, float ws, float as, float bias, int m, int n,
                                           int32_t acc) {
   const int64_t off = (int64_t)m * e.ldo + n;
   if (e.acc_out) e.acc_out[off] = acc;
   if (!e.out) return;
-  float y = __fmul_rn(__fmul_rn((float)acc, ws), as);
-  if (e.bias) y = __fadd_rn(y, bias);
+  const float y = epi_y(e, ws, as, bias, acc);
   if (e.out_dtype == WFB_F32) reinterpret_cast<float*>(e.out)[off] = y;
   else reinterpret_cast<uint16_t*>(e.out)[off] = f32_to_bf16_rne(y);
+}
+
+// Argmax key of output (m, n) (store included); 0 when (m, n) is out of range.
+__device__ __forceinline__ uint64_t epi_store_key(const Epilogue& e, float ws, float as, float bias, int m, int n,
+                                                  int32_t acc, bool valid) {
+  if (!valid) return 0;
+  epi_store(e, ws, as, bias, m, n, acc);
+  float y = epi_y(e, ws, as, bias, acc);
+  if (e.amax_dt == WFB_BF16) y = bf16_bits_to_f32(f32_to_bf16_rne(y));
+  return amax_key(y, n);
 }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -232,6 +277,14 @@ hipError_t launch_gqa_decode(int dt, int d, int g, const void* q, int64_t ldq, c
                              const void* vn, int64_t ldv, const float* rc, const float* rs, void* kc, void* vc,
                              int64_t max_len, const int64_t* pos, int b, int hkv, float scale, void* out, int64_t ldo,
                              hipStream_t s);
+hipError_t launch_argmax_finalize(const uint64_t* parts, int64_t n_parts, int64_t m, int64_t* tokens, hipStream_t s);
+hipError_t launch_lm_head_argmax(const void* x, int xdt, int64_t ldx, const void* gamma, int gdt, float eps,
+                                 const void* w, int wdt, int64_t ldw, int64_t m, int64_t n, int64_t h, float* logits,
+                                 int64_t ldo, uint64_t* parts, hipStream_t s);
+// 3 <= M <= 64 through the split-K skinny kernel (grid = ceil(N / 16) workgroups of 16 rows); needs
+// N*K/4 and (M-1)*lda + K below 2^31
+hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
+                                  const Epilogue& e, hipStream_t s);
 hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                            const Epilogue& e, hipStream_t s);
 

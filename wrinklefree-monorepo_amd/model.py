@@ -11,8 +11,11 @@ group, so the norm before q/k/v (and before gate/up) is fused with the activatio
 shared by the projections that read it, and one call for the MLP middle (act(gate) * up -> SubLN ->
 quantise -> down).  ``HipBackend`` runs libwfbitnet -- with ``fused=True`` the projections of a group
 run as one segmented launch (q|k|v, gate|up) and the gated activation, SubLN and quantiser as one
-kernel; a test can substitute another backend with the same two methods to compare the quantised
-path while the float code (embedding, RoPE, attention, residuals, LM head) stays identical.
+kernel; a ternary LM head runs its argmax fused in (``norm_linear_argmax``).  A test can substitute
+another backend with the same three methods to compare the quantised path while the float code stays
+identical: embedding, residuals, the prefill attention (torch), the decode-step rotary embedding +
+cache append + GQA attention (one libwfbitnet kernel, or torch ops with ``decode_attention="torch"``)
+and the tied LM head with its final norm and greedy argmax (one libwfbitnet kernel).
 """
 
 from __future__ import annotations
@@ -23,8 +26,8 @@ from typing import Dict, List, Optional, Sequence
 
 import torch
 
-from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_segmented, glu_rmsnorm_quantize_i8, gqa_decode_attention,
-                  pack_ternary_i2s, rmsnorm_quantize_i8)
+from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_segmented, glu_rmsnorm_quantize_i8,
+                  gqa_decode_attention, lm_head_argmax, pack_ternary_i2s, rmsnorm_quantize_i8)
 
 
 @dataclass(frozen=True)
@@ -116,6 +119,15 @@ class HipBackend:
                      linears: Sequence[PackedLinear]) -> List[torch.Tensor]:
         q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=linears[0].k_pad)
         return self._linears(q, a_scale, linears)
+
+    def norm_linear_argmax(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], eps: float,
+                           linear: PackedLinear) -> torch.Tensor:
+        """Greedy next tokens int64 [M] of a ternary LM head: norm + quantise, then the linear with the argmax
+        fused in (logits compared as rounded to out_dtype, never stored)."""
+        q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=linear.k_pad)
+        if self.keep_acc:
+            self._linears(q, a_scale, [linear])
+        return bitnet_linear_argmax(linear.qweight, q, linear.scale, a_scale=a_scale, logits_dtype=self.out_dtype)
 
     def glu_norm_linears(self, gate: torch.Tensor, up: torch.Tensor, act: str, norm_weight: Optional[torch.Tensor],
                          eps: float, linears: Sequence[PackedLinear]) -> List[torch.Tensor]:
@@ -264,8 +276,6 @@ class BitNetDecoder:
         # cos/sin of pos * inv_freq for every cache position (the values _rope computes per call)
         freqs = self._key_pos.to(torch.float32)[:, None] * self.inv_freq[None, :]
         self._rope_cos, self._rope_sin = freqs.cos().contiguous(), freqs.sin().contiguous()
-        if self.lm_head is None and getattr(self, "_lm_t", None) is None:
-            self._lm_t = self.embed.to(torch.float32).t().contiguous()  # tied LM head, [H, vocab]
 
     def _layers(self, x: torch.Tensor, attend) -> torch.Tensor:
         cfg, be = self.cfg, self.backend
@@ -287,11 +297,22 @@ class BitNetDecoder:
         if self.lm_head is not None:
             (logits,) = self.backend.norm_linears(last.contiguous(), self.final_norm, cfg.rms_eps, [self.lm_head])
             return logits.to(torch.float32)
+        if getattr(self, "_lm_t", None) is None:
+            self._lm_t = self.embed.to(torch.float32).t().contiguous()  # tied LM head, [H, vocab]
         hn = self._rmsnorm(last, self.final_norm, cfg.rms_eps).to(torch.float32)
         return torch.matmul(hn, self._lm_t)
 
-    def forward(self, ids: torch.Tensor, start: int) -> torch.Tensor:
-        """ids [B, T] at positions start..start+T-1; returns fp32 logits of the last position [B, vocab]."""
+    def _next_tokens(self, last: torch.Tensor) -> torch.Tensor:
+        """Greedy next token ids int64 [B] from the last hidden states [B, H]: the final norm, LM head and
+        argmax on the device (ternary head through the backend, tied head through lm_head_argmax)."""
+        cfg = self.cfg
+        if self.lm_head is not None:
+            return self.backend.norm_linear_argmax(last.contiguous(), self.final_norm, cfg.rms_eps, self.lm_head)
+        return lm_head_argmax(last.contiguous(), self.embed, self.final_norm, cfg.rms_eps)
+
+    def forward(self, ids: torch.Tensor, start: int, tokens: bool = False) -> torch.Tensor:
+        """ids [B, T] at positions start..start+T-1; returns fp32 logits of the last position [B, vocab], or
+        with ``tokens`` the greedy next ids [B]."""
         b, t = ids.shape
         cfg = self.cfg
         pos = torch.arange(start, start + t, device=self.device)
@@ -302,14 +323,15 @@ class BitNetDecoder:
             return self._attention(li, q, k, v.reshape(b, t, cfg.num_kv_heads, cfg.head_dim), start)
 
         x = self._layers(self.embed[ids], attend)
-        return self._logits(x[:, -1, :])
+        return self._next_tokens(x[:, -1, :]) if tokens else self._logits(x[:, -1, :])
 
-    def decode_step(self, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+    def decode_step(self, ids: torch.Tensor, pos: torch.Tensor, tokens: bool = False) -> torch.Tensor:
         """One token per sequence, ids [B, 1] at the device positions pos int64 [B]; fixed shapes and no
-        host values, so the step can be captured once and replayed.  Returns fp32 logits [B, vocab]."""
+        host values, so the step can be captured once and replayed.  Returns fp32 logits [B, vocab], or
+        with ``tokens`` the greedy next ids [B]."""
         attend = self._attention_step_hip if self.decode_attention == "hip" else self._attention_step_torch
         x = self._layers(self.embed[ids], lambda li, q, k, v: attend(li, q, k, v, pos))
-        return self._logits(x[:, -1, :])
+        return self._next_tokens(x[:, -1, :]) if tokens else self._logits(x[:, -1, :])
 
     @torch.no_grad()
     def generate(self, prompt: torch.Tensor, new_tokens: int, graph: bool = False) -> torch.Tensor:
@@ -318,7 +340,7 @@ class BitNetDecoder:
         HIP graph capture, the next ids, position and output column updated on the device."""
         b, t0 = prompt.shape
         self.reset(b, t0 + new_tokens)
-        nxt = torch.argmax(self.forward(prompt.to(self.device), 0), dim=-1)
+        nxt = self.forward(prompt.to(self.device), 0, tokens=True)
         out = torch.empty((b, new_tokens), dtype=torch.long, device=self.device)
         out[:, 0] = nxt
         ids = nxt[:, None].clone()
@@ -326,7 +348,7 @@ class BitNetDecoder:
         col = torch.ones(1, dtype=torch.long, device=self.device)
 
         def step():
-            n = torch.argmax(self.decode_step(ids, pos), dim=-1)
+            n = self.decode_step(ids, pos, tokens=True)
             out.index_copy_(1, col, n[:, None])
             ids.copy_(n[:, None])
             pos.add_(1)

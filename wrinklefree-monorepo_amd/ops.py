@@ -386,6 +386,89 @@ def glu_rmsnorm_quantize_i8(
     return (q if kpa == kp else q[..., :kp]), a_scale
 
 
+# ---- greedy decoding: LM head + argmax ----------------------------------------------------------
+
+
+def _argmax_ws(name: str, workspace: Optional[torch.Tensor], m: int, n: int, dev: torch.device) -> torch.Tensor:
+    need = (n + 15) // 16 * m
+    if workspace is None:
+        return torch.empty(need, dtype=torch.int64, device=dev)
+    if workspace.dtype not in (torch.int64, torch.uint64) or workspace.numel() < need or workspace.device != dev \
+            or not workspace.is_contiguous():
+        raise RuntimeError(f"{name}: workspace must be {need} contiguous 64-bit elements on {dev}")
+    return workspace
+
+
+def bitnet_linear_argmax(
+    packed_weights: torch.Tensor, activations: torch.Tensor, scale: Scale, a_scale: Optional[torch.Tensor] = None,
+    logits_dtype: torch.dtype = torch.float32, return_logits: bool = False,
+    workspace: Optional[torch.Tensor] = None,
+):
+    """Greedy next tokens of a ternary LM head: int64 [M] = first argmax over n of the BitLinear logits
+    acc * scale * a_scale[m] rounded to ``logits_dtype`` (M <= 64).  With ``return_logits`` also the
+    logits [M, N].  ``workspace``: optional 64-bit device buffer of ceil(N/16) * M elements."""
+    name = "bitnet_linear_argmax"
+    if packed_weights.dtype != torch.uint8 or packed_weights.dim() != 2:
+        raise RuntimeError(f"{name}: packed_weights must be uint8 2D [out_features, in_features/4]")
+    if activations.dtype != torch.int8 or activations.dim() != 2:
+        raise RuntimeError(f"{name}: activations must be int8 [batch, in_features]")
+    n, kb = packed_weights.shape
+    k = kb * 4
+    if k % QK_I2_S != 0 or activations.shape[1] != k:
+        raise ValueError(f"{name}: in_features must be a multiple of {QK_I2_S} and match the weights")
+    m = activations.shape[0]
+    dev = _require_gpu(name, packed_weights, a_scale)
+    a2 = activations
+    if a2.device != dev:
+        raise RuntimeError(f"{name}: activations are on {a2.device}, weights on {dev}")
+    if a2.stride(1) != 1 or (m > 1 and a2.stride(0) % 16 != 0) or a2.data_ptr() % 16 != 0:
+        a2 = a2.contiguous()
+    if a_scale is not None and (a_scale.dtype != torch.float32 or a_scale.numel() != m):
+        raise RuntimeError(f"{name}: a_scale must be fp32 with one element per token ({m})")
+    if logits_dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError(f"{name}: logits_dtype must be float32 or bfloat16")
+    ws_dev, ws = _scale_args(name, scale, dev)
+    logits = torch.empty((m, n), dtype=logits_dtype, device=dev) if return_logits else None
+    tokens = torch.empty(m, dtype=torch.int64, device=dev)
+    wsp = _argmax_ws(name, workspace, m, n, dev)
+    lda = a2.stride(0) if m > 1 else k
+    with torch.cuda.device(dev):
+        _lib.call("wfb_linear_i2s_argmax", _p(packed_weights), n, k, _p(a2), m, lda, _p(a_scale), ws_dev, ws,
+                  _p(logits), _DT[logits_dtype], n, _p(wsp), _p(tokens), _stream(dev))
+    return (tokens, logits) if return_logits else tokens
+
+
+def lm_head_argmax(
+    x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
+    return_logits: bool = False, workspace: Optional[torch.Tensor] = None,
+):
+    """Greedy next tokens int64 [M] of a dense LM head with the final RMSNorm fused:
+    y = x * rsqrt(mean(x^2) + eps) * norm_weight (rounded to x.dtype), logits = y @ weight.T (fp32),
+    token = first argmax.  x [M, H] (M <= 16) float32/bfloat16, weight [vocab, H] float32/bfloat16 (e.g. a
+    tied embedding).  With ``return_logits`` also the fp32 logits [M, vocab]."""
+    name = "lm_head_argmax"
+    dev = _require_gpu(name, weight, norm_weight)
+    if x.device != dev or x.dim() != 2 or x.stride(-1) != 1:
+        raise RuntimeError(f"{name}: x must be [M, H] with contiguous rows on {dev}")
+    if x.dtype not in (torch.float32, torch.bfloat16) or weight.dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError(f"{name}: x and weight must be float32 or bfloat16")
+    m, h = x.shape
+    if weight.dim() != 2 or weight.shape[1] != h:
+        raise RuntimeError(f"{name}: weight must be [vocab, {h}]")
+    n = weight.shape[0]
+    if norm_weight is not None and norm_weight.numel() != h:
+        raise RuntimeError(f"{name}: norm_weight must have {h} elements")
+    gdt = _float_dtype(name, norm_weight) if norm_weight is not None else WFB_F32
+    logits = torch.empty((m, n), dtype=torch.float32, device=dev) if return_logits else None
+    tokens = torch.empty(m, dtype=torch.int64, device=dev)
+    wsp = _argmax_ws(name, workspace, m, n, dev)
+    ldx = x.stride(0) if m > 1 else h
+    with torch.cuda.device(dev):
+        _lib.call("wfb_lm_head_argmax", _p(x), _DT[x.dtype], ldx, _p(norm_weight), gdt, float(eps), _p(weight),
+                  _DT[weight.dtype], h, m, n, h, _p(logits), n, _p(wsp), _p(tokens), _stream(dev))
+    return (tokens, logits) if return_logits else tokens
+
+
 # ---- GQA decode attention over a KV cache -------------------------------------------------------
 
 
