@@ -14,7 +14,7 @@ M = 512, 2048, 8192 in int8 TOP/s vs the 5.0 POP/s dense int8 peak,
 RMSNorm+quant kernel, one BitNet-2B decode layer's quantised path with separate vs fused launches
 (decode_layer_2b), and the reference CPU kernel timed on this host (cpu_baseline).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--e2e] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-e2e] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -52,8 +52,8 @@ def parse():
     p.add_argument("--sweep", action="store_true", help="also run the batched M sweep (configs[2])")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--e2e", action="store_true",
-                   help="also run the end-to-end models (configs[4] Llama-3-8B shape, configs[0] SmolLM2 shape)")
+    p.add_argument("--no-e2e", action="store_true",
+                   help="skip the end-to-end models (configs[4] Llama-3-8B shape, configs[0] SmolLM2 shape)")
     return p.parse_args()
 
 
@@ -225,13 +225,15 @@ def decode_layer_bench(torch, L, orc, dev, steps, warmup, n_layers=30):
     }
 
 
-def e2e_bench(pkg, torch, dev):
+def e2e_bench(pkg, torch, dev, cpu: bool = True):
     """Greedy decoding on the fused HIP backend (BitLinears on libwfbitnet, float glue in torch).
     Llama-3-8B shape, every linear ternary, random init on the device; prefill of 8
     prompts x 256 tokens (2048 tokens, one M = 2048 GEMM per projection), then 256 decode steps at
     batch 8.  configs[0]: SmolLM2-135M shape, 32-token prompt, 128 new tokens at batch 1.
     Wall-clock times around synchronised regions (host launch overhead included); decode is timed
-    both with eager launches and replayed from one HIP graph capture of the decode step."""
+    both with eager launches and replayed from one HIP graph capture of the decode step.  ``cpu``: also
+    the SmolLM2 model decoded on the host (float glue in torch on the CPU, every quantised group on the
+    numpy oracle; a bounded sample of new tokens) as the end-to-end CPU baseline."""
     M = pkg.model
     res = {}
 
@@ -247,7 +249,7 @@ def e2e_bench(pkg, torch, dev):
             torch.cuda.synchronize()
             model.reset(batch, t0 + new)
             ta = time.perf_counter()
-            torch.argmax(model.forward(prompt, 0), dim=-1)
+            model.forward(prompt, 0, tokens=True)
             torch.cuda.synchronize()
             prefill_s = time.perf_counter() - ta
             timings = {}
@@ -272,12 +274,38 @@ def e2e_bench(pkg, torch, dev):
             "decode_eager_tok_s": round(batch * steps / timings["eager"], 1),
             "distinct_tokens": int(out.unique().numel()),
         }
+        if cpu and name == "smollm2_135m":
+            res[name]["cpu_baseline"] = e2e_cpu_baseline(M, model, prompt, torch)
         del model
         torch.cuda.empty_cache()
 
     run(M.LLAMA3_8B, 8, 256, 256, torch.bfloat16, "llama3_8b")
     run(M.SMOLLM2_135M, 1, 32, 128, torch.float32, "smollm2_135m")
     return res
+
+
+def e2e_cpu_baseline(M, model, prompt, torch, new_tokens: int = 12):
+    """The same model decoded on the host: float glue as torch CPU ops, quantised groups on the numpy
+    oracle (oracle/model_backend.py).  Bounded sample: the prompt plus ``new_tokens`` greedy tokens."""
+    from oracle.model_backend import OracleBackend
+    host = model.on_host(OracleBackend(M.quantised_linears(model).values(), "cpu"))
+    p = prompt.cpu()
+    t = time.perf_counter()
+    with torch.no_grad():
+        host.reset(p.shape[0], p.shape[1] + new_tokens)
+        host.forward(p, 0, tokens=True)
+    t_prefill = time.perf_counter() - t
+    t = time.perf_counter()
+    with torch.no_grad():
+        host.generate(p, new_tokens)
+    t_all = time.perf_counter() - t
+    steps = new_tokens - 1
+    decode_s = max(t_all - t_prefill, 1e-9)
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(p.shape[0] * steps / decode_s, 2), "unit": "tok/s", "cores": cores,
+            "kind": "port", "ms_per_token": round(decode_s / steps * 1e3, 1),
+            "sample": f"SmolLM2-135M shape, batch {p.shape[0]}, {p.shape[1]}-token prompt + {new_tokens} greedy "
+                      f"tokens on the host (torch CPU float glue, numpy-oracle BitLinears, BLAS threads = cores)"}
 
 
 def measured_traffic(n: int, k: int):
@@ -454,7 +482,7 @@ def main():
                               "TOPS": round(2 * m * n * k / (ms * 1e-3) / 1e12, 2)})
             del copies
 
-    e2e = e2e_bench(__graft_entry__.load_package(), torch, dev) if args.e2e else None
+    e2e = None if args.no_e2e else e2e_bench(__graft_entry__.load_package(), torch, dev, cpu=not args.no_cpu)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 

@@ -10,50 +10,14 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import bitnet_oracle as orc
+from oracle.model_backend import OracleBackend as _OracleBackend
 
 pytestmark = pytest.mark.gpu
 
 
-class OracleBackend:
-    """Quantised BitLinear groups computed by the numpy oracle on the host."""
-
-    def __init__(self, model, dev):
-        self.dev = dev
-        self.acc_log = []
-        self.w = {}
-        for lin in model.backend_linears:
-            packed = lin.qweight.cpu().numpy()
-            self.w[id(lin)] = (orc.unpack_i2s(packed).astype(np.float32), np.float32(lin.scale.item()))
-
-    def norm_linears(self, x, norm_weight, eps, linears):
-        xn = x.float().cpu().numpy()
-        g = None if norm_weight is None else norm_weight.float().cpu().numpy()
-        q, s = orc.rmsnorm_quant(xn, g, eps, k_pad=linears[0].k_pad)
-        outs = []
-        for lin in linears:
-            w, ws = self.w[id(lin)]
-            acc = (q.astype(np.float32) @ w.T).astype(np.int64)  # exact: |partial sums| < 2^24
-            self.acc_log.append(acc)
-            outs.append(torch.from_numpy(orc.rescale(acc, ws, s)).to(self.dev))
-        return outs
-
-    def norm_linear_argmax(self, x, norm_weight, eps, linear):
-        (logits,) = self.norm_linears(x, norm_weight, eps, [linear])
-        return torch.argmax(logits, dim=-1)  # first maximum, like the fused kernel
-
-    def glu_norm_linears(self, gate, up, act, norm_weight, eps, linears):
-        g = None if norm_weight is None else norm_weight.float().cpu().numpy()
-        code = orc.ACT_SILU if act == "silu" else orc.ACT_RELU2
-        q, s = orc.glu_rmsnorm_quant(gate.float().cpu().numpy(), up.float().cpu().numpy(), code, g, eps,
-                                     k_pad=linears[0].k_pad)
-        outs = []
-        for lin in linears:
-            w, ws = self.w[id(lin)]
-            acc = (q.astype(np.float32) @ w.T).astype(np.int64)
-            self.acc_log.append(acc)
-            outs.append(torch.from_numpy(orc.rescale(acc, ws, s)).to(self.dev))
-        return outs
+def OracleBackend(model, dev):
+    """The numpy-oracle backend over every ternary linear of the model (oracle/model_backend.py)."""
+    return _OracleBackend(model.backend_linears, dev)
 
 
 @pytest.mark.parametrize("fused", [False, True])
@@ -179,3 +143,24 @@ def test_hip_decode_attention_matches_torch_decode(pkg, dev, dtype):
     # the int8 activations downstream move them by well under 1%
     assert float(diff.max()) <= (2e-2 if dtype == torch.float32 else 5e-2) * span
     assert float(diff.mean()) <= (2e-3 if dtype == torch.float32 else 1e-2) * span
+
+
+def test_host_copy_runs_the_same_model(pkg, dev):
+    """on_host (the end-to-end CPU baseline): the same weights with torch-CPU float glue and the oracle
+    BitLinears give the GPU model's prefill logits to a float tolerance, and decode on the host."""
+    M = pkg.model
+    cfg = M.BitNetConfig(vocab_size=2048, hidden_size=256, intermediate_size=512, num_layers=2, num_heads=4,
+                         num_kv_heads=2, head_dim=64, rope_theta=10000.0)
+    model = M.BitNetDecoder(cfg, seed=8, device=dev, backend=M.HipBackend(out_dtype=torch.float32, fused=True))
+    lins = list(M.quantised_linears(model).values())
+    host = model.on_host(_OracleBackend(lins, "cpu"))
+    prompt = torch.randint(0, cfg.vocab_size, (2, 10), generator=torch.Generator().manual_seed(2))
+    with torch.no_grad():
+        model.reset(2, 16)
+        lg = model.forward(prompt.to(dev), 0).cpu()
+        host.reset(2, 16)
+        lh = host.forward(prompt, 0)
+    assert lh.device.type == "cpu"
+    assert float((lg - lh).abs().max()) <= 2e-2 * float(lg.abs().max())
+    toks = host.generate(prompt, 5)
+    assert toks.shape == (2, 5) and toks.device.type == "cpu"

@@ -20,6 +20,7 @@ and the tied LM head with its final norm and greedy argmax (one libwfbitnet kern
 
 from __future__ import annotations
 
+import copy
 import math
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Sequence
@@ -308,7 +309,26 @@ class BitNetDecoder:
         cfg = self.cfg
         if self.lm_head is not None:
             return self.backend.norm_linear_argmax(last.contiguous(), self.final_norm, cfg.rms_eps, self.lm_head)
+        if self.device.type != "cuda":  # host copy of the model (see on_host)
+            return torch.argmax(self._logits(last), dim=-1)
         return lm_head_argmax(last.contiguous(), self.embed, self.final_norm, cfg.rms_eps)
+
+    def on_host(self, backend) -> "BitNetDecoder":
+        """A copy whose float glue runs on the CPU (torch ops, decode attention included) and whose
+        quantised groups go to ``backend`` (a host backend holding its own copy of the packed weights);
+        the packed weights themselves are shared, not copied."""
+        cpu = torch.device("cpu")
+        m = copy.copy(self)
+        m.device, m.backend, m.decode_attention = cpu, backend, "torch"
+        m.embed, m.final_norm, m.inv_freq = self.embed.to(cpu), self.final_norm.to(cpu), self.inv_freq.to(cpu)
+        m.layers = []
+        for L in self.layers:
+            c = copy.copy(L)
+            for n in ("input_norm", "attn_sub_norm", "post_attn_norm", "ffn_sub_norm"):
+                setattr(c, n, getattr(L, n).to(cpu))
+            m.layers.append(c)
+        m.kv, m._lm_t = [], None
+        return m
 
     def forward(self, ids: torch.Tensor, start: int, tokens: bool = False) -> torch.Tensor:
         """ids [B, T] at positions start..start+T-1; returns fp32 logits of the last position [B, vocab], or
