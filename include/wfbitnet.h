@@ -78,6 +78,25 @@ int wfb_pack_i2s(const void* w, int w_dtype, int64_t n, int64_t k, int64_t ldw,
  * Same decode as the scalar reference dot, bitnet_engine.cpp:51-81. */
 int wfb_unpack_i2s(const uint8_t* qweight, int64_t n, int64_t k, int8_t* w_out, void* stream);
 
+/* Load-time conversion of the HF "offline" ternary layout to I2_S.
+ *   packed_hf : uint8 [NB, K], NB = ceil(N/4); byte (j, k) = codes (w + 1) of column k of rows j, j+NB,
+ *               j+2NB, j+3NB in bits 1:0, 3:2, 5:4, 7:6 (packages/inference/scripts/quantize_dlm_to_offline.py:27-98)
+ *   qweight   : uint8 [N, k_pad/4] I2_S (columns K..k_pad-1 zero weights); 4*(NB-1) < N <= 4*NB,
+ *               k_pad >= K a multiple of 128
+ *   scale_out : fp32 [1] device.  scale_mode WFB_SCALE_REFERENCE: weight_scale * nnz / (4*NB*K) (< 1e-8 -> 1),
+ *               what the reference converter's repack yields; WFB_SCALE_CHECKPOINT: weight_scale itself.
+ *   weight_scale: read from weight_scale_dev[0] (scale_dtype WFB_F32 or WFB_BF16) or, if that is NULL,
+ *               the host value weight_scale.
+ *   workspace : WFB_CONVERT_WS(N, k_pad) int64 of device memory.
+ * Replaces the offline branch of convert_checkpoint (packages/inference/scripts/convert_to_sglkernel.py:221-246). */
+#define WFB_SCALE_REFERENCE 0
+#define WFB_SCALE_CHECKPOINT 1
+#define WFB_CONVERT_WS(n, k_pad) (((n) * ((k_pad) / 16) + 255) / 256)
+int wfb_convert_hf_offline_i2s(const uint8_t* packed_hf, int64_t nb, int64_t n, int64_t k, int64_t k_pad,
+                               const void* weight_scale_dev, int scale_dtype, float weight_scale,
+                               int scale_mode, uint8_t* qweight, float* scale_out, int64_t* workspace,
+                               void* stream);
+
 /* ---- a2: activation quantisation ------------------------------------------------------- */
 
 /* Per-token absmax int8 quantisation of x [M, H] (row stride ldx elements) into q [M, k_pad]

@@ -28,6 +28,11 @@ How each function is pinned (see tests/test_oracle.py):
                        float64 exp2 / silu (relative error bound), exact powers of two, the
                        relu^2 closed form; the composition glu_rmsnorm_quant = rmsnorm_quant(glu).
   rescale_segmented    equals rescale of each segment with its own scale (the separate-call form).
+  unpack_hf_offline    transformers' own BitNet pack_weights (an independent implementation of the
+                       layout) round trips through it; the 8-row example of its unpack_weights
+                       docstring and the byte/row mapping comment of quantize_dlm_to_offline.py:31-33.
+  convert_hf_offline   codes = unpack_hf_offline then pack_i2s; the scale's closed form checked against
+                       an fp64 mean of |w * weight_scale|.
 """
 
 from __future__ import annotations
@@ -110,6 +115,42 @@ def pack_ternary(w: np.ndarray, scale=None):
 
 
 # ---- a2: activation quantisation ---------------------------------------------------------------
+
+
+def unpack_hf_offline(packed: np.ndarray, n: int | None = None) -> np.ndarray:
+    """HF offline ternary layout uint8 [NB, K] -> int8 [n, K] (default n = 4*NB): row r is
+    ((packed[r % NB] >> 2*(r // NB)) & 3) - 1 (PACK:221-236 unpack loop; layout stated in
+    packages/inference/scripts/quantize_dlm_to_offline.py:72-96).  Code 3 is never written; the
+    reference's repack clamps its +2 to +1, so it maps to +1 here."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    nb = packed.shape[0]
+    n = 4 * nb if n is None else n
+    rows = np.arange(n)
+    codes = (packed[rows % nb] >> (2 * (rows // nb))[:, None].astype(np.uint8)) & 3
+    return (np.minimum(codes, 2).astype(np.int8) - 1)
+
+
+def convert_hf_offline(packed: np.ndarray, weight_scale, n: int | None = None, k_pad: int | None = None,
+                       mode: str = "reference"):
+    """(I2_S qweight [n, k_pad/4], fp32 scale) of an HF offline tensor.  mode "reference": the scale the
+    reference converter writes, mean(|w * weight_scale|) over all 4*NB rows and K columns (PACK:240-242
+    repacking through pack_ternary_sglkernel), i.e. weight_scale * nnz / (4*NB*K) rounded once to fp32
+    (< 1e-8 -> 1); mode "checkpoint": weight_scale.  The codes are the unpacked ternary values."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    nb, k = packed.shape
+    w_all = unpack_hf_offline(packed)
+    n = 4 * nb if n is None else n
+    kp = -(-k // QK_I2_S) * QK_I2_S if k_pad is None else k_pad
+    w = np.zeros((n, kp), dtype=np.int8)
+    w[:, :k] = w_all[:n]
+    ws = float(np.float32(weight_scale))
+    if mode == "reference":
+        s = np.float32(ws * (np.count_nonzero(w_all) / float(4 * nb * k)))
+        if float(s) < 1e-8:
+            s = np.float32(1.0)
+    else:
+        s = np.float32(ws)
+    return pack_i2s(w), s
 
 
 def quantize_row_params(mx: np.ndarray):

@@ -362,3 +362,52 @@ def test_rescale_segmented_equals_per_segment_rescale():
         parts.append(orc.rescale(acc[:, r0:r0 + r], w, a_s))
         r0 += r
     assert np.array_equal(y, np.concatenate(parts, axis=1))
+
+
+# ---- HF offline ternary layout (load-time conversion) ----------------------------------------
+
+
+def test_hf_offline_unpack_docstring_example():
+    """The 8-row example of transformers' BitNet unpack_weights docstring (an independent statement of
+    the layout: byte j holds rows j, j+NB, j+2NB, j+3NB from the low bits up)."""
+    packed = np.array([[0b10100001, 0b00011000], [0b10010000, 0b00001010]], dtype=np.uint8)
+    expect = [[0, -1], [-1, 1], [-1, 1], [-1, 1], [1, 0], [0, -1], [1, -1], [1, -1]]
+    assert orc.unpack_hf_offline(packed).tolist() == expect
+
+
+@pytest.mark.parametrize("n,k", [(8, 3), (12, 256), (13, 130), (4, 1)])
+def test_hf_offline_unpack_matches_transformers_pack(n, k):
+    """Round trip through transformers' own pack_weights (its rows past n are code 0, i.e. -1)."""
+    tb = pytest.importorskip("transformers.integrations.bitnet")
+    rng = np.random.default_rng(n * 100 + k)
+    w = rng.integers(-1, 2, size=(n, k)).astype(np.int8)
+    packed = tb.pack_weights(torch.from_numpy(w.copy())).numpy()
+    assert packed.shape == ((n + 3) // 4, k)
+    assert np.array_equal(orc.unpack_hf_offline(packed, n), w)
+
+
+def test_hf_offline_layout_comment_of_the_reference_packer():
+    """quantize_dlm_to_offline.py:31-33: for 8 rows byte 0 has rows [0,2,4,6], byte 1 has [1,3,5,7]."""
+    w = np.zeros((8, 1), dtype=np.int8)
+    w[[0, 2, 4, 6], 0] = 1   # code 2 in every field of byte 0
+    packed = np.zeros((2, 1), dtype=np.uint8)
+    packed[0, 0] = 0b10101010
+    packed[1, 0] = 0b01010101
+    assert np.array_equal(orc.unpack_hf_offline(packed), w)
+
+
+def test_hf_offline_convert_scale_closed_form():
+    rng = np.random.default_rng(4)
+    w = rng.integers(-1, 2, size=(40, 256)).astype(np.int8)
+    w[:, :7] = 0
+    packed = np.zeros((10, 256), dtype=np.uint8)
+    for i in range(4):
+        packed |= ((w[10 * i:10 * (i + 1)] + 1).astype(np.uint8) << (2 * i))
+    ws = np.float32(0.0371)
+    q, s = orc.convert_hf_offline(packed, ws)
+    assert np.array_equal(orc.unpack_i2s(q), w)
+    # the reference repack: mean(|w * ws|) -- here in float64, rounded once
+    assert s == np.float32(np.abs(w.astype(np.float64) * np.float64(ws)).mean())
+    assert orc.convert_hf_offline(packed, ws, mode="checkpoint")[1] == ws
+    z = np.full((2, 128), 0x55, dtype=np.uint8)  # all zero weights -> scale 1
+    assert orc.convert_hf_offline(z, ws)[1] == np.float32(1.0)

@@ -15,6 +15,7 @@ from .ops import (
     bitnet_linear_argmax,
     bitnet_linear_segmented,
     check_kernel_available,
+    convert_hf_offline_i2s,
     glu_rmsnorm_quantize_i8,
     gqa_decode_attention,
     lm_head_argmax,
@@ -24,7 +25,8 @@ from .ops import (
     rmsnorm_quantize_i8,
     unpack_i2s,
 )
-from . import model
+from . import model, sglbitnt
+from .sglbitnt import SGLBitNetFile, write_sglbitnt
 from .bitlinear import (
     BitLinear,
     BitNetLinearMethod,
@@ -36,9 +38,9 @@ from .bitlinear import (
 
 __all__ = [
     "LIB_PATH", "library_available", "QK_I2_S", "absmean_scale", "bitnet_gemm", "bitnet_gemv", "bitnet_linear",
-    "bitnet_linear_argmax", "bitnet_linear_segmented", "check_kernel_available", "glu_rmsnorm_quantize_i8", "gqa_decode_attention",
-    "lm_head_argmax", "pack_ternary_i2s",
+    "bitnet_linear_argmax", "bitnet_linear_segmented", "check_kernel_available", "convert_hf_offline_i2s",
+    "glu_rmsnorm_quantize_i8", "gqa_decode_attention", "lm_head_argmax", "pack_ternary_i2s",
     "quantize_activations_i8", "quantize_activations_i8_per_token", "rmsnorm_quantize_i8", "unpack_i2s",
     "BitLinear", "BitNetLinearMethod", "BitNetLinearNative", "SubLNBitLinear", "convert_linear_to_bitlinear",
-    "patch_model_with_native_kernels", "model",
+    "patch_model_with_native_kernels", "model", "sglbitnt", "SGLBitNetFile", "write_sglbitnt",
 ]

@@ -22,6 +22,8 @@ WFB_QK_I2S = 128
 WFB_ABSMEAN_WS_DOUBLES = 1024
 WFB_NORM_MAX_H = 16384
 WFB_MAX_SEGMENTS = 8
+WFB_SCALE_REFERENCE = 0
+WFB_SCALE_CHECKPOINT = 1
 WFB_ACT_SILU = 1
 WFB_ACT_RELU2 = 2
 
@@ -44,6 +46,7 @@ SIGNATURES = {
     "wfb_linear_i2s_segmented": [_vp, _i64, _i64, _int, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _int, _vp, _int, _i64,
                                  _vp, _vp],
     "wfb_glu_rmsnorm_quant_i8": [_vp, _vp, _int, _i64, _int, _vp, _int, _f32, _i64, _i64, _vp, _i64, _i64, _vp, _vp],
+    "wfb_convert_hf_offline_i2s": [_vp, _i64, _i64, _i64, _i64, _vp, _int, _f32, _int, _vp, _vp, _vp, _vp],
     "wfb_linear_i2s_argmax": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _int, _i64, _vp, _vp, _vp],
     "wfb_lm_head_argmax": [_vp, _int, _i64, _vp, _int, _f32, _vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp,
                            _vp],

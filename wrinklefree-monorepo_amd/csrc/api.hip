@@ -240,6 +240,29 @@ int wfb_glu_rmsnorm_quant_i8(const void* gate, const void* up, int x_dtype, int6
                     name);
 }
 
+int wfb_convert_hf_offline_i2s(const uint8_t* packed_hf, int64_t nb, int64_t n, int64_t k, int64_t k_pad,
+                               const void* weight_scale_dev, int scale_dtype, float weight_scale, int scale_mode,
+                               uint8_t* qweight, float* scale_out, int64_t* workspace, void* stream) {
+  const char* name = "wfb_convert_hf_offline_i2s";
+  if (nb <= 0 || k <= 0 || n <= 4 * (nb - 1) || n > 4 * nb)
+    return fail(WFB_EINVAL, "%s: need 4*(NB-1) < N <= 4*NB and K > 0 (NB=%lld N=%lld K=%lld)", name, (long long)nb,
+                (long long)n, (long long)k);
+  if (k_pad < k || k_pad % WFB_QK_I2S != 0)
+    return fail(WFB_EINVAL, "%s: k_pad (%lld) must be >= K and a multiple of %d", name, (long long)k_pad, WFB_QK_I2S);
+  if (n * (k_pad / 16) > (int64_t)INT32_MAX * 64 || nb * k > ((int64_t)1 << 40))
+    return fail(WFB_EINVAL, "%s: tensor too large", name);
+  if (scale_mode != WFB_SCALE_REFERENCE && scale_mode != WFB_SCALE_CHECKPOINT)
+    return fail(WFB_EINVAL, "%s: bad scale mode %d", name, scale_mode);
+  if (weight_scale_dev && scale_dtype != WFB_F32 && scale_dtype != WFB_BF16)
+    return fail(WFB_EINVAL, "%s: weight scale dtype must be WFB_F32 or WFB_BF16", name);
+  if (!packed_hf || !qweight || !scale_out || !workspace) return fail(WFB_EINVAL, "%s: null pointer", name);
+  if (!aligned(qweight, 4)) return fail(WFB_EINVAL, "%s: qweight must be 4-byte aligned", name);
+  return hip_status(wfb::launch_convert_hf_offline(packed_hf, nb, n, k, k_pad, weight_scale_dev, scale_dtype,
+                                                   weight_scale, scale_mode, qweight, scale_out, workspace,
+                                                   as_stream(stream)),
+                    name);
+}
+
 int wfb_linear_i2s_argmax(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m, int64_t lda,
                           const float* a_scale, const float* w_scale_dev, float w_scale, void* logits,
                           int logits_dtype, int64_t ldo, uint64_t* workspace, int64_t* token_out, void* stream) {

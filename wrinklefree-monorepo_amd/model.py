@@ -27,6 +27,7 @@ from typing import Dict, List, Optional, Sequence
 
 import torch
 
+from .sglbitnt import SGLBitNetFile, write_sglbitnt
 from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_segmented, glu_rmsnorm_quantize_i8,
                   gqa_decode_attention, lm_head_argmax, pack_ternary_i2s, rmsnorm_quantize_i8)
 
@@ -68,6 +69,17 @@ class PackedLinear:
         self.out_features, self.in_features = weight.shape
         self.k_pad = _pad_k(self.in_features)
         self.qweight, self.scale = pack_ternary_i2s(weight.contiguous(), k_pad=self.k_pad)
+
+    @classmethod
+    def from_packed(cls, qweight: torch.Tensor, scale: torch.Tensor, in_features: int) -> "PackedLinear":
+        """Wrap an already packed I2_S weight (uint8 [out, k_pad/4]) and its fp32 scale [1]."""
+        lin = cls.__new__(cls)
+        lin.out_features, lin.k_pad = qweight.shape[0], qweight.shape[1] * 4
+        if lin.k_pad % QK_I2_S != 0 or not in_features <= lin.k_pad < in_features + QK_I2_S:
+            raise ValueError(f"packed weight of {lin.k_pad} columns does not fit in_features={in_features}")
+        lin.in_features = in_features
+        lin.qweight, lin.scale = qweight.contiguous(), scale.reshape(1).to(torch.float32).contiguous()
+        return lin
 
 
 class HipBackend:
@@ -165,14 +177,7 @@ class BitNetDecoder:
         models) instead of the host generator (the default, reproducible across devices).
         ``decode_attention``: "hip" runs each decode step's rotary embedding, cache append and GQA attention
         as one libwfbitnet kernel; "torch" runs them as torch ops (prefill always uses torch)."""
-        if decode_attention not in ("hip", "torch"):
-            raise ValueError("decode_attention must be 'hip' or 'torch'")
-        self.decode_attention = decode_attention
-        self.cfg = cfg
-        self.device = torch.device(device)
-        self.dtype = dtype
-        self.backend = backend if backend is not None else HipBackend(out_dtype=dtype if dtype == torch.float32
-                                                                       else torch.bfloat16)
+        self._setup(cfg, device, dtype, backend, decode_attention)
         gen = torch.Generator(device=self.device if init_on_device else "cpu").manual_seed(seed)
         self.embed = (torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen, device=gen.device) * 0.02).to(
             self.device, dtype)
@@ -184,9 +189,109 @@ class BitNetDecoder:
                                         .to(self.device))
         else:
             self.lm_head = None  # tied to the embedding
+        self.head_weight = self.embed
+
+    def _setup(self, cfg: BitNetConfig, device, dtype: torch.dtype, backend, decode_attention: str) -> None:
+        if decode_attention not in ("hip", "torch"):
+            raise ValueError("decode_attention must be 'hip' or 'torch'")
+        self.decode_attention = decode_attention
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.backend = backend if backend is not None else HipBackend(out_dtype=dtype if dtype == torch.float32
+                                                                       else torch.bfloat16)
         inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, dtype=torch.float32) / cfg.head_dim))
         self.inv_freq = inv.to(self.device)
         self.kv: List[Optional[List[torch.Tensor]]] = []
+        self._lm_t = None
+
+    # ---- SGLBITNT files (the reference engine's packed-model format) ----------------------------
+
+    _LINEARS = (("q", "self_attn.q_proj"), ("k", "self_attn.k_proj"), ("v", "self_attn.v_proj"),
+                ("o", "self_attn.o_proj"), ("gate", "mlp.gate_proj"), ("up", "mlp.up_proj"),
+                ("down", "mlp.down_proj"))
+    _NORMS = (("input_norm", "input_layernorm"), ("post_attn_norm", "post_attention_layernorm"),
+              ("attn_sub_norm", "self_attn.attn_sub_norm"), ("ffn_sub_norm", "mlp.ffn_sub_norm"))
+
+    def save_sglbitnt(self, path) -> None:
+        """Write the model as an SGLBITNT file with the tensor names the reference engine loads
+        (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:622-668): packed linears uint8 [out, k_pad/4] with
+        their scale, embedding and norms as float32, a ternary LM head as lm_head.weight."""
+        cfg = self.cfg
+        config = {"vocab_size": cfg.vocab_size, "hidden_size": cfg.hidden_size,
+                  "intermediate_size": cfg.intermediate_size, "num_hidden_layers": cfg.num_layers,
+                  "num_attention_heads": cfg.num_heads, "num_key_value_heads": cfg.num_kv_heads,
+                  "head_dim": cfg.head_dim, "rope_theta": cfg.rope_theta, "rms_norm_eps": cfg.rms_eps,
+                  "subln_eps": cfg.subln_eps, "tie_word_embeddings": self.lm_head is None,
+                  "hidden_act": cfg.hidden_act, "max_position_embeddings": 4096}
+        t = {"model.embed_tokens.weight": (self.embed.float(), None)}
+        for i, L in enumerate(self.layers):
+            pre = f"model.layers.{i}."
+            for attr, name in self._LINEARS:
+                lin = getattr(L, attr)
+                t[pre + name + ".weight"] = (lin.qweight, float(lin.scale.item()))
+            for attr, name in self._NORMS:
+                t[pre + name + ".weight"] = (getattr(L, attr).float(), None)
+        t["model.norm.weight"] = (self.final_norm.float(), None)
+        if self.lm_head is not None:
+            t["lm_head.weight"] = (self.lm_head.qweight, float(self.lm_head.scale.item()))
+        write_sglbitnt(path, config, t)
+
+    @classmethod
+    def from_sglbitnt(cls, path, device="cuda", dtype: torch.dtype = torch.float32, backend=None,
+                      decode_attention: str = "hip") -> "BitNetDecoder":
+        """Build the model from an SGLBITNT file (memory-mapped; tensors go to ``device`` one at a time).
+        Packed linears keep their I2_S bytes and scale; a uint8 lm_head.weight is a ternary LM head, a float
+        one a dense head, none a head tied to the embedding.  Missing SubLN weights are ones (the engine
+        skips them, bitnet_engine.cpp:664-668)."""
+        f = SGLBitNetFile(path)
+        c = f.config
+        heads = int(c["num_attention_heads"])
+        head_t = f.tensors.get("lm_head.weight")
+        cfg = BitNetConfig(vocab_size=int(c["vocab_size"]), hidden_size=int(c["hidden_size"]),
+                           intermediate_size=int(c["intermediate_size"]), num_layers=int(c["num_hidden_layers"]),
+                           num_heads=heads, num_kv_heads=int(c.get("num_key_value_heads", heads)),
+                           head_dim=int(c.get("head_dim", int(c["hidden_size"]) // heads)),
+                           rope_theta=float(c.get("rope_theta", 10000.0)),
+                           rms_eps=float(c.get("rms_norm_eps", 1e-5)), subln_eps=float(c.get("subln_eps", 1e-6)),
+                           tie_embeddings=head_t is None,
+                           ternary_lm_head=head_t is not None and head_t.dtype_id == 0,
+                           hidden_act=str(c.get("hidden_act", "silu")))
+        m = cls.__new__(cls)
+        m._setup(cfg, device, dtype, backend, decode_attention)
+        dev = m.device
+
+        def packed(name, in_features):
+            info = f.tensors[name]
+            if info.dtype_id != 0 or len(info.shape) != 2:
+                raise ValueError(f"{name}: expected a packed uint8 [out, in/4] weight")
+            scale = torch.tensor([1.0 if info.scale is None else info.scale], dtype=torch.float32, device=dev)
+            return PackedLinear.from_packed(f.tensor(name, dev), scale, in_features)
+
+        def floats(name, n):
+            if name not in f:
+                return torch.ones(n, device=dev, dtype=dtype)
+            return f.tensor(name, dev).to(dtype).reshape(n)
+
+        h, inter = cfg.hidden_size, cfg.intermediate_size
+        qd = cfg.num_heads * cfg.head_dim
+        ins = {"q": h, "k": h, "v": h, "o": qd, "gate": h, "up": h, "down": inter}
+        sizes = {"input_norm": h, "post_attn_norm": h, "attn_sub_norm": qd, "ffn_sub_norm": inter}
+        m.embed = f.tensor("model.embed_tokens.weight", dev).to(dtype)
+        m.layers = []
+        for i in range(cfg.num_layers):
+            L = _Layer.__new__(_Layer)
+            pre = f"model.layers.{i}."
+            for attr, name in cls._LINEARS:
+                setattr(L, attr, packed(pre + name + ".weight", ins[attr]))
+            for attr, name in cls._NORMS:
+                setattr(L, attr, floats(pre + name + ".weight", sizes[attr]))
+            m.layers.append(L)
+        m.final_norm = floats("model.norm.weight", h)
+        m.lm_head = packed("lm_head.weight", h) if cfg.ternary_lm_head else None
+        m.head_weight = m.embed if head_t is None else (m.embed if cfg.ternary_lm_head else
+                                                        f.tensor("lm_head.weight", dev).to(dtype))
+        return m
 
     # ---- float glue --------------------------------------------------------------------------
 
@@ -299,7 +404,7 @@ class BitNetDecoder:
             (logits,) = self.backend.norm_linears(last.contiguous(), self.final_norm, cfg.rms_eps, [self.lm_head])
             return logits.to(torch.float32)
         if getattr(self, "_lm_t", None) is None:
-            self._lm_t = self.embed.to(torch.float32).t().contiguous()  # tied LM head, [H, vocab]
+            self._lm_t = self.head_weight.to(torch.float32).t().contiguous()  # dense LM head, [H, vocab]
         hn = self._rmsnorm(last, self.final_norm, cfg.rms_eps).to(torch.float32)
         return torch.matmul(hn, self._lm_t)
 
@@ -311,7 +416,7 @@ class BitNetDecoder:
             return self.backend.norm_linear_argmax(last.contiguous(), self.final_norm, cfg.rms_eps, self.lm_head)
         if self.device.type != "cuda":  # host copy of the model (see on_host)
             return torch.argmax(self._logits(last), dim=-1)
-        return lm_head_argmax(last.contiguous(), self.embed, self.final_norm, cfg.rms_eps)
+        return lm_head_argmax(last.contiguous(), self.head_weight, self.final_norm, cfg.rms_eps)
 
     def on_host(self, backend) -> "BitNetDecoder":
         """A copy whose float glue runs on the CPU (torch ops, decode attention included) and whose
@@ -321,6 +426,7 @@ class BitNetDecoder:
         m = copy.copy(self)
         m.device, m.backend, m.decode_attention = cpu, backend, "torch"
         m.embed, m.final_norm, m.inv_freq = self.embed.to(cpu), self.final_norm.to(cpu), self.inv_freq.to(cpu)
+        m.head_weight = m.embed if self.head_weight is self.embed else self.head_weight.to(cpu)
         m.layers = []
         for L in self.layers:
             c = copy.copy(L)

@@ -21,7 +21,7 @@ import torch
 
 from . import _lib
 from ._lib import (WFB_ABSMEAN_WS_DOUBLES, WFB_ACT_RELU2, WFB_ACT_SILU, WFB_BF16, WFB_F16, WFB_F32,
-                   WFB_MAX_SEGMENTS, WFB_QK_I2S)
+                   WFB_MAX_SEGMENTS, WFB_QK_I2S, WFB_SCALE_CHECKPOINT, WFB_SCALE_REFERENCE)
 
 QK_I2_S = WFB_QK_I2S
 
@@ -133,6 +133,47 @@ def unpack_i2s(packed_weights: torch.Tensor) -> torch.Tensor:
     with torch.cuda.device(dev):
         _lib.call("wfb_unpack_i2s", _p(packed_weights), n, kb * 4, _p(out), _stream(dev))
     return out
+
+
+_SCALE_MODES = {"reference": WFB_SCALE_REFERENCE, "checkpoint": WFB_SCALE_CHECKPOINT}
+
+
+def convert_hf_offline_i2s(
+    packed_hf: torch.Tensor, weight_scale: Scale = 1.0, out_features: Optional[int] = None,
+    k_pad: Optional[int] = None, scale_mode: str = "reference",
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """HF offline ternary layout uint8 [ceil(N/4), K] -> (I2_S qweight uint8 [N, k_pad/4], scale fp32 [1]).
+
+    Byte (j, k) of the source holds column k of rows j, j + NB, j + 2NB, j + 3NB (bits 1:0 .. 7:6, code =
+    w + 1; packages/inference/scripts/quantize_dlm_to_offline.py:27-98).  ``out_features`` drops the
+    padding rows (default 4 * NB).  ``scale_mode="reference"`` gives the scale the reference converter
+    writes (its repack takes mean|w * weight_scale|, convert_to_sglkernel.py:221-246);
+    ``"checkpoint"`` keeps ``weight_scale``.  ``weight_scale``: float, or a 1-element fp32/bf16 tensor on
+    the device (the checkpoint's ``weight_scale``)."""
+    name = "convert_hf_offline_i2s"
+    if packed_hf.dtype != torch.uint8 or packed_hf.dim() != 2:
+        raise RuntimeError(f"{name}: packed_hf must be uint8 [ceil(out/4), in]")
+    if scale_mode not in _SCALE_MODES:
+        raise ValueError(f"{name}: scale_mode must be one of {sorted(_SCALE_MODES)}")
+    dev = _require_gpu(name, packed_hf)
+    nb, k = packed_hf.shape
+    n = 4 * nb if out_features is None else int(out_features)
+    kp = (k + QK_I2_S - 1) // QK_I2_S * QK_I2_S if k_pad is None else int(k_pad)
+    ws_ptr, ws_dt, ws_host = None, WFB_F32, 1.0
+    if isinstance(weight_scale, torch.Tensor):
+        if weight_scale.numel() != 1 or weight_scale.dtype not in (torch.float32, torch.bfloat16):
+            raise RuntimeError(f"{name}: weight_scale tensor must be one fp32 or bf16 element")
+        wst = weight_scale.to(dev).contiguous()
+        ws_ptr, ws_dt = _p(wst), _DT[wst.dtype]
+    else:
+        ws_host = float(weight_scale)
+    qweight = torch.empty((n, kp // 4), dtype=torch.uint8, device=dev)
+    scale = torch.empty(1, dtype=torch.float32, device=dev)
+    work = torch.empty((n * (kp // 16) + 255) // 256 + 1, dtype=torch.int64, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("wfb_convert_hf_offline_i2s", _p(packed_hf), nb, n, k, kp, ws_ptr, ws_dt, ws_host,
+                  _SCALE_MODES[scale_mode], _p(qweight), _p(scale), _p(work), _stream(dev))
+    return qweight, scale
 
 
 # ---- a2 / a3: activation quantisation ----------------------------------------------------------
