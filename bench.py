@@ -22,6 +22,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import sys
 import time
@@ -42,6 +43,42 @@ N_COPIES = 64
 
 def gemv_bytes(m: int, n: int, k: int) -> int:
     return n * k // 4 + m * k + 2 * m * n + 4 + 4 * m
+
+
+class Synth:
+    """Seeded synthetic inputs on the device (bench-local; the oracle is used only by the CPU baseline):
+    ternary weights with P(0) = 0.33, P(+-1) = 0.335 packed I2_S (byte j of 128-weight block b = codes
+    of k = 128b + j, +32, +64, +96 from the high bits down, code = w + 1), int8 activations U[-127, 127],
+    scales exp(U(ln 1e-3, 0)), bf16-ready hidden states N(0, 1) with 1% of entries set to +-20."""
+
+    def __init__(self, torch, dev, seed):
+        self.torch, self.dev = torch, dev
+        self.g = torch.Generator(device=dev).manual_seed(seed)
+
+    def packed(self, n, k, rows=4096):
+        t = self.torch
+        out = t.empty((n, k // 4), dtype=t.uint8, device=self.dev)
+        for r0 in range(0, n, rows):
+            r1 = min(n, r0 + rows)
+            u = t.rand((r1 - r0, k), generator=self.g, device=self.dev)
+            c = ((u > 0.335).to(t.uint8) + (u > 0.665).to(t.uint8)).view(r1 - r0, k // 128, 4, 32)
+            out[r0:r1] = (c[:, :, 0] << 6 | c[:, :, 1] << 4 | c[:, :, 2] << 2 | c[:, :, 3]).reshape(r1 - r0, k // 4)
+        return out
+
+    def int8(self, m, k):
+        t = self.torch
+        return t.randint(-127, 128, (m, k), generator=self.g, device=self.dev, dtype=t.int16).to(t.int8)
+
+    def log_uniform(self, size):
+        t = self.torch
+        return t.exp(t.rand(size, generator=self.g, device=self.dev) * math.log(1e-3) * -1.0 + math.log(1e-3))
+
+    def hidden(self, m, h):
+        t = self.torch
+        x = t.randn((m, h), generator=self.g, device=self.dev)
+        sel = t.rand((m, h), generator=self.g, device=self.dev) < 0.01
+        sign = t.where(t.rand((m, h), generator=self.g, device=self.dev) < 0.5, -20.0, 20.0)
+        return t.where(sel, sign, x)
 
 
 def parse():
@@ -101,6 +138,33 @@ class Launcher:
         call.keep = seg  # the host array must outlive the call object
         return call
 
+    def lm_head_args(self, x, m, h, w, n, ws, tok, xdt=1, wdt=1):
+        vp = ctypes.c_void_p
+        args = (vp(x.data_ptr()), xdt, h, None, 0, ctypes.c_float(1e-5), vp(w.data_ptr()), wdt, h, m, n, h, None, n,
+                vp(ws.data_ptr()), vp(tok.data_ptr()), self.stream)
+        return self._wrap("wfb_lm_head_argmax", args)
+
+    def linear_argmax_args(self, qw, n, k, a, m, a_scale, ws_dev, ws, tok):
+        vp = ctypes.c_void_p
+        args = (vp(qw.data_ptr()), n, k, vp(a.data_ptr()), m, k, vp(a_scale.data_ptr()), vp(ws_dev.data_ptr()),
+                ctypes.c_float(0.0), None, 1, n, vp(ws.data_ptr()), vp(tok.data_ptr()), self.stream)
+        return self._wrap("wfb_linear_i2s_argmax", args)
+
+    def attention_args(self, q, kn, vn, dt, cos, sin, kc, vc, pos, b, hq, hkv, d, out):
+        vp = ctypes.c_void_p
+        max_len = kc.shape[2]
+        args = (vp(q.data_ptr()), hq * d, vp(kn.data_ptr()), hkv * d, vp(vn.data_ptr()), hkv * d, dt,
+                vp(cos.data_ptr()), vp(sin.data_ptr()), vp(kc.data_ptr()), vp(vc.data_ptr()), max_len,
+                vp(pos.data_ptr()), b, hq, hkv, d, ctypes.c_float(1.0 / d ** 0.5), vp(out.data_ptr()), hq * d,
+                self.stream)
+        return self._wrap("wfb_gqa_decode_attention", args)
+
+    def convert_args(self, src, nb, n, k, qw, scale, work):
+        vp = ctypes.c_void_p
+        args = (vp(src.data_ptr()), nb, n, k, k, None, 0, ctypes.c_float(1.0), 0, vp(qw.data_ptr()),
+                vp(scale.data_ptr()), vp(work.data_ptr()), self.stream)
+        return self._wrap("wfb_convert_hf_offline_i2s", args)
+
     def _wrap(self, fn, args):
         f = getattr(self.lib, fn)
 
@@ -156,16 +220,16 @@ def _sleep_cycles(torch, seconds):
 LAYER_2B = dict(h=2560, q=2560, kv=320, f=6912)
 
 
-def decode_layer_bench(torch, L, orc, dev, steps, warmup, n_layers=30):
+def decode_layer_bench(torch, L, dev, steps, warmup, n_layers=30):
     """Device time of the quantised part of one BitNet-2B decode layer at batch 1 (attention math
     excluded), weights rotated over n_layers copies (0.77 GB, past the 256 MB Infinity Cache):
       separate: norm+quant, q, k, v, SubLN+quant, o, norm+quant, gate, up, relu2*up+SubLN+quant, down
       fused:    norm+quant, q|k|v, SubLN+quant, o, norm+quant, gate|up, relu2*up+SubLN+quant, down"""
     h, qd, kv, f = LAYER_2B["h"], LAYER_2B["q"], LAYER_2B["kv"], LAYER_2B["f"]
-    rng = np.random.default_rng(4000)
+    syn = Synth(torch, dev, 4000)
     shapes = {"q": (qd, h), "k": (kv, h), "v": (kv, h), "o": (h, qd), "gate": (f, h), "up": (f, h), "down": (h, f)}
-    base = {nm: torch.from_numpy(orc.pack_i2s(orc.random_ternary(rng, n, k))).to(dev) for nm, (n, k) in shapes.items()}
-    scales = {nm: torch.from_numpy(orc.log_uniform(rng, 1)).to(dev) for nm in shapes}
+    base = {nm: syn.packed(n, k) for nm, (n, k) in shapes.items()}
+    scales = {nm: syn.log_uniform(1) for nm in shapes}
     wbytes = sum(t.numel() for t in base.values())
     layers = []
     for _ in range(n_layers):
@@ -223,6 +287,71 @@ def decode_layer_bench(torch, L, orc, dev, steps, warmup, n_layers=30):
         "fused": {"launches": len(fus[0]), "us": round(ms_fus * 1e3, 2),
                   "GB/s": round(wbytes / (ms_fus * 1e-3) / 1e9, 1)},
     }
+
+
+def next_rows_bench(torch, L, dev, steps, warmup):
+    """HBM roofline of the kernels around the BitLinear: the greedy LM heads (dense tied bf16 head of
+    SmolLM2, ternary head of Llama-3-8B), decode attention at the configs[4] shape and at a 4k
+    context, and the load-time HF-offline -> I2_S conversion.  Inputs rotated over copies larger than
+    the 256 MB Infinity Cache where they are large; bytes are the algorithmic ones stated per entry."""
+    res = {}
+
+    def entry(name, ms, nbytes, what):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "bytes": int(nbytes), "GB/s": round(gbs, 1),
+                     "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes_counted": what}
+
+    bf = torch.bfloat16
+    # dense tied head, SmolLM2-135M: 49152 x 576 bf16 (56.6 MB), 8 copies
+    n, h = 49152, 576
+    heads = [(torch.randn((n, h), device=dev) * 0.02).to(bf) for _ in range(8)]
+    for m in (1, 8):
+        x = torch.randn((m, h), device=dev).to(bf)
+        ws = torch.empty((n + 15) // 16 * m, dtype=torch.int64, device=dev)
+        tok = torch.empty(m, dtype=torch.int64, device=dev)
+        calls = [[L.lm_head_args(x, m, h, w, n, ws, tok)] for w in heads]
+        entry(f"lm_head_dense_smollm2_m{m}", timed(torch, calls, steps, warmup), n * h * 2 + m * h * 2,
+              "bf16 head weights + x")
+    del heads
+    # ternary head, Llama-3-8B: 128256 x 4096 I2_S (131 MB), 3 copies, batch 8
+    n, k, m = 128256, 4096, 8
+    syn = Synth(torch, dev, 77)
+    base = syn.packed(n, k)
+    copies = [base] + [base.clone() for _ in range(2)]
+    a = syn.int8(m, k)
+    a_s = torch.ones(m, dtype=torch.float32, device=dev)
+    w_s = torch.ones(1, dtype=torch.float32, device=dev)
+    ws = torch.empty((n + 15) // 16 * m, dtype=torch.int64, device=dev)
+    tok = torch.empty(m, dtype=torch.int64, device=dev)
+    calls = [[L.linear_argmax_args(c, n, k, a, m, a_s, w_s, ws, tok)] for c in copies]
+    entry("lm_head_ternary_llama3_m8", timed(torch, calls, steps, warmup), n * k // 4 + m * k,
+          "packed head + int8 activations")
+    del copies, base
+    # decode attention: Llama-3-8B batch 8 (32/8 heads, D 128, bf16 cache) at 512 and 4096 positions
+    for ctx, ncopy in ((512, 24), (4096, 3)):
+        b, hq, hkv, d = 8, 32, 8, 128
+        caches = [(torch.randn((b, hkv, ctx, d), device=dev).to(bf), torch.randn((b, hkv, ctx, d), device=dev).to(bf))
+                  for _ in range(ncopy)]
+        q = torch.randn((b, hq * d), device=dev).to(bf)
+        kv = torch.randn((b, hkv * d), device=dev).to(bf)
+        freqs = torch.arange(ctx, device=dev, dtype=torch.float32)[:, None] * torch.rand(d // 2, device=dev)[None, :]
+        cos, sin = freqs.cos().contiguous(), freqs.sin().contiguous()
+        pos = torch.full((b,), ctx - 1, dtype=torch.int64, device=dev)
+        out = torch.empty((b, hq * d), dtype=bf, device=dev)
+        calls = [[L.attention_args(q, kv, kv, 1, cos, sin, kc, vc, pos, b, hq, hkv, d, out)] for kc, vc in caches]
+        entry(f"attention_llama3_b8_ctx{ctx}", timed(torch, calls, steps, warmup), 2 * b * hkv * ctx * d * 2,
+              "K and V cache reads (bf16)")
+        del caches
+    # load-time conversion, 13824 x 2560 (8.8 MB in, 8.8 MB out), 16 copies
+    n, k = 13824, 2560
+    srcs = [torch.randint(0, 255, (n // 4, k), dtype=torch.uint8, device=dev) for _ in range(16)]
+    qw = torch.empty((n, k // 4), dtype=torch.uint8, device=dev)
+    sc = torch.empty(1, dtype=torch.float32, device=dev)
+    work = torch.empty((n * (k // 16) + 255) // 256, dtype=torch.int64, device=dev)
+    calls = [[L.convert_args(src, n // 4, n, k, qw, sc, work)] for src in srcs]
+    entry("convert_hf_offline_13824x2560", timed(torch, calls, steps, warmup), 2 * n * k // 4,
+          "offline bytes read + I2_S bytes written")
+    return res
 
 
 def e2e_bench(pkg, torch, dev, cpu: bool = True):
@@ -388,22 +517,19 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
-    from oracle import bitnet_oracle as orc
-
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     L = Launcher(pkg, torch)
-    rng = np.random.default_rng(1000)
 
     # ---- batch-1 decode GEMV at the four 2B shapes, rotated weights ----------------
     shapes = []
     for idx, (n, k) in enumerate(GEMV_SHAPES):
-        r = np.random.default_rng(1000 + idx)
-        packed = torch.from_numpy(orc.pack_i2s(orc.random_ternary(r, n, k))).to(dev)
+        syn = Synth(torch, dev, 1000 + idx)
+        packed = syn.packed(n, k)
         copies = [packed.clone() for _ in range(N_COPIES)]
-        a = torch.from_numpy(orc.random_int8(r, 1, k)).to(dev)
-        a_scale = torch.from_numpy(orc.log_uniform(r, 1)).to(dev)
-        ws = torch.from_numpy(orc.log_uniform(r, 1)).to(dev)
+        a = syn.int8(1, k)
+        a_scale = syn.log_uniform(1)
+        ws = syn.log_uniform(1)
         out = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
         calls = [L.linear_args("wfb_linear_i2s", c, n, k, a, 1, a_scale, ws, out) for c in copies]
         shapes.append(dict(n=n, k=k, calls=calls, bytes=gemv_bytes(1, n, k), copies=copies))
@@ -430,12 +556,12 @@ def main():
     # ---- prefill GEMM, M in {512, 2048, 8192} ---------------------------------------
     prefill = []
     for n, k in PREFILL_SHAPES:
-        r = np.random.default_rng(3000 + n)
-        packed = torch.from_numpy(orc.pack_i2s(orc.random_ternary(r, n, k))).to(dev)
-        ws = torch.from_numpy(orc.log_uniform(r, 1)).to(dev)
+        syn = Synth(torch, dev, 3000 + n)
+        packed = syn.packed(n, k)
+        ws = syn.log_uniform(1)
         for m in (512, 2048, 8192):
-            a = torch.from_numpy(orc.random_int8(r, m, k)).to(dev)
-            a_scale = torch.from_numpy(orc.log_uniform(r, m)).to(dev)
+            a = syn.int8(m, k)
+            a_scale = syn.log_uniform(m)
             out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
             call = L.linear_args("wfb_linear_i2s", packed, n, k, a, m, a_scale, ws, out)
             ms = timed(torch, [[call]], max(10, args.steps // 10), 3)
@@ -447,9 +573,9 @@ def main():
     # ---- fused RMSNorm + per-token quant (configs[2] input distribution) -----------------------
     normq = []
     for m, h in ((1, 2560), (2048, 2560), (16, 6912)):
-        r = np.random.default_rng(5000 + m + h)
-        x = torch.from_numpy(orc.outlier_hidden(r, m, h)).to(torch.bfloat16).to(dev)
-        g = torch.from_numpy((1 + 0.1 * r.standard_normal(h)).astype(np.float32)).to(torch.bfloat16).to(dev)
+        syn = Synth(torch, dev, 5000 + m + h)
+        x = syn.hidden(m, h).to(torch.bfloat16)
+        g = (1 + 0.1 * torch.randn(h, generator=syn.g, device=dev)).to(torch.bfloat16)
         q = torch.empty((m, h), dtype=torch.int8, device=dev)
         sc = torch.empty(m, dtype=torch.float32, device=dev)
         vp = ctypes.c_void_p
@@ -461,17 +587,17 @@ def main():
         normq.append({"M": m, "H": h, "us": round(ms * 1e3, 3), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1)})
 
     # ---- fused decode layer (configs[1] shapes as one BitNet-2B layer) -------------------------
-    layer = decode_layer_bench(torch, L, orc, dev, max(50, args.steps // 2), 5)
+    layer = decode_layer_bench(torch, L, dev, max(50, args.steps // 2), 5)
 
     sweep = None
     if args.sweep:
         sweep = []
         for n, k in ((2560, 2560), (2560, 6912), (13824, 2560)):
-            r = np.random.default_rng(6000 + n + k)
-            base = torch.from_numpy(orc.pack_i2s(orc.random_ternary(r, n, k))).to(dev)
+            syn = Synth(torch, dev, 6000 + n + k)
+            base = syn.packed(n, k)
             copies = [base.clone() for _ in range(max(8, int(1.2e9 // (n * k // 4) // 4)))]
             for m in (1, 2, 4, 8, 16, 32, 64):
-                a = torch.from_numpy(orc.random_int8(r, m, k)).to(dev)
+                a = syn.int8(m, k)
                 a_scale = torch.ones(m, dtype=torch.float32, device=dev)
                 ws = torch.ones(1, dtype=torch.float32, device=dev)
                 out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
@@ -481,6 +607,9 @@ def main():
                 sweep.append({"M": m, "N": n, "K": k, "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                               "TOPS": round(2 * m * n * k / (ms * 1e-3) / 1e12, 2)})
             del copies
+
+    print("[bench] lm heads, attention, conversion", file=sys.stderr, flush=True)
+    nxt = next_rows_bench(torch, L, dev, min(args.steps, 100), 5)
 
     e2e = None if args.no_e2e else e2e_bench(__graft_entry__.load_package(), torch, dev, cpu=not args.no_cpu)
 
@@ -510,6 +639,7 @@ def main():
         "prefill_gemm": prefill,
         "rmsnorm_quant": normq,
         "decode_layer_2b": layer,
+        "lm_head_attention_convert": nxt,
     }
     if sweep is not None:
         line["batched_sweep"] = sweep

@@ -328,3 +328,28 @@ def test_serving_method_per_tensor_matches_reference_contract(pkg, dev):
     assert np.array_equal(y.cpu().numpy(), y_ref)
     with pytest.raises(ValueError):
         meth.create_weights(torch.nn.Module(), 600, [64], 600, 64, torch.bfloat16, device=dev)
+
+
+@pytest.mark.parametrize("h", [576, 2560, 4096, 4104, 6912, 14336, 16384])
+def test_norm_quant_batch_invariant(pkg, dev, h):
+    """A row quantises to the same codes and scale whether it comes in a batch of 8 (one 1024-thread
+    workgroup per row) or of 100 (one wave per row, or 256 threads per row above H = 4096): every kernel
+    keeps the one summation order the row length defines.  Also checked against the oracle."""
+    rng = np.random.default_rng(h)
+    x = orc.outlier_hidden(rng, 100, h).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(h)).astype(np.float32)
+    xt, gt = torch.from_numpy(x).to(dev).to(torch.bfloat16), torch.from_numpy(g).to(dev)
+    q_big, s_big = pkg.rmsnorm_quantize_i8(xt, gt, eps=1e-6)
+    q_small, s_small = pkg.rmsnorm_quantize_i8(xt[:8].contiguous(), gt, eps=1e-6)
+    assert torch.equal(q_big[:8], q_small) and torch.equal(s_big[:8], s_small)
+    q_ref, s_ref = orc.rmsnorm_quant(xt[:8].float().cpu().numpy(), g, 1e-6)
+    assert np.array_equal(q_small.cpu().numpy(), q_ref) and np.array_equal(s_small.cpu().numpy(), s_ref)
+    for act in ("silu", "relu2"):
+        up = torch.from_numpy(orc.outlier_hidden(rng, 100, h).astype(np.float32)).to(dev)
+        gate = xt.float()
+        qb, sb = pkg.glu_rmsnorm_quantize_i8(gate, up, act, gt, eps=1e-6)
+        qs, ss = pkg.glu_rmsnorm_quantize_i8(gate[:3].contiguous(), up[:3].contiguous(), act, gt, eps=1e-6)
+        assert torch.equal(qb[:3], qs) and torch.equal(sb[:3], ss)
+    qp, sp = pkg.quantize_activations_i8_per_token(xt)
+    qp8, sp8 = pkg.quantize_activations_i8_per_token(xt[:8].contiguous())
+    assert torch.equal(qp[:8], qp8) and torch.equal(sp[:8], sp8)

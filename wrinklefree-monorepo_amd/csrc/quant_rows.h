@@ -259,6 +259,143 @@ __global__ __launch_bounds__(256) void quant_rows_wave_kernel(const void* __rest
   for (int64_t e = h + lane; e < k_pad; e += 64) qr[e] = 0;
 }
 
+// Few rows (M <= kWideMaxM): one 1024-thread workgroup per row, so the per-element work (loads, gated
+// activation, scaling, quantisation, stores) is spread over 16 waves instead of one (at M = 8 a wave per
+// row leaves the GPU nearly idle and every wave instruction-latency-bound).  The element values go
+// through LDS so that the sum of squares is still taken in exactly the documented order of the kernel
+// the row length selects (the wave order for H <= kWaveMaxH, the 256-thread block order above it):
+// results are bit-identical to quant_rows_wave_kernel / quant_rows_kernel, whatever the batch size.
+constexpr int kWideThreads = 1024;
+constexpr int kWideMaxM = 64;
+constexpr int kWideMaxH = 15360;  // 60 KB of fp32 row in LDS
+
+template <int DT, int GDT, bool NORM, int GLU>
+__global__ __launch_bounds__(kWideThreads) void quant_rows_wide_kernel(
+    const void* __restrict__ x, const void* __restrict__ up, int64_t ldx, const void* __restrict__ gamma, float eps,
+    int h, int8_t* __restrict__ q, int64_t k_pad, int64_t ldq, float* __restrict__ a_scale, bool vec) {
+  extern __shared__ float xs[];  // the row, fp32 (after the gated activation)
+  __shared__ float red[kWideThreads / 64];
+  __shared__ float bcast;
+  constexpr int VPT = 2;  // 8-element vectors per thread (h <= 16384)
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int64_t row = blockIdx.x;
+  const int64_t roff = row * ldx * (DT == WFB_F32 ? 4 : 2);
+  const void* xr = reinterpret_cast<const char*>(x) + roff;
+  const void* ur = GLU != 0 ? reinterpret_cast<const char*>(up) + roff : nullptr;
+  const int nvec = (h + kVec - 1) / kVec;
+
+  float v[VPT][kVec];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int vi = t + kWideThreads * i;
+    if (vi < nvec) {
+      load_row8<DT, GLU>(xr, ur, vi * kVec, h, vec, v[i]);
+      if constexpr (NORM) {
+#pragma unroll
+        for (int e = 0; e < kVec; ++e)
+          if (vi * kVec + e < h) xs[vi * kVec + e] = v[i][e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) v[i][e] = 0.0f;
+    }
+  }
+
+  if constexpr (NORM) {
+    __syncthreads();
+    auto at = [&](int idx) { return idx < h ? xs[idx] : 0.0f; };
+    if (h <= kWaveMaxH) {  // wave order: lane l adds elements (l + 64j)*8 + e, j ascending, e = 0..7
+      if (w == 0) {
+        float ss = 0.0f;
+        for (int j = 0; j * 64 * kVec < h; ++j)
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) {
+            const float a = at((lane + 64 * j) * kVec + e);
+            ss = __fadd_rn(ss, __fmul_rn(a, a));
+          }
+        ss = wave_sum_fixed(ss);
+        if (lane == 0) bcast = ss;
+      }
+    } else {  // block order: thread t < 256 adds elements (it*256 + t)*8 + e, then waves 0..3 in order
+      if (w < kTPB / 64) {
+        float ss = 0.0f;
+        for (int it = 0; it * kTPB * kVec < h; ++it)
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) {
+            const float a = at((it * kTPB + t) * kVec + e);
+            ss = __fadd_rn(ss, __fmul_rn(a, a));
+          }
+        ss = wave_sum_fixed(ss);
+        if (lane == 0) red[w] = ss;
+      }
+      __syncthreads();
+      if (t == 0) {
+        float tot = red[0];
+#pragma unroll
+        for (int k = 1; k < kTPB / 64; ++k) tot = __fadd_rn(tot, red[k]);
+        bcast = tot;
+      }
+    }
+    __syncthreads();
+    const float r = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(bcast, (float)h), eps)));
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int vi = t + kWideThreads * i;
+      if (vi >= nvec) continue;
+      const int e0 = vi * kVec;
+      float g[kVec];
+      if (gamma == nullptr) {
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) g[e] = 1.0f;
+      } else if (vec && e0 + kVec <= h) {
+        load8<GDT>(gamma, e0, g);
+      } else {
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) g[e] = (e0 + e < h) ? load_elem<GDT>(gamma, e0 + e) : 1.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) v[i][e] = __fmul_rn(__fmul_rn(v[i][e], r), g[e]);
+    }
+  }
+
+  float mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i)
+#pragma unroll
+    for (int e = 0; e < kVec; ++e)
+      if ((t + kWideThreads * i) * kVec + e < h) mx = fmaxf(mx, fabsf(v[i][e]));
+  mx = wave_max(mx);
+  if (lane == 0) red[w] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int k = 1; k < kWideThreads / 64; ++k) mx = fmaxf(mx, red[k]);
+  if (mx < 1e-6f) mx = 1.0f;
+  const float inv = __fdiv_rn(127.0f, mx);
+  if (t == 0) a_scale[row] = __fdiv_rn(mx, 127.0f);
+
+  int8_t* qr = q + row * ldq;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e0 = (t + kWideThreads * i) * kVec;
+    if (e0 >= h) break;
+    if (e0 + kVec <= h) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lo |= (uint32_t)(quant_i8(v[i][e], inv) & 0xff) << (8 * e);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hi |= (uint32_t)(quant_i8(v[i][4 + e], inv) & 0xff) << (8 * e);
+      *reinterpret_cast<uint2*>(qr + e0) = make_uint2(lo, hi);
+    } else {
+#pragma unroll
+      for (int e = 0; e < kVec; ++e)
+        if (e0 + e < h) qr[e0 + e] = (int8_t)quant_i8(v[i][e], inv);
+    }
+  }
+  for (int64_t e = h + t; e < k_pad; e += kWideThreads) qr[e] = 0;
+}
+
 template <int DT, int GDT, bool NORM, int VPL, int GLU>
 void launch_wave(const void* x, const void* up, int64_t ldx, const void* gamma, float eps, int64_t m, int64_t h,
                  int8_t* q, int64_t k_pad, int64_t ldq, float* a_scale, bool vec, hipStream_t s) {
@@ -275,7 +412,11 @@ hipError_t launch_rows_t(const void* x, const void* up, int64_t ldx, const void*
                    (gamma == nullptr || (uintptr_t)gamma % (8 * gsz > 16 ? 16 : 8 * gsz) == 0);
   const int vpl = (int)((h + 64 * kVec - 1) / (64 * kVec));
 #define WFB_WAVE(V) launch_wave<DT, GDT, NORM, V, GLU>(x, up, ldx, gamma, eps, m, h, q, k_pad, ldq, a_scale, vec, s)
-  if (h <= kWaveMaxH) {
+  if (m <= kWideMaxM && h <= kWideMaxH) {
+    const size_t lds = NORM ? (size_t)h * sizeof(float) : 0;
+    hipLaunchKernelGGL((quant_rows_wide_kernel<DT, GDT, NORM, GLU>), dim3((unsigned)m), dim3(kWideThreads), lds, s, x,
+                       up, ldx, gamma, eps, (int)h, q, k_pad, ldq, a_scale, vec);
+  } else if (h <= kWaveMaxH) {
     switch (vpl) {
       case 1: WFB_WAVE(1); break;
       case 2: WFB_WAVE(2); break;
