@@ -267,7 +267,6 @@ __global__ __launch_bounds__(256) void quant_rows_wave_kernel(const void* __rest
 // results are bit-identical to quant_rows_wave_kernel / quant_rows_kernel, whatever the batch size.
 constexpr int kWideThreads = 1024;
 constexpr int kWideMaxM = 64;
-constexpr int kWideMaxH = 15360;  // 60 KB of fp32 row in LDS
 
 template <int DT, int GDT, bool NORM, int GLU>
 __global__ __launch_bounds__(kWideThreads) void quant_rows_wide_kernel(
@@ -292,9 +291,15 @@ __global__ __launch_bounds__(kWideThreads) void quant_rows_wide_kernel(
     if (vi < nvec) {
       load_row8<DT, GLU>(xr, ur, vi * kVec, h, vec, v[i]);
       if constexpr (NORM) {
+        if (vi * kVec + kVec <= h) {
+          float4* d = reinterpret_cast<float4*>(xs + vi * kVec);
+          d[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+          d[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < kVec; ++e)
-          if (vi * kVec + e < h) xs[vi * kVec + e] = v[i][e];
+          for (int e = 0; e < kVec; ++e)
+            if (vi * kVec + e < h) xs[vi * kVec + e] = v[i][e];
+        }
       }
     } else {
 #pragma unroll
@@ -304,28 +309,32 @@ __global__ __launch_bounds__(kWideThreads) void quant_rows_wide_kernel(
 
   if constexpr (NORM) {
     __syncthreads();
-    auto at = [&](int idx) { return idx < h ? xs[idx] : 0.0f; };
+    // adds the squares of elements base .. base+7 to ss in order (elements past h count as 0)
+    auto add8 = [&](float ss, int base) {
+      float a[kVec];
+      if (base + kVec <= h) {
+        const float4* p = reinterpret_cast<const float4*>(xs + base);
+        const float4 lo = p[0], hi = p[1];
+        a[0] = lo.x; a[1] = lo.y; a[2] = lo.z; a[3] = lo.w; a[4] = hi.x; a[5] = hi.y; a[6] = hi.z; a[7] = hi.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) a[e] = base + e < h ? xs[base + e] : 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) ss = __fadd_rn(ss, __fmul_rn(a[e], a[e]));
+      return ss;
+    };
     if (h <= kWaveMaxH) {  // wave order: lane l adds elements (l + 64j)*8 + e, j ascending, e = 0..7
       if (w == 0) {
         float ss = 0.0f;
-        for (int j = 0; j * 64 * kVec < h; ++j)
-#pragma unroll
-          for (int e = 0; e < kVec; ++e) {
-            const float a = at((lane + 64 * j) * kVec + e);
-            ss = __fadd_rn(ss, __fmul_rn(a, a));
-          }
+        for (int j = 0; j * 64 * kVec < h; ++j) ss = add8(ss, (lane + 64 * j) * kVec);
         ss = wave_sum_fixed(ss);
         if (lane == 0) bcast = ss;
       }
     } else {  // block order: thread t < 256 adds elements (it*256 + t)*8 + e, then waves 0..3 in order
       if (w < kTPB / 64) {
         float ss = 0.0f;
-        for (int it = 0; it * kTPB * kVec < h; ++it)
-#pragma unroll
-          for (int e = 0; e < kVec; ++e) {
-            const float a = at((it * kTPB + t) * kVec + e);
-            ss = __fadd_rn(ss, __fmul_rn(a, a));
-          }
+        for (int it = 0; it * kTPB * kVec < h; ++it) ss = add8(ss, (it * kTPB + t) * kVec);
         ss = wave_sum_fixed(ss);
         if (lane == 0) red[w] = ss;
       }
@@ -412,7 +421,11 @@ hipError_t launch_rows_t(const void* x, const void* up, int64_t ldx, const void*
                    (gamma == nullptr || (uintptr_t)gamma % (8 * gsz > 16 ? 16 : 8 * gsz) == 0);
   const int vpl = (int)((h + 64 * kVec - 1) / (64 * kVec));
 #define WFB_WAVE(V) launch_wave<DT, GDT, NORM, V, GLU>(x, up, ldx, gamma, eps, m, h, q, k_pad, ldq, a_scale, vec, s)
-  if (m <= kWideMaxM && h <= kWideMaxH) {
+  // wide kernel where a wave per row has the most serial work: rows of the wave order with 5-8 vectors
+  // per lane (H > 2048) and gated rows (measured on MI355X; the 256-thread block kernel stays faster
+  // above kWaveMaxH)
+  const bool wide = m <= kWideMaxM && h <= kWaveMaxH && (h > 2048 || (GLU != 0 && (m > 1 || h > 1024)));
+  if (wide) {
     const size_t lds = NORM ? (size_t)h * sizeof(float) : 0;
     hipLaunchKernelGGL((quant_rows_wide_kernel<DT, GDT, NORM, GLU>), dim3((unsigned)m), dim3(kWideThreads), lds, s, x,
                        up, ldx, gamma, eps, (int)h, q, k_pad, ldq, a_scale, vec);
