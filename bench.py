@@ -150,13 +150,13 @@ class Launcher:
                 ctypes.c_float(0.0), None, 1, n, vp(ws.data_ptr()), vp(tok.data_ptr()), self.stream)
         return self._wrap("wfb_linear_i2s_argmax", args)
 
-    def attention_args(self, q, kn, vn, dt, cos, sin, kc, vc, pos, b, hq, hkv, d, out):
+    def attention_args(self, q, kn, vn, dt, cos, sin, kc, vc, pos, b, hq, hkv, d, out, work):
         vp = ctypes.c_void_p
         max_len = kc.shape[2]
         args = (vp(q.data_ptr()), hq * d, vp(kn.data_ptr()), hkv * d, vp(vn.data_ptr()), hkv * d, dt,
                 vp(cos.data_ptr()), vp(sin.data_ptr()), vp(kc.data_ptr()), vp(vc.data_ptr()), max_len,
                 vp(pos.data_ptr()), b, hq, hkv, d, ctypes.c_float(1.0 / d ** 0.5), vp(out.data_ptr()), hq * d,
-                self.stream)
+                vp(work.data_ptr()), self.stream)
         return self._wrap("wfb_gqa_decode_attention", args)
 
     def convert_args(self, src, nb, n, k, qw, scale, work):
@@ -338,7 +338,9 @@ def next_rows_bench(torch, L, dev, steps, warmup):
         cos, sin = freqs.cos().contiguous(), freqs.sin().contiguous()
         pos = torch.full((b,), ctx - 1, dtype=torch.int64, device=dev)
         out = torch.empty((b, hq * d), dtype=bf, device=dev)
-        calls = [[L.attention_args(q, kv, kv, 1, cos, sin, kc, vc, pos, b, hq, hkv, d, out)] for kc, vc in caches]
+        work = torch.empty(b * hq * (d + 2) * ((ctx + 63) // 64), dtype=torch.float32, device=dev)
+        calls = [[L.attention_args(q, kv, kv, 1, cos, sin, kc, vc, pos, b, hq, hkv, d, out, work)]
+                 for kc, vc in caches]
         entry(f"attention_llama3_b8_ctx{ctx}", timed(torch, calls, steps, warmup), 2 * b * hkv * ctx * d * 2,
               "K and V cache reads (bf16)")
         del caches

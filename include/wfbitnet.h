@@ -242,16 +242,21 @@ int wfb_lm_head_argmax(const void* x, int x_dtype, int64_t ldx, const void* gamm
  * ldv), out row stride ldo, all in elements.  dtype WFB_F32 or WFB_BF16 for every buffer;
  * head_dim 64 or 128; G <= 8.  A position outside [0, max_len) writes NaN to that sequence's output
  * and leaves the cache untouched (positions live on the device and are not checked on the host).
+ * workspace: WFB_ATTN_WS(batch, num_heads, head_dim, max_len) floats of device memory for the
+ * split-context pass (keys cut into splits chosen from max_len and the grid size, merged by a second
+ * kernel), or NULL for one workgroup per (kv head, sequence) over all keys.
  * Replaces attention_forward (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:381-441) with the
  * cache writes of kv_cache_update_key / kv_cache_update_value
  * (SGB/sgl-kernel/csrc/inference/kv_cache.h:81-101) and the rotary embedding of the stage-1 HF model
  * (WF/training/stage1.py:169-214). */
+#define WFB_ATTN_WS(batch, num_heads, head_dim, max_len) \
+  ((batch) * (num_heads) * ((head_dim) + 2) * (((max_len) + 63) / 64))
 int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int64_t ldk,
                              const void* v_new, int64_t ldv, int dtype,
                              const float* rope_cos, const float* rope_sin,
                              void* k_cache, void* v_cache, int64_t max_len, const int64_t* pos,
                              int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-                             float scale, void* out, int64_t ldo, void* stream);
+                             float scale, void* out, int64_t ldo, float* workspace, void* stream);
 
 #ifdef __cplusplus
 }

@@ -124,7 +124,8 @@ def test_attention_argument_errors(pkg):
 
     def st(**kw):
         a = dict(q=vp(16), ldq=512, k=vp(16), ldk=128, v=vp(16), ldv=128, dtype=1, rc=None, rs=None, kc=vp(16),
-                 vc=vp(16), max_len=64, pos=vp(16), b=1, hq=8, hkv=2, d=64, scale=0.125, out=vp(16), ldo=512)
+                 vc=vp(16), max_len=64, pos=vp(16), b=1, hq=8, hkv=2, d=64, scale=0.125, out=vp(16), ldo=512,
+                 work=None)
         a.update(kw)
         return pkg._lib.status("wfb_gqa_decode_attention", *a.values(), None)
 

@@ -55,7 +55,7 @@ def _reference(q, k_new, v_new, kc, vc, pos, cos, sin, hq, scale):
     return out, kc_ref, vc_ref
 
 
-def _run_case(pkg, dev, b, hq, hkv, d, max_len, pos, dtype, rope, strided=False, seed=0):
+def _run_case(pkg, dev, b, hq, hkv, d, max_len, pos, dtype, rope, strided=False, seed=0, split=True):
     gen = torch.Generator().manual_seed(seed)
     qkv = torch.randn((b, (hq + 2 * hkv) * d), generator=gen).to(dtype)
     q, k_new, v_new = qkv[:, :hq * d], qkv[:, hq * d:(hq + hkv) * d], qkv[:, (hq + hkv) * d:]
@@ -73,7 +73,7 @@ def _run_case(pkg, dev, b, hq, hkv, d, max_len, pos, dtype, rope, strided=False,
         qd, kd, vd = qkv_d[:, :hq * d], qkv_d[:, hq * d:(hq + hkv) * d], qkv_d[:, (hq + hkv) * d:]
     else:
         qd, kd, vd = q.contiguous().to(dev), k_new.contiguous().to(dev), v_new.contiguous().to(dev)
-    out = pkg.gqa_decode_attention(qd, kd, vd, kc_d, vc_d, pos_d, *tabs, scale=scale)
+    out = pkg.gqa_decode_attention(qd, kd, vd, kc_d, vc_d, pos_d, *tabs, scale=scale, split=split)
     torch.cuda.synchronize()
     assert torch.equal(kc_d.cpu(), kc_ref), "key cache differs (appended row or untouched rows)"
     assert torch.equal(vc_d.cpu(), vc_ref), "value cache differs"
@@ -97,13 +97,19 @@ CASES = [
     (2, 12, 2, 64, 520, [511, 512], torch.bfloat16, False),                            # G = 6, chunk edges
     (1, 7, 1, 128, 129, [127], torch.float32, True),                                   # G = 7
     (4, 2, 1, 64, 40, [3, 39, 0, 20], torch.bfloat16, True),                           # G = 2
+    (8, 16, 8, 128, 1100, [1099, 0, 63, 64, 255, 256, 700, 1023], torch.bfloat16, True),  # 256-key splits
+    (8, 8, 8, 64, 1100, [1099, 511, 512, 0, 128, 129, 1000, 7], torch.float32, True),    # fp32, 2 chunks/split
 ]
 
 
+@pytest.mark.parametrize("split", [True, False], ids=["split", "single"])
 @pytest.mark.parametrize("case", CASES, ids=[f"b{c[0]}_h{c[1]}x{c[2]}_d{c[3]}_L{c[4]}_{str(c[6])[6:]}" for c in CASES])
-def test_decode_attention_matches_torch(pkg, dev, case):
+def test_decode_attention_matches_torch(pkg, dev, case, split):
+    """Both forms: key splits on separate workgroups merged by the combine kernel (split; the split
+    length grows from 64 keys so the grid stays near 512 workgroups), and one workgroup per (kv head,
+    sequence) over all keys (single)."""
     b, hq, hkv, d, max_len, pos, dtype, rope = case
-    _run_case(pkg, dev, b, hq, hkv, d, max_len, pos, dtype, rope, seed=hq * 7 + max_len)
+    _run_case(pkg, dev, b, hq, hkv, d, max_len, pos, dtype, rope, seed=hq * 7 + max_len, split=split)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -144,13 +150,14 @@ def test_decode_attention_position_out_of_range(pkg, dev):
     vn = torch.randn((b, hkv * d), generator=gen)
     kc = torch.randn((b, hkv, max_len, d), generator=gen)
     vc = torch.randn((b, hkv, max_len, d), generator=gen)
-    kc_d, vc_d = kc.to(dev), vc.to(dev)
-    out = pkg.gqa_decode_attention(q.to(dev), kn.to(dev), vn.to(dev), kc_d, vc_d,
-                                   torch.tensor([max_len, 5, -1], device=dev))
-    o = out.cpu()
-    assert torch.isnan(o[0]).all() and torch.isnan(o[2]).all() and not torch.isnan(o[1]).any()
-    assert torch.equal(kc_d.cpu()[0], kc[0]) and torch.equal(kc_d.cpu()[2], kc[2])
-    assert torch.equal(vc_d.cpu()[0], vc[0]) and torch.equal(vc_d.cpu()[2], vc[2])
+    for split in (True, False):
+        kc_d, vc_d = kc.to(dev), vc.to(dev)
+        out = pkg.gqa_decode_attention(q.to(dev), kn.to(dev), vn.to(dev), kc_d, vc_d,
+                                       torch.tensor([max_len, 5, -1], device=dev), split=split)
+        o = out.cpu()
+        assert torch.isnan(o[0]).all() and torch.isnan(o[2]).all() and not torch.isnan(o[1]).any()
+        assert torch.equal(kc_d.cpu()[0], kc[0]) and torch.equal(kc_d.cpu()[2], kc[2])
+        assert torch.equal(vc_d.cpu()[0], vc[0]) and torch.equal(vc_d.cpu()[2], vc[2])
 
 
 def test_decode_attention_python_errors(pkg, dev):

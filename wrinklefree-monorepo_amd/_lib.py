@@ -51,7 +51,7 @@ SIGNATURES = {
     "wfb_lm_head_argmax": [_vp, _int, _i64, _vp, _int, _f32, _vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp,
                            _vp],
     "wfb_gqa_decode_attention": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
-                                 _i64, _i64, _f32, _vp, _i64, _vp],
+                                 _i64, _i64, _f32, _vp, _i64, _vp, _vp],
 }
 
 _lib = None

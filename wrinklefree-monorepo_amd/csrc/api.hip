@@ -308,7 +308,7 @@ int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int6
                              int64_t ldv, int dtype, const float* rope_cos, const float* rope_sin, void* k_cache,
                              void* v_cache, int64_t max_len, const int64_t* pos, int64_t batch, int64_t num_heads,
                              int64_t num_kv_heads, int64_t head_dim, float scale, void* out, int64_t ldo,
-                             void* stream) {
+                             float* workspace, void* stream) {
   const char* name = "wfb_gqa_decode_attention";
   if (dtype != WFB_F32 && dtype != WFB_BF16) return fail(WFB_EINVAL, "%s: dtype must be WFB_F32 or WFB_BF16", name);
   if (head_dim != 64 && head_dim != 128) return fail(WFB_EINVAL, "%s: head_dim (%lld) must be 64 or 128", name, (long long)head_dim);
@@ -334,7 +334,7 @@ int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int6
   if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return fail(WFB_EINVAL, "%s: caches must be 16-byte aligned", name);
   return hip_status(wfb::launch_gqa_decode(dtype, (int)head_dim, (int)(num_heads / num_kv_heads), q, ldq, k_new, ldk,
                                            v_new, ldv, rope_cos, rope_sin, k_cache, v_cache, max_len, pos, (int)batch,
-                                           (int)num_kv_heads, scale, out, ldo, as_stream(stream)),
+                                           (int)num_kv_heads, scale, out, ldo, workspace, as_stream(stream)),
                     name);
 }
 

@@ -16,6 +16,14 @@
 // value at pos and attends over keys 0..pos, taking key pos from its own LDS copy (no read-back of its
 // own global store).  The G = heads / kv_heads query heads of the group share every K/V load.
 //
+// Split context (flash decoding).  With few sequences and kv heads a workgroup per (kv head, sequence)
+// leaves most of the GPU idle, so the keys are cut into ceil(max_len / KS) splits of KS keys, one
+// workgroup each (grid z); split s covers keys [s*KS, min(pos+1, (s+1)*KS)) and writes its unnormalised
+// output with its running max m and sum l to a workspace, and gqa_combine_kernel merges the splits that
+// hold keys (out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), M = max_s m_s).  The split holding pos
+// appends the new key and value.  KS is chosen from max_len and the grid size (not from pos, which lives
+// on the device), so a captured HIP graph stays valid as pos advances.
+//
 // Work mapping (4 waves).  A key is read by LPK = D/8 lanes, 8 elements each (one 16-byte load for
 // 16-bit caches), so one wave instruction covers 64/LPK whole keys and a wave's loads are contiguous.
 // Keys are processed in chunks of CH; per chunk each wave loads its CH/4 keys of K and V up front,
@@ -32,6 +40,7 @@ namespace wfb {
 namespace {
 
 constexpr int kAttnThreads = 256;
+constexpr int64_t kAttnTargetGrid = 512;  // workgroups the split choice aims for (2 per CU)
 
 template <int DT>
 __device__ __forceinline__ float round_to(float x) {
@@ -89,16 +98,15 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return v;
 }
 
-template <int DT, int D, int G>
+template <int DT, int D, int G, int CH>
 __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
     const void* __restrict__ q, int64_t ldq, const void* __restrict__ kn, int64_t ldk, const void* __restrict__ vn,
     int64_t ldv, const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, void* __restrict__ kc,
     void* __restrict__ vc, int64_t max_len, const int64_t* __restrict__ pos_arr, int hkv, float scale,
-    void* __restrict__ out, int64_t ldo) {
+    void* __restrict__ out, int64_t ldo, int ks, float* __restrict__ part) {
   constexpr int LPK = D / 8;           // lanes per key
   constexpr int KPW = 64 / LPK;        // keys per wave instruction
-  constexpr int CH = DT == WFB_F32 ? 128 : 256;  // keys per chunk
-  constexpr int KW = CH / 4;           // keys per wave per chunk
+  constexpr int KW = CH / 4;           // keys per wave per chunk (CH keys per chunk)
   constexpr int R = KW / KPW;          // load rounds per wave per chunk
   constexpr int ESZ = DT == WFB_F32 ? 4 : 2;
   constexpr int HD = D / 2;
@@ -111,15 +119,20 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   __shared__ float alpha_s[G], lsum_s[G];
   __shared__ float red[4][G][D];
 
-  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int kvh = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int64_t pos = pos_arr[b];
   const int64_t obase = (int64_t)b * ldo + (int64_t)kvh * G * D;
   if (pos < 0 || pos >= max_len) {  // uniform over the workgroup: flag the rows, touch no cache
-    for (int i = t; i < G * D; i += kAttnThreads) store_elem<DT>(out, obase + i, __builtin_nanf(""));
-    return;
+    if (!part)
+      for (int i = t; i < G * D; i += kAttnThreads) store_elem<DT>(out, obase + i, __builtin_nanf(""));
+    return;  // (split mode: the combine kernel flags the rows)
   }
+  const int k0 = split * ks;
+  if (k0 > pos) return;  // no keys in this split (the combine kernel skips it)
+  const int k1 = (int)(pos + 1 < (int64_t)k0 + ks ? pos + 1 : (int64_t)k0 + ks);
+  const bool owns_new = pos < k1;  // the split holding key pos appends the new key and value
   const int64_t cbase = ((int64_t)b * hkv + kvh) * max_len * D;  // element offset of this cache slice
 
   // ---- rotary embedding of the new query heads and key; append key and value ------------------
@@ -139,7 +152,8 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
     qs[g][j] = x1;
     qs[g][j + HD] = x2;
   }
-  if (t < HD) {
+  if (!owns_new) {
+  } else if (t < HD) {
     const int64_t ko = (int64_t)b * ldk + (int64_t)kvh * D;
     float x1 = load_elem<DT>(kn, ko + t), x2 = load_elem<DT>(kn, ko + t + HD);
     if (cs) {
@@ -180,13 +194,13 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
     l_run[h] = 0.0f;
   }
 
-  // keys 0..pos-1 come from the cache (loads past them read zeros); key pos from knew / vnew
-  const uint32_t kbytes = (uint32_t)(pos * D * ESZ);
+  // keys k0..min(pos, k1)-1 come from the cache (loads past them read zeros); key pos from knew / vnew
+  const int kend = owns_new ? (int)pos : k1;
+  const uint32_t kbytes = (uint32_t)((int64_t)kend * D * ESZ);
   const buf_t kb = make_buf(reinterpret_cast<const char*>(kc) + cbase * ESZ, kbytes);
   const buf_t vb = make_buf(reinterpret_cast<const char*>(vc) + cbase * ESZ, kbytes);
-  const int nk = (int)pos + 1;
 
-  for (int c0 = 0; c0 < nk; c0 += CH) {
+  for (int c0 = k0; c0 < k1; c0 += CH) {
     Raw8<DT> kr[R], vr[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -216,7 +230,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) s += qf[g][e] * kf[e];
         s = group_sum_f32<LPK>(s);
-        if (lane % LPK == 0) sc[g][key - c0] = key <= pos ? s * scale : -__builtin_inff();
+        if (lane % LPK == 0) sc[g][key - c0] = key < k1 ? s * scale : -__builtin_inff();
       }
     }
     __syncthreads();
@@ -276,7 +290,10 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   if (lane == 0) {
 #pragma unroll
     for (int h = 0; h < HPW; ++h)
-      if (w + 4 * h < G) lsum_s[w + 4 * h] = l_run[h];
+      if (w + 4 * h < G) {
+        lsum_s[w + 4 * h] = l_run[h];
+        alpha_s[w + 4 * h] = m_run[h];  // the running max (alpha_s is free after the last chunk)
+      }
   }
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -288,6 +305,18 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
       if (kl == 0) red[w][g][d0 + e] = v;
     }
   __syncthreads();
+  if (part) {  // split: unnormalised output, then m and l, per head
+    float* pp = part + ((((int64_t)b * hkv + kvh) * gridDim.z + split) * G) * (D + 2);
+    for (int i = t; i < G * D; i += kAttnThreads) {
+      const int g = i / D, d = i % D;
+      pp[g * (D + 2) + d] = (red[0][g][d] + red[1][g][d]) + (red[2][g][d] + red[3][g][d]);
+    }
+    if (t < G) {
+      pp[t * (D + 2) + D] = alpha_s[t];
+      pp[t * (D + 2) + D + 1] = lsum_s[t];
+    }
+    return;
+  }
   for (int i = t; i < G * D; i += kAttnThreads) {
     const int g = i / D, d = i % D;
     const float s = (red[0][g][d] + red[1][g][d]) + (red[2][g][d] + red[3][g][d]);
@@ -295,21 +324,72 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   }
 }
 
+// Merges the splits of one (kv head, sequence) that hold keys: splits 0 .. pos / KS.
+template <int DT, int D, int G>
+__global__ __launch_bounds__(kAttnThreads) void gqa_combine_kernel(const float* __restrict__ part,
+                                                                   const int64_t* __restrict__ pos_arr,
+                                                                   int64_t max_len, int hkv, int ks, int nsplit,
+                                                                   void* __restrict__ out, int64_t ldo) {
+  const int kvh = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int64_t pos = pos_arr[b];
+  const int64_t obase = (int64_t)b * ldo + (int64_t)kvh * G * D;
+  if (pos < 0 || pos >= max_len) {
+    for (int i = t; i < G * D; i += kAttnThreads) store_elem<DT>(out, obase + i, __builtin_nanf(""));
+    return;
+  }
+  const int ns = (int)(pos / ks) + 1;
+  const float* pp = part + (((int64_t)b * hkv + kvh) * nsplit) * G * (D + 2);
+  for (int i = t; i < G * D; i += kAttnThreads) {
+    const int g = i / D, d = i % D;
+    float mx = -__builtin_inff();
+    for (int s = 0; s < ns; ++s) mx = fmaxf(mx, pp[(s * G + g) * (D + 2) + D]);
+    float num = 0.0f, den = 0.0f;
+    for (int s = 0; s < ns; ++s) {
+      const float* ps = pp + (s * G + g) * (D + 2);
+      const float wgt = __expf(ps[D] - mx);
+      num += ps[d] * wgt;
+      den += ps[D + 1] * wgt;
+    }
+    store_elem<DT>(out, obase + i, num / den);
+  }
+}
+
 template <int DT, int D, int G>
 hipError_t launch_attn_g(const void* q, int64_t ldq, const void* kn, int64_t ldk, const void* vn, int64_t ldv,
                          const float* rc, const float* rs, void* kc, void* vc, int64_t max_len, const int64_t* pos,
-                         int b, int hkv, float scale, void* out, int64_t ldo, hipStream_t s) {
-  hipLaunchKernelGGL((gqa_decode_kernel<DT, D, G>), dim3(hkv, b), dim3(kAttnThreads), 0, s, q, ldq, kn, ldk, vn, ldv,
-                     rc, rs, kc, vc, max_len, pos, hkv, scale, out, ldo);
+                         int b, int hkv, float scale, void* out, int64_t ldo, float* part, hipStream_t s) {
+  // keys per split: 64, doubled while the grid would exceed kAttnTargetGrid workgroups; one split
+  // (no workspace pass) when a single split covers max_len or no workspace is given
+  int64_t ks = 64;
+  while (ks < max_len && (int64_t)b * hkv * ((max_len + ks - 1) / ks) > kAttnTargetGrid) ks *= 2;
+  const int64_t nsplit = (max_len + ks - 1) / ks;
+  if (nsplit == 1 || part == nullptr) {
+    constexpr int CH = DT == WFB_F32 ? 128 : 256;
+    hipLaunchKernelGGL((gqa_decode_kernel<DT, D, G, CH>), dim3(hkv, b, 1), dim3(kAttnThreads), 0, s, q, ldq, kn, ldk,
+                       vn, ldv, rc, rs, kc, vc, max_len, pos, hkv, scale, out, ldo, (int)(max_len + 1),
+                       (float*)nullptr);
+    return hipGetLastError();
+  }
+  if (ks == 64)
+    hipLaunchKernelGGL((gqa_decode_kernel<DT, D, G, 64>), dim3(hkv, b, nsplit), dim3(kAttnThreads), 0, s, q, ldq, kn,
+                       ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, hkv, scale, out, ldo, (int)ks, part);
+  else
+    hipLaunchKernelGGL((gqa_decode_kernel<DT, D, G, DT == WFB_F32 ? 128 : 256>), dim3(hkv, b, nsplit),
+                       dim3(kAttnThreads), 0, s, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, hkv, scale, out,
+                       ldo, (int)ks, part);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((gqa_combine_kernel<DT, D, G>), dim3(hkv, b), dim3(kAttnThreads), 0, s, part, pos, max_len, hkv,
+                     (int)ks, (int)nsplit, out, ldo);
   return hipGetLastError();
 }
 
 template <int DT, int D>
 hipError_t launch_attn_d(int g, const void* q, int64_t ldq, const void* kn, int64_t ldk, const void* vn, int64_t ldv,
                          const float* rc, const float* rs, void* kc, void* vc, int64_t max_len, const int64_t* pos,
-                         int b, int hkv, float scale, void* out, int64_t ldo, hipStream_t s) {
+                         int b, int hkv, float scale, void* out, int64_t ldo, float* part, hipStream_t s) {
 #define WFB_ATTN_G(GG) \
-  case GG: return launch_attn_g<DT, D, GG>(q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, s)
+  case GG: return launch_attn_g<DT, D, GG>(q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, part, s)
   switch (g) {
     WFB_ATTN_G(1);
     WFB_ATTN_G(2);
@@ -329,15 +409,15 @@ hipError_t launch_attn_d(int g, const void* q, int64_t ldq, const void* kn, int6
 hipError_t launch_gqa_decode(int dt, int d, int g, const void* q, int64_t ldq, const void* kn, int64_t ldk,
                              const void* vn, int64_t ldv, const float* rc, const float* rs, void* kc, void* vc,
                              int64_t max_len, const int64_t* pos, int b, int hkv, float scale, void* out, int64_t ldo,
-                             hipStream_t s) {
+                             float* part, hipStream_t s) {
   if (dt == WFB_F32 && d == 64)
-    return launch_attn_d<WFB_F32, 64>(g, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, s);
+    return launch_attn_d<WFB_F32, 64>(g, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, part, s);
   if (dt == WFB_F32 && d == 128)
-    return launch_attn_d<WFB_F32, 128>(g, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, s);
+    return launch_attn_d<WFB_F32, 128>(g, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, part, s);
   if (dt == WFB_BF16 && d == 64)
-    return launch_attn_d<WFB_BF16, 64>(g, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, s);
+    return launch_attn_d<WFB_BF16, 64>(g, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, part, s);
   if (dt == WFB_BF16 && d == 128)
-    return launch_attn_d<WFB_BF16, 128>(g, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, s);
+    return launch_attn_d<WFB_BF16, 128>(g, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, part, s);
   return hipErrorInvalidValue;
 }
 

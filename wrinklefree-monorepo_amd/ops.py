@@ -524,7 +524,7 @@ def _rows2d(name: str, t: torch.Tensor, b: int, width: int) -> Tuple[torch.Tenso
 def gqa_decode_attention(
     q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     pos: torch.Tensor, rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None,
-    scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None, out: Optional[torch.Tensor] = None, split: bool = True,
 ) -> torch.Tensor:
     """One decode token per sequence: rotary embedding of q / k_new, append k/v at pos[b] to the caches,
     attention over positions 0..pos[b].  Returns out [batch, num_heads * head_dim].
@@ -533,8 +533,10 @@ def gqa_decode_attention(
     [batch, num_kv_heads*head_dim]; caches [batch, num_kv_heads, max_len, head_dim] (contiguous, same
     dtype as q: float32 or bfloat16); pos int64 [batch] on the device; rope tables fp32
     [max_len, head_dim/2] (cos and sin of pos * inv_freq) or None.  2-D inputs may be column slices of
-    one q|k|v projection output (row strides are passed through).  Counterpart of the C engine's
-    attention_forward (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:381-441).
+    one q|k|v projection output (row strides are passed through).  ``split``: cut long caches into
+    key splits on separate workgroups (a workspace is allocated), else one workgroup per (kv head,
+    sequence).  Counterpart of the C engine's attention_forward
+    (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:381-441).
     """
     name = "gqa_decode_attention"
     _require_gpu(name, k_cache, v_cache, pos, rope_cos, rope_sin)
@@ -569,10 +571,11 @@ def gqa_decode_attention(
         raise RuntimeError(f"{name}: out must be [{b}, {hq * d}] {q.dtype} with contiguous rows")
     ldo = out.stride(0) if b > 1 else hq * d
     sc = 1.0 / float(d) ** 0.5 if scale is None else float(scale)
+    work = torch.empty(b * hq * (d + 2) * ((max_len + 63) // 64), dtype=torch.float32, device=dev) if split else None
     with torch.cuda.device(dev):
         _lib.call(
             "wfb_gqa_decode_attention", _p(q2), ldq, _p(k2), ldk, _p(v2), ldv, _DT[q.dtype], _p(rope_cos),
-            _p(rope_sin), _p(k_cache), _p(v_cache), max_len, _p(pos), b, hq, hkv, d, sc, _p(out), ldo,
+            _p(rope_sin), _p(k_cache), _p(v_cache), max_len, _p(pos), b, hq, hkv, d, sc, _p(out), ldo, _p(work),
             _stream(dev),
         )
     return out
