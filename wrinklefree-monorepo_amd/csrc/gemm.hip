@@ -84,28 +84,32 @@ __global__ __launch_bounds__(64 * WPB) void gemm_i2s_mfma16_kernel(const uint8_t
 }
 
 // Batched decode (3 <= M <= 64 tokens): v_mfma_i32_16x16x64_i8 over MT tiles of 16 tokens.  A
-// workgroup owns 16 weight rows and splits K over its S waves: wave w takes the 256-weight K-steps
-// w, w + S, w + 2S, ..., so the waves of a workgroup read adjacent 64-byte chunks of the same rows.
-// Lane (nl, g) loads 16 packed bytes of row n0 + nl, chunk 4t + g (64 weights; field f covers
-// k = 128*(c/2) + 32f + 16*(c%2) + 0..15), the B operands of four MFMAs.  Fields enter masked but not
-// shifted -- bits 1:0 (x1), 3:2 (x4), 5:4 and (7:6 >> 2) (x16) -- into three accumulators (5 VALU per
-// packed dword); the code offset is removed with each token's sum(a): acc = acc1 + acc4/4 + acc16/16 -
-// sum(a).  Partial 16 x 16 tiles of the S waves are summed through LDS.  Loads go through raw buffer
-// descriptors: rows past N or M and chunks past K read as zeros.
-template <int MT, int S>
+// workgroup owns NT tiles of 16 weight rows and splits K over its S waves: wave w takes the
+// 256-weight K-steps w, w + S, w + 2S, ..., so the waves of a workgroup read adjacent 64-byte chunks
+// of the same rows.  Lane (nl, g) loads 16 packed bytes of row n0 + 16*nt + nl, chunk 4t + g (64
+// weights; field f covers k = 128*(c/2) + 32f + 16*(c%2) + 0..15), the B operands of four MFMAs; the
+// activation fragments of a step are loaded once and shared by the NT row tiles.  Fields enter masked
+// but not shifted -- bits 1:0 (x1), 3:2 (x4), 5:4 and (7:6 >> 2) (x16) -- into three accumulators (5
+// VALU per packed dword); the code offset is removed with each token's sum(a): acc = acc1 + acc4/4 +
+// acc16/16 - sum(a).  Partial 16 x 16 tiles of the S waves are summed through LDS; wave nt < NT
+// finishes row tile nt.  Loads go through raw buffer descriptors: rows past N or M and chunks past K
+// read as zeros.
+template <int MT, int S, int NT>
 __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* __restrict__ W,
                                                                  const int8_t* __restrict__ A, int64_t lda,
                                                                  int M, int N, int C, Epilogue ep) {
-  __shared__ int red[S][MT][4][64];
+  static_assert(NT <= S, "one wave per row tile in the epilogue");
+  __shared__ int red[S][NT][MT][4][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * NT;
   const int nl = lane & 15, g = lane >> 4;
-  const int n = n0 + nl;
   const uint32_t row_bytes = (uint32_t)C * 16;
   const uint32_t w_end = (uint32_t)N * row_bytes, a_end = (uint32_t)((int64_t)(M - 1) * lda + (int64_t)C * 64);
   const buf_t wb = make_buf(W, w_end);
   const buf_t ab = make_buf(A, a_end);
-  const uint32_t woff = (uint32_t)n * row_bytes + 16 * g;
+  uint32_t woff[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) woff[nt] = (uint32_t)(n0 + nt * 16 + nl) * row_bytes + 16 * g;
   uint32_t aoff[MT];
   bool tok_ok[MT];
 #pragma unroll
@@ -114,45 +118,53 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
     aoff[mt] = (uint32_t)((int64_t)(mt * 16 + nl) * lda);
   }
 
-  v4i acc1[MT], acc4[MT], acc16[MT];
+  v4i acc1[NT][MT], acc4[NT][MT], acc16[NT][MT];
   int sa[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    acc1[mt] = acc4[mt] = acc16[mt] = v4i{0, 0, 0, 0};
-    sa[mt] = 0;
-  }
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc1[nt][mt] = acc4[nt][mt] = acc16[nt][mt] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) sa[mt] = 0;
   const int T = (C + 3) >> 2;
 #pragma unroll 2
   for (int t = w; t < T; t += S) {
     const int c = 4 * t + g;
     const bool ok = c < C;
-    const v4i wv = buf_load16(wb, ok ? woff + 64u * t : w_end);
+    v4i wv[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) wv[nt] = buf_load16(wb, ok ? woff[nt] + 64u * t : w_end);
     const uint32_t ab0 = 128u * (c >> 1) + 16u * (c & 1);
     v4i av[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int f = 0; f < 4; ++f) av[mt][f] = buf_load16(ab, (ok && tok_ok[mt]) ? aoff[mt] + ab0 + 32 * f : a_end);
-    v4i b0, b1, b2, b3;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int d = wv[e];
-      b0[e] = (d >> 2) & 0x30303030;
-      b1[e] = d & 0x30303030;
-      b2[e] = d & 0x0C0C0C0C;
-      b3[e] = d & 0x03030303;
+    for (int nt = 0; nt < NT; ++nt) {
+      v4i b0, b1, b2, b3;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = wv[nt][e];
+        b0[e] = (d >> 2) & 0x30303030;
+        b1[e] = d & 0x30303030;
+        b2[e] = d & 0x0C0C0C0C;
+        b3[e] = d & 0x03030303;
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc16[nt][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][0], b0, acc16[nt][mt], 0, 0, 0);
+        acc16[nt][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][1], b1, acc16[nt][mt], 0, 0, 0);
+        acc4[nt][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][2], b2, acc4[nt][mt], 0, 0, 0);
+        acc1[nt][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][3], b3, acc1[nt][mt], 0, 0, 0);
+      }
     }
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      acc16[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][0], b0, acc16[mt], 0, 0, 0);
-      acc16[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][1], b1, acc16[mt], 0, 0, 0);
-      acc4[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][2], b2, acc4[mt], 0, 0, 0);
-      acc1[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][3], b3, acc1[mt], 0, 0, 0);
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int f = 0; f < 4; ++f)
 #pragma unroll
         for (int e = 0; e < 4; ++e) sa[mt] = __builtin_amdgcn_sdot4(av[mt][f][e], 0x01010101, sa[mt], false);
-    }
   }
   // C layout of a 16x16 tile: lane (nl, g) holds tokens 4g + j (j < 4) of weight row nl.  sum(a) of
   // token nl over this wave's K range: add the 4 lane groups, then fetch token 4g + j's from lane 4g + j.
@@ -164,11 +176,15 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int sj = __shfl(s, 4 * g + j, 64);
-      red[w][mt][j][lane] = acc1[mt][j] + (acc4[mt][j] >> 2) + (acc16[mt][j] >> 4) - sj;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        red[w][nt][mt][j][lane] = acc1[nt][mt][j] + (acc4[nt][mt][j] >> 2) + (acc16[nt][mt][j] >> 4) - sj;
     }
   }
   __syncthreads();
-  if (w != 0) return;
+  if (w >= NT) return;
+  const int nt = w;
+  const int n = n0 + nt * 16 + nl;
   if (ep.amax) {  // argmax epilogue: max over the 16 rows (lanes 16g .. 16g + 15) of each token
     const float ws = n < N ? epi_wscale(ep, n) : 0.0f;
     const float bias = n < N ? epi_bias(ep, n) : 0.0f;
@@ -177,13 +193,14 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int tok = mt * 16 + 4 * g + j;
-        int tot = red[0][mt][j][lane];
+        int tot = red[0][nt][mt][j][lane];
 #pragma unroll
-        for (int k = 1; k < S; ++k) tot += red[k][mt][j][lane];
+        for (int k = 1; k < S; ++k) tot += red[k][nt][mt][j][lane];
         const bool valid = tok < M && n < N;
         const uint64_t key = group_max_u64<16>(epi_store_key(ep, ws, valid ? epi_ascale(ep, tok) : 0.0f, bias, tok, n,
                                                              tot, valid));
-        if (nl == 0 && tok < M) ep.amax[(int64_t)blockIdx.x * M + tok] = key;
+        const int slot = blockIdx.x * NT + nt;  // one slot per 16 rows
+        if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
       }
     return;
   }
@@ -195,22 +212,40 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int tok = mt * 16 + 4 * g + j;
-      int tot = red[0][mt][j][lane];
+      int tot = red[0][nt][mt][j][lane];
 #pragma unroll
-      for (int k = 1; k < S; ++k) tot += red[k][mt][j][lane];
+      for (int k = 1; k < S; ++k) tot += red[k][nt][mt][j][lane];
       if (tok < M) epi_store(ep, ws, epi_ascale(ep, tok), bias, tok, n, tot);
     }
 }
 
+// Launch shape from sweeps on MI355X over the Llama-3-8B / BitNet-2B decode shapes (M = 1..16):
+// enough workgroups for 256 CUs first, then more rows per workgroup (fewer, longer waves and shared
+// activation loads): 4 row tiles x 4 waves for N >= 24576, 2 row tiles x 8 waves for N >= 6144 with
+// K <= 8192, else one row tile x 8 waves (4 for short K).  NT > 1 only at MT <= 2 (LDS).
 template <int MT>
 hipError_t launch_skinny(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
                          hipStream_t s) {
   const int T = (C + 3) / 4;
-  const dim3 grid((n + 15) / 16);
-  if (T >= 8)
-    hipLaunchKernelGGL((gemm_i2s_skinny_kernel<MT, 8>), grid, dim3(512), 0, s, W, A, lda, m, n, C, e);
-  else
-    hipLaunchKernelGGL((gemm_i2s_skinny_kernel<MT, 4>), grid, dim3(256), 0, s, W, A, lda, m, n, C, e);
+  if constexpr (MT == 1) {
+    if (n >= 24576) {
+      hipLaunchKernelGGL((gemm_i2s_skinny_kernel<MT, 4, 4>), dim3((n + 63) / 64), dim3(256), 0, s, W, A, lda, m, n, C,
+                         e);
+      return hipGetLastError();
+    }
+  }
+  if constexpr (MT <= 2) {
+    if (n >= 6144 && C <= 128) {
+      hipLaunchKernelGGL((gemm_i2s_skinny_kernel<MT, 8, 2>), dim3((n + 31) / 32), dim3(512), 0, s, W, A, lda, m, n, C,
+                         e);
+      return hipGetLastError();
+    }
+  }
+  if (T >= 8) {
+    hipLaunchKernelGGL((gemm_i2s_skinny_kernel<MT, 8, 1>), dim3((n + 15) / 16), dim3(512), 0, s, W, A, lda, m, n, C, e);
+  } else {
+    hipLaunchKernelGGL((gemm_i2s_skinny_kernel<MT, 4, 1>), dim3((n + 15) / 16), dim3(256), 0, s, W, A, lda, m, n, C, e);
+  }
   return hipGetLastError();
 }
 

@@ -284,7 +284,7 @@ hipError_t launch_argmax_finalize(const uint64_t* parts, int64_t n_parts, int64_
 hipError_t launch_lm_head_argmax(const void* x, int xdt, int64_t ldx, const void* gamma, int gdt, float eps,
                                  const void* w, int wdt, int64_t ldw, int64_t m, int64_t n, int64_t h, float* logits,
                                  int64_t ldo, uint64_t* parts, hipStream_t s);
-// 3 <= M <= 64 through the split-K skinny kernel (grid = ceil(N / 16) workgroups of 16 rows); needs
+// 3 <= M <= 64 through the split-K skinny kernel (16, 32 or 64 rows per workgroup); needs
 // N*K/4 and (M-1)*lda + K below 2^31
 hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                                   const Epilogue& e, hipStream_t s);
