@@ -196,6 +196,17 @@ int wfb_glu_rmsnorm_quant_i8(const void* gate, const void* up, int x_dtype, int6
                              const void* gamma, int gamma_dtype, float eps, int64_t m, int64_t h,
                              int8_t* q, int64_t k_pad, int64_t ldq, float* a_scale, void* stream);
 
+/* The BitLinear with the residual connection fused into the epilogue:
+ *   out[m, n] = ((float)acc * w_scale) * a_scale[m] + residual[m, n]   (fp32 add, then out_dtype)
+ * residual [M, N] of residual_dtype (WFB_F32 or WFB_BF16, row stride ldr); out may be the residual
+ * buffer itself (each element is read and written by the same thread).  Other arguments as
+ * wfb_linear_i2s.  Replaces the linear + residual add of the engine's layer step
+ * (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:517-536: hidden = residual + attn_out / mlp_out). */
+int wfb_linear_i2s_residual(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m,
+                            int64_t lda, const float* a_scale, const float* w_scale_dev, float w_scale,
+                            const void* residual, int residual_dtype, int64_t ldr, void* out, int out_dtype,
+                            int64_t ldo, void* stream);
+
 /* ---- greedy decoding: LM head + argmax ------------------------------------------------------ */
 
 /* uint64 elements of the workspace of the argmax entry points for M tokens and N vocabulary rows

@@ -45,6 +45,19 @@ class OracleBackend:
         (logits,) = self.norm_linears(x, norm_weight, eps, [linear])
         return torch.argmax(logits, dim=-1)  # first maximum
 
+    def _residual(self, y, residual):
+        # the fused epilogue: fp32 add of the rescaled output and the residual, then the residual's dtype
+        r = residual.float().cpu().numpy()
+        return torch.from_numpy((y.float().cpu().numpy() + r).astype(np.float32)).to(self.dev).to(residual.dtype)
+
+    def norm_linear_residual(self, x, norm_weight, eps, linear, residual):
+        (y,) = self.norm_linears(x, norm_weight, eps, [linear])
+        return self._residual(y, residual)
+
+    def glu_norm_linear_residual(self, gate, up, act, norm_weight, eps, linear, residual):
+        (y,) = self.glu_norm_linears(gate, up, act, norm_weight, eps, [linear])
+        return self._residual(y, residual)
+
     def glu_norm_linears(self, gate, up, act, norm_weight, eps, linears):
         g = None if norm_weight is None else norm_weight.float().cpu().numpy()
         code = orc.ACT_SILU if act == "silu" else orc.ACT_RELU2

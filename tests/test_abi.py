@@ -165,3 +165,16 @@ def test_argmax_argument_errors(pkg):
     st = pkg._lib.status("wfb_lm_head_argmax", vp(16), 0, 64, None, 0, 1e-5, vp(8), 0, 64, 1, 100, 64, None, 100,
                          vp(16), vp(16), None)
     assert st == -1 and "aligned" in pkg._lib.last_error()
+
+
+def test_residual_argument_errors(pkg):
+    vp = ctypes.c_void_p
+    st = pkg._lib.status("wfb_linear_i2s_residual", vp(16), 64, 128, vp(16), 2, 128, None, None, 1.0, vp(16), 2, 64,
+                         vp(16), 1, 64, None)
+    assert st == -1 and "residual dtype" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_linear_i2s_residual", vp(16), 64, 128, vp(16), 2, 128, None, None, 1.0, None, 1, 64,
+                         vp(16), 1, 64, None)
+    assert st == -1 and "null residual" in pkg._lib.last_error()
+    st = pkg._lib.status("wfb_linear_i2s_residual", vp(16), 64, 128, vp(16), 2, 128, None, None, 1.0, vp(16), 1, 32,
+                         vp(16), 1, 64, None)
+    assert st == -1 and "residual row stride" in pkg._lib.last_error()

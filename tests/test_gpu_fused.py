@@ -124,3 +124,23 @@ def test_bitnet_linear_native_module(pkg, dev):
         acc = orc.accumulate(packed, q.reshape(m, k))
         y_ref = orc.rescale(acc, ws, np.full(m, a_s, np.float32), bias)
         assert np.array_equal(y, y_ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 2560, 2560), (8, 4096, 14336), (3, 640, 1024), (200, 2560, 6912), (64, 520, 512)])
+@pytest.mark.parametrize("rdt", [torch.float32, torch.bfloat16])
+def test_linear_residual_matches_oracle(pkg, dev, m, n, k, rdt):
+    """out = residual + acc * w_scale * a_scale in one launch (GEMV, skinny and tile kernels): the fp32
+    sum of the oracle's rescaled output and the residual, rounded to the residual's dtype; in place too."""
+    rng = np.random.default_rng(m + n + k)
+    packed = orc.pack_i2s(orc.random_ternary(rng, n, k))
+    a = orc.random_int8(rng, m, k)
+    ws, a_s = orc.log_uniform(rng), orc.log_uniform(rng, m)
+    res = torch.from_numpy(rng.standard_normal((m, n)).astype(np.float32)).to(rdt)
+    acc = (a.astype(np.float32) @ orc.unpack_i2s(packed).astype(np.float32).T).astype(np.int64)
+    want = torch.from_numpy(orc.rescale(acc, np.float32(ws), a_s) + res.float().numpy()).to(rdt)
+    pw, at, st = (torch.from_numpy(x).to(dev) for x in (packed, a, a_s))
+    got = pkg.bitnet_linear_residual(pw, at, float(ws), res.to(dev), a_scale=st)
+    assert torch.equal(got.cpu(), want)
+    buf = res.to(dev)
+    pkg.bitnet_linear_residual(pw, at, float(ws), buf, a_scale=st, out=buf)
+    assert torch.equal(buf.cpu(), want)

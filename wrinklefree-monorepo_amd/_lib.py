@@ -47,6 +47,8 @@ SIGNATURES = {
                                  _vp, _vp],
     "wfb_glu_rmsnorm_quant_i8": [_vp, _vp, _int, _i64, _int, _vp, _int, _f32, _i64, _i64, _vp, _i64, _i64, _vp, _vp],
     "wfb_convert_hf_offline_i2s": [_vp, _i64, _i64, _i64, _i64, _vp, _int, _f32, _int, _vp, _vp, _vp, _vp],
+    "wfb_linear_i2s_residual": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _int, _i64, _vp, _int, _i64,
+                                _vp],
     "wfb_linear_i2s_argmax": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _int, _i64, _vp, _vp, _vp],
     "wfb_lm_head_argmax": [_vp, _int, _i64, _vp, _int, _f32, _vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp,
                            _vp],

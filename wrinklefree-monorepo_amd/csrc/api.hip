@@ -52,7 +52,8 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
                 int64_t m, int64_t lda, const float* a_scale, const float* w_scale_dev, float w_scale,
                 const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo, int32_t* acc_out,
                 void* stream, int n_seg = 1, const int64_t* seg_rows = nullptr, uint64_t* amax = nullptr,
-                int amax_dt = WFB_F32, int64_t* tokens = nullptr) {
+                int amax_dt = WFB_F32, int64_t* tokens = nullptr, const void* res = nullptr, int res_dtype = 0,
+                int64_t ldr = 0) {
   if (n <= 0 || k <= 0 || m < 0) return fail(WFB_EINVAL, "%s: bad sizes m=%lld n=%lld k=%lld", name, (long long)m, (long long)n, (long long)k);
   if (k % WFB_QK_I2S != 0)
     return fail(WFB_EINVAL, "%s: K (%lld) must be multiple of %d", name, (long long)k, WFB_QK_I2S);
@@ -91,6 +92,9 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
   e.acc_out = acc_out;
   e.amax = amax;
   e.amax_dt = amax_dt;
+  e.res = res;
+  e.res_dtype = res_dtype;
+  e.ldr = ldr;
 
   const bool gemv = kind == Kernel::Gemv || (kind == Kernel::Auto && use_gemv(m, n, k, lda));
   if (amax) {  // greedy argmax: GEMV (M <= 2) or the skinny MFMA kernel, then the cross-workgroup maximum
@@ -261,6 +265,19 @@ int wfb_convert_hf_offline_i2s(const uint8_t* packed_hf, int64_t nb, int64_t n, 
                                                    weight_scale, scale_mode, qweight, scale_out, workspace,
                                                    as_stream(stream)),
                     name);
+}
+
+int wfb_linear_i2s_residual(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m, int64_t lda,
+                            const float* a_scale, const float* w_scale_dev, float w_scale, const void* residual,
+                            int residual_dtype, int64_t ldr, void* out, int out_dtype, int64_t ldo, void* stream) {
+  const char* name = "wfb_linear_i2s_residual";
+  if (residual_dtype != WFB_F32 && residual_dtype != WFB_BF16)
+    return fail(WFB_EINVAL, "%s: residual dtype must be WFB_F32 or WFB_BF16", name);
+  if (m > 0 && (!residual || !out)) return fail(WFB_EINVAL, "%s: null residual or out", name);
+  if (ldr < n) return fail(WFB_EINVAL, "%s: residual row stride (%lld) < N (%lld)", name, (long long)ldr, (long long)n);
+  return linear_impl(Kernel::Auto, name, qweight, n, k, act, m, lda, a_scale, w_scale_dev, w_scale, nullptr, 0, out,
+                     out_dtype, ldo, nullptr, stream, 1, nullptr, nullptr, WFB_F32, nullptr, residual, residual_dtype,
+                     ldr);
 }
 
 int wfb_linear_i2s_argmax(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m, int64_t lda,

@@ -516,7 +516,7 @@ hipError_t launch_tile(const uint8_t* W, int n, int k, const int8_t* A, int m, i
   const int nwg = tiles_n * tiles_m;
   const int grid = ((nwg + 7) / 8) * 8;
   const bool vec_out = e.ldo % 4 == 0 && (uintptr_t)e.out % 16 == 0 && (uintptr_t)e.acc_out % 16 == 0;
-  const bool bf16_only = e.out && e.out_dtype == WFB_BF16 && !e.bias && !e.acc_out && e.ldo % 8 == 0 &&
+  const bool bf16_only = e.out && e.out_dtype == WFB_BF16 && !e.bias && !e.acc_out && !e.res && e.ldo % 8 == 0 &&
                          (uintptr_t)e.out % 16 == 0;
   if (bf16_only)
     hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 1>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,

@@ -138,7 +138,17 @@ struct Epilogue {
   // is y rounded to amax_dt (WFB_F32 or WFB_BF16), i.e. the logit as stored.
   uint64_t* amax;
   int amax_dt;
+  // Residual added to every output before it is stored (y = ... + res[m, n]), or null.
+  const void* res;
+  int res_dtype;
+  int64_t ldr;
 };
+
+__device__ __forceinline__ float epi_res(const Epilogue& e, int m, int n) {
+  const int64_t off = (int64_t)m * e.ldr + n;
+  if (e.res_dtype == WFB_F32) return reinterpret_cast<const float*>(e.res)[off];
+  return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(e.res)[off]);
+}
 
 // Orderable 64-bit key of (value y, row n): larger y wins, and among equal values the smaller row
 // (the first maximum, as std::max_element and torch.argmax pick).  Never 0 for n < 2^32 - 1.
@@ -195,7 +205,8 @@ __device__ __forceinline__ void epi_store(const Epilogue& e, float ws, float as,
   const int64_t off = (int64_t)m * e.ldo + n;
   if (e.acc_out) e.acc_out[off] = acc;
   if (!e.out) return;
-  const float y = epi_y(e, ws, as, bias, acc);
+  float y = epi_y(e, ws, as, bias, acc);
+  if (e.res) y = __fadd_rn(y, epi_res(e, m, n));
   if (e.out_dtype == WFB_F32) reinterpret_cast<float*>(e.out)[off] = y;
   else reinterpret_cast<uint16_t*>(e.out)[off] = f32_to_bf16_rne(y);
 }
@@ -206,6 +217,7 @@ __device__ __forceinline__ uint64_t epi_store_key(const Epilogue& e, float ws, f
   if (!valid) return 0;
   epi_store(e, ws, as, bias, m, n, acc);
   float y = epi_y(e, ws, as, bias, acc);
+  if (e.res) y = __fadd_rn(y, epi_res(e, m, n));
   if (e.amax_dt == WFB_BF16) y = bf16_bits_to_f32(f32_to_bf16_rne(y));
   return amax_key(y, n);
 }
@@ -234,6 +246,7 @@ __device__ __forceinline__ void epi_store4(const Epilogue& e, float ws, float as
   for (int j = 0; j < 4; ++j) {
     y[j] = __fmul_rn(__fmul_rn((float)v[j], ws), as);
     if (e.bias && n + j < N) y[j] = __fadd_rn(y[j], epi_bias(e, n + j));
+    if (e.res && n + j < N) y[j] = __fadd_rn(y[j], epi_res(e, m, n + j));
   }
   if (e.out_dtype == WFB_F32) {
     float* o = reinterpret_cast<float*>(e.out) + off;

@@ -28,8 +28,9 @@ from typing import Dict, List, Optional, Sequence
 import torch
 
 from .sglbitnt import SGLBitNetFile, write_sglbitnt
-from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_segmented, glu_rmsnorm_quantize_i8,
-                  gqa_decode_attention, lm_head_argmax, pack_ternary_i2s, rmsnorm_quantize_i8)
+from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_residual, bitnet_linear_segmented,
+                  glu_rmsnorm_quantize_i8, gqa_decode_attention, lm_head_argmax, pack_ternary_i2s,
+                  rmsnorm_quantize_i8)
 
 
 @dataclass(frozen=True)
@@ -142,6 +143,28 @@ class HipBackend:
             self._linears(q, a_scale, [linear])
         return bitnet_linear_argmax(linear.qweight, q, linear.scale, a_scale=a_scale, logits_dtype=self.out_dtype)
 
+    def _linear_residual(self, q: torch.Tensor, a_scale: torch.Tensor, linear: PackedLinear,
+                         residual: torch.Tensor) -> torch.Tensor:
+        if self.keep_acc:
+            self._linears(q, a_scale, [linear])[0]
+        return bitnet_linear_residual(linear.qweight, q, linear.scale, residual.contiguous(), a_scale=a_scale)
+
+    def norm_linear_residual(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], eps: float,
+                             linear: PackedLinear, residual: torch.Tensor) -> torch.Tensor:
+        """residual + linear(quantise(norm(x))), the add fused into the linear's epilogue (fp32 add, then
+        the residual's dtype)."""
+        q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=linear.k_pad)
+        return self._linear_residual(q, a_scale, linear, residual)
+
+    def glu_norm_linear_residual(self, gate: torch.Tensor, up: torch.Tensor, act: str,
+                                 norm_weight: Optional[torch.Tensor], eps: float, linear: PackedLinear,
+                                 residual: torch.Tensor) -> torch.Tensor:
+        """residual + linear(quantise(SubLN(act(gate) * up)))."""
+        if gate.stride(-1) != 1 or up.stride(-1) != 1 or gate.stride(0) != up.stride(0):
+            gate, up = gate.contiguous(), up.contiguous()
+        q, a_scale = glu_rmsnorm_quantize_i8(gate, up, act, norm_weight, eps=eps, k_pad=linear.k_pad)
+        return self._linear_residual(q, a_scale, linear, residual)
+
     def glu_norm_linears(self, gate: torch.Tensor, up: torch.Tensor, act: str, norm_weight: Optional[torch.Tensor],
                          eps: float, linears: Sequence[PackedLinear]) -> List[torch.Tensor]:
         """act(gate) * up -> SubLN -> per-token int8 -> linears (one kernel before the projections)."""
@@ -195,6 +218,7 @@ class BitNetDecoder:
         if decode_attention not in ("hip", "torch"):
             raise ValueError("decode_attention must be 'hip' or 'torch'")
         self.decode_attention = decode_attention
+        self.fuse_residual = True  # residual adds in the o / down epilogues when the backend offers it
         self.cfg = cfg
         self.device = torch.device(device)
         self.dtype = dtype
@@ -390,12 +414,20 @@ class BitNetDecoder:
             h2 = x.reshape(b * t, cfg.hidden_size)
             q, k, v = be.norm_linears(h2, L.input_norm, cfg.rms_eps, [L.q, L.k, L.v])
             attn = attend(li, q.to(self.dtype), k.to(self.dtype), v.to(self.dtype)).reshape(b * t, -1)
-            (o,) = be.norm_linears(attn, L.attn_sub_norm, cfg.subln_eps, [L.o])
-            x = x + o.reshape(b, t, -1).to(self.dtype)
+            fused_res = self.fuse_residual and hasattr(be, "norm_linear_residual")
+            if fused_res:
+                x = be.norm_linear_residual(attn, L.attn_sub_norm, cfg.subln_eps, L.o, h2).reshape(b, t, -1)
+            else:
+                (o,) = be.norm_linears(attn, L.attn_sub_norm, cfg.subln_eps, [L.o])
+                x = x + o.reshape(b, t, -1).to(self.dtype)
             h2 = x.reshape(b * t, cfg.hidden_size)
             gate, up = be.norm_linears(h2, L.post_attn_norm, cfg.rms_eps, [L.gate, L.up])
-            (down,) = be.glu_norm_linears(gate, up, cfg.hidden_act, L.ffn_sub_norm, cfg.subln_eps, [L.down])
-            x = x + down.reshape(b, t, -1).to(self.dtype)
+            if fused_res:
+                x = be.glu_norm_linear_residual(gate, up, cfg.hidden_act, L.ffn_sub_norm, cfg.subln_eps, L.down,
+                                                h2).reshape(b, t, -1)
+            else:
+                (down,) = be.glu_norm_linears(gate, up, cfg.hidden_act, L.ffn_sub_norm, cfg.subln_eps, [L.down])
+                x = x + down.reshape(b, t, -1).to(self.dtype)
         return x
 
     def _logits(self, last: torch.Tensor) -> torch.Tensor:

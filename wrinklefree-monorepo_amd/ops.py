@@ -427,6 +427,46 @@ def glu_rmsnorm_quantize_i8(
     return (q if kpa == kp else q[..., :kp]), a_scale
 
 
+def bitnet_linear_residual(
+    packed_weights: torch.Tensor, activations: torch.Tensor, scale: Scale, residual: torch.Tensor,
+    a_scale: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """residual + BitLinear in one launch: out[m, n] = acc * scale * a_scale[m] + residual[m, n] (fp32 add,
+    stored in residual's dtype, float32 or bfloat16).  ``out`` may be ``residual`` itself (in place)."""
+    name = "bitnet_linear_residual"
+    if packed_weights.dtype != torch.uint8 or packed_weights.dim() != 2:
+        raise RuntimeError(f"{name}: packed_weights must be uint8 2D [out_features, in_features/4]")
+    if activations.dtype != torch.int8 or activations.dim() != 2:
+        raise RuntimeError(f"{name}: activations must be int8 [batch, in_features]")
+    n, kb = packed_weights.shape
+    k = kb * 4
+    if k % QK_I2_S != 0 or activations.shape[1] != k:
+        raise ValueError(f"{name}: in_features must be a multiple of {QK_I2_S} and match the weights")
+    m = activations.shape[0]
+    dev = _require_gpu(name, packed_weights, a_scale)
+    a2 = activations
+    if a2.device != dev or residual.device != dev:
+        raise RuntimeError(f"{name}: tensors must be on {dev}")
+    if a2.stride(1) != 1 or (m > 1 and a2.stride(0) % 16 != 0) or a2.data_ptr() % 16 != 0:
+        a2 = a2.contiguous()
+    if a_scale is not None and (a_scale.dtype != torch.float32 or a_scale.numel() != m):
+        raise RuntimeError(f"{name}: a_scale must be fp32 with one element per token ({m})")
+    if residual.dtype not in (torch.float32, torch.bfloat16) or residual.shape != (m, n) or residual.stride(-1) != 1:
+        raise RuntimeError(f"{name}: residual must be float32/bfloat16 [{m}, {n}] with contiguous rows")
+    if out is None:
+        out = torch.empty((m, n), dtype=residual.dtype, device=dev)
+    elif out.dtype != residual.dtype or out.shape != (m, n) or out.stride(-1) != 1:
+        raise RuntimeError(f"{name}: out must match the residual's dtype and shape")
+    ws_dev, ws = _scale_args(name, scale, dev)
+    lda = a2.stride(0) if m > 1 else k
+    ldr = residual.stride(0) if m > 1 else n
+    ldo = out.stride(0) if m > 1 else n
+    with torch.cuda.device(dev):
+        _lib.call("wfb_linear_i2s_residual", _p(packed_weights), n, k, _p(a2), m, lda, _p(a_scale), ws_dev, ws,
+                  _p(residual), _DT[residual.dtype], ldr, _p(out), _DT[out.dtype], ldo, _stream(dev))
+    return out
+
+
 # ---- greedy decoding: LM head + argmax ----------------------------------------------------------
 
 
