@@ -439,6 +439,25 @@ def e2e_cpu_baseline(M, model, prompt, torch, new_tokens: int = 12):
                       f"tokens on the host (torch CPU float glue, numpy-oracle BitLinears, BLAS threads = cores)"}
 
 
+def device_copy_gbs(torch, dev, nbytes: int = 1 << 30) -> float:
+    """Measured HBM bandwidth of a plain device-to-device copy of 1 GiB (bytes read + written per
+    second), the practical ceiling next to the 8 TB/s peak."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / 10
+    del src, dst
+    return 2 * nbytes / sec / 1e9
+
+
 def measured_traffic(n: int, k: int):
     """HBM bytes per launch of the M=1 GEMV at (n, k) from the committed FETCH_SIZE / WRITE_SIZE
     profile (profiles/gemv_i2s_decode_bitnet2b.txt, calibrated against a plain copy kernel), or None."""
@@ -537,12 +556,17 @@ def main():
         shapes.append(dict(n=n, k=k, calls=calls, bytes=gemv_bytes(1, n, k), copies=copies))
     torch.cuda.synchronize()
 
+    copy_gbs = device_copy_gbs(torch, dev)
     per_shape = []
     for s in shapes:
         ms = timed(torch, [[c] for c in s["calls"]], args.steps, args.warmup)
+        ms_warm = timed(torch, [[s["calls"][0]]], args.steps, args.warmup)  # same weights every launch
         gbs = s["bytes"] / (ms * 1e-3) / 1e9
         per_shape.append({"N": s["n"], "K": s["k"], "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-                          "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+                          "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                          "frac_measured_copy": round(gbs / copy_gbs, 4),
+                          "warm_us": round(ms_warm * 1e3, 3),
+                          "warm_GB/s": round(s["bytes"] / (ms_warm * 1e-3) / 1e9, 1)})
     step_fns = [[s["calls"][i] for s in shapes] for i in range(N_COPIES)]
     ms_step = timed(torch, step_fns, args.steps, args.warmup)
     step_bytes = sum(s["bytes"] for s in shapes)
@@ -637,6 +661,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "device_copy_GB/s": round(copy_gbs, 1),
         "gemv_per_shape": per_shape,
         "prefill_gemm": prefill,
         "rmsnorm_quant": normq,
