@@ -363,9 +363,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
       const int R = (wn * TN + tn) * 32 + i;
       boffs[u][tn] = R * BROW + (((2 * u + g) ^ bswz(R)) * 16);
     }
-  const int srow = wn * (BM / 4) + l / LPR;  // wave wn sums rows [wn BM/4, (wn + 1) BM/4)
+  // Wave wn sums rows [wn BM/4, (wn + 1) BM/4); lane part l % LPR of a row reads its SCH chunk positions
+  // starting at a row-dependent rotation, so 16 consecutive lanes hit 16 distinct 16-byte bank groups
+  // (without it, rows 256 B apart read the same group: a 4-way conflict).  The sum does not depend on
+  // the order in which a row's chunks are read.
+  const int srow = wn * (BM / 4) + l / LPR;
 #pragma unroll
-  for (int j = 0; j < SCH; ++j) soffs[j] = srow * AROW + ((l % LPR) * SCH + j) * 16;
+  for (int j = 0; j < SCH; ++j) soffs[j] = srow * AROW + ((l % LPR) * SCH + ((j + srow + (srow >> 2)) % SCH)) * 16;
   int ssum = 0;
 
   v16i acc[TN][TM];
