@@ -118,6 +118,17 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
     aoff[mt] = (uint32_t)((int64_t)(mt * 16 + nl) * lda);
   }
 
+  // Epilogue operands of the column this lane stores (waves w < NT; tokens 16 mt + 4 g + j), loaded
+  // here, ahead of the weight stream -- measured on MI355X: 5-10% faster at M = 8..64 on 4096-row
+  // outputs -- except with four row tiles (N >= 24576), where loading them after the final barrier is
+  // 3% faster (fewer registers).
+  constexpr bool PRE = NT < 4;
+  int toks[4 * MT];
+#pragma unroll
+  for (int j = 0; j < 4 * MT; ++j) toks[j] = (j / 4) * 16 + 4 * g + (j % 4);
+  EpiCol<4 * MT> col;
+  if (PRE && w < NT) col.load(ep, n0 + w * 16 + nl, N, toks, M);
+
   v4i acc1[NT][MT], acc4[NT][MT], acc16[NT][MT];
   int sa[MT];
 #pragma unroll
@@ -186,8 +197,8 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
   const int nt = w;
   const int n = n0 + nt * 16 + nl;
   if (ep.amax) {  // argmax epilogue: max over the 16 rows (lanes 16g .. 16g + 15) of each token
-    const float ws = n < N ? epi_wscale(ep, n) : 0.0f;
-    const float bias = n < N ? epi_bias(ep, n) : 0.0f;
+    const float ws = PRE ? col.ws : n < N ? epi_wscale(ep, n) : 0.0f;
+    const float bias = PRE ? col.bias : n < N ? epi_bias(ep, n) : 0.0f;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -197,16 +208,20 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
 #pragma unroll
         for (int k = 1; k < S; ++k) tot += red[k][nt][mt][j][lane];
         const bool valid = tok < M && n < N;
-        const uint64_t key = group_max_u64<16>(epi_store_key(ep, ws, valid ? epi_ascale(ep, tok) : 0.0f, bias, tok, n,
-                                                             tot, valid));
+        uint64_t key;
+        if constexpr (PRE)
+          key = epi_store_key_r(ep, ws, col.as[4 * mt + j], bias, col.res[4 * mt + j], tok, n, tot, valid);
+        else
+          key = epi_store_key(ep, ws, valid ? epi_ascale(ep, tok) : 0.0f, bias, tok, n, tot, valid);
+        key = group_max_u64<16>(key);
         const int slot = blockIdx.x * NT + nt;  // one slot per 16 rows
         if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
       }
     return;
   }
   if (n >= N) return;
-  const float ws = epi_wscale(ep, n);
-  const float bias = epi_bias(ep, n);
+  const float ws = PRE ? col.ws : epi_wscale(ep, n);
+  const float bias = PRE ? col.bias : epi_bias(ep, n);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -215,7 +230,10 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
       int tot = red[0][nt][mt][j][lane];
 #pragma unroll
       for (int k = 1; k < S; ++k) tot += red[k][nt][mt][j][lane];
-      if (tok < M) epi_store(ep, ws, epi_ascale(ep, tok), bias, tok, n, tot);
+      if (tok < M) {
+        if constexpr (PRE) epi_store_r(ep, ws, col.as[4 * mt + j], bias, col.res[4 * mt + j], tok, n, tot);
+        else epi_store(ep, ws, epi_ascale(ep, tok), bias, tok, n, tot);
+      }
     }
 }
 
@@ -295,7 +313,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
   constexpr int BLPR = BROW / 16;                  // lanes per weight row in a load instruction
   constexpr int X = 4 * KB;                        // (block, field) MFMA steps per stage
   constexpr int LPR = 256 / BM, SCH = CH / LPR;    // sum(a): lanes per row, chunks per lane
-  static_assert(AI >= 1 && BI >= 1 && ASZ >= 8192 && BSZ >= 8192 && SCH >= 1 && SCH <= X, "tile shape");
+  static_assert(AI >= 1 && BI >= 1 && ASZ >= 8192 && BSZ >= 8192 && SCH >= 1 && SCH <= X && LPR <= 8, "tile shape");
   __shared__ __attribute__((aligned(16))) int8_t lds_a0[ASZ];
   __shared__ __attribute__((aligned(16))) int8_t lds_a1[ASZ];
   __shared__ __attribute__((aligned(16))) uint8_t lds_b0[BSZ];
@@ -441,8 +459,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
   }
 
   // sum(a) per row: the LPR lanes of a row (consecutive) hold partial sums of its chunks
-  ssum += __builtin_amdgcn_update_dpp(0, ssum, 0xB1, 0xF, 0xF, false);    // quad_perm 1,0,3,2
-  if constexpr (LPR == 4) ssum += __builtin_amdgcn_update_dpp(0, ssum, 0x4E, 0xF, 0xF, false);  // 2,3,0,1
+  if constexpr (LPR >= 2) ssum += __builtin_amdgcn_update_dpp(0, ssum, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+  if constexpr (LPR >= 4) ssum += __builtin_amdgcn_update_dpp(0, ssum, 0x4E, 0xF, 0xF, false);  // 2,3,0,1
+  if constexpr (LPR >= 8) ssum += __shfl_xor(ssum, 4);
   if ((l % LPR) == 0) rowsum[srow] = ssum;
   __syncthreads();  // also: every wave is done reading the operand buffers
 
@@ -568,11 +587,15 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   if (m <= 16) return launch_mt<1>(W, n, C, A, m, lda, e, s);
   if (m <= 32) return launch_mt<2>(W, n, C, A, m, lda, e, s);
   if (m <= 64) return launch_mt<4>(W, n, C, A, m, lda, e, s);
-  // measured on MI355X: 128-row tiles (half the weight unpack per MFMA) pay off for wide N and enough
-  // rows; for narrow N or M <= 512 (few tiles) 64-row tiles with 256-weight stages keep more
-  // workgroups busy (M = 512, N = 13824: 27.0 -> 24.9 us)
-  if (n >= 4096 && m > 512) return launch_tile<4, 1, 2>(W, n, k, A, m, lda, e, s);
-  return launch_tile<2, 2, 2>(W, n, k, A, m, lda, e, s);
+  // Tile height by the number of 256-column tiles (512 workgroup slots at two per CU), measured on
+  // MI355X: 128-row tiles (half the weight unpack per MFMA) once there are enough of them (wide N and
+  // M > 512, or >= 512 tiles: M = 8192, N = 2560 172.6 vs 179.5 us); 64-row tiles in between; 32-row
+  // tiles when even 64-row ones leave most of the chip idle (M = 512, N = 2560, K = 6912: 21.7 vs
+  // 30.8 us).
+  const int64_t tn = (n + 255) / 256, t128 = tn * ((m + 127) / 128), t64 = tn * ((m + 63) / 64);
+  if ((n >= 4096 && m > 512) || t128 >= 512) return launch_tile<4, 1, 2>(W, n, k, A, m, lda, e, s);
+  if (t64 >= 160) return launch_tile<2, 2, 2>(W, n, k, A, m, lda, e, s);
+  return launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
 }
 
 }  // namespace wfb

@@ -40,7 +40,7 @@ __device__ __forceinline__ int wave_sum(int v) {
   return v;
 }
 
-template <int M, int L, int CPL, int RP, int S, bool EXACT>
+template <int M, int L, int CPL, int RP, int S, bool EXACT, bool PRE>
 __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restrict__ W,
                                                           const int8_t* __restrict__ A, int64_t lda, int N,
                                                           int C, Epilogue ep) {
@@ -69,6 +69,17 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
       if (!EXACT && c >= C) wv[p][i] = v4i{0, 0, 0, 0};
     }
   }
+  // Epilogue operands of the row this thread stores (thread t < RB stores row row0 + t): loaded here
+  // (PRE) or after the final barrier.  Measured on MI355X: loading them early saves 2-3% on grids of a
+  // few hundred short workgroups and costs 4-8% on the tall shapes (N >= 8192).
+  const int t = threadIdx.x;
+  const int n = row0 + t;
+  int toks[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) toks[m] = m;
+  EpiCol<M> col;
+  if (PRE && t < RB) col.load(ep, n, N, toks, M);
+
   // a[m][i][q] = a_m[128b + 32q + j0 .. +15] for chunk c (b = c/2, j0 = 16*(c%2))
   v4i a[M][CPL][4];
 #pragma unroll
@@ -133,13 +144,11 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
     }
   }
   __syncthreads();
-  const int t = threadIdx.x;
-  const int n = row0 + t;
   if (ep.amax) {  // argmax epilogue: the RB <= 64 rows sit in wave 0
     if (t >= 64) return;
     const bool valid = t < RB && n < N;
-    const float ws = valid ? epi_wscale(ep, n) : 0.0f;
-    const float bias = valid ? epi_bias(ep, n) : 0.0f;
+    const float ws = PRE ? col.ws : valid ? epi_wscale(ep, n) : 0.0f;
+    const float bias = PRE ? col.bias : valid ? epi_bias(ep, n) : 0.0f;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       int tot = 0;
@@ -148,7 +157,10 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
 #pragma unroll
         for (int k = 1; k < S; ++k) tot += red[k][m][t];
       }
-      const uint64_t key = group_max_u64<64>(epi_store_key(ep, ws, epi_ascale(ep, m), bias, m, n, tot, valid));
+      uint64_t key;
+      if constexpr (PRE) key = epi_store_key_r(ep, ws, col.as[m], bias, col.res[m], m, n, tot, valid);
+      else key = epi_store_key(ep, ws, epi_ascale(ep, m), bias, m, n, tot, valid);
+      key = group_max_u64<64>(key);
       // slots are per 16 rows: the workgroup's first slot takes its maximum, the others key 0
       const int slot = row0 / 16 + t;
       if (t < RB / 16 && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + m] = t == 0 ? key : 0;
@@ -157,26 +169,27 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   }
   if (t >= RB) return;
   if (n >= N) return;
-  const float ws = epi_wscale(ep, n);
-  const float bias = epi_bias(ep, n);
+  const float ws = PRE ? col.ws : epi_wscale(ep, n);
+  const float bias = PRE ? col.bias : epi_bias(ep, n);
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     int tot = red[0][m][t];
 #pragma unroll
     for (int k = 1; k < S; ++k) tot += red[k][m][t];
-    epi_store(ep, ws, epi_ascale(ep, m), bias, m, n, tot);
+    if constexpr (PRE) epi_store_r(ep, ws, col.as[m], bias, col.res[m], m, n, tot);
+    else epi_store(ep, ws, epi_ascale(ep, m), bias, m, n, tot);
   }
 }
 
-template <int M, int L, int CPL, int RP, int S>
+template <int M, int L, int CPL, int RP, int S, bool PRE = true>
 hipError_t launch_cfg(const uint8_t* W, int n, int C, const int8_t* A, int64_t lda, const Epilogue& e,
                       hipStream_t st) {
   constexpr int RB = RP * (64 / L);
   const dim3 grid((n + RB - 1) / RB), block(64 * S);
   if (C == L * CPL * S)
-    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true>), grid, block, 0, st, W, A, lda, n, C, e);
+    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true, PRE>), grid, block, 0, st, W, A, lda, n, C, e);
   else
-    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, false>), grid, block, 0, st, W, A, lda, n, C, e);
+    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, false, PRE>), grid, block, 0, st, W, A, lda, n, C, e);
   return hipGetLastError();
 }
 
@@ -189,8 +202,10 @@ hipError_t launch_m(const uint8_t* W, int n, int C, const int8_t* A, int64_t lda
   if (C <= 8) return launch_cfg<M, 8, 1, 2, 1>(W, n, C, A, lda, e, s);
   if (C <= 16) return launch_cfg<M, 8, 1, 2, 2>(W, n, C, A, lda, e, s);
   if (C <= 24) return launch_cfg<M, 8, 1, 2, 3>(W, n, C, A, lda, e, s);
-  if (C <= 40) return tall ? launch_cfg<M, 8, 1, 4, 5>(W, n, C, A, lda, e, s) : launch_cfg<M, 8, 1, 2, 5>(W, n, C, A, lda, e, s);
-  if (C <= 64) return tall ? launch_cfg<M, 8, 1, 4, 8>(W, n, C, A, lda, e, s) : launch_cfg<M, 8, 1, 2, 8>(W, n, C, A, lda, e, s);
+  if (C <= 40)
+    return tall ? launch_cfg<M, 8, 1, 4, 5, false>(W, n, C, A, lda, e, s) : launch_cfg<M, 8, 1, 2, 5>(W, n, C, A, lda, e, s);
+  if (C <= 64)
+    return tall ? launch_cfg<M, 8, 1, 4, 8, false>(W, n, C, A, lda, e, s) : launch_cfg<M, 8, 1, 2, 8>(W, n, C, A, lda, e, s);
   if (C <= 112) return launch_cfg<M, 16, 1, 4, 7>(W, n, C, A, lda, e, s);
   if (C <= 224) return launch_cfg<M, 16, 1, 4, 14>(W, n, C, A, lda, e, s);
   if (C <= 256) return launch_cfg<M, 16, 1, 4, 16>(W, n, C, A, lda, e, s);

@@ -200,6 +200,18 @@ __device__ __forceinline__ float epi_y(const Epilogue& e, float ws, float as, fl
   return y;
 }
 
+// Store of output (m, n) with the residual value res (used when e.res is set) already loaded.
+__device__ __forceinline__ void epi_store_r(const Epilogue& e, float ws, float as, float bias, float res, int m,
+                                            int n, int32_t acc) {
+  const int64_t off = (int64_t)m * e.ldo + n;
+  if (e.acc_out) e.acc_out[off] = acc;
+  if (!e.out) return;
+  float y = epi_y(e, ws, as, bias, acc);
+  if (e.res) y = __fadd_rn(y, res);
+  if (e.out_dtype == WFB_F32) reinterpret_cast<float*>(e.out)[off] = y;
+  else reinterpret_cast<uint16_t*>(e.out)[off] = f32_to_bf16_rne(y);
+}
+
 __device__ __forceinline__ void epi_store(const Epilogue& e, float ws, float as, float bias, int m, int n,
                                           int32_t acc) {
   const int64_t off = (int64_t)m * e.ldo + n;
@@ -212,6 +224,16 @@ __device__ __forceinline__ void epi_store(const Epilogue& e, float ws, float as,
 }
 
 // Argmax key of output (m, n) (store included); 0 when (m, n) is out of range.
+__device__ __forceinline__ uint64_t epi_store_key_r(const Epilogue& e, float ws, float as, float bias, float res,
+                                                    int m, int n, int32_t acc, bool valid) {
+  if (!valid) return 0;
+  epi_store_r(e, ws, as, bias, res, m, n, acc);
+  float y = epi_y(e, ws, as, bias, acc);
+  if (e.res) y = __fadd_rn(y, res);
+  if (e.amax_dt == WFB_BF16) y = bf16_bits_to_f32(f32_to_bf16_rne(y));
+  return amax_key(y, n);
+}
+
 __device__ __forceinline__ uint64_t epi_store_key(const Epilogue& e, float ws, float as, float bias, int m, int n,
                                                   int32_t acc, bool valid) {
   if (!valid) return 0;
@@ -221,6 +243,29 @@ __device__ __forceinline__ uint64_t epi_store_key(const Epilogue& e, float ws, f
   if (e.amax_dt == WFB_BF16) y = bf16_bits_to_f32(f32_to_bf16_rne(y));
   return amax_key(y, n);
 }
+
+// Epilogue operands of output column n for T tokens tok[j] (weight scale, bias, token scales and
+// residuals), loaded at kernel entry so their latency overlaps the weight stream instead of following
+// the final reduction (a kernel's first touch of them misses the cache).  Entries of tokens >= M or of
+// n >= N are not loaded.
+template <int T>
+struct EpiCol {
+  float ws = 0.0f, bias = 0.0f;
+  float as[T], res[T];
+  __device__ __forceinline__ void load(const Epilogue& e, int n, int N, const int (&tok)[T], int M) {
+#pragma unroll
+    for (int j = 0; j < T; ++j) as[j] = res[j] = 0.0f;
+    if (n >= N) return;
+    ws = epi_wscale(e, n);
+    bias = epi_bias(e, n);
+#pragma unroll
+    for (int j = 0; j < T; ++j)
+      if (tok[j] < M) {
+        as[j] = epi_ascale(e, tok[j]);
+        if (e.res) res[j] = epi_res(e, tok[j], n);
+      }
+  }
+};
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
