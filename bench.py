@@ -12,7 +12,10 @@ events on the launch stream measure device time of back-to-back kernels (host la
 excluded); warmup steps run first.  Extra fields: per-shape GEMV numbers, the prefill GEMM at
 M = 512, 2048, 8192 in int8 TOP/s vs the 5.0 POP/s dense int8 peak, the fused
 RMSNorm+quant kernel, one BitNet-2B decode layer's quantised path with separate vs fused launches
-(decode_layer_2b), and the reference CPU kernel timed on this host (cpu_baseline).
+(decode_layer_2b), and the reference CPU kernel timed on this host (cpu_baseline).  Context for the
+roofline fractions: launch_context (an empty kernel's per-launch time, a plain copy moving the same
+bytes as the dominant GEMV, the GEMV on a 131 MB matrix) and, per prefill entry, the vendor library's
+plain int8 GEMM (torch._int_mm on hipBLASLt) on the same M, N, K.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-e2e] [--no-cpu]
 """
@@ -458,6 +461,36 @@ def device_copy_gbs(torch, dev, nbytes: int = 1 << 30) -> float:
     return 2 * nbytes / sec / 1e9
 
 
+def launch_context(torch, dev, L, steps: int, warmup: int, dom_bytes: int) -> dict:
+    """What one launch costs on this device, next to the GEMV numbers (same timing as they use):
+    a 1-element torch add (the fixed cost of any kernel launched back to back on one stream), a plain
+    device copy moving the dominant GEMV's bytes (half read, half written; 64 rotated buffer pairs, so
+    cold like the GEMV's weights), and the M=1 GEMV on one large matrix (Llama-3-8B LM head shape
+    128256 x 4096, 8 rotated copies), where the fixed cost is amortised."""
+    x = torch.zeros(1, device=dev)
+    floor_ms = timed(torch, [[lambda: x.add_(1)]], steps, warmup)
+    half = dom_bytes // 2
+    pairs = [(torch.empty(half, dtype=torch.uint8, device=dev), torch.empty(half, dtype=torch.uint8, device=dev))
+             for _ in range(N_COPIES)]
+    copy_ms = timed(torch, [[lambda d=d, s=s: d.copy_(s)] for s, d in pairs], steps, warmup)
+    del pairs
+    n, k = 128256, 4096
+    syn = Synth(torch, dev, 4242)
+    copies = [syn.packed(n, k) for _ in range(8)]
+    a, a_scale, ws = syn.int8(1, k), syn.log_uniform(1), syn.log_uniform(1)
+    out = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+    calls = [[L.linear_args("wfb_linear_i2s", c, n, k, a, 1, a_scale, ws, out)] for c in copies]
+    big_ms = timed(torch, calls, max(20, steps // 4), 3)
+    big_bytes = gemv_bytes(1, n, k)
+    del copies
+    return {"empty_kernel_us": round(floor_ms * 1e3, 3),
+            "copy_same_bytes_us": round(copy_ms * 1e3, 3),
+            "copy_same_bytes_GB/s": round(2 * half / (copy_ms * 1e-3) / 1e9, 1),
+            "gemv_128256x4096_us": round(big_ms * 1e3, 2),
+            "gemv_128256x4096_GB/s": round(big_bytes / (big_ms * 1e-3) / 1e9, 1),
+            "gemv_128256x4096_frac_hbm_peak": round(big_bytes / (big_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def measured_traffic(n: int, k: int):
     """HBM bytes per launch of the M=1 GEMV at (n, k) from the committed FETCH_SIZE / WRITE_SIZE
     profile (profiles/gemv_i2s_decode_bitnet2b.txt, calibrated against a plain copy kernel), or None."""
@@ -578,12 +611,16 @@ def main():
                 "traffic": measured_traffic(d["N"], d["K"]),
                 "kernel": f"gemv_i2s M=1 N={d['N']} K={d['K']}",
                 "bytes_per_launch": shapes[dom]["bytes"]}
+    launch = launch_context(torch, dev, L, args.steps, args.warmup, shapes[dom]["bytes"])
 
     # ---- prefill GEMM, M in {512, 2048, 8192} ---------------------------------------
+    # Beside each: the vendor library's plain int8 GEMM on the same M, N, K (torch._int_mm, hipBLASLt;
+    # int8 x int8 -> int32 with unpacked int8 weights, i.e. 4x the weight bytes and no unpack work).
     prefill = []
     for n, k in PREFILL_SHAPES:
         syn = Synth(torch, dev, 3000 + n)
         packed = syn.packed(n, k)
+        w8t = torch.randint(-1, 2, (n, k), dtype=torch.int8, device=dev, generator=syn.g).t()
         ws = syn.log_uniform(1)
         for m in (512, 2048, 8192):
             a = syn.int8(m, k)
@@ -592,9 +629,13 @@ def main():
             call = L.linear_args("wfb_linear_i2s", packed, n, k, a, m, a_scale, ws, out)
             ms = timed(torch, [[call]], max(10, args.steps // 10), 3)
             tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            lib_ms = timed(torch, [[lambda a=a: torch._int_mm(a, w8t)]], max(10, args.steps // 10), 3)
             prefill.append({"M": m, "N": n, "K": k, "us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
-                            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)})
+                            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                            "library_int8_us": round(lib_ms * 1e3, 2),
+                            "library_int8_frac_peak": round(2.0 * m * n * k / (lib_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)})
             del a, out
+        del w8t
 
     # ---- fused RMSNorm + per-token quant (configs[2] input distribution) -----------------------
     normq = []
@@ -662,6 +703,7 @@ def main():
         "cpu_baseline": cpu,
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "device_copy_GB/s": round(copy_gbs, 1),
+        "launch_context": launch,
         "gemv_per_shape": per_shape,
         "prefill_gemm": prefill,
         "rmsnorm_quant": normq,
