@@ -536,6 +536,28 @@ def cpu_baseline(seconds: float):
         total_bytes += gemv_bytes(1, n, k) * reps
         total_t += dt
         reps_done.append(reps)
+    # the same op on one thread (a shorter sample; the OpenMP runtime the library links is told directly)
+    one_thread = None
+    try:
+        gomp = ctypes.CDLL("libgomp.so.1")
+        gomp.omp_set_num_threads(1)
+        b1, t1 = 0, 0.0
+        rng1 = np.random.default_rng(1002)
+        for n, k in GEMV_SHAPES:
+            packed = orc.pack_i2s(orc.random_ternary(rng1, n, k))
+            a = orc.random_int8(rng1, 1, k)[0]
+            out = np.zeros(n, np.float32)
+            run(packed, a, out)
+            reps, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < seconds / (4 * len(GEMV_SHAPES)):
+                run(packed, a, out)
+                reps += 1
+            t1 += time.perf_counter() - t0
+            b1 += gemv_bytes(1, n, k) * reps
+        gomp.omp_set_num_threads(threads)
+        one_thread = round(b1 / t1 / 1e9, 3)
+    except OSError:
+        pass
     cpu_model = ""
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -549,6 +571,8 @@ def cpu_baseline(seconds: float):
         "unit": "GB/s",
         "cores": threads,
         "kind": kind,
+        "one_thread_GB/s": one_thread,
+        "host_nproc": os.cpu_count(),
         "sample": f"reference I2_S GEMV op (AVX2, OpenMP {threads} threads) on the 4 BitNet-2B decode shapes, "
                   f"{'/'.join(map(str, reps_done))} calls each over {seconds:.0f} s, same byte formula; "
                   f"host CPU: {cpu_model}",

@@ -422,9 +422,11 @@ hipError_t launch_rows_t(const void* x, const void* up, int64_t ldx, const void*
   const int vpl = (int)((h + 64 * kVec - 1) / (64 * kVec));
 #define WFB_WAVE(V) launch_wave<DT, GDT, NORM, V, GLU>(x, up, ldx, gamma, eps, m, h, q, k_pad, ldq, a_scale, vec, s)
   // wide kernel where a wave per row has the most serial work: rows of the wave order with 5-8 vectors
-  // per lane (H > 2048) and gated rows (measured on MI355X; the 256-thread block kernel stays faster
-  // above kWaveMaxH)
-  const bool wide = m <= kWideMaxM && h <= kWaveMaxH && (h > 2048 || (GLU != 0 && (m > 1 || h > 1024)));
+  // per lane (H > 2048) and gated rows (measured on MI355X; above kWaveMaxH the 256-thread block kernel
+  // stays faster for plain rows, 5.2 vs 5.9 us at H = 6912, M = 8, while the gated ones gain from 16
+  // waves, 9.5 vs 9.8 us at H = 14336; the row is staged in LDS as fp32, kept under 64 KB)
+  const bool wide = m <= kWideMaxM && ((h <= kWaveMaxH && (h > 2048 || (GLU != 0 && (m > 1 || h > 1024)))) ||
+                                       (GLU != 0 && h > kWaveMaxH && h <= 15360));
   if (wide) {
     const size_t lds = NORM ? (size_t)h * sizeof(float) : 0;
     hipLaunchKernelGGL((quant_rows_wide_kernel<DT, GDT, NORM, GLU>), dim3((unsigned)m), dim3(kWideThreads), lds, s, x,
