@@ -491,6 +491,29 @@ def launch_context(torch, dev, L, steps: int, warmup: int, dom_bytes: int) -> di
             "gemv_128256x4096_frac_hbm_peak": round(big_bytes / (big_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def mfma_ceiling(torch, dev, L) -> dict:
+    """Measured rate of back-to-back int8 MFMA on this device (library diagnostic wfb_diag_mfma_i8:
+    2048 workgroups x 4 waves, 8 independent 32x32x32 accumulators per wave), with constant operands
+    and with pseudo-random int8 operands (what a GEMM feeds).  The practical ceiling beside the
+    nominal 5.0 POP/s dense int8 peak."""
+    blocks, iters = 2048, 1000
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    f = L.lib.wfb_diag_mfma_i8
+    res = {}
+    for rnd in (0, 1):
+        args = (rnd, blocks, iters, ctypes.c_void_p(sink.data_ptr()), L.stream)
+
+        def call(args=args):
+            if f(*args) != 0:
+                raise RuntimeError(L.lib.wfb_last_error().decode())
+
+        ms = timed(torch, [[call]], 5, 2)
+        tops = 65536.0 * 8 * iters * blocks * 4 / (ms * 1e-3) / 1e12
+        res["random_operands_TOPS" if rnd else "constant_operands_TOPS"] = round(tops, 1)
+    res["random_frac_nominal"] = round(res["random_operands_TOPS"] / INT8_PEAK_TOPS, 4)
+    return res
+
+
 def measured_traffic(n: int, k: int):
     """HBM bytes per launch of the M=1 GEMV at (n, k) from the committed FETCH_SIZE / WRITE_SIZE
     profile (profiles/gemv_i2s_decode_bitnet2b.txt, calibrated against a plain copy kernel), or None."""
@@ -639,7 +662,9 @@ def main():
 
     # ---- prefill GEMM, M in {512, 2048, 8192} ---------------------------------------
     # Beside each: the vendor library's plain int8 GEMM on the same M, N, K (torch._int_mm, hipBLASLt;
-    # int8 x int8 -> int32 with unpacked int8 weights, i.e. 4x the weight bytes and no unpack work).
+    # int8 x int8 -> int32 with unpacked int8 weights, i.e. 4x the weight bytes and no unpack work), and
+    # the fraction of the measured MFMA rate with random operands (the practical ceiling).
+    mfma = mfma_ceiling(torch, dev, L)
     prefill = []
     for n, k in PREFILL_SHAPES:
         syn = Synth(torch, dev, 3000 + n)
@@ -656,6 +681,7 @@ def main():
             lib_ms = timed(torch, [[lambda a=a: torch._int_mm(a, w8t)]], max(10, args.steps // 10), 3)
             prefill.append({"M": m, "N": n, "K": k, "us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
                             "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                            "frac_measured_mfma_rate": round(tops / mfma["random_operands_TOPS"], 4),
                             "library_int8_us": round(lib_ms * 1e3, 2),
                             "library_int8_frac_peak": round(2.0 * m * n * k / (lib_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)})
             del a, out
@@ -729,6 +755,7 @@ def main():
         "device_copy_GB/s": round(copy_gbs, 1),
         "launch_context": launch,
         "gemv_per_shape": per_shape,
+        "int8_mfma_measured": mfma,
         "prefill_gemm": prefill,
         "rmsnorm_quant": normq,
         "decode_layer_2b": layer,

@@ -178,3 +178,11 @@ def test_residual_argument_errors(pkg):
     st = pkg._lib.status("wfb_linear_i2s_residual", vp(16), 64, 128, vp(16), 2, 128, None, None, 1.0, vp(16), 1, 32,
                          vp(16), 1, 64, None)
     assert st == -1 and "residual row stride" in pkg._lib.last_error()
+
+
+def test_diag_mfma_argument_errors(pkg):
+    vp = ctypes.c_void_p
+    assert pkg._lib.status("wfb_diag_mfma_i8", 1, 0, 10, vp(16), None) == -1
+    assert "blocks" in pkg._lib.last_error()
+    assert pkg._lib.status("wfb_diag_mfma_i8", 1, 4, 10, None, None) == -1
+    assert "null sink" in pkg._lib.last_error()

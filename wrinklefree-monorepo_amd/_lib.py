@@ -54,6 +54,7 @@ SIGNATURES = {
                            _vp],
     "wfb_gqa_decode_attention": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
                                  _i64, _i64, _f32, _vp, _i64, _vp, _vp],
+    "wfb_diag_mfma_i8": [_int, _i64, _i64, _vp, _vp],
 }
 
 _lib = None
