@@ -330,6 +330,10 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_combine_kernel(const float* 
                                                                    const int64_t* __restrict__ pos_arr,
                                                                    int64_t max_len, int hkv, int ks, int nsplit,
                                                                    void* __restrict__ out, int64_t ldo) {
+  // LDS: the running max m and sum l of every (split, head), then the per-head denominators.  The
+  // partials are read with independent loads (m and l once per workgroup, the accumulators unrolled
+  // over the splits) rather than as a chain of dependent loops per output element.
+  extern __shared__ float cw[];
   const int kvh = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const int64_t pos = pos_arr[b];
   const int64_t obase = (int64_t)b * ldo + (int64_t)kvh * G * D;
@@ -339,18 +343,32 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_combine_kernel(const float* 
   }
   const int ns = (int)(pos / ks) + 1;
   const float* pp = part + (((int64_t)b * hkv + kvh) * nsplit) * G * (D + 2);
+  float* sm = cw;                // [ns * G]: m, then the split weights e^(m_s - M)
+  float* sl = cw + nsplit * G;   // [ns * G]: l
+  float* sden = sl + nsplit * G; // [G]
+  for (int i = t; i < ns * G; i += kAttnThreads) {
+    sm[i] = pp[i * (D + 2) + D];
+    sl[i] = pp[i * (D + 2) + D + 1];
+  }
+  __syncthreads();
+  if (t < G) {
+    float mx = -__builtin_inff();
+    for (int s = 0; s < ns; ++s) mx = fmaxf(mx, sm[s * G + t]);
+    float den = 0.0f;
+    for (int s = 0; s < ns; ++s) {
+      const float wgt = __expf(sm[s * G + t] - mx);
+      sm[s * G + t] = wgt;
+      den += sl[s * G + t] * wgt;
+    }
+    sden[t] = den;
+  }
+  __syncthreads();
   for (int i = t; i < G * D; i += kAttnThreads) {
     const int g = i / D, d = i % D;
-    float mx = -__builtin_inff();
-    for (int s = 0; s < ns; ++s) mx = fmaxf(mx, pp[(s * G + g) * (D + 2) + D]);
-    float num = 0.0f, den = 0.0f;
-    for (int s = 0; s < ns; ++s) {
-      const float* ps = pp + (s * G + g) * (D + 2);
-      const float wgt = __expf(ps[D] - mx);
-      num += ps[d] * wgt;
-      den += ps[D + 1] * wgt;
-    }
-    store_elem<DT>(out, obase + i, num / den);
+    float num = 0.0f;
+#pragma unroll 8
+    for (int s = 0; s < ns; ++s) num += pp[(s * G + g) * (D + 2) + d] * sm[s * G + g];
+    store_elem<DT>(out, obase + i, num / sden[g]);
   }
 }
 
@@ -379,8 +397,9 @@ hipError_t launch_attn_g(const void* q, int64_t ldq, const void* kn, int64_t ldk
                        ldo, (int)ks, part);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((gqa_combine_kernel<DT, D, G>), dim3(hkv, b), dim3(kAttnThreads), 0, s, part, pos, max_len, hkv,
-                     (int)ks, (int)nsplit, out, ldo);
+  const size_t lds = (size_t)(2 * nsplit * G + G) * sizeof(float);  // nsplit <= kAttnTargetGrid
+  hipLaunchKernelGGL((gqa_combine_kernel<DT, D, G>), dim3(hkv, b), dim3(kAttnThreads), lds, s, part, pos, max_len,
+                     hkv, (int)ks, (int)nsplit, out, ldo);
   return hipGetLastError();
 }
 
