@@ -269,6 +269,27 @@ int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int6
                              int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
                              float scale, void* out, int64_t ldo, float* workspace, void* stream);
 
+/* Decode-time fusion of wfb_rmsnorm_quant_i8 and the BitLinear that consumes its codes (one launch):
+ *   q, a_scale = rmsnorm_quant(x, gamma, eps)          (exactly wfb_rmsnorm_quant_i8, codes zero past H)
+ *   out = linear_i2s_segmented(qweight, q, a_scale)      (exactly wfb_linear_i2s_segmented; one segment =
+ *                                                         wfb_linear_i2s with a device scale)
+ *         (+ residual, exactly as wfb_linear_i2s_residual when residual is not NULL)
+ * x [M, H] (x_dtype WFB_F32 or WFB_BF16, row stride ldx elements, rows 16-byte aligned), gamma [H]
+ * (WFB_F32 or WFB_BF16, 16-byte aligned) or NULL; 1 <= M <= 16, H % 8 == 0, H <= K <= 4096,
+ * M * (K + 16) + H * sizeof(gamma) <= 49152 (codes and gamma live in LDS; larger calls take the
+ * two-call path).  seg_rows /
+ * w_scales_dev as wfb_linear_i2s_segmented (n_seg = 1 with seg_rows NULL: one segment of N rows).
+ * out [M, N] WFB_F32 or WFB_BF16 (row stride ldo); residual [M, N] WFB_F32 or WFB_BF16 (row stride ldr)
+ * or NULL; out may alias residual.  Every workgroup recomputes the codes of the M rows in the
+ * quantiser's own summation order, so results are bit-identical to the two calls.
+ * Replaces, per decode token, SubLN/RMSNorm -> activation_quant -> BitLinear
+ * (WF/models/subln.py:42-59, 64-97; WF/models/bitlinear.py:66-113) as fused by
+ * bitnet_qkv_fused / bitnet_mlp_fused (SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:150-231, 289-375). */
+int wfb_rmsnorm_linear_i2s(const void* x, int x_dtype, int64_t ldx, const void* gamma, int gamma_dtype, float eps,
+                           int64_t m, int64_t h, const uint8_t* qweight, int64_t n, int64_t k, int n_seg,
+                           const int64_t* seg_rows, const float* w_scales_dev, const void* residual,
+                           int residual_dtype, int64_t ldr, void* out, int out_dtype, int64_t ldo, void* stream);
+
 /* Diagnostic, with no counterpart in the reference: the rate of back-to-back int8 MFMA
  * (v_mfma_i32_32x32x32_i8, 8 independent accumulators per wave) on this device, the practical
  * ceiling to read the prefill GEMM's rate against, next to the nominal dense int8 peak.  Launches

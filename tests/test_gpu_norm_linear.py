@@ -1,0 +1,81 @@
+"""wfb_rmsnorm_linear_i2s (RMSNorm + per-token quant in the prologue of the decode BitLinear): outputs
+bit-identical to the two-call path (wfb_rmsnorm_quant_i8, then the segmented / residual linear), which
+the parity tests pin against the oracle; one shape also checked against the oracle directly."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bitnet_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(rng, m, h, rows, k, xdt, gdt):
+    n = sum(rows)
+    packed = torch.from_numpy(orc.pack_i2s(orc.random_ternary(rng, n, k)))
+    x = torch.from_numpy(orc.outlier_hidden(rng, m, h).astype(np.float32)).to(xdt)
+    g = None if gdt is None else torch.from_numpy((1 + 0.1 * rng.standard_normal(h)).astype(np.float32)).to(gdt)
+    scales = torch.from_numpy(orc.log_uniform(rng, len(rows)).astype(np.float32))
+    return packed, x, g, scales
+
+
+CASES = [
+    # m, h, segment rows, k, x dtype, gamma dtype
+    (8, 4096, [4096, 1024, 1024], 4096, torch.bfloat16, torch.bfloat16),   # Llama-3-8B q|k|v
+    (8, 4096, [14336, 14336], 4096, torch.bfloat16, torch.bfloat16),       # Llama-3-8B gate|up
+    (1, 576, [576, 192, 192], 640, torch.float32, torch.float32),          # SmolLM2 q|k|v, K padded
+    (1, 2560, [2560], 2560, torch.bfloat16, torch.float32),                # BitNet-2B o
+    (2, 2560, [6912, 6912], 2560, torch.float32, torch.bfloat16),          # BitNet-2B gate|up
+    (3, 1536, [1000, 24], 1536, torch.bfloat16, None),                     # ragged tile, no gamma
+    (16, 2560, [3200], 2560, torch.bfloat16, torch.bfloat16),              # M = 16
+    (7, 4000, [136], 4096, torch.float32, torch.float32),                  # H < K, odd M
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"m{c[0]}_h{c[1]}_n{sum(c[2])}_{str(c[4])[6:]}" for c in CASES])
+def test_fused_equals_two_calls(pkg, dev, case):
+    m, h, rows, k, xdt, gdt = case
+    rng = np.random.default_rng(m * 131 + h + sum(rows))
+    packed, x, g, scales = (t.to(dev) if t is not None else None for t in _inputs(rng, m, h, rows, k, xdt, gdt))
+    y = pkg.rmsnorm_linear(x, g, packed, scales, rows, eps=1e-6)
+    q, a_scale = pkg.rmsnorm_quantize_i8(x, g, eps=1e-6, k_pad=k)
+    y_ref = pkg.bitnet_linear_segmented(packed, rows, scales, q, a_scale=a_scale)
+    assert torch.equal(y, y_ref)
+
+
+@pytest.mark.parametrize("rdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("in_place", [False, True])
+def test_fused_residual_equals_two_calls(pkg, dev, rdt, in_place):
+    rng = np.random.default_rng(7)
+    m, h, n = 8, 4096, 4096
+    packed, x, g, scales = (t.to(dev) for t in _inputs(rng, m, h, [n], h, torch.bfloat16, torch.bfloat16))
+    res = torch.from_numpy(rng.standard_normal((m, n)).astype(np.float32)).to(rdt).to(dev)
+    q, a_scale = pkg.rmsnorm_quantize_i8(x, g, eps=1e-5)
+    y_ref = pkg.bitnet_linear_residual(packed, q, scales, res.clone(), a_scale=a_scale)
+    r = res.clone()
+    y = pkg.rmsnorm_linear(x, g, packed, scales, eps=1e-5, residual=r, out=r if in_place else None)
+    assert torch.equal(y, y_ref)
+    if in_place:
+        assert y.data_ptr() == r.data_ptr()
+
+
+def test_fused_matches_oracle(pkg, dev):
+    rng = np.random.default_rng(99)
+    m, h, rows = 4, 2560, [2560, 640]
+    packed, x, g, scales = _inputs(rng, m, h, rows, h, torch.float32, torch.float32)
+    y = pkg.rmsnorm_linear(x.to(dev), g.to(dev), packed.to(dev), scales.to(dev), rows, eps=1e-6, out_dtype=torch.float32)
+    q_ref, s_ref = orc.rmsnorm_quant(x.numpy(), g.numpy(), 1e-6)
+    acc = (q_ref.astype(np.float32) @ orc.unpack_i2s(packed.numpy()).astype(np.float32).T).astype(np.int64)
+    y_ref = orc.rescale_segmented(acc, rows, scales.numpy(), s_ref)
+    assert np.array_equal(y.cpu().numpy(), y_ref)
+
+
+def test_fused_rejects_unsupported_sizes(pkg, dev):
+    packed = torch.zeros((64, 1024), dtype=torch.uint8, device=dev)
+    sc = torch.ones(1, device=dev)
+    with pytest.raises(RuntimeError, match="fused path"):
+        pkg.rmsnorm_linear(torch.zeros((17, 4096), device=dev), None, packed, sc)
+    with pytest.raises(RuntimeError, match="fused path"):
+        pkg.rmsnorm_linear(torch.zeros((2, 4100), device=dev), None, torch.zeros((64, 1280), dtype=torch.uint8, device=dev), sc)
+    assert not pkg.rmsnorm_linear_supported(16, 4096, 4096) and pkg.rmsnorm_linear_supported(8, 4096, 4096)

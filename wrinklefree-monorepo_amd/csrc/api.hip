@@ -355,6 +355,65 @@ int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int6
                     name);
 }
 
+int wfb_rmsnorm_linear_i2s(const void* x, int x_dtype, int64_t ldx, const void* gamma, int gamma_dtype, float eps,
+                           int64_t m, int64_t h, const uint8_t* qweight, int64_t n, int64_t k, int n_seg,
+                           const int64_t* seg_rows, const float* w_scales_dev, const void* residual,
+                           int residual_dtype, int64_t ldr, void* out, int out_dtype, int64_t ldo, void* stream) {
+  const char* name = "wfb_rmsnorm_linear_i2s";
+  if (x_dtype != WFB_F32 && x_dtype != WFB_BF16) return fail(WFB_EINVAL, "%s: x dtype must be WFB_F32 or WFB_BF16", name);
+  if (gamma && gamma_dtype != WFB_F32 && gamma_dtype != WFB_BF16)
+    return fail(WFB_EINVAL, "%s: gamma dtype must be WFB_F32 or WFB_BF16", name);
+  if (m < 0 || m > 16) return fail(WFB_EINVAL, "%s: M (%lld) must be in 0..16", name, (long long)m);
+  if (h <= 0 || h % 8 != 0 || h > k || k % WFB_QK_I2S != 0 || k > 4096)
+    return fail(WFB_EINVAL, "%s: need H %% 8 == 0, H <= K <= 4096, K %% %d == 0 (got H=%lld K=%lld)", name, WFB_QK_I2S,
+                (long long)h, (long long)k);
+  const int64_t lds = m * (k + 16) + (gamma ? h * (gamma_dtype == WFB_F32 ? 4 : 2) : 0);
+  if (lds > 49152)
+    return fail(WFB_EINVAL,
+                "%s: M * (K + 16) + H * sizeof(gamma) = %lld exceeds 49152 (use wfb_rmsnorm_quant_i8 + wfb_linear_i2s)",
+                name, (long long)lds);
+  if (n <= 0 || n > INT32_MAX / 2 || n * (k / 4) > INT32_MAX)
+    return fail(WFB_EINVAL, "%s: bad N (%lld) for K %lld", name, (long long)n, (long long)k);
+  if (ldx < h || ldo < n || (residual && ldr < n)) return fail(WFB_EINVAL, "%s: row strides too small", name);
+  if (!(eps >= 0.0f)) return fail(WFB_EINVAL, "%s: eps must be >= 0", name);
+  if (!out || (out_dtype != WFB_F32 && out_dtype != WFB_BF16))
+    return fail(WFB_EINVAL, "%s: out must be non-null WFB_F32 or WFB_BF16", name);
+  if (residual && residual_dtype != WFB_F32 && residual_dtype != WFB_BF16)
+    return fail(WFB_EINVAL, "%s: residual dtype must be WFB_F32 or WFB_BF16", name);
+  if (!w_scales_dev) return fail(WFB_EINVAL, "%s: null w_scales_dev", name);
+  if (n_seg < 1 || n_seg > WFB_MAX_SEGMENTS || (n_seg > 1 && !seg_rows))
+    return fail(WFB_EINVAL, "%s: n_seg (%d) must be in 1..%d with seg_rows for more than one", name, n_seg,
+                WFB_MAX_SEGMENTS);
+  wfb::Epilogue e{};  // everything not set below is null / zero
+  e.nseg = n_seg;
+  if (n_seg > 1) {
+    int64_t total = 0;
+    for (int j = 0; j < n_seg; ++j) {
+      if (seg_rows[j] <= 0 || seg_rows[j] % 8 != 0)
+        return fail(WFB_EINVAL, "%s: segment %d has %lld rows (must be a positive multiple of 8)", name, j,
+                    (long long)seg_rows[j]);
+      total += seg_rows[j];
+      if (j + 1 < n_seg) e.seg_end[j] = (int)total;
+    }
+    if (total != n) return fail(WFB_EINVAL, "%s: segment rows sum to %lld, N is %lld", name, (long long)total, (long long)n);
+  }
+  if (m == 0) return ok();
+  if (!x || !qweight) return fail(WFB_EINVAL, "%s: null x or qweight", name);
+  const int esz = x_dtype == WFB_F32 ? 4 : 2;
+  if (!aligned(x, 16) || (ldx * esz) % 16 != 0 || (gamma && !aligned(gamma, 16)) || !aligned(qweight, 16))
+    return fail(WFB_EINVAL, "%s: x rows, gamma and qweight must be 16-byte aligned", name);
+  e.ws_dev = w_scales_dev;
+  e.out = out;
+  e.out_dtype = out_dtype;
+  e.ldo = ldo;
+  e.res = residual;
+  e.res_dtype = residual_dtype;
+  e.ldr = ldr;
+  return hip_status(wfb::launch_norm_linear(x, x_dtype, ldx, gamma, gamma_dtype, eps, (int)h, qweight, (int)m, (int)n,
+                                            (int)k, e, as_stream(stream)),
+                    name);
+}
+
 int wfb_diag_mfma_i8(int random_operands, int64_t blocks, int64_t iters, int* sink, void* stream) {
   if (blocks <= 0 || blocks > 65535 || iters <= 0 || iters > (int64_t)1 << 24)
     return fail(WFB_EINVAL, "wfb_diag_mfma_i8: blocks must be in 1..65535 and iters in 1..2^24 (got %lld, %lld)",

@@ -349,5 +349,8 @@ hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* 
 hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                            const Epilogue& e, hipStream_t s);
 hipError_t launch_mfma_rate(bool random_operands, int64_t blocks, int64_t iters, int* sink, hipStream_t s);
+// RMSNorm + quant in the prologue of the batched-decode linear (M <= 16, H <= K <= 4096)
+hipError_t launch_norm_linear(const void* x, int xdt, int64_t ldx, const void* gamma, int gdt, float eps, int h,
+                              const uint8_t* W, int m, int n, int k, const Epilogue& e, hipStream_t s);
 
 }  // namespace wfb

@@ -467,6 +467,76 @@ def bitnet_linear_residual(
     return out
 
 
+def rmsnorm_linear_supported(m: int, h: int, k: int, gamma_bytes: int = 2) -> bool:
+    """Whether rmsnorm_linear takes these sizes (decode batches: the codes of the M rows and gamma live in
+    LDS; ``gamma_bytes`` per gamma element, 0 without gamma)."""
+    return (1 <= m <= 16 and h % 8 == 0 and 0 < h <= k <= 4096 and k % QK_I2_S == 0
+            and m * (k + 16) + h * gamma_bytes <= 49152)
+
+
+def rmsnorm_linear_preferred(m: int, h: int, n: int, k: int, gamma_bytes: int = 2) -> bool:
+    """Whether the fused launch is the faster choice (measured on MI355X): supported sizes whose grid of
+    16-row tiles fits one workgroup per CU (256)."""
+    nt = 4 if n >= 24576 else (2 if n >= 6144 and k <= 8192 else 1)
+    return rmsnorm_linear_supported(m, h, k, gamma_bytes) and (n + 16 * nt - 1) // (16 * nt) <= 256
+
+
+def rmsnorm_linear(
+    x: torch.Tensor, weight: Optional[torch.Tensor], packed_weights: torch.Tensor, scales: torch.Tensor,
+    seg_rows=None, eps: float = 1e-6, residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+    out_dtype: torch.dtype = torch.bfloat16,
+) -> torch.Tensor:
+    """RMSNorm/SubLN + per-token int8 quantisation + (multi-segment) BitLinear (+ residual) in one launch
+    for decode batches (``rmsnorm_linear_supported``): equal, bit for bit, to ``rmsnorm_quantize_i8``
+    followed by ``bitnet_linear_segmented`` (``bitnet_linear_residual`` when ``residual`` is given, the
+    output then taking the residual's dtype; ``out`` may be ``residual`` itself).
+
+    x: float32/bfloat16 [M, H]; weight: [H] or None; packed_weights: uint8 [N, K/4] with K >= H (codes
+    past H are zero); scales: fp32 [n_seg] on the device; seg_rows: row counts (None = one segment).
+    """
+    name = "rmsnorm_linear"
+    if x.dim() != 2 or x.dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError(f"{name}: x must be float32/bfloat16 [batch, hidden]")
+    if packed_weights.dtype != torch.uint8 or packed_weights.dim() != 2:
+        raise RuntimeError(f"{name}: packed_weights must be uint8 2D [out_features, in_features/4]")
+    m, h = x.shape
+    n, kb = packed_weights.shape
+    k = kb * 4
+    rows = [n] if seg_rows is None else [int(r) for r in seg_rows]
+    if sum(rows) != n:
+        raise ValueError(f"{name}: segment rows sum to {sum(rows)}, packed_weights has {n}")
+    if scales.dtype != torch.float32 or scales.numel() != len(rows):
+        raise RuntimeError(f"{name}: scales must be fp32 with one element per segment")
+    gbytes = 0 if weight is None else weight.element_size()
+    if not rmsnorm_linear_supported(m, h, k, gbytes):
+        raise RuntimeError(f"{name}: M={m}, H={h}, K={k} outside the fused path (M <= 16, H % 8 == 0, "
+                           f"H <= K <= 4096, M*(K+16) + H*{gbytes} <= 49152)")
+    dev = _require_gpu(name, x, weight, packed_weights, scales, residual)
+    if weight is not None and (weight.numel() != h or weight.dtype not in (torch.float32, torch.bfloat16)):
+        raise RuntimeError(f"{name}: weight must be float32/bfloat16 with {h} elements")
+    if x.stride(1) != 1 or (x.stride(0) * x.element_size()) % 16 != 0 or x.data_ptr() % 16 != 0:
+        x = x.contiguous()
+    if weight is not None:
+        weight = weight.contiguous()
+    if residual is not None:
+        if residual.dtype not in (torch.float32, torch.bfloat16) or residual.shape != (m, n) or residual.stride(-1) != 1:
+            raise RuntimeError(f"{name}: residual must be float32/bfloat16 [{m}, {n}] with contiguous rows")
+        out_dtype = residual.dtype
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    elif out.dtype != out_dtype or out.shape != (m, n) or out.stride(-1) != 1:
+        raise RuntimeError(f"{name}: out must be {out_dtype} [{m}, {n}] with contiguous rows")
+    seg = (ctypes.c_int64 * len(rows))(*rows)
+    with torch.cuda.device(dev):
+        _lib.call("wfb_rmsnorm_linear_i2s", _p(x), _DT[x.dtype], x.stride(0), _p(weight),
+                  _DT[weight.dtype] if weight is not None else WFB_F32, float(eps), m, h, _p(packed_weights), n, k,
+                  len(rows), ctypes.cast(seg, ctypes.c_void_p), _p(scales), _p(residual),
+                  _DT[residual.dtype] if residual is not None else WFB_F32,
+                  residual.stride(0) if residual is not None else n, _p(out), _DT[out.dtype], out.stride(0),
+                  _stream(dev))
+    return out
+
+
 # ---- greedy decoding: LM head + argmax ----------------------------------------------------------
 
 
