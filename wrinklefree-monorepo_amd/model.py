@@ -10,8 +10,10 @@ Every quantised op goes through a *BitLinear backend*: one call per (norm -> qua
 group, so the norm before q/k/v (and before gate/up) is fused with the activation quantiser and
 shared by the projections that read it, and one call for the MLP middle (act(gate) * up -> SubLN ->
 quantise -> down).  ``HipBackend`` runs libwfbitnet -- with ``fused=True`` the projections of a group
-run as one segmented launch (q|k|v, gate|up) and the gated activation, SubLN and quantiser as one
-kernel; a ternary LM head runs its argmax fused in (``norm_linear_argmax``).  A test can substitute
+run as one segmented launch (q|k|v, gate|up), the gated activation, SubLN and quantiser as one
+kernel, and, for decode batches where it is faster (q|k|v and o), the norm + quantiser inside the
+linear's own launch (``rmsnorm_linear``); a ternary LM head runs its argmax fused in
+(``norm_linear_argmax``).  A test can substitute
 another backend with the same three methods to compare the quantised path while the float code stays
 identical: embedding, residuals, the prefill attention (torch), the decode-step rotary embedding +
 cache append + GQA attention (one libwfbitnet kernel, or torch ops with ``decode_attention="torch"``)
@@ -29,8 +31,8 @@ import torch
 
 from .sglbitnt import SGLBitNetFile, write_sglbitnt
 from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_residual, bitnet_linear_segmented,
-                  glu_rmsnorm_quantize_i8, gqa_decode_attention, lm_head_argmax, pack_ternary_i2s,
-                  rmsnorm_quantize_i8)
+                  glu_rmsnorm_quantize_i8, gqa_decode_attention, lm_head_argmax, pack_ternary_i2s, rmsnorm_linear,
+                  rmsnorm_linear_preferred, rmsnorm_quantize_i8)
 
 
 @dataclass(frozen=True)
@@ -88,8 +90,11 @@ class HipBackend:
     then the projections with the rescale fused in their epilogue.
 
     ``fused=True``: the projections of a group (q|k|v, gate|up) run as one segmented launch on their
-    concatenated weights, so a decode layer takes 8 library launches (norm+quant, q|k|v, SubLN+quant,
-    o, norm+quant, gate|up, act+SubLN+quant, down) instead of 11."""
+    concatenated weights, residual adds ride in the o/down epilogues, and for decode batches the
+    norm + quantiser before q|k|v and o runs in the linear's prologue where that is measured faster
+    (``rmsnorm_linear_preferred``): a Llama-3-8B decode layer takes 8 kernel launches (norm+q|k|v,
+    attention and its split combine, SubLN+o+residual, norm+quant, gate|up, act+SubLN+quant,
+    down+residual) instead of 12."""
 
     def __init__(self, out_dtype: torch.dtype = torch.float32, keep_acc: bool = False, fused: bool = False):
         self.out_dtype = out_dtype
@@ -129,8 +134,25 @@ class HipBackend:
             outs.append(y)
         return outs
 
+    def _fused_norm(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], n: int, k: int) -> bool:
+        """Norm + quant in the linear's prologue (one launch) where that is the faster choice."""
+        if not self.fused or self.keep_acc or x.dim() != 2 or x.dtype not in (torch.float32, torch.bfloat16):
+            return False
+        if norm_weight is not None and norm_weight.dtype not in (torch.float32, torch.bfloat16):
+            return False
+        gb = 0 if norm_weight is None else norm_weight.element_size()
+        return rmsnorm_linear_preferred(x.shape[0], x.shape[1], n, k, gb)
+
     def norm_linears(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], eps: float,
                      linears: Sequence[PackedLinear]) -> List[torch.Tensor]:
+        n = sum(l.out_features for l in linears)
+        if self._fused_norm(x, norm_weight, n, linears[0].k_pad):
+            if len(linears) > 1:
+                qw, sc, rows = self._group(linears)
+            else:
+                qw, sc, rows = linears[0].qweight, linears[0].scale.reshape(1), [n]
+            y = rmsnorm_linear(x, norm_weight, qw, sc, rows, eps=eps, out_dtype=self.out_dtype)
+            return list(torch.split(y, rows, dim=1))
         q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=linears[0].k_pad)
         return self._linears(q, a_scale, linears)
 
@@ -153,6 +175,10 @@ class HipBackend:
                              linear: PackedLinear, residual: torch.Tensor) -> torch.Tensor:
         """residual + linear(quantise(norm(x))), the add fused into the linear's epilogue (fp32 add, then
         the residual's dtype)."""
+        if self._fused_norm(x, norm_weight, linear.out_features, linear.k_pad) and residual.dtype in (
+                torch.float32, torch.bfloat16):
+            return rmsnorm_linear(x, norm_weight, linear.qweight, linear.scale.reshape(1), eps=eps,
+                                  residual=residual.contiguous())
         q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=linear.k_pad)
         return self._linear_residual(q, a_scale, linear, residual)
 
