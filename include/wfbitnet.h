@@ -290,6 +290,19 @@ int wfb_rmsnorm_linear_i2s(const void* x, int x_dtype, int64_t ldx, const void* 
                            const int64_t* seg_rows, const float* w_scales_dev, const void* residual,
                            int residual_dtype, int64_t ldr, void* out, int out_dtype, int64_t ldo, void* stream);
 
+/* The gated MLP middle in the gate|up linear's epilogue (decode batches, M <= 64):
+ *   out[m, j] = act(y[m, j]) * y[m, half + j],  j < half = N / 2,
+ * where y is exactly what wfb_linear_i2s_segmented stores for qweight = gate|up (two segments of half
+ * rows, w_scales_dev[2]) with out_dtype = mid_dtype (WFB_F32 or WFB_BF16), and act(g) * u is formed
+ * with the same fixed fp32 operations as wfb_glu_rmsnorm_quant_i8 (act WFB_ACT_SILU / WFB_ACT_RELU2).
+ * out: fp32 [M, half], row stride ldo.  So wfb_rmsnorm_quant_i8 on out gives, bit for bit, the codes
+ * of wfb_glu_rmsnorm_quant_i8 on the stored gate and up.  half % 32 == 0; N * K / 4 and
+ * (M - 1) * lda + K below 2^31.  Replaces the gate/up GEMV + act * up of bitnet_mlp_fused
+ * (SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:189-216). */
+int wfb_linear_i2s_glu(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m, int64_t lda,
+                       const float* a_scale, const float* w_scales_dev, int act_kind, int mid_dtype, float* out,
+                       int64_t ldo, void* stream);
+
 /* Diagnostic, with no counterpart in the reference: the rate of back-to-back int8 MFMA
  * (v_mfma_i32_32x32x32_i8, 8 independent accumulators per wave) on this device, the practical
  * ceiling to read the prefill GEMM's rate against, next to the nominal dense int8 peak.  Launches

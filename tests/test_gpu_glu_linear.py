@@ -1,0 +1,52 @@
+"""wfb_linear_i2s_glu (act(gate) * up in the gate|up linear's epilogue): the fp32 output equals the
+oracle's gated product of the segmented linear's stored outputs, and re-quantising it gives the same
+codes as the unfused path (wfb_glu_rmsnorm_quant_i8 on the stored gate and up), bit for bit."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bitnet_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # m, half, k, mid dtype
+    (8, 14336, 4096, torch.bfloat16),   # Llama-3-8B gate|up (4 row tiles x 4 waves)
+    (1, 6912, 2560, torch.bfloat16),    # BitNet-2B
+    (3, 1536, 640, torch.float32),      # SmolLM2 (fp32 model), K padded
+    (17, 2048, 1024, torch.bfloat16),   # two token tiles
+    (64, 4096, 512, torch.float32),     # four token tiles
+]
+
+
+@pytest.mark.parametrize("act", ["silu", "relu2"])
+@pytest.mark.parametrize("case", CASES, ids=[f"m{c[0]}_h{c[1]}_k{c[2]}_{str(c[3])[6:]}" for c in CASES])
+def test_glu_linear_matches_oracle_and_unfused(pkg, dev, case, act):
+    m, half, k, mid = case
+    rng = np.random.default_rng(m * 7 + half + k)
+    packed = torch.from_numpy(orc.pack_i2s(orc.random_ternary(rng, 2 * half, k))).to(dev)
+    a = torch.from_numpy(orc.random_int8(rng, m, k)).to(dev)
+    a_scale = torch.from_numpy(orc.log_uniform(rng, m).astype(np.float32)).to(dev)
+    scales = torch.from_numpy(orc.log_uniform(rng, 2).astype(np.float32) * 4).to(dev)
+    x = pkg.bitnet_linear_glu(packed, scales, a, act, a_scale=a_scale, mid_dtype=mid)
+    # unfused: the stored gate|up, then the gated norm-quant
+    y = pkg.bitnet_linear_segmented(packed, [half, half], scales, a, a_scale=a_scale, out_dtype=mid)
+    code = orc.ACT_SILU if act == "silu" else orc.ACT_RELU2
+    yf = y.float().cpu().numpy()
+    assert np.array_equal(x.cpu().numpy(), orc.glu(yf[:, :half], yf[:, half:], code))
+    g = (1 + 0.1 * torch.randn(half, generator=torch.Generator().manual_seed(half))).to(torch.bfloat16).to(dev)
+    q1, s1 = pkg.glu_rmsnorm_quantize_i8(y[:, :half], y[:, half:], act, g, eps=1e-6)
+    q2, s2 = pkg.rmsnorm_quantize_i8(x, g, eps=1e-6)
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+
+
+def test_glu_linear_errors(pkg, dev):
+    packed = torch.zeros((96, 32), dtype=torch.uint8, device=dev)
+    a = torch.zeros((2, 128), dtype=torch.int8, device=dev)
+    sc = torch.ones(2, device=dev)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        pkg.bitnet_linear_glu(packed, sc, a)
+    with pytest.raises(RuntimeError, match="64 tokens"):
+        pkg.bitnet_linear_glu(torch.zeros((128, 32), dtype=torch.uint8, device=dev), sc,
+                              torch.zeros((65, 128), dtype=torch.int8, device=dev))

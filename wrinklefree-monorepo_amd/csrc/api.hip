@@ -95,6 +95,7 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
   e.res = res;
   e.res_dtype = res_dtype;
   e.ldr = ldr;
+  e.mid_dtype = 0;
 
   const bool gemv = kind == Kernel::Gemv || (kind == Kernel::Auto && use_gemv(m, n, k, lda));
   if (amax) {  // greedy argmax: GEMV (M <= 2) or the skinny MFMA kernel, then the cross-workgroup maximum
@@ -411,6 +412,37 @@ int wfb_rmsnorm_linear_i2s(const void* x, int x_dtype, int64_t ldx, const void* 
   e.ldr = ldr;
   return hip_status(wfb::launch_norm_linear(x, x_dtype, ldx, gamma, gamma_dtype, eps, (int)h, qweight, (int)m, (int)n,
                                             (int)k, e, as_stream(stream)),
+                    name);
+}
+
+int wfb_linear_i2s_glu(const uint8_t* qweight, int64_t n, int64_t k, const int8_t* act, int64_t m, int64_t lda,
+                       const float* a_scale, const float* w_scales_dev, int act_kind, int mid_dtype, float* out,
+                       int64_t ldo, void* stream) {
+  const char* name = "wfb_linear_i2s_glu";
+  if (act_kind != WFB_ACT_SILU && act_kind != WFB_ACT_RELU2) return fail(WFB_EINVAL, "%s: bad activation %d", name, act_kind);
+  if (mid_dtype != WFB_F32 && mid_dtype != WFB_BF16)
+    return fail(WFB_EINVAL, "%s: mid dtype must be WFB_F32 or WFB_BF16", name);
+  if (m < 0 || m > 64) return fail(WFB_EINVAL, "%s: M (%lld) must be in 0..64", name, (long long)m);
+  if (n <= 0 || n % 64 != 0 || k <= 0 || k % WFB_QK_I2S != 0)
+    return fail(WFB_EINVAL, "%s: N (%lld) must be 2 x a multiple of 32 and K (%lld) a multiple of %d", name,
+                (long long)n, (long long)k, WFB_QK_I2S);
+  if (n * (k / 4) > INT32_MAX || (m > 0 && (m - 1) * lda + k > INT32_MAX))
+    return fail(WFB_EINVAL, "%s: sizes too large for 32-bit offsets", name);
+  if (lda < k || lda % 16 != 0) return fail(WFB_EINVAL, "%s: activation row stride must be >= K and a multiple of 16", name);
+  if (ldo < n / 2) return fail(WFB_EINVAL, "%s: output row stride (%lld) < N/2 (%lld)", name, (long long)ldo, (long long)(n / 2));
+  if (m == 0) return ok();
+  if (!qweight || !act || !w_scales_dev || !out) return fail(WFB_EINVAL, "%s: null pointer", name);
+  if (!aligned(qweight, 16) || !aligned(act, 16)) return fail(WFB_EINVAL, "%s: qweight and activations must be 16-byte aligned", name);
+  wfb::Epilogue e{};
+  e.nseg = 2;
+  e.seg_end[0] = (int)(n / 2);
+  e.a_scale = a_scale;
+  e.ws_dev = w_scales_dev;
+  e.out = out;
+  e.out_dtype = WFB_F32;
+  e.ldo = ldo;
+  e.mid_dtype = mid_dtype;
+  return hip_status(wfb::launch_gemm_i2s_glu(qweight, (int)n, (int)k, act, (int)m, lda, act_kind, e, as_stream(stream)),
                     name);
 }
 

@@ -94,14 +94,20 @@ __global__ __launch_bounds__(64 * WPB) void gemm_i2s_mfma16_kernel(const uint8_t
 // acc16/16 - sum(a).  Partial 16 x 16 tiles of the S waves are summed through LDS; wave nt < NT
 // finishes row tile nt.  Loads go through raw buffer descriptors: rows past N or M and chunks past K
 // read as zeros.
-template <int MT, int S, int NT>
+// Gated mode (GLUE = 1: SiLU, 2: relu^2): W is gate|up (N = 2 * half rows, two segments of scales); a
+// workgroup takes gate row tiles 0 .. NT/2 - 1 and the up row tiles of the same rows, and wave nt <
+// NT/2 stores x[m, n] = act(gate) * up for its 16 columns: both products rescaled as a plain linear
+// would store them (rounded to ep.mid_dtype), then the fixed-operation gated activation, stored fp32.
+template <int MT, int S, int NT, int GLUE = 0>
 __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* __restrict__ W,
                                                                  const int8_t* __restrict__ A, int64_t lda,
                                                                  int M, int N, int C, Epilogue ep) {
   static_assert(NT <= S, "one wave per row tile in the epilogue");
+  static_assert(GLUE == 0 || NT % 2 == 0, "gated mode pairs gate and up tiles");
   __shared__ int red[S][NT][MT][4][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * 16 * NT;
+  const int half = N / 2;
+  const int n0 = GLUE ? blockIdx.x * 16 * (NT / 2) : blockIdx.x * 16 * NT;
   const int nl = lane & 15, g = lane >> 4;
   const uint32_t row_bytes = (uint32_t)C * 16;
   const uint32_t w_end = (uint32_t)N * row_bytes, a_end = (uint32_t)((int64_t)(M - 1) * lda + (int64_t)C * 64);
@@ -109,7 +115,10 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
   const buf_t ab = make_buf(A, a_end);
   uint32_t woff[NT];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) woff[nt] = (uint32_t)(n0 + nt * 16 + nl) * row_bytes + 16 * g;
+  for (int nt = 0; nt < NT; ++nt) {
+    const int r0 = !GLUE ? n0 + nt * 16 : nt < NT / 2 ? n0 + nt * 16 : half + n0 + (nt - NT / 2) * 16;
+    woff[nt] = (uint32_t)(r0 + nl) * row_bytes + 16 * g;
+  }
   uint32_t aoff[MT];
   bool tok_ok[MT];
 #pragma unroll
@@ -122,7 +131,7 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
   // here, ahead of the weight stream -- measured on MI355X: 5-10% faster at M = 8..64 on 4096-row
   // outputs -- except with four row tiles (N >= 24576), where loading them after the final barrier is
   // 3% faster (fewer registers).
-  constexpr bool PRE = NT < 4;
+  constexpr bool PRE = NT < 4 && GLUE == 0;
   int toks[4 * MT];
 #pragma unroll
   for (int j = 0; j < 4 * MT; ++j) toks[j] = (j / 4) * 16 + 4 * g + (j % 4);
@@ -193,6 +202,33 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
     }
   }
   __syncthreads();
+  if constexpr (GLUE != 0) {
+    if (w >= NT / 2) return;
+    const int n = n0 + w * 16 + nl;  // output column = gate row; its up row is half + n
+    if (n >= half) return;
+    const float wsg = epi_wscale(ep, n), wsu = epi_wscale(ep, half + n);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tok = mt * 16 + 4 * g + j;
+        if (tok >= M) continue;
+        int tg = red[0][w][mt][j][lane], tu = red[0][w + NT / 2][mt][j][lane];
+#pragma unroll
+        for (int k = 1; k < S; ++k) {
+          tg += red[k][w][mt][j][lane];
+          tu += red[k][w + NT / 2][mt][j][lane];
+        }
+        const float as = epi_ascale(ep, tok);
+        float yg = __fmul_rn(__fmul_rn((float)tg, wsg), as), yu = __fmul_rn(__fmul_rn((float)tu, wsu), as);
+        if (ep.mid_dtype == WFB_BF16) {
+          yg = bf16_bits_to_f32(f32_to_bf16_rne(yg));
+          yu = bf16_bits_to_f32(f32_to_bf16_rne(yu));
+        }
+        reinterpret_cast<float*>(ep.out)[(int64_t)tok * ep.ldo + n] = glu<GLUE>(yg, yu);
+      }
+    return;
+  }
   if (w >= NT) return;
   const int nt = w;
   const int n = n0 + nt * 16 + nl;
@@ -562,6 +598,19 @@ hipError_t launch_mt(const uint8_t* W, int n, int C, const int8_t* A, int m, int
 
 }  // namespace
 
+template <int MT, int GLUE>
+hipError_t launch_skinny_glu(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
+                             hipStream_t s) {
+  const int half = n / 2;
+  if (MT == 1 && n >= 24576)
+    hipLaunchKernelGGL((gemm_i2s_skinny_kernel<MT, 4, 4, GLUE>), dim3((half + 31) / 32), dim3(256), 0, s, W, A, lda, m,
+                       n, C, e);
+  else
+    hipLaunchKernelGGL((gemm_i2s_skinny_kernel<MT, 8, 2, GLUE>), dim3((half + 15) / 16), dim3(512), 0, s, W, A, lda, m,
+                       n, C, e);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                                   const Epilogue& e, hipStream_t s) {
   const int C = k / 64;
@@ -569,6 +618,18 @@ hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* 
   if (m <= 32) return launch_skinny<2>(W, n, C, A, m, lda, e, s);
   if (m <= 64) return launch_skinny<4>(W, n, C, A, m, lda, e, s);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemm_i2s_glu(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, int act,
+                               const Epilogue& e, hipStream_t s) {
+  const int C = k / 64;
+#define WFB_GLU(MT)                                                                              \
+  return act == WFB_ACT_SILU ? launch_skinny_glu<MT, WFB_ACT_SILU>(W, n, C, A, m, lda, e, s) \
+                             : launch_skinny_glu<MT, WFB_ACT_RELU2>(W, n, C, A, m, lda, e, s)
+  if (m <= 16) WFB_GLU(1);
+  if (m <= 32) WFB_GLU(2);
+  WFB_GLU(4);
+#undef WFB_GLU
 }
 
 hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, const Epilogue& e,

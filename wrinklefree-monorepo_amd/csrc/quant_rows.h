@@ -32,36 +32,6 @@ __device__ __forceinline__ float wave_sum_fixed(float v) {
   return v;
 }
 
-// Gated activations (GLU = 1: silu(g) * u, GLU = 2: relu(g)^2 * u).  Every step is one correctly
-// rounded fp32 operation (no FMA), so a float32 CPU restatement reproduces the result bit for bit.
-// 2^t = 2^n * p(t - n), n = rint(t) with t clamped to [-125, 125] (2^n stays a normal number),
-// p the degree-7 Taylor polynomial of 2^f = exp(f ln 2) on |f| <= 1/2 (remainder < 6e-9).
-__device__ __forceinline__ float exp2_fixed(float t) {
-  t = fminf(fmaxf(t, -125.0f), 125.0f);
-  const float n = rintf(t);
-  const float f = __fsub_rn(t, n);
-  float p = 1.525273380405984e-05f;  // ln(2)^7 / 7!
-  p = __fadd_rn(__fmul_rn(p, f), 1.5403530393381606e-04f);
-  p = __fadd_rn(__fmul_rn(p, f), 1.3333558146428443e-03f);
-  p = __fadd_rn(__fmul_rn(p, f), 9.618129107628477e-03f);
-  p = __fadd_rn(__fmul_rn(p, f), 5.550410866482158e-02f);
-  p = __fadd_rn(__fmul_rn(p, f), 2.402265069591007e-01f);
-  p = __fadd_rn(__fmul_rn(p, f), 6.931471805599453e-01f);
-  p = __fadd_rn(__fmul_rn(p, f), 1.0f);
-  return __fmul_rn(p, __int_as_float(((int)n + 127) << 23));
-}
-
-template <int GLU>
-__device__ __forceinline__ float glu(float g, float u) {
-  if constexpr (GLU == 1) {
-    const float e = exp2_fixed(__fmul_rn(-g, 1.4426950408889634f));  // exp(-g)
-    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
-  } else {
-    const float r = fmaxf(g, 0.0f);
-    return __fmul_rn(__fmul_rn(r, r), u);
-  }
-}
-
 // 8 consecutive row elements from element e0 (h = row length): x itself (GLU = 0) or the gated
 // product of x (gate) and u (up).
 template <int DT, int GLU>

@@ -142,12 +142,44 @@ struct Epilogue {
   const void* res;
   int res_dtype;
   int64_t ldr;
+  // Gated (gate|up) epilogue only: the type the two products are rounded to before the activation.
+  int mid_dtype;
 };
 
 __device__ __forceinline__ float epi_res(const Epilogue& e, int m, int n) {
   const int64_t off = (int64_t)m * e.ldr + n;
   if (e.res_dtype == WFB_F32) return reinterpret_cast<const float*>(e.res)[off];
   return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(e.res)[off]);
+}
+
+// Gated activations (GLU = 1: silu(g) * u, GLU = 2: relu(g)^2 * u).  Every step is one correctly
+// rounded fp32 operation (no FMA), so a float32 CPU restatement reproduces the result bit for bit.
+// 2^t = 2^n * p(t - n), n = rint(t) with t clamped to [-125, 125] (2^n stays a normal number),
+// p the degree-7 Taylor polynomial of 2^f = exp(f ln 2) on |f| <= 1/2 (remainder < 6e-9).
+__device__ __forceinline__ float exp2_fixed(float t) {
+  t = fminf(fmaxf(t, -125.0f), 125.0f);
+  const float n = rintf(t);
+  const float f = __fsub_rn(t, n);
+  float p = 1.525273380405984e-05f;  // ln(2)^7 / 7!
+  p = __fadd_rn(__fmul_rn(p, f), 1.5403530393381606e-04f);
+  p = __fadd_rn(__fmul_rn(p, f), 1.3333558146428443e-03f);
+  p = __fadd_rn(__fmul_rn(p, f), 9.618129107628477e-03f);
+  p = __fadd_rn(__fmul_rn(p, f), 5.550410866482158e-02f);
+  p = __fadd_rn(__fmul_rn(p, f), 2.402265069591007e-01f);
+  p = __fadd_rn(__fmul_rn(p, f), 6.931471805599453e-01f);
+  p = __fadd_rn(__fmul_rn(p, f), 1.0f);
+  return __fmul_rn(p, __int_as_float(((int)n + 127) << 23));
+}
+
+template <int GLU>
+__device__ __forceinline__ float glu(float g, float u) {
+  if constexpr (GLU == 1) {
+    const float e = exp2_fixed(__fmul_rn(-g, 1.4426950408889634f));  // exp(-g)
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
+  } else {
+    const float r = fmaxf(g, 0.0f);
+    return __fmul_rn(__fmul_rn(r, r), u);
+  }
 }
 
 // Orderable 64-bit key of (value y, row n): larger y wins, and among equal values the smaller row
@@ -349,6 +381,10 @@ hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* 
 hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                            const Epilogue& e, hipStream_t s);
 hipError_t launch_mfma_rate(bool random_operands, int64_t blocks, int64_t iters, int* sink, hipStream_t s);
+// gate|up linear with the gated activation in its epilogue (M <= 64; n = 2 * half, half % 32 == 0;
+// fp32 output [M, half] at e.out / e.ldo)
+hipError_t launch_gemm_i2s_glu(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, int act,
+                               const Epilogue& e, hipStream_t s);
 // RMSNorm + quant in the prologue of the batched-decode linear (M <= 16, H <= K <= 4096)
 hipError_t launch_norm_linear(const void* x, int xdt, int64_t ldx, const void* gamma, int gdt, float eps, int h,
                               const uint8_t* W, int m, int n, int k, const Epilogue& e, hipStream_t s);

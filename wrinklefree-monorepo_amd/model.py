@@ -30,9 +30,9 @@ from typing import Dict, List, Optional, Sequence
 import torch
 
 from .sglbitnt import SGLBitNetFile, write_sglbitnt
-from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_residual, bitnet_linear_segmented,
-                  glu_rmsnorm_quantize_i8, gqa_decode_attention, lm_head_argmax, pack_ternary_i2s, rmsnorm_linear,
-                  rmsnorm_linear_preferred, rmsnorm_quantize_i8)
+from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_glu,
+                  bitnet_linear_residual, bitnet_linear_segmented, glu_rmsnorm_quantize_i8, gqa_decode_attention,
+                  lm_head_argmax, pack_ternary_i2s, rmsnorm_linear, rmsnorm_linear_preferred, rmsnorm_quantize_i8)
 
 
 @dataclass(frozen=True)
@@ -181,6 +181,22 @@ class HipBackend:
                                   residual=residual.contiguous())
         q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=linear.k_pad)
         return self._linear_residual(q, a_scale, linear, residual)
+
+    def mlp_residual(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], eps: float, gate: PackedLinear,
+                     up: PackedLinear, act: str, sub_norm: Optional[torch.Tensor], sub_eps: float, down: PackedLinear,
+                     residual: torch.Tensor) -> torch.Tensor:
+        """residual + down(quantise(SubLN(act(gate(h)) * up(h)))), h = quantise(norm(x)).  For decode batches
+        the gated product rides in the gate|up launch's epilogue (``bitnet_linear_glu``, fp32), and SubLN +
+        quantise runs on it as a plain row quantiser -- the same codes as the separate gated kernel."""
+        half = gate.out_features
+        if (self.fused and not self.keep_acc and x.dim() == 2 and x.shape[0] <= 64 and up.out_features == half
+                and half % 32 == 0 and act in ("silu", "relu2")):
+            q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=gate.k_pad)
+            qw, sc, _ = self._group([gate, up])
+            mid = bitnet_linear_glu(qw, sc, q, act, a_scale=a_scale, mid_dtype=self.out_dtype)
+            return self.norm_linear_residual(mid, sub_norm, sub_eps, down, residual)
+        g, u = self.norm_linears(x, norm_weight, eps, [gate, up])
+        return self.glu_norm_linear_residual(g, u, act, sub_norm, sub_eps, down, residual)
 
     def glu_norm_linear_residual(self, gate: torch.Tensor, up: torch.Tensor, act: str,
                                  norm_weight: Optional[torch.Tensor], eps: float, linear: PackedLinear,
@@ -447,6 +463,10 @@ class BitNetDecoder:
                 (o,) = be.norm_linears(attn, L.attn_sub_norm, cfg.subln_eps, [L.o])
                 x = x + o.reshape(b, t, -1).to(self.dtype)
             h2 = x.reshape(b * t, cfg.hidden_size)
+            if fused_res and hasattr(be, "mlp_residual"):
+                x = be.mlp_residual(h2, L.post_attn_norm, cfg.rms_eps, L.gate, L.up, cfg.hidden_act, L.ffn_sub_norm,
+                                    cfg.subln_eps, L.down, h2).reshape(b, t, -1)
+                continue
             gate, up = be.norm_linears(h2, L.post_attn_norm, cfg.rms_eps, [L.gate, L.up])
             if fused_res:
                 x = be.glu_norm_linear_residual(gate, up, cfg.hidden_act, L.ffn_sub_norm, cfg.subln_eps, L.down,

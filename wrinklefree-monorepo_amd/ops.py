@@ -537,6 +537,53 @@ def rmsnorm_linear(
     return out
 
 
+def bitnet_linear_glu(
+    packed_weights: torch.Tensor, scales: torch.Tensor, activations: torch.Tensor, act: str = "silu",
+    a_scale: Optional[torch.Tensor] = None, mid_dtype: torch.dtype = torch.bfloat16,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """act(gate) * up from the gate|up projection in one launch (decode batches, M <= 64): fp32 [M, half].
+
+    ``packed_weights`` is gate|up (2 * half rows, half % 32 == 0), ``scales`` fp32 [2] on the device.
+    Equal, bit for bit, to ``bitnet_linear_segmented`` with ``out_dtype=mid_dtype`` followed by the gated
+    product of ``glu_rmsnorm_quantize_i8`` (so ``rmsnorm_quantize_i8`` of the result equals
+    ``glu_rmsnorm_quantize_i8`` of the stored gate and up)."""
+    name = "bitnet_linear_glu"
+    if act not in _ACTS:
+        raise ValueError(f"{name}: act must be one of {sorted(_ACTS)}")
+    if packed_weights.dtype != torch.uint8 or packed_weights.dim() != 2:
+        raise RuntimeError(f"{name}: packed_weights must be uint8 2D [2 * half, in_features/4]")
+    n, kb = packed_weights.shape
+    k = kb * 4
+    if n % 64 != 0:
+        raise ValueError(f"{name}: gate|up rows ({n}) must be 2 x a multiple of 32")
+    if activations.dtype != torch.int8 or activations.dim() != 2 or activations.shape[1] != k:
+        raise RuntimeError(f"{name}: activations must be int8 [batch, {k}]")
+    m = activations.shape[0]
+    if m > 64:
+        raise RuntimeError(f"{name}: at most 64 tokens (got {m})")
+    if scales.dtype != torch.float32 or scales.numel() != 2:
+        raise RuntimeError(f"{name}: scales must be fp32 [2] (gate, up)")
+    if mid_dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError(f"{name}: mid_dtype must be float32 or bfloat16")
+    dev = _require_gpu(name, packed_weights, scales, activations, a_scale)
+    a2 = activations
+    if a2.stride(1) != 1 or (m > 1 and a2.stride(0) % 16 != 0) or a2.data_ptr() % 16 != 0:
+        a2 = a2.contiguous()
+    if a_scale is not None and (a_scale.dtype != torch.float32 or a_scale.numel() != m):
+        raise RuntimeError(f"{name}: a_scale must be fp32 with one element per token ({m})")
+    half = n // 2
+    if out is None:
+        out = torch.empty((m, half), dtype=torch.float32, device=dev)
+    elif out.dtype != torch.float32 or out.shape != (m, half) or out.stride(-1) != 1:
+        raise RuntimeError(f"{name}: out must be float32 [{m}, {half}] with contiguous rows")
+    lda = a2.stride(0) if m > 1 else k
+    with torch.cuda.device(dev):
+        _lib.call("wfb_linear_i2s_glu", _p(packed_weights), n, k, _p(a2), m, lda, _p(a_scale), _p(scales),
+                  _ACTS[act], _DT[mid_dtype], _p(out), out.stride(0) if m > 1 else half, _stream(dev))
+    return out
+
+
 # ---- greedy decoding: LM head + argmax ----------------------------------------------------------
 
 
