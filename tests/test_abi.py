@@ -186,3 +186,39 @@ def test_diag_mfma_argument_errors(pkg):
     assert "blocks" in pkg._lib.last_error()
     assert pkg._lib.status("wfb_diag_mfma_i8", 1, 4, 10, None, None) == -1
     assert "null sink" in pkg._lib.last_error()
+
+
+def test_rmsnorm_linear_argument_errors(pkg):
+    vp = ctypes.c_void_p
+    seg = (ctypes.c_int64 * 2)(64, 64)
+
+    def st(x_dt=1, g_dt=1, m=8, h=4096, n=128, k=4096, n_seg=1, segp=None, res=None, res_dt=1, out_dt=1, x=16):
+        return pkg._lib.status("wfb_rmsnorm_linear_i2s", vp(x) if x else None, x_dt, h, vp(16), g_dt, 1e-5, m, h,
+                               vp(16), n, k, n_seg, segp, vp(16), res, res_dt, n, vp(16), out_dt, n, None)
+
+    assert st(x_dt=2) == -1 and "x dtype" in pkg._lib.last_error()
+    assert st(g_dt=2) == -1 and "gamma dtype" in pkg._lib.last_error()
+    assert st(m=17) == -1 and "M (17)" in pkg._lib.last_error()
+    assert st(h=4100, k=4224) == -1 and "H <= K <= 4096" in pkg._lib.last_error()
+    assert st(m=16) == -1 and "exceeds 49152" in pkg._lib.last_error()
+    assert st(n_seg=2) == -1 and "seg_rows" in pkg._lib.last_error()
+    assert st(n_seg=2, segp=ctypes.cast(seg, vp), n=136) == -1 and "sum to 128" in pkg._lib.last_error()
+    assert st(res=vp(16), res_dt=2) == -1 and "residual dtype" in pkg._lib.last_error()
+    assert st(out_dt=2) == -1 and "out must be" in pkg._lib.last_error()
+    assert st(x=8) == -1 and "16-byte aligned" in pkg._lib.last_error()
+
+
+def test_linear_glu_argument_errors(pkg):
+    vp = ctypes.c_void_p
+
+    def st(n=128, k=256, m=4, act=1, mid=1, lda=256, ldo=64):
+        return pkg._lib.status("wfb_linear_i2s_glu", vp(16), n, k, vp(16), m, lda, None, vp(16), act, mid, vp(16), ldo,
+                               None)
+
+    assert st(act=3) == -1 and "activation" in pkg._lib.last_error()
+    assert st(mid=2) == -1 and "mid dtype" in pkg._lib.last_error()
+    assert st(m=65) == -1 and "0..64" in pkg._lib.last_error()
+    assert st(n=96) == -1 and "multiple of 32" in pkg._lib.last_error()
+    assert st(lda=200) == -1 and "row stride" in pkg._lib.last_error()
+    assert st(ldo=32) == -1 and "N/2" in pkg._lib.last_error()
+    assert st(m=0) == 0
