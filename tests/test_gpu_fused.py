@@ -126,7 +126,8 @@ def test_bitnet_linear_native_module(pkg, dev):
         assert np.array_equal(y, y_ref)
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 2560, 2560), (8, 4096, 14336), (3, 640, 1024), (200, 2560, 6912), (64, 520, 512)])
+@pytest.mark.parametrize("m,n,k", [(1, 2560, 2560), (8, 4096, 14336), (3, 640, 1024), (200, 2560, 6912), (64, 520, 512),
+                                   (300, 1016, 640), (1024, 6144, 512), (2048, 6144, 256)])
 @pytest.mark.parametrize("rdt", [torch.float32, torch.bfloat16])
 def test_linear_residual_matches_oracle(pkg, dev, m, n, k, rdt):
     """out = residual + acc * w_scale * a_scale in one launch (GEMV, skinny and tile kernels): the fp32
@@ -144,3 +145,21 @@ def test_linear_residual_matches_oracle(pkg, dev, m, n, k, rdt):
     buf = res.to(dev)
     pkg.bitnet_linear_residual(pw, at, float(ws), buf, a_scale=st, out=buf)
     assert torch.equal(buf.cpu(), want)
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 1004, 640), (100, 2560, 384), (1024, 6144, 512), (2048, 6144, 256)])
+@pytest.mark.parametrize("odt", [torch.float32, torch.bfloat16])
+def test_tile_epilogue_out_types_match_oracle(pkg, dev, m, n, k, odt):
+    """Prefill tile kernel outputs without an accumulator copy (the staged epilogues: fp32 or bf16, whole
+    and partial column groups, 32/64/128-row tiles) equal the oracle's rescale bit for bit."""
+    if odt == torch.bfloat16 and n % 8:
+        pytest.skip("bf16 rows need N % 8 == 0 for 16-byte aligned rows")
+    rng = np.random.default_rng(3 * m + n + k)
+    packed = orc.pack_i2s(orc.random_ternary(rng, n, k))
+    a = orc.random_int8(rng, m, k)
+    ws, a_s = orc.log_uniform(rng), orc.log_uniform(rng, m)
+    acc = (a.astype(np.float32) @ orc.unpack_i2s(packed).astype(np.float32).T).astype(np.int64)
+    want = torch.from_numpy(orc.rescale(acc, np.float32(ws), a_s)).to(odt)
+    pw, at, st = (torch.from_numpy(x).to(dev) for x in (packed, a, a_s))
+    got = pkg.bitnet_linear(pw, at, float(ws), a_scale=st, out_dtype=odt)
+    assert torch.equal(got.cpu(), want)

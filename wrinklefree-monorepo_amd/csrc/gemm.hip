@@ -547,6 +547,77 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
         }
       }
     }
+  } else if constexpr (EPI == 2) {
+    // per 32-row MFMA tile: stage the fp32 outputs (32 rows x 64 columns, 256-byte rows, 16-byte chunks
+    // XOR-swizzled by row) in this wave's own LDS buffer; each lane then takes 8 consecutive outputs of
+    // a row, adds the residual read with one coalesced load (fp32 add, as epi_store), and stores them in
+    // the output type with one or two 16-byte stores -- whole lines, like EPI = 1
+    float* st = wn == 0 ? reinterpret_cast<float*>(lds_a0)
+              : wn == 1 ? reinterpret_cast<float*>(lds_a1)
+              : wn == 2 ? reinterpret_cast<float*>(lds_b0) : reinterpret_cast<float*>(lds_b1);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      const int rs = rowsum[tm * 32 + i];
+      const float as = epi_ascale(ep, min(m0 + tm * 32 + i, M - 1));
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float4 y;
+          y.x = __fmul_rn(__fmul_rn((float)(acc[tn][tm][4 * q + 0] - rs), wsg[tn][q]), as);
+          y.y = __fmul_rn(__fmul_rn((float)(acc[tn][tm][4 * q + 1] - rs), wsg[tn][q]), as);
+          y.z = __fmul_rn(__fmul_rn((float)(acc[tn][tm][4 * q + 2] - rs), wsg[tn][q]), as);
+          y.w = __fmul_rn(__fmul_rn((float)(acc[tn][tm][4 * q + 3] - rs), wsg[tn][q]), as);
+          const int c = tn * 8 + 2 * q + g;  // 16-byte chunk of the row: columns 4c .. 4c + 3
+          *reinterpret_cast<float4*>(st + i * 64 + ((c ^ (i & 15)) * 4)) = y;
+        }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 8 * j + (l >> 3), c8 = l & 7;
+        const float4 ya = *reinterpret_cast<const float4*>(st + r * 64 + (((2 * c8) ^ (r & 15)) * 4));
+        const float4 yb = *reinterpret_cast<const float4*>(st + r * 64 + (((2 * c8 + 1) ^ (r & 15)) * 4));
+        float y[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
+        const int m = m0 + tm * 32 + r, n = n0 + wn * 64 + c8 * 8;
+        if (m >= M) continue;
+        const bool full = n + 7 < N;
+        if (ep.res) {
+          float rv[8];
+          if (full) {
+            if (ep.res_dtype == WFB_BF16) load8<WFB_BF16>(ep.res, (int64_t)m * ep.ldr + n, rv);
+            else load8<WFB_F32>(ep.res, (int64_t)m * ep.ldr + n, rv);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) rv[e] = n + e < N ? epi_res(ep, m, n + e) : 0.0f;
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) y[e] = __fadd_rn(y[e], rv[e]);
+        }
+        if (ep.out_dtype == WFB_BF16) {
+          uint16_t* o = reinterpret_cast<uint16_t*>(ep.out) + (int64_t)m * ep.ldo + n;
+          if (full) {
+            uint32_t w4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              w4[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){y[2 * e], y[2 * e + 1]}, bf16x2_t));
+            *reinterpret_cast<uint4*>(o) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (n + e < N) o[e] = f32_to_bf16_rne(y[e]);
+          }
+        } else {
+          float* o = reinterpret_cast<float*>(ep.out) + (int64_t)m * ep.ldo + n;
+          if (full) {
+            *reinterpret_cast<float4*>(o) = make_float4(y[0], y[1], y[2], y[3]);
+            *reinterpret_cast<float4*>(o + 4) = make_float4(y[4], y[5], y[6], y[7]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (n + e < N) o[e] = y[e];
+          }
+        }
+      }
+    }
   } else {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
@@ -577,8 +648,15 @@ hipError_t launch_tile(const uint8_t* W, int n, int k, const int8_t* A, int m, i
   const bool vec_out = e.ldo % 4 == 0 && (uintptr_t)e.out % 16 == 0 && (uintptr_t)e.acc_out % 16 == 0;
   const bool bf16_only = e.out && e.out_dtype == WFB_BF16 && !e.bias && !e.acc_out && !e.res && e.ldo % 8 == 0 &&
                          (uintptr_t)e.out % 16 == 0;
+  // staged fp32 epilogue: fp32 or bf16 out with an optional residual, 16-byte aligned rows
+  const int osz = e.out_dtype == WFB_F32 ? 4 : 2, rsz = e.res_dtype == WFB_F32 ? 4 : 2;
+  const bool staged = e.out && !e.bias && !e.acc_out && (e.ldo * osz) % 16 == 0 && (uintptr_t)e.out % 16 == 0 &&
+                      (!e.res || ((e.ldr * rsz) % 16 == 0 && (uintptr_t)e.res % 16 == 0));
   if (bf16_only)
     hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 1>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
+                       tiles_m, tiles_n, nwg, vec_out, e);
+  else if (staged)
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 2>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
                        tiles_m, tiles_n, nwg, vec_out, e);
   else
     hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 0>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
@@ -648,13 +726,13 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   if (m <= 16) return launch_mt<1>(W, n, C, A, m, lda, e, s);
   if (m <= 32) return launch_mt<2>(W, n, C, A, m, lda, e, s);
   if (m <= 64) return launch_mt<4>(W, n, C, A, m, lda, e, s);
-  // Tile height by the number of 256-column tiles (512 workgroup slots at two per CU), measured on
-  // MI355X: 128-row tiles (half the weight unpack per MFMA) once there are enough of them (wide N and
-  // M > 512, or >= 512 tiles: M = 8192, N = 2560 172.6 vs 179.5 us); 64-row tiles in between; 32-row
-  // tiles when even 64-row ones leave most of the chip idle (M = 512, N = 2560, K = 6912: 21.7 vs
-  // 30.8 us).
+  // Tile height by the number of 256-column tiles (512 workgroup slots at two per CU), from a sweep on
+  // MI355X over M = 1024..8192 and the BitNet-2B / Llama-3-8B shapes: 128-row tiles (half the weight
+  // unpack per MFMA) from 320 of them (M = 2048, N = 6144: 58.8 vs 66.5 us), 64-row tiles below that
+  // (M = 1024, N = 4096, K = 14336: 69.1 vs 107.5 us), 32-row tiles when even 64-row ones leave most
+  // of the chip idle (M = 512, N = 2560, K = 6912: 21.7 vs 30.8 us).
   const int64_t tn = (n + 255) / 256, t128 = tn * ((m + 127) / 128), t64 = tn * ((m + 63) / 64);
-  if ((n >= 4096 && m > 512) || t128 >= 512) return launch_tile<4, 1, 2>(W, n, k, A, m, lda, e, s);
+  if (t128 >= 320) return launch_tile<4, 1, 2>(W, n, k, A, m, lda, e, s);
   if (t64 >= 160) return launch_tile<2, 2, 2>(W, n, k, A, m, lda, e, s);
   return launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
 }
