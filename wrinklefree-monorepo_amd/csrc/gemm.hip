@@ -326,8 +326,10 @@ hipError_t launch_skinny(const uint8_t* W, int n, int C, const int8_t* A, int m,
 //  * Tile order: XCD-aware (each XCD takes a contiguous range of tiles) and grouped by kGroupM tile
 //    rows, so the workgroups resident on one XCD share activation rows and weight columns in its L2.
 //  * EPI = 1 (bf16 output, no bias, no accumulator copy): the tile is converted in registers, staged
-//    through LDS and written with 16-byte stores that fill whole output lines.  EPI = 0: any output
-//    type, bias, accumulator copy, stored from registers.
+//    through LDS and written with 16-byte stores that fill whole output lines.  EPI = 2 (fp32 or bf16
+//    output with an optional residual, aligned rows): fp32 outputs staged through LDS, the residual
+//    added after a coalesced 16-byte load, whole-line stores.  EPI = 0: any output type, bias,
+//    accumulator copy, stored from registers.
 constexpr int kGroupM = 8;
 
 typedef __attribute__((address_space(3))) void lds_void;
