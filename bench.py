@@ -364,7 +364,8 @@ def e2e_bench(pkg, torch, dev, cpu: bool = True):
     Llama-3-8B shape, every linear ternary, random init on the device; prefill of 8
     prompts x 256 tokens (2048 tokens, one M = 2048 GEMM per projection), then 256 decode steps at
     batch 8.  configs[0]: SmolLM2-135M shape, 32-token prompt, 128 new tokens at batch 1.
-    Wall-clock times around synchronised regions (host launch overhead included); decode is timed
+    Wall-clock times around synchronised regions (host launch overhead included); the prefill is the
+    mean of 3 prompt forwards after one at the same size (fresh caches each time); decode is timed
     both with eager launches and replayed from one HIP graph capture of the decode step.  ``cpu``: also
     the SmolLM2 model decoded on the host (float glue in torch on the CPU, every quantised group on the
     numpy oracle; a bounded sample of new tokens) as the end-to-end CPU baseline."""
@@ -380,12 +381,16 @@ def e2e_bench(pkg, torch, dev, cpu: bool = True):
         prompt = torch.randint(0, cfg.vocab_size, (batch, t0), generator=torch.Generator().manual_seed(5)).to(dev)
         with torch.no_grad():
             model.generate(prompt[:, :8], 4, graph=True)       # warm-up (kernels, allocator, graph path)
-            torch.cuda.synchronize()
             model.reset(batch, t0 + new)
-            ta = time.perf_counter()
-            model.forward(prompt, 0, tokens=True)
+            model.forward(prompt, 0, tokens=True)              # warm-up at the timed prompt size
             torch.cuda.synchronize()
-            prefill_s = time.perf_counter() - ta
+            reps = 3
+            ta = time.perf_counter()
+            for _ in range(reps):
+                model.reset(batch, t0 + new)
+                model.forward(prompt, 0, tokens=True)
+            torch.cuda.synchronize()
+            prefill_s = (time.perf_counter() - ta) / reps
             timings = {}
             for mode in ("eager", "graph"):
                 tb = time.perf_counter()

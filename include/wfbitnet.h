@@ -269,6 +269,29 @@ int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int6
                              int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
                              float scale, void* out, int64_t ldo, float* workspace, void* stream);
 
+/* Causal GQA attention of a prefill chunk: T new tokens per sequence at positions start .. start+T-1.
+ * Rotary embedding of the new queries and keys (rope_cos / rope_sin fp32 [max_len, head_dim/2], or both
+ * NULL for none), cache append of the T keys and values at their positions, then for token i of
+ * sequence b and query head h: softmax(q . k_j * scale, j = 0 .. start+i) . v over the cache of kv head
+ * h / (num_heads / num_kv_heads).  bf16 only (dtype WFB_BF16): q rows [batch*T, ldq] (row b*T + i holds
+ * the num_heads*head_dim query elements), k_new / v_new rows [batch*T, ldk / ldv] (num_kv_heads*head_dim
+ * each); the three may be column slices of one q|k|v projection output.  Caches [batch, num_kv_heads,
+ * max_len, head_dim], 16-byte aligned; out [batch*T, ldo] (num_heads*head_dim per row).  head_dim 64 or
+ * 128, num_heads / num_kv_heads in 1..8, start + T <= max_len, row strides multiples of 8 elements and
+ * row bases 16-byte aligned.  The cache rows written are bit-identical to the rotary + append of the
+ * decode call; scores, softmax and the weighted sum are fp32 (products of bf16 operands on the matrix
+ * cores, the probabilities as two bf16 parts), the output rounded to bf16.
+ * Replaces attention_forward (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:381-441) run once per
+ * prompt token, with the cache writes of kv_cache_update_key / kv_cache_update_value
+ * (SGB/sgl-kernel/csrc/inference/kv_cache.h:81-101) and the stage-1 rotary embedding
+ * (WF/training/stage1.py:169-214). */
+int wfb_gqa_prefill_attention(const void* q, int64_t ldq, const void* k_new, int64_t ldk,
+                              const void* v_new, int64_t ldv, int dtype,
+                              const float* rope_cos, const float* rope_sin,
+                              void* k_cache, void* v_cache, int64_t max_len, int64_t start,
+                              int64_t batch, int64_t t, int64_t num_heads, int64_t num_kv_heads,
+                              int64_t head_dim, float scale, void* out, int64_t ldo, void* stream);
+
 /* Decode-time fusion of wfb_rmsnorm_quant_i8 and the BitLinear that consumes its codes (one launch):
  *   q, a_scale = rmsnorm_quant(x, gamma, eps)          (exactly wfb_rmsnorm_quant_i8, codes zero past H)
  *   out = linear_i2s_segmented(qweight, q, a_scale)      (exactly wfb_linear_i2s_segmented; one segment =

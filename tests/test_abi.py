@@ -142,6 +142,30 @@ def test_attention_argument_errors(pkg):
     assert st(b=0) == 0
 
 
+def test_prefill_attention_argument_errors(pkg):
+    vp = ctypes.c_void_p
+
+    def st(**kw):
+        a = dict(q=vp(16), ldq=512, k=vp(16), ldk=128, v=vp(16), ldv=128, dtype=1, rc=None, rs=None, kc=vp(16),
+                 vc=vp(16), max_len=64, start=0, b=1, t=8, hq=8, hkv=2, d=64, scale=0.125, out=vp(16), ldo=512)
+        a.update(kw)
+        return pkg._lib.status("wfb_gqa_prefill_attention", *a.values(), None)
+
+    assert st(dtype=0) == -1 and "WFB_BF16" in pkg._lib.last_error()
+    assert st(d=96) == -1 and "head_dim" in pkg._lib.last_error()
+    assert st(hq=18, ldq=18 * 64, ldo=18 * 64) == -1 and "num_heads" in pkg._lib.last_error()
+    assert st(start=60) == -1 and "within max_len" in pkg._lib.last_error()
+    assert st(start=-1) == -1 and "within max_len" in pkg._lib.last_error()
+    assert st(ldq=256) == -1 and "strides" in pkg._lib.last_error()
+    assert st(ldq=516, ldo=516) == -1 and "multiples of 8" in pkg._lib.last_error()
+    assert st(rc=vp(16)) == -1 and "rope" in pkg._lib.last_error()
+    assert st(max_len=1 << 30) == -1 and "max_len" in pkg._lib.last_error()
+    assert st(kc=vp(8)) == -1 and "aligned" in pkg._lib.last_error()
+    assert st(out=None) == -1 and "null" in pkg._lib.last_error()
+    assert st(scale=float("nan")) == -1 and "finite" in pkg._lib.last_error()
+    assert st(b=0) == 0 and st(t=0) == 0
+
+
 def test_argmax_argument_errors(pkg):
     vp = ctypes.c_void_p
     st = pkg._lib.status("wfb_linear_i2s_argmax", vp(16), 64, 128, vp(16), 65, 128, None, None, 1.0, None, 0, 64,

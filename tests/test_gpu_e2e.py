@@ -145,6 +145,37 @@ def test_hip_decode_attention_matches_torch_decode(pkg, dev, dtype):
     assert float(diff.mean()) <= (2e-3 if dtype == torch.float32 else 1e-2) * span
 
 
+def test_hip_prefill_attention_matches_torch_prefill(pkg, dev):
+    """A bf16 model's prompt forward with the matrix-core prefill attention kernel against the same
+    forward as torch ops: layer 0's cache is bit-identical (same inputs, same rotary arithmetic; deeper
+    layers see hidden states that already differ by float rounding) and the logits agree to the float
+    tolerance of the decode comparison; greedy decode then continues from either cache."""
+    M = pkg.model
+    cfg = M.BitNetConfig(vocab_size=4096, hidden_size=512, intermediate_size=1024, num_layers=3, num_heads=8,
+                         num_kv_heads=2, head_dim=128, rope_theta=500000.0)
+    prompt = torch.randint(0, cfg.vocab_size, (3, 45), generator=torch.Generator().manual_seed(9)).to(dev)
+    runs = {}
+    for mode in ("torch", "hip"):
+        model = M.BitNetDecoder(cfg, seed=5, device=dev, dtype=torch.bfloat16, prefill_attention=mode,
+                                backend=M.HipBackend(out_dtype=torch.bfloat16, fused=True))
+        assert model._hip_prefill() == (mode == "hip")
+        with torch.no_grad():
+            model.reset(3, 64)
+            logits = model.forward(prompt, 0)
+            toks = model.generate(prompt, 6)
+        runs[mode] = (logits.cpu(), [c.cpu() for kv in model.kv for c in kv], toks.cpu())
+    lt, ct, tt = runs["torch"]
+    lh, ch, th = runs["hip"]
+    assert torch.equal(ct[0][:, :, :45], ch[0][:, :, :45]) and torch.equal(ct[1][:, :, :45], ch[1][:, :, :45])
+    for a, b in zip(ct[2:], ch[2:]):
+        assert float((a.float() - b.float()).abs().max()) <= 5e-2 * float(a.float().abs().max())
+    span = float(lt.abs().max())
+    diff = (lt - lh).abs()
+    assert float(diff.max()) <= 5e-2 * span
+    assert float(diff.mean()) <= 1e-2 * span
+    assert tt.shape == th.shape == (3, 6)
+
+
 def test_host_copy_runs_the_same_model(pkg, dev):
     """on_host (the end-to-end CPU baseline): the same weights with torch-CPU float glue and the oracle
     BitLinears give the GPU model's prefill logits to a float tolerance, and decode on the host."""

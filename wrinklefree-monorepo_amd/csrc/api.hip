@@ -356,6 +356,44 @@ int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int6
                     name);
 }
 
+int wfb_gqa_prefill_attention(const void* q, int64_t ldq, const void* k_new, int64_t ldk, const void* v_new,
+                              int64_t ldv, int dtype, const float* rope_cos, const float* rope_sin, void* k_cache,
+                              void* v_cache, int64_t max_len, int64_t start, int64_t batch, int64_t t,
+                              int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, float scale, void* out,
+                              int64_t ldo, void* stream) {
+  const char* name = "wfb_gqa_prefill_attention";
+  if (dtype != WFB_BF16) return fail(WFB_EINVAL, "%s: dtype must be WFB_BF16", name);
+  if (head_dim != 64 && head_dim != 128) return fail(WFB_EINVAL, "%s: head_dim (%lld) must be 64 or 128", name, (long long)head_dim);
+  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > 8)
+    return fail(WFB_EINVAL, "%s: num_heads (%lld) must be 1..8 times num_kv_heads (%lld)", name, (long long)num_heads,
+                (long long)num_kv_heads);
+  if (batch < 0 || batch > 65535 || num_kv_heads > 65535 || t < 0 || t > INT32_MAX / 2)
+    return fail(WFB_EINVAL, "%s: batch (%lld) and num_kv_heads must be <= 65535, T (%lld) in range", name,
+                (long long)batch, (long long)t);
+  if (max_len <= 0 || max_len * head_dim * 2 > INT32_MAX)
+    return fail(WFB_EINVAL, "%s: max_len (%lld) must be positive with max_len*head_dim*2 < 2^31", name, (long long)max_len);
+  if (start < 0 || start + t > max_len)
+    return fail(WFB_EINVAL, "%s: start (%lld) + T (%lld) must be within max_len (%lld)", name, (long long)start,
+                (long long)t, (long long)max_len);
+  if (ldq < num_heads * head_dim || ldo < num_heads * head_dim || ldk < num_kv_heads * head_dim ||
+      ldv < num_kv_heads * head_dim)
+    return fail(WFB_EINVAL, "%s: row strides must cover num_heads*head_dim (q, out) and num_kv_heads*head_dim (k, v)",
+                name);
+  if (ldq % 8 || ldo % 8) return fail(WFB_EINVAL, "%s: q and out row strides must be multiples of 8 elements", name);
+  if ((rope_cos == nullptr) != (rope_sin == nullptr))
+    return fail(WFB_EINVAL, "%s: rope_cos and rope_sin must both be given or both be NULL", name);
+  if (!(scale == scale) || scale == __builtin_inff() || scale == -__builtin_inff())
+    return fail(WFB_EINVAL, "%s: scale must be finite", name);
+  if (batch == 0 || t == 0) return ok();
+  if (!q || !k_new || !v_new || !k_cache || !v_cache || !out) return fail(WFB_EINVAL, "%s: null pointer", name);
+  if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(q, 16) || !aligned(out, 16))
+    return fail(WFB_EINVAL, "%s: q, out and the caches must be 16-byte aligned", name);
+  return hip_status(wfb::launch_gqa_prefill((int)head_dim, (int)(num_heads / num_kv_heads), q, ldq, k_new, ldk, v_new,
+                                            ldv, rope_cos, rope_sin, k_cache, v_cache, max_len, (int)batch,
+                                            (int)num_kv_heads, (int)t, start, scale, out, ldo, as_stream(stream)),
+                    name);
+}
+
 int wfb_rmsnorm_linear_i2s(const void* x, int x_dtype, int64_t ldx, const void* gamma, int gamma_dtype, float eps,
                            int64_t m, int64_t h, const uint8_t* qweight, int64_t n, int64_t k, int n_seg,
                            const int64_t* seg_rows, const float* w_scales_dev, const void* residual,

@@ -367,6 +367,9 @@ hipError_t launch_gqa_decode(int dt, int d, int g, const void* q, int64_t ldq, c
                              const void* vn, int64_t ldv, const float* rc, const float* rs, void* kc, void* vc,
                              int64_t max_len, const int64_t* pos, int b, int hkv, float scale, void* out, int64_t ldo,
                              float* part, hipStream_t s);
+hipError_t launch_gqa_prefill(int d, int g, const void* q, int64_t ldq, const void* kn, int64_t ldk, const void* vn,
+                              int64_t ldv, const float* rc, const float* rs, void* kc, void* vc, int64_t max_len, int b,
+                              int hkv, int t, int64_t start, float scale, void* out, int64_t ldo, hipStream_t s);
 hipError_t launch_convert_hf_offline(const uint8_t* src, int64_t nb, int64_t n, int64_t k, int64_t k_pad,
                                      const void* ws_dev, int ws_dt, float ws_host, int mode, uint8_t* qw,
                                      float* scale_out, int64_t* parts, hipStream_t s);

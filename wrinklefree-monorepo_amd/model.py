@@ -15,9 +15,11 @@ kernel, and, for decode batches where it is faster (q|k|v and o), the norm + qua
 linear's own launch (``rmsnorm_linear``); a ternary LM head runs its argmax fused in
 (``norm_linear_argmax``).  A test can substitute
 another backend with the same three methods to compare the quantised path while the float code stays
-identical: embedding, residuals, the prefill attention (torch), the decode-step rotary embedding +
-cache append + GQA attention (one libwfbitnet kernel, or torch ops with ``decode_attention="torch"``)
-and the tied LM head with its final norm and greedy argmax (one libwfbitnet kernel).
+identical: embedding, residuals, the prefill rotary embedding + cache append + causal GQA attention
+(libwfbitnet's matrix-core kernel for bf16 models, or torch ops with ``prefill_attention="torch"`` and
+for fp32 models), the decode-step rotary embedding + cache append + GQA attention (one libwfbitnet
+kernel, or torch ops with ``decode_attention="torch"``) and the tied LM head with its final norm and
+greedy argmax (one libwfbitnet kernel).
 """
 
 from __future__ import annotations
@@ -32,6 +34,7 @@ import torch
 from .sglbitnt import SGLBitNetFile, write_sglbitnt
 from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_glu,
                   bitnet_linear_residual, bitnet_linear_segmented, glu_rmsnorm_quantize_i8, gqa_decode_attention,
+                  gqa_prefill_attention,
                   lm_head_argmax, pack_ternary_i2s, rmsnorm_linear, rmsnorm_linear_preferred, rmsnorm_quantize_i8)
 
 
@@ -237,12 +240,16 @@ class BitNetDecoder:
     """Decoder-only BitNet model with a per-layer KV cache; float glue in ``dtype``."""
 
     def __init__(self, cfg: BitNetConfig, seed: int = 0, device: str = "cuda", dtype: torch.dtype = torch.float32,
-                 backend=None, init_on_device: bool = False, decode_attention: str = "hip"):
+                 backend=None, init_on_device: bool = False, decode_attention: str = "hip",
+                 prefill_attention: str = "hip"):
         """``init_on_device``: draw the random weights with a generator on ``device`` (fast for 8B-scale
         models) instead of the host generator (the default, reproducible across devices).
         ``decode_attention``: "hip" runs each decode step's rotary embedding, cache append and GQA attention
-        as one libwfbitnet kernel; "torch" runs them as torch ops (prefill always uses torch)."""
-        self._setup(cfg, device, dtype, backend, decode_attention)
+        as one libwfbitnet kernel; "torch" runs them as torch ops.  ``prefill_attention``: "hip" runs a
+        prompt's rotary embedding, cache append and causal attention on libwfbitnet's matrix-core kernel
+        (bf16 models with head_dim 64/128 and at most 8 query heads per kv head; other models use torch);
+        "torch" always uses torch ops."""
+        self._setup(cfg, device, dtype, backend, decode_attention, prefill_attention)
         gen = torch.Generator(device=self.device if init_on_device else "cpu").manual_seed(seed)
         self.embed = (torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen, device=gen.device) * 0.02).to(
             self.device, dtype)
@@ -256,10 +263,12 @@ class BitNetDecoder:
             self.lm_head = None  # tied to the embedding
         self.head_weight = self.embed
 
-    def _setup(self, cfg: BitNetConfig, device, dtype: torch.dtype, backend, decode_attention: str) -> None:
-        if decode_attention not in ("hip", "torch"):
-            raise ValueError("decode_attention must be 'hip' or 'torch'")
+    def _setup(self, cfg: BitNetConfig, device, dtype: torch.dtype, backend, decode_attention: str,
+               prefill_attention: str = "hip") -> None:
+        if decode_attention not in ("hip", "torch") or prefill_attention not in ("hip", "torch"):
+            raise ValueError("decode_attention and prefill_attention must be 'hip' or 'torch'")
         self.decode_attention = decode_attention
+        self.prefill_attention = prefill_attention
         self.fuse_residual = True  # residual adds in the o / down epilogues when the backend offers it
         self.cfg = cfg
         self.device = torch.device(device)
@@ -305,7 +314,7 @@ class BitNetDecoder:
 
     @classmethod
     def from_sglbitnt(cls, path, device="cuda", dtype: torch.dtype = torch.float32, backend=None,
-                      decode_attention: str = "hip") -> "BitNetDecoder":
+                      decode_attention: str = "hip", prefill_attention: str = "hip") -> "BitNetDecoder":
         """Build the model from an SGLBITNT file (memory-mapped; tensors go to ``device`` one at a time).
         Packed linears keep their I2_S bytes and scale; a uint8 lm_head.weight is a ternary LM head, a float
         one a dense head, none a head tied to the embedding.  Missing SubLN weights are ones (the engine
@@ -324,7 +333,7 @@ class BitNetDecoder:
                            ternary_lm_head=head_t is not None and head_t.dtype_id == 0,
                            hidden_act=str(c.get("hidden_act", "silu")))
         m = cls.__new__(cls)
-        m._setup(cfg, device, dtype, backend, decode_attention)
+        m._setup(cfg, device, dtype, backend, decode_attention, prefill_attention)
         dev = m.device
 
         def packed(name, in_features):
@@ -502,7 +511,7 @@ class BitNetDecoder:
         the packed weights themselves are shared, not copied."""
         cpu = torch.device("cpu")
         m = copy.copy(self)
-        m.device, m.backend, m.decode_attention = cpu, backend, "torch"
+        m.device, m.backend, m.decode_attention, m.prefill_attention = cpu, backend, "torch", "torch"
         m.embed, m.final_norm, m.inv_freq = self.embed.to(cpu), self.final_norm.to(cpu), self.inv_freq.to(cpu)
         m.head_weight = m.embed if self.head_weight is self.embed else self.head_weight.to(cpu)
         m.layers = []
@@ -522,12 +531,22 @@ class BitNetDecoder:
         pos = torch.arange(start, start + t, device=self.device)
 
         def attend(li, q, k, v):
+            if self._hip_prefill():
+                kc, vc = self._cache(li, b)
+                return gqa_prefill_attention(q, k, v, kc, vc, start, t, self._rope_cos, self._rope_sin,
+                                             scale=1.0 / math.sqrt(cfg.head_dim))
             q = self._rope(q.reshape(b, t, cfg.num_heads, cfg.head_dim), pos)
             k = self._rope(k.reshape(b, t, cfg.num_kv_heads, cfg.head_dim), pos)
             return self._attention(li, q, k, v.reshape(b, t, cfg.num_kv_heads, cfg.head_dim), start)
 
         x = self._layers(self.embed[ids], attend)
         return self._next_tokens(x[:, -1, :]) if tokens else self._logits(x[:, -1, :])
+
+    def _hip_prefill(self) -> bool:
+        cfg = self.cfg
+        return (self.prefill_attention == "hip" and self.device.type == "cuda" and self.dtype == torch.bfloat16
+                and cfg.head_dim in (64, 128) and cfg.num_heads % cfg.num_kv_heads == 0
+                and cfg.num_heads // cfg.num_kv_heads <= 8)
 
     def decode_step(self, ids: torch.Tensor, pos: torch.Tensor, tokens: bool = False) -> torch.Tensor:
         """One token per sequence, ids [B, 1] at the device positions pos int64 [B]; fixed shapes and no

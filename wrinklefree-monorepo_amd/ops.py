@@ -738,6 +738,64 @@ def gqa_decode_attention(
     return out
 
 
+def gqa_prefill_attention(
+    q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+    start: int, t: int, rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """A prefill chunk of t tokens per sequence at positions start..start+t-1: rotary embedding of q / k_new,
+    append k/v to the caches, causal GQA attention (token i over positions 0..start+i).  Returns out
+    [batch*t, num_heads*head_dim] (row b*t + i).
+
+    q [batch*t, num_heads*head_dim] (or any shape with those elements, token-major); k_new / v_new
+    [batch*t, num_kv_heads*head_dim]; the three may be column slices of one q|k|v output.  bfloat16 only;
+    caches [batch, num_kv_heads, max_len, head_dim] (contiguous); rope tables fp32 [max_len, head_dim/2]
+    or None.  The same contract as ``gqa_decode_attention`` for each token of the chunk.
+    """
+    name = "gqa_prefill_attention"
+    _require_gpu(name, k_cache, v_cache, rope_cos, rope_sin)
+    dev = k_cache.device
+    for x in (q, k_new, v_new) + ((out,) if out is not None else ()):
+        if x.device != dev:
+            raise RuntimeError(f"{name}: tensors must be on {dev}")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise RuntimeError(f"{name}: caches must be [batch, kv_heads, max_len, head_dim] of one shape")
+    b, hkv, max_len, d = k_cache.shape
+    for x in (q, k_new, v_new, k_cache, v_cache):
+        if x.dtype != torch.bfloat16:
+            raise RuntimeError(f"{name}: q, k_new, v_new and the caches must be bfloat16, got {x.dtype}")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise RuntimeError(f"{name}: caches must be contiguous")
+    rows = b * t
+    if rows == 0:
+        return torch.empty((0, q.numel() // max(1, d)), dtype=q.dtype, device=dev) if out is None else out
+    if q.numel() % (rows * d) != 0:
+        raise RuntimeError(f"{name}: q has {q.numel()} elements, not a multiple of batch*t*head_dim")
+    hq = q.numel() // (rows * d)
+    q2, ldq = _rows2d(name, q, rows, hq * d)
+    k2, ldk = _rows2d(name, k_new, rows, hkv * d)
+    v2, ldv = _rows2d(name, v_new, rows, hkv * d)
+    if (rope_cos is None) != (rope_sin is None):
+        raise RuntimeError(f"{name}: give both rope tables or neither")
+    if rope_cos is not None:
+        for x in (rope_cos, rope_sin):
+            if x.dtype != torch.float32 or x.shape != (max_len, d // 2) or not x.is_contiguous():
+                raise RuntimeError(f"{name}: rope tables must be contiguous fp32 [{max_len}, {d // 2}]")
+    if out is None:
+        out = torch.empty((rows, hq * d), dtype=q.dtype, device=dev)
+    elif out.dtype != q.dtype or out.shape != (rows, hq * d) or out.stride(-1) != 1:
+        raise RuntimeError(f"{name}: out must be [{rows}, {hq * d}] {q.dtype} with contiguous rows")
+    ldo = out.stride(0) if rows > 1 else hq * d
+    sc = 1.0 / float(d) ** 0.5 if scale is None else float(scale)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "wfb_gqa_prefill_attention", _p(q2), ldq, _p(k2), ldk, _p(v2), ldv, _DT[q.dtype], _p(rope_cos),
+            _p(rope_sin), _p(k_cache), _p(v_cache), max_len, int(start), b, int(t), hq, hkv, d, sc, _p(out), ldo,
+            _stream(dev),
+        )
+    return out
+
+
 def bitnet_gemv(packed_weights: torch.Tensor, activations: torch.Tensor, scale: Scale) -> torch.Tensor:
     """fp32 [out] = acc * scale for one int8 token [in] (reference: bitnet.py:73-111)."""
     if activations.dim() != 1:
