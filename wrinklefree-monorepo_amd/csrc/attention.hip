@@ -135,6 +135,30 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   const bool owns_new = pos < k1;  // the split holding key pos appends the new key and value
   const int64_t cbase = ((int64_t)b * hkv + kvh) * max_len * D;  // element offset of this cache slice
 
+  // keys k0..min(pos, k1)-1 come from the cache (loads past them read zeros); key pos from knew / vnew.
+  // The first chunk's K and V rows are requested before the rotary / append phase: the range never
+  // includes pos, so they do not wait for this workgroup's own append.
+  const int kl = lane / LPK;        // key slot of the lane within a wave instruction
+  const int d0 = 8 * (lane % LPK);  // first of the lane's 8 elements
+  const int kend = owns_new ? (int)pos : k1;
+  const uint32_t kbytes = (uint32_t)((int64_t)kend * D * ESZ);
+  const buf_t kb = make_buf(reinterpret_cast<const char*>(kc) + cbase * ESZ, kbytes);
+  const buf_t vb = make_buf(reinterpret_cast<const char*>(vc) + cbase * ESZ, kbytes);
+  Raw8<DT> kr[R], vr[R];
+  auto load_chunk = [&](int c0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int key = c0 + w * KW + r * KPW + kl;
+      kr[r] = load_raw8<DT>(kb, (uint32_t)(key * D + d0) * ESZ);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int key = c0 + w * KW + r * KPW + kl;
+      vr[r] = load_raw8<DT>(vb, (uint32_t)(key * D + d0) * ESZ);
+    }
+  };
+  load_chunk(k0);
+
   // ---- rotary embedding of the new query heads and key; append key and value ------------------
   const float* cs = rope_cos ? rope_cos + pos * HD : nullptr;
   const float* sn = rope_sin ? rope_sin + pos * HD : nullptr;
@@ -175,8 +199,6 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   }
   __syncthreads();
 
-  const int kl = lane / LPK;        // key slot of the lane within a wave instruction
-  const int d0 = 8 * (lane % LPK);  // first of the lane's 8 elements
   float qf[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -194,26 +216,8 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
     l_run[h] = 0.0f;
   }
 
-  // keys k0..min(pos, k1)-1 come from the cache (loads past them read zeros); key pos from knew / vnew
-  const int kend = owns_new ? (int)pos : k1;
-  const uint32_t kbytes = (uint32_t)((int64_t)kend * D * ESZ);
-  const buf_t kb = make_buf(reinterpret_cast<const char*>(kc) + cbase * ESZ, kbytes);
-  const buf_t vb = make_buf(reinterpret_cast<const char*>(vc) + cbase * ESZ, kbytes);
-
   for (int c0 = k0; c0 < k1; c0 += CH) {
-    Raw8<DT> kr[R], vr[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int key = c0 + w * KW + r * KPW + kl;
-      const uint32_t off = (uint32_t)(key * D + d0) * ESZ;
-      kr[r] = load_raw8<DT>(kb, off);
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int key = c0 + w * KW + r * KPW + kl;
-      const uint32_t off = (uint32_t)(key * D + d0) * ESZ;
-      vr[r] = load_raw8<DT>(vb, off);
-    }
+    if (c0 != k0) load_chunk(c0);
     // scores
 #pragma unroll
     for (int r = 0; r < R; ++r) {
