@@ -276,7 +276,8 @@ int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int6
  * h / (num_heads / num_kv_heads).  bf16 only (dtype WFB_BF16): q rows [batch*T, ldq] (row b*T + i holds
  * the num_heads*head_dim query elements), k_new / v_new rows [batch*T, ldk / ldv] (num_kv_heads*head_dim
  * each); the three may be column slices of one q|k|v projection output.  Caches [batch, num_kv_heads,
- * max_len, head_dim], 16-byte aligned; out [batch*T, ldo] (num_heads*head_dim per row).  head_dim 64 or
+ * max_len, head_dim], 16-byte aligned, as are q, out and the rope tables; out [batch*T, ldo]
+ * (num_heads*head_dim per row).  head_dim 64 or
  * 128, num_heads / num_kv_heads in 1..8, start + T <= max_len, row strides multiples of 8 elements and
  * row bases 16-byte aligned.  The cache rows written are bit-identical to the rotary + append of the
  * decode call; scores, softmax and the weighted sum are fp32 (products of bf16 operands on the matrix

@@ -67,6 +67,8 @@ CASES = [
     (2, 16, 2, 64, 90, 5, 1, True),         # G = 8, one token
     (1, 10, 2, 128, 200, 0, 130, True),     # G = 5
     (2, 14, 2, 64, 140, 63, 70, True),      # G = 7, start on a block edge - 1
+    (1, 4, 2, 128, 80, 0, 33, True),        # G = 2
+    (1, 12, 2, 64, 100, 9, 40, True),       # G = 6
 ]
 
 
@@ -100,6 +102,23 @@ def test_prefill_attention_matches_reference(pkg, dev, case, strided):
     err = (got - ref).abs() / ref.abs().clamp_min(1e-2)
     assert float(err.max()) <= 1e-2, float(err.max())
     assert float(err.mean()) <= 2e-3, float(err.mean())
+
+
+def test_prefill_attention_unaligned_key_value_rows(pkg, dev):
+    """Key / value rows that are not 16-byte aligned take the element-wise append path: same caches
+    and output as the aligned call."""
+    b, hq, hkv, d, max_len, t = 2, 8, 2, 64, 48, 21
+    gen = torch.Generator().manual_seed(11)
+    q = torch.randn((b * t, hq * d), generator=gen).to(torch.bfloat16).to(dev)
+    kv = torch.randn((b * t, 1 + 2 * hkv * d), generator=gen).to(torch.bfloat16).to(dev)
+    k_odd, v_odd = kv[:, 1:1 + hkv * d], kv[:, 1 + hkv * d:]  # 2 bytes past a 16-byte boundary
+    cos, sin = (x.to(dev) for x in _tables(max_len, d))
+    caches = [torch.zeros((b, hkv, max_len, d), dtype=torch.bfloat16, device=dev) for _ in range(4)]
+    out_odd = pkg.gqa_prefill_attention(q, k_odd, v_odd, caches[0], caches[1], 3, t, cos, sin)
+    out_al = pkg.gqa_prefill_attention(q, k_odd.contiguous(), v_odd.contiguous(), caches[2], caches[3], 3, t, cos, sin)
+    torch.cuda.synchronize()
+    assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
+    assert torch.equal(out_odd, out_al)
 
 
 def test_prefill_then_decode_continues_the_cache(pkg, dev):

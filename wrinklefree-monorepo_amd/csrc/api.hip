@@ -386,8 +386,9 @@ int wfb_gqa_prefill_attention(const void* q, int64_t ldq, const void* k_new, int
     return fail(WFB_EINVAL, "%s: scale must be finite", name);
   if (batch == 0 || t == 0) return ok();
   if (!q || !k_new || !v_new || !k_cache || !v_cache || !out) return fail(WFB_EINVAL, "%s: null pointer", name);
-  if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(q, 16) || !aligned(out, 16))
-    return fail(WFB_EINVAL, "%s: q, out and the caches must be 16-byte aligned", name);
+  if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(q, 16) || !aligned(out, 16) ||
+      !aligned(rope_cos, 16) || !aligned(rope_sin, 16))
+    return fail(WFB_EINVAL, "%s: q, out, the caches and the rope tables must be 16-byte aligned", name);
   return hip_status(wfb::launch_gqa_prefill((int)head_dim, (int)(num_heads / num_kv_heads), q, ldq, k_new, ldk, v_new,
                                             ldv, rope_cos, rope_sin, k_cache, v_cache, max_len, (int)batch,
                                             (int)num_kv_heads, (int)t, start, scale, out, ldo, as_stream(stream)),

@@ -53,11 +53,50 @@ __global__ __launch_bounds__(256) void gqa_append_kernel(const uint16_t* __restr
                                                          const float* __restrict__ rope_cos,
                                                          const float* __restrict__ rope_sin, uint16_t* __restrict__ kc,
                                                          uint16_t* __restrict__ vc, int64_t max_len, int hkv, int T,
-                                                         int64_t start) {
+                                                         int64_t start, bool vec) {
   constexpr int HD = D / 2;
   const int i = blockIdx.x, b = blockIdx.y;
   const int64_t pos = start + i;
   const int64_t row = (int64_t)b * T + i;
+  if (vec) {  // 16-byte pieces: 8 rotary pairs of a key, or 8 value elements, per thread
+    constexpr int KI = HD / 8, VI = D / 8;
+    for (int e = threadIdx.x; e < hkv * (KI + VI); e += blockDim.x) {
+      if (e < hkv * KI) {
+        const int g = e / KI, j0 = 8 * (e % KI);
+        const uint16_t* kr = kn + row * ldk + (int64_t)g * D;
+        uint16_t* dst = kc + (((int64_t)b * hkv + g) * max_len + pos) * D;
+        Frag8 x1, x2;
+        x1.q = *reinterpret_cast<const v4i*>(kr + j0);
+        x2.q = *reinterpret_cast<const v4i*>(kr + j0 + HD);
+        if (rope_cos) {
+          const float4* cp = reinterpret_cast<const float4*>(rope_cos + pos * HD + j0);
+          const float4* sp = reinterpret_cast<const float4*>(rope_sin + pos * HD + j0);
+          const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+          const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+          const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+          float y1[8], y2[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float a = bf16f(x1.h[j]), c = bf16f(x2.h[j]);
+            y1[j] = __fadd_rn(__fmul_rn(a, cs[j]), __fmul_rn(-c, sn[j]));
+            y2[j] = __fadd_rn(__fmul_rn(c, cs[j]), __fmul_rn(a, sn[j]));
+          }
+#pragma unroll
+          for (int j = 0; j < 8; j += 2) {  // bf16, round to nearest even (v_cvt_pk_bf16_f32)
+            x1.u[j / 2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){y1[j], y1[j + 1]}, bf16x2_t));
+            x2.u[j / 2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){y2[j], y2[j + 1]}, bf16x2_t));
+          }
+        }
+        *reinterpret_cast<v4i*>(dst + j0) = x1.q;
+        *reinterpret_cast<v4i*>(dst + j0 + HD) = x2.q;
+      } else {
+        const int e2 = e - hkv * KI, g = e2 / VI, j0 = 8 * (e2 % VI);
+        *reinterpret_cast<v4i*>(vc + (((int64_t)b * hkv + g) * max_len + pos) * D + j0) =
+            *reinterpret_cast<const v4i*>(vn + row * ldv + (int64_t)g * D + j0);
+      }
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < hkv * HD; e += blockDim.x) {
     const int g = e / HD, j = e % HD;
     const uint16_t* kr = kn + row * ldk + (int64_t)g * D;
@@ -103,6 +142,8 @@ __global__ __launch_bounds__(64 * G) void gqa_prefill_kernel(const uint16_t* __r
   const int qi = i0 + (lane & 15);  // this lane's query token (S^T / O^T column)
   const bool qvalid = qi < T;
   const int64_t qpos = start + qi;
+  const int qpos32 = (int)qpos;                // positions < max_len < 2^23 (host-checked)
+  const int qpos_first = (int)(start + i0);    // the workgroup's first query position
 
   // roped query fragments: lane holds Q[qi][32ks + 8grp .. +7] for each ks
   Frag8 qf[KS];
@@ -116,16 +157,28 @@ __global__ __launch_bounds__(64 * G) void gqa_prefill_kernel(const uint16_t* __r
     } else if (rope_cos) {
       constexpr int HD = D / 2;
 #pragma unroll
-      for (int s = 0; s < KS / 2; ++s)
+      for (int s = 0; s < KS / 2; ++s) {
+        // elements d = 32s + 8grp + j (< D/2) and their partners d + D/2 (fragment s + KS/2, slot j);
+        // the 8 table entries of d are contiguous (16-byte aligned tables, host-checked)
+        const float4* cp = reinterpret_cast<const float4*>(rope_cos + qpos * HD + 32 * s + 8 * grp);
+        const float4* sp = reinterpret_cast<const float4*>(rope_sin + qpos * HD + 32 * s + 8 * grp);
+        const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+        const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        float y1[8], y2[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int d = 32 * s + 8 * grp + j;  // d < D/2; its partner d + D/2 is fragment s + KS/2, slot j
-          uint16_t y1, y2;
-          rope_pair(bf16f(qf[s].h[j]), bf16f(qf[s + KS / 2].h[j]), rope_cos[qpos * HD + d], rope_sin[qpos * HD + d],
-                    y1, y2);
-          qf[s].h[j] = y1;
-          qf[s + KS / 2].h[j] = y2;
+          const float x1 = bf16f(qf[s].h[j]), x2 = bf16f(qf[s + KS / 2].h[j]);
+          y1[j] = __fadd_rn(__fmul_rn(x1, cs[j]), __fmul_rn(-x2, sn[j]));
+          y2[j] = __fadd_rn(__fmul_rn(x2, cs[j]), __fmul_rn(x1, sn[j]));
         }
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {  // round to bf16, nearest even (v_cvt_pk_bf16_f32)
+          qf[s].u[j / 2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){y1[j], y1[j + 1]}, bf16x2_t));
+          qf[s + KS / 2].u[j / 2] =
+              __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){y2[j], y2[j + 1]}, bf16x2_t));
+        }
+      }
     }
   }
 
@@ -142,27 +195,68 @@ __global__ __launch_bounds__(64 * G) void gqa_prefill_kernel(const uint16_t* __r
   for (int db = 0; db < DB; ++db) o[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = -__builtin_inff(), l_run = 0.0f;
 
+  // Tile staging, software-pipelined: the global loads of block kb + 1 are issued right after block kb
+  // is written to LDS, so they are in flight while block kb is computed.  Trip counts are compile-time
+  // constants, so every load of a tile is issued before the first LDS write waits for one.
+  constexpr int KP = KB * (D / 8);        // 16-byte pieces of the K tile
+  constexpr int KIT = (KP + NT - 1) / NT;
+  constexpr int VP = (KB / 2) * (D / 8);  // (key pair, 8-element chunk) items of the V tile
+  constexpr int VIT = (VP + NT - 1) / NT;
+  v4i kreg[KIT];
+  Frag8 va[VIT], vb2[VIT];
+  auto load_tile = [&](int key0) {
+#pragma unroll
+    for (int it = 0; it < KIT; ++it) {
+      const int p = t + it * NT;
+      if (KP % NT == 0 || p < KP) {
+        const int r = p / (D / 8), c = p % (D / 8);
+        kreg[it] = buf_load16(kb_, (uint32_t)(((key0 + r) * D + 8 * c) * 2));
+      }
+    }
+    // V: 16 consecutive lanes take 16 consecutive key pairs of one 8-element chunk, the next 16 lanes
+    // the next chunk, so the transposed row stores below spread over all banks (rows 8c + j of chunks
+    // c and c + 1 sit 16 banks apart) while each key row is still read as 64-byte pieces
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int p = t + it * NT;
+      if (VP % NT == 0 || p < VP) {
+        const int rest = p / 16, c = rest % (D / 8);
+        const int r = 2 * ((p % 16) + 16 * (rest / (D / 8)));
+        va[it].q = buf_load16(vb_, (uint32_t)(((key0 + r) * D + 8 * c) * 2));
+        vb2[it].q = buf_load16(vb_, (uint32_t)(((key0 + r + 1) * D + 8 * c) * 2));
+      }
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int it = 0; it < KIT; ++it) {
+      const int p = t + it * NT;
+      if (KP % NT == 0 || p < KP) {
+        const int r = p / (D / 8), c = p % (D / 8);
+        *reinterpret_cast<v4i*>(&ks_[r * KROW + 8 * c]) = kreg[it];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int p = t + it * NT;
+      if (VP % NT == 0 || p < VP) {
+        const int rest = p / 16, c = rest % (D / 8);
+        const int r = 2 * ((p % 16) + 16 * (rest / (D / 8)));
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          *reinterpret_cast<uint32_t*>(&vs_[(8 * c + jj) * VROW + r]) =
+              (uint32_t)va[it].h[jj] | ((uint32_t)vb2[it].h[jj] << 16);
+      }
+    }
+  };
+
+  load_tile(0);
   for (int kb = 0; kb < nkb; ++kb) {
     const int key0 = kb * KB;
     __syncthreads();  // the previous block's tiles are no longer read
-    // K tile: KB rows x D, 16-byte pieces
-    for (int p = t; p < KB * (D / 8); p += NT) {
-      const int r = p / (D / 8), c = p % (D / 8);
-      const v4i x = buf_load16(kb_, (uint32_t)(((key0 + r) * D + 8 * c) * 2));
-      *reinterpret_cast<v4i*>(&ks_[r * KROW + 8 * c]) = x;
-    }
-    // V^T tile: pairs of keys x 8 elements -> 8 dwords (key, key + 1) into rows d
-    for (int p = t; p < (KB / 2) * (D / 8); p += NT) {
-      const int r2 = p / (D / 8), c = p % (D / 8);
-      const int r = 2 * r2;
-      Frag8 a, bb;
-      a.q = buf_load16(vb_, (uint32_t)(((key0 + r) * D + 8 * c) * 2));
-      bb.q = buf_load16(vb_, (uint32_t)(((key0 + r + 1) * D + 8 * c) * 2));
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        *reinterpret_cast<uint32_t*>(&vs_[(8 * c + j) * VROW + r]) = (uint32_t)a.h[j] | ((uint32_t)bb.h[j] << 16);
-    }
+    store_tile();
     __syncthreads();
+    if (kb + 1 < nkb) load_tile(key0 + KB);
 
     // S^T = K Q^T for the 4 sub-blocks of 16 keys
     f32x4_t s[4];
@@ -176,14 +270,15 @@ __global__ __launch_bounds__(64 * G) void gqa_prefill_kernel(const uint16_t* __r
         s[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, qf[k].v, s[nb], 0, 0, 0);
       }
     }
-    // scale, causal mask, block max of this lane's query
+    // scale, causal mask (only blocks reaching past the workgroup's first query), block max
     float bmax = -__builtin_inff();
+    const bool masked = key0 + KB - 1 > qpos_first;  // uniform
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = key0 + 16 * nb + 4 * grp + i;
-        const float v = key <= qpos ? s[nb][i] * scale : -__builtin_inff();
+        const float v = !masked || key <= qpos32 ? s[nb][i] * scale : -__builtin_inff();
         s[nb][i] = v;
         bmax = fmaxf(bmax, v);
       }
@@ -210,13 +305,14 @@ __global__ __launch_bounds__(64 * G) void gqa_prefill_kernel(const uint16_t* __r
     // O^T += V^T P^T over two chunks of 32 keys (slots j < 4: sub-block 2c, j >= 4: sub-block 2c + 1)
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      Frag8 phi, plo;
+      Frag8 phi, plo;  // hi = bf16(p), lo = bf16(p - hi), both round-to-nearest-even (v_cvt_pk_bf16_f32)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float p = s[2 * c + (j >> 2)][j & 3];
-        const uint16_t hi = f32_to_bf16_rne(p);
-        phi.h[j] = hi;
-        plo.h[j] = f32_to_bf16_rne(p - bf16f(hi));
+      for (int j = 0; j < 8; j += 2) {
+        const float p0 = s[2 * c + (j >> 2)][j & 3], p1 = s[2 * c + (j >> 2)][(j & 3) + 1];
+        const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){p0, p1}, bf16x2_t));
+        const float r0 = p0 - __uint_as_float(hi << 16), r1 = p1 - __uint_as_float(hi & 0xffff0000u);
+        phi.u[j / 2] = hi;
+        plo.u[j / 2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){r0, r1}, bf16x2_t));
       }
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
@@ -237,11 +333,12 @@ __global__ __launch_bounds__(64 * G) void gqa_prefill_kernel(const uint16_t* __r
   if (!qvalid) return;
   // lane holds O^T[16db + 4grp + i][qi]: four consecutive elements of the output row per db
   uint16_t* orow = out + ((int64_t)b * T + qi) * ldo + (int64_t)h * D;
+  const float inv_l = 1.0f / l_run;
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
     uint2 v;
-    v.x = (uint32_t)f32_to_bf16_rne(o[db][0] / l_run) | ((uint32_t)f32_to_bf16_rne(o[db][1] / l_run) << 16);
-    v.y = (uint32_t)f32_to_bf16_rne(o[db][2] / l_run) | ((uint32_t)f32_to_bf16_rne(o[db][3] / l_run) << 16);
+    v.x = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){o[db][0] * inv_l, o[db][1] * inv_l}, bf16x2_t));
+    v.y = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){o[db][2] * inv_l, o[db][3] * inv_l}, bf16x2_t));
     *reinterpret_cast<uint2*>(orow + 16 * db + 4 * grp) = v;
   }
 }
@@ -260,8 +357,10 @@ hipError_t launch_prefill_d(int g, const uint16_t* q, int64_t ldq, const uint16_
                             int64_t ldv, const float* rc, const float* rs, uint16_t* kc, uint16_t* vc, int64_t max_len,
                             int b, int hkv, int t, int64_t start, float scale, uint16_t* out, int64_t ldo,
                             hipStream_t s) {
+  // 16-byte path when the key / value rows allow it (q|k|v column slices of one projection output do)
+  const bool vec = (uintptr_t)kn % 16 == 0 && (uintptr_t)vn % 16 == 0 && ldk % 8 == 0 && ldv % 8 == 0;
   hipLaunchKernelGGL((gqa_append_kernel<D>), dim3(t, b), dim3(256), 0, s, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len,
-                     hkv, t, start);
+                     hkv, t, start, vec);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
 #define WFB_PF_G(GG) \
