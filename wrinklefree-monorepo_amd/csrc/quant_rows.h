@@ -57,6 +57,50 @@ __device__ __forceinline__ void load_row8(const void* xr, const void* ur, int e0
   }
 }
 
+// Whole-vector rows (16-byte aligned, h % kVec == 0): 8 elements through a buffer descriptor bounded at
+// the row end, so vectors past it read as zeros without a branch.  With no element-wise alternative in
+// the same code path, every load of a thread is issued before the first one is waited for.
+template <int DT>
+__device__ __forceinline__ void load8_buf(buf_t b, int e0, float (&v)[kVec]) {
+  if constexpr (DT == WFB_F32) {
+    const v4i a = buf_load16(b, (uint32_t)e0 * 4), c = buf_load16(b, (uint32_t)e0 * 4 + 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = __int_as_float(a[e]);
+      v[4 + e] = __int_as_float(c[e]);
+    }
+  } else {
+    const v4i a = buf_load16(b, (uint32_t)e0 * 2);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = (uint32_t)a[e];
+      if constexpr (DT == WFB_BF16) {
+        v[2 * e] = __uint_as_float(w << 16);
+        v[2 * e + 1] = __uint_as_float(w & 0xffff0000u);
+      } else {
+        v[2 * e] = f16_bits_to_f32((uint16_t)(w & 0xffffu));
+        v[2 * e + 1] = f16_bits_to_f32((uint16_t)(w >> 16));
+      }
+    }
+  }
+}
+
+template <int DT, int GLU>
+__device__ __forceinline__ void load_row8_full(buf_t xb, buf_t ub, int e0, float (&v)[kVec]) {
+  load8_buf<DT>(xb, e0, v);
+  if constexpr (GLU != 0) {
+    float u[kVec];
+    load8_buf<DT>(ub, e0, u);
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) v[e] = glu<GLU>(v[e], u[e]);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ buf_t row_buf(const void* r, int h) {
+  return make_buf(r, (uint32_t)h * (DT == WFB_F32 ? 4u : 2u));
+}
+
 template <int DT, int GDT, bool NORM, int GLU>
 __global__ __launch_bounds__(kTPB) void quant_rows_kernel(const void* __restrict__ x, const void* __restrict__ up,
                                                           int64_t ldx, const void* __restrict__ gamma, float eps,
@@ -72,14 +116,28 @@ __global__ __launch_bounds__(kTPB) void quant_rows_kernel(const void* __restrict
   const void* ur = GLU != 0 ? reinterpret_cast<const char*>(up) + roff : nullptr;
 
   float v[kMaxIt][kVec];
+  const bool full = vec && h % kVec == 0;  // uniform
+  if (full) {
+    const buf_t xb = row_buf<DT>(xr, h), ub = GLU != 0 ? row_buf<DT>(ur, h) : xb;
 #pragma unroll
-  for (int it = 0; it < kMaxIt; ++it) {
-    const int e0 = (it * kTPB + t) * kVec;
-    if (it * kTPB * kVec >= h) {  // uniform over the block
+    for (int it = 0; it < kMaxIt; ++it) {
+      if (it * kTPB * kVec >= h) {  // uniform over the block
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) v[it][e] = 0.0f;
-    } else {
-      load_row8<DT, GLU>(xr, ur, e0, h, vec, v[it]);
+        for (int e = 0; e < kVec; ++e) v[it][e] = 0.0f;
+      } else {
+        load_row8_full<DT, GLU>(xb, ub, (it * kTPB + t) * kVec, v[it]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int it = 0; it < kMaxIt; ++it) {
+      const int e0 = (it * kTPB + t) * kVec;
+      if (it * kTPB * kVec >= h) {  // uniform over the block
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) v[it][e] = 0.0f;
+      } else {
+        load_row8<DT, GLU>(xr, ur, e0, h, vec, v[it]);
+      }
     }
   }
 
@@ -106,6 +164,8 @@ __global__ __launch_bounds__(kTPB) void quant_rows_kernel(const void* __restrict
       if (gamma == nullptr) {
 #pragma unroll
         for (int e = 0; e < kVec; ++e) g[e] = 1.0f;
+      } else if (full) {
+        load8_buf<GDT>(row_buf<GDT>(gamma, h), e0, g);
       } else if (vec && e0 + kVec <= h) {
         load8<GDT>(gamma, e0, g);
       } else {
@@ -164,15 +224,23 @@ __global__ __launch_bounds__(256) void quant_rows_wave_kernel(const void* __rest
                                                               int h, int m, int8_t* __restrict__ q, int64_t k_pad,
                                                               int64_t ldq, float* __restrict__ a_scale, bool vec) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // wave-uniform row (readfirstlane), so the row's buffer descriptor lives in scalar registers
+  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= m) return;
   const int64_t roff = row * ldx * (DT == WFB_F32 ? 4 : 2);
   const void* xr = reinterpret_cast<const char*>(x) + roff;
   const void* ur = GLU != 0 ? reinterpret_cast<const char*>(up) + roff : nullptr;
 
   float v[VPL][kVec];
+  const bool full = vec && h % kVec == 0;  // uniform
+  if (full) {
+    const buf_t xb = row_buf<DT>(xr, h), ub = GLU != 0 ? row_buf<DT>(ur, h) : xb;
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) load_row8<DT, GLU>(xr, ur, (lane + 64 * j) * kVec, h, vec, v[j]);
+    for (int j = 0; j < VPL; ++j) load_row8_full<DT, GLU>(xb, ub, (lane + 64 * j) * kVec, v[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) load_row8<DT, GLU>(xr, ur, (lane + 64 * j) * kVec, h, vec, v[j]);
+  }
   if constexpr (NORM) {
     float g[VPL][kVec];
 #pragma unroll
@@ -181,6 +249,8 @@ __global__ __launch_bounds__(256) void quant_rows_wave_kernel(const void* __rest
       if (gamma == nullptr) {
 #pragma unroll
         for (int e = 0; e < kVec; ++e) g[j][e] = 1.0f;
+      } else if (full) {
+        load8_buf<GDT>(row_buf<GDT>(gamma, h), e0, g[j]);
       } else if (vec && e0 + kVec <= h) {
         load8<GDT>(gamma, e0, g[j]);
       } else {
@@ -255,11 +325,17 @@ __global__ __launch_bounds__(kWideThreads) void quant_rows_wide_kernel(
   const int nvec = (h + kVec - 1) / kVec;
 
   float v[VPT][kVec];
+  const bool full = vec && h % kVec == 0;  // uniform
+  if (full) {  // every load in flight before the first wait (vectors past the row read as zeros)
+    const buf_t xb = row_buf<DT>(xr, h), ub = GLU != 0 ? row_buf<DT>(ur, h) : xb;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) load_row8_full<DT, GLU>(xb, ub, (t + kWideThreads * i) * kVec, v[i]);
+  }
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int vi = t + kWideThreads * i;
     if (vi < nvec) {
-      load_row8<DT, GLU>(xr, ur, vi * kVec, h, vec, v[i]);
+      if (!full) load_row8<DT, GLU>(xr, ur, vi * kVec, h, vec, v[i]);
       if constexpr (NORM) {
         if (vi * kVec + kVec <= h) {
           float4* d = reinterpret_cast<float4*>(xs + vi * kVec);
@@ -327,6 +403,8 @@ __global__ __launch_bounds__(kWideThreads) void quant_rows_wide_kernel(
       if (gamma == nullptr) {
 #pragma unroll
         for (int e = 0; e < kVec; ++e) g[e] = 1.0f;
+      } else if (full) {
+        load8_buf<GDT>(row_buf<GDT>(gamma, h), e0, g);
       } else if (vec && e0 + kVec <= h) {
         load8<GDT>(gamma, e0, g);
       } else {
