@@ -26,7 +26,7 @@ __device__ __forceinline__ uint32_t code_at(const uint8_t* src, int64_t srow, in
 
 __global__ __launch_bounds__(256) void convert_hf_kernel(const uint8_t* __restrict__ src, int64_t nb, int64_t n,
                                                          int64_t k, int64_t k_pad, uint32_t* __restrict__ qw,
-                                                         int64_t* __restrict__ part_nnz) {
+                                                         int64_t* __restrict__ part_nnz, bool vec4) {
   __shared__ int red[4];
   const int64_t per_row = k_pad / 16;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -38,16 +38,37 @@ __global__ __launch_bounds__(256) void convert_hf_kernel(const uint8_t* __restri
     const int64_t srow = r % nb;
     const int sh = 2 * (int)(r / nb);
     uint32_t out = 0;
+    if (vec4) {
+      // the 4 source bytes j0..j0+3 of each field f are one dword (K % 4 == 0): 4 loads in flight,
+      // bounded at the source row's end (dwords past it read as 0; their columns take code 1 below)
+      const buf_t rb = make_buf(src + srow * k, (uint32_t)k);
+      uint32_t w4[4];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      uint32_t byte = 0;
+      for (int f = 0; f < 4; ++f) w4[f] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rb, (int)(128 * b + 32 * f + j0), 0, 0);
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        const uint32_t c = code_at(src, srow, k, 128 * b + 32 * f + j0 + jj, sh);
-        byte |= c << (6 - 2 * f);
-        nnz += c != 1u;
+      for (int jj = 0; jj < 4; ++jj) {
+        uint32_t byte = 0;
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          uint32_t c = (w4[f] >> (8 * jj + sh)) & 3u;
+          c = 128 * b + 32 * f + j0 + jj < k ? (c == 3u ? 2u : c) : 1u;
+          byte |= c << (6 - 2 * f);
+          nnz += c != 1u;
+        }
+        out |= byte << (8 * jj);
       }
-      out |= byte << (8 * jj);
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        uint32_t byte = 0;
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          const uint32_t c = code_at(src, srow, k, 128 * b + 32 * f + j0 + jj, sh);
+          byte |= c << (6 - 2 * f);
+          nnz += c != 1u;
+        }
+        out |= byte << (8 * jj);
+      }
     }
     qw[idx] = out;
   }
@@ -97,8 +118,10 @@ hipError_t launch_convert_hf_offline(const uint8_t* src, int64_t nb, int64_t n, 
                                      float* scale_out, int64_t* parts, hipStream_t s) {
   const int64_t total = n * (k_pad / 16);
   const int64_t blocks = (total + 255) / 256;
+  // dword source loads when every source row starts 4-byte aligned and its bytes fit a buffer range
+  const bool vec4 = k % 4 == 0 && (uintptr_t)src % 4 == 0 && k < (int64_t)1 << 31;
   hipLaunchKernelGGL(convert_hf_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, nb, n, k, k_pad,
-                     reinterpret_cast<uint32_t*>(qw), parts);
+                     reinterpret_cast<uint32_t*>(qw), parts, vec4);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(convert_scale_kernel, dim3(1), dim3(256), 0, s, parts, blocks, src, nb, n, k, ws_dev, ws_dt,
