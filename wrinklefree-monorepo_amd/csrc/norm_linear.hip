@@ -111,9 +111,10 @@ __global__ __launch_bounds__(64 * S) void norm_linear_kernel(const void* __restr
       for (int j = 0; j < 4; ++j) toks[j] = tok0 + j;
       col.load(ep, ncol, N, toks, 0);  // M = 0: no token scales from memory
       if (ep.res) {
+        bool ok[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (tok0 + j < M && ncol < N) col.res[j] = epi_res(ep, tok0 + j, ncol);
+        for (int j = 0; j < 4; ++j) ok[j] = tok0 + j < M && ncol < N;
+        load_res_col<4>(ep, toks, ok, ncol, col.res);
       }
     }
 

@@ -280,6 +280,30 @@ __device__ __forceinline__ uint64_t epi_store_key(const Epilogue& e, float ws, f
 // residuals), loaded at kernel entry so their latency overlaps the weight stream instead of following
 // the final reduction (a kernel's first touch of them misses the cache).  Entries of tokens >= M or of
 // n >= N are not loaded.
+// Residuals res[tok[j], n] of the tokens with ok[j] (0 for the others).  Every load is issued before
+// the first wait: entries not wanted load element 0 (in bounds whenever a residual is given) and are
+// zeroed afterwards, so no branch encloses a load (a test and a conversion per element made each load
+// wait for the previous one).
+template <int T>
+__device__ __forceinline__ void load_res_col(const Epilogue& e, const int (&tok)[T], const bool (&ok)[T], int n,
+                                             float (&res)[T]) {
+  if (e.res_dtype == WFB_F32) {
+    const float* r = reinterpret_cast<const float*>(e.res);
+    float v[T];
+#pragma unroll
+    for (int j = 0; j < T; ++j) v[j] = r[ok[j] ? (int64_t)tok[j] * e.ldr + n : 0];
+#pragma unroll
+    for (int j = 0; j < T; ++j) res[j] = ok[j] ? v[j] : 0.0f;
+  } else {
+    const uint16_t* r = reinterpret_cast<const uint16_t*>(e.res);
+    uint16_t v[T];
+#pragma unroll
+    for (int j = 0; j < T; ++j) v[j] = r[ok[j] ? (int64_t)tok[j] * e.ldr + n : 0];
+#pragma unroll
+    for (int j = 0; j < T; ++j) res[j] = ok[j] ? bf16_bits_to_f32(v[j]) : 0.0f;
+  }
+}
+
 template <int T>
 struct EpiCol {
   float ws = 0.0f, bias = 0.0f;
@@ -292,10 +316,13 @@ struct EpiCol {
     bias = epi_bias(e, n);
 #pragma unroll
     for (int j = 0; j < T; ++j)
-      if (tok[j] < M) {
-        as[j] = epi_ascale(e, tok[j]);
-        if (e.res) res[j] = epi_res(e, tok[j], n);
-      }
+      if (tok[j] < M) as[j] = epi_ascale(e, tok[j]);
+    if (e.res) {
+      bool ok[T];
+#pragma unroll
+      for (int j = 0; j < T; ++j) ok[j] = tok[j] < M;
+      load_res_col<T>(e, tok, ok, n, res);
+    }
   }
 };
 
