@@ -232,6 +232,16 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
   if (w >= NT) return;
   const int nt = w;
   const int n = n0 + nt * 16 + nl;
+  // token scales of the late (non-PRE) epilogue, all loaded before the first is used: an index clamped
+  // into range instead of a branch around each load
+  float asl[4 * MT];
+  if constexpr (!PRE) {
+#pragma unroll
+    for (int j = 0; j < 4 * MT; ++j) {
+      const int tok = (j / 4) * 16 + 4 * g + (j % 4);
+      asl[j] = ep.a_scale ? ep.a_scale[tok < M ? tok : 0] : 1.0f;
+    }
+  }
   if (ep.amax) {  // argmax epilogue: max over the 16 rows (lanes 16g .. 16g + 15) of each token
     const float ws = PRE ? col.ws : n < N ? epi_wscale(ep, n) : 0.0f;
     const float bias = PRE ? col.bias : n < N ? epi_bias(ep, n) : 0.0f;
@@ -248,7 +258,7 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
         if constexpr (PRE)
           key = epi_store_key_r(ep, ws, col.as[4 * mt + j], bias, col.res[4 * mt + j], tok, n, tot, valid);
         else
-          key = epi_store_key(ep, ws, valid ? epi_ascale(ep, tok) : 0.0f, bias, tok, n, tot, valid);
+          key = epi_store_key(ep, ws, valid ? asl[4 * mt + j] : 0.0f, bias, tok, n, tot, valid);
         key = group_max_u64<16>(key);
         const int slot = blockIdx.x * NT + nt;  // one slot per 16 rows
         if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
@@ -268,7 +278,7 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
       for (int k = 1; k < S; ++k) tot += red[k][nt][mt][j][lane];
       if (tok < M) {
         if constexpr (PRE) epi_store_r(ep, ws, col.as[4 * mt + j], bias, col.res[4 * mt + j], tok, n, tot);
-        else epi_store(ep, ws, epi_ascale(ep, tok), bias, tok, n, tot);
+        else epi_store(ep, ws, asl[4 * mt + j], bias, tok, n, tot);
       }
     }
 }
