@@ -17,7 +17,7 @@ roofline fractions: launch_context (an empty kernel's per-launch time, a plain c
 bytes as the dominant GEMV, the GEMV on a 131 MB matrix) and, per prefill entry, the vendor library's
 plain int8 GEMM (torch._int_mm on hipBLASLt) on the same M, N, K.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-e2e] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-e2e] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -89,7 +89,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--sweep", action="store_true", help="also run the batched M sweep (configs[2])")
+    p.add_argument("--sweep", action="store_true", help="run the batched M sweep (configs[2]; the default)")
+    p.add_argument("--no-sweep", action="store_true", help="skip the batched M sweep (configs[2])")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-e2e", action="store_true",
@@ -732,7 +733,8 @@ def main():
     layer = decode_layer_bench(torch, L, dev, max(50, args.steps // 2), 5)
 
     sweep = None
-    if args.sweep:
+    if not args.no_sweep:
+        print("[bench] batched M sweep (configs[2])", file=sys.stderr, flush=True)
         sweep = []
         for n, k in ((2560, 2560), (2560, 6912), (13824, 2560)):
             syn = Synth(torch, dev, 6000 + n + k)
@@ -747,6 +749,7 @@ def main():
                 ms = timed(torch, calls, args.steps, 5)
                 gbs = gemv_bytes(m, n, k) / (ms * 1e-3) / 1e9
                 sweep.append({"M": m, "N": n, "K": k, "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                              "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                               "TOPS": round(2 * m * n * k / (ms * 1e-3) / 1e12, 2)})
             del copies
 
