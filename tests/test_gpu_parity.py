@@ -175,10 +175,13 @@ def test_batched_sweep_mfma(pkg, dev, n, k, m):
         _check_linear(pkg, dev, packed, a, 1.0, np.ones(m, np.float32), kernel="auto", check_fp32=False)
 
 
-@pytest.mark.parametrize("m,n,k", [(12, 32800, 128), (24, 16400, 256), (64, 8200, 384), (9, 40, 8192)])
+@pytest.mark.parametrize("m,n,k", [(12, 32800, 128), (24, 16400, 256), (64, 8200, 384), (9, 40, 8192),
+                                   (24, 9216, 2560), (24, 9200, 2560), (40, 6144, 8192), (40, 6144, 8320),
+                                   (40, 12000, 8320), (17, 18432, 256)])
 def test_batched_kernel_choice_boundaries(pkg, dev, m, n, k):
-    # 3 <= M <= 64 runs the split-K skinny kernel while N * ceil(M/16) <= 32768 (always for M <= 8) and
-    # the whole-K wave-per-rows kernel beyond; these shapes sit just past that boundary
+    # 3 <= M <= 64: the 32-row tile kernel for M > 16 when N * ceil(M/16) >= 18432 and K <= 8192, else the
+    # split-K skinny kernel while N * ceil(M/16) <= 32768 (always for M <= 8), else the whole-K
+    # wave-per-rows kernel; these shapes sit on either side of those boundaries
     rng = np.random.default_rng(2500 + m + n + k)
     packed = _packed(rng, n, k)
     a = orc.random_int8(rng, m, k)

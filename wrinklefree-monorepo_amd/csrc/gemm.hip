@@ -730,6 +730,13 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   // M <= 8, for larger M while N * (16-token tiles) <= 32768); it addresses through 32-bit offsets.
   const int mt = (m + 15) / 16;
   const bool small_offsets = (int64_t)n * (k / 4) <= INT32_MAX && (int64_t)(m - 1) * lda + k <= INT32_MAX;
+  // 17 <= M <= 64 on wide outputs: the 32-row tile kernel (one or two tile rows, its time nearly flat
+  // in M), measured on MI355X against the skinny and whole-K kernels over M = 9..64 and the BitNet-2B /
+  // Llama-3-8B shapes: faster from N * ceil(M/16) >= 18432 with K <= 8192 (M = 64: 28672 x 4096
+  // 67.1 -> 15.0 us, 13824 x 2560 26.1 -> 10.0, 6144 x 4096 25.8 -> 13.3; M = 24: 13824 x 2560 10.5 -> 9.8),
+  // the split-K kernels below that and for longer rows (M = 64, 4096 x 14336: 33.5 vs 37.2 us).
+  if (m > 16 && m <= 64 && small_offsets && (int64_t)n * mt >= 18432 && k <= 8192)
+    return launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
   if (m <= 64 && small_offsets && (m <= 8 || (int64_t)n * (mt == 3 ? 4 : mt) <= 32768)) {
     if (m <= 16) return launch_skinny<1>(W, n, C, A, m, lda, e, s);
     if (m <= 32) return launch_skinny<2>(W, n, C, A, m, lda, e, s);
