@@ -347,6 +347,11 @@ def test_norm_quant_batch_invariant(pkg, dev, h):
     assert torch.equal(q_big[:8], q_small) and torch.equal(s_big[:8], s_small)
     q_ref, s_ref = orc.rmsnorm_quant(xt[:8].float().cpu().numpy(), g, 1e-6)
     assert np.array_equal(q_small.cpu().numpy(), q_ref) and np.array_equal(s_small.cpu().numpy(), s_ref)
+    xf = xt.float()  # fp32 rows (the gated product's dtype in the decode layer): same values, same codes
+    qf_big, sf_big = pkg.rmsnorm_quantize_i8(xf, gt, eps=1e-6)
+    qf_small, sf_small = pkg.rmsnorm_quantize_i8(xf[:8].contiguous(), gt, eps=1e-6)
+    assert torch.equal(qf_big[:8], qf_small) and torch.equal(sf_big[:8], sf_small)
+    assert np.array_equal(qf_small.cpu().numpy(), q_ref) and np.array_equal(sf_small.cpu().numpy(), s_ref)
     for act in ("silu", "relu2"):
         up = torch.from_numpy(orc.outlier_hidden(rng, 100, h).astype(np.float32)).to(dev)
         gate = xt.float()
