@@ -497,29 +497,6 @@ def launch_context(torch, dev, L, steps: int, warmup: int, dom_bytes: int) -> di
             "gemv_128256x4096_frac_hbm_peak": round(big_bytes / (big_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def mfma_ceiling(torch, dev, L) -> dict:
-    """Measured rate of back-to-back int8 MFMA on this device (library diagnostic wfb_diag_mfma_i8:
-    2048 workgroups x 4 waves, 8 independent 32x32x32 accumulators per wave), with constant operands
-    and with pseudo-random int8 operands (what a GEMM feeds).  The practical ceiling beside the
-    nominal 5.0 POP/s dense int8 peak."""
-    blocks, iters = 2048, 1000
-    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
-    f = L.lib.wfb_diag_mfma_i8
-    res = {}
-    for rnd in (0, 1):
-        args = (rnd, blocks, iters, ctypes.c_void_p(sink.data_ptr()), L.stream)
-
-        def call(args=args):
-            if f(*args) != 0:
-                raise RuntimeError(L.lib.wfb_last_error().decode())
-
-        ms = timed(torch, [[call]], 5, 2)
-        tops = 65536.0 * 8 * iters * blocks * 4 / (ms * 1e-3) / 1e12
-        res["random_operands_TOPS" if rnd else "constant_operands_TOPS"] = round(tops, 1)
-    res["random_frac_nominal"] = round(res["random_operands_TOPS"] / INT8_PEAK_TOPS, 4)
-    return res
-
-
 def measured_traffic(n: int, k: int):
     """HBM bytes per launch of the M=1 GEMV at (n, k) from the committed FETCH_SIZE / WRITE_SIZE
     profile (profiles/gemv_i2s_decode_bitnet2b.txt, calibrated against a plain copy kernel), or None."""
@@ -535,21 +512,18 @@ def measured_traffic(n: int, k: int):
 
 
 def cpu_baseline(seconds: float):
-    """The reference's own CPU GEMV op (oracle/_ref build of bitnet_gemv.cpp; OpenMP over rows as in
-    torch_extension_cpu.cpp:355-366) on the same four shapes; falls back to the C restatement."""
+    """The CPU baseline: oracle/c/i2s_cpu_avx2.c, this build's AVX2 port of the reference CPU GEMV op
+    (the vpmaddubsw I2_S dot of bitnet_gemv.cpp:516-685 with the OpenMP row loop of
+    torch_extension_cpu.cpp:355-366; bit-equal to the reference build, tests/test_oracle.py), on the
+    same four shapes and byte formula.  Nothing built from the reference runs here."""
     from oracle import bitnet_oracle as orc
     from oracle import refbind
 
     threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
     os.environ["OMP_NUM_THREADS"] = str(threads)
-    kind = "reference"
-    if refbind.RefLib.exists(refbind.REF_AVX2):
-        lib = refbind.RefLib(refbind.REF_AVX2)
-        run = lambda p, a, out: lib.gemv(p, a, 1.0, out)  # noqa: E731
-    else:
-        kind = "port"
-        c = refbind.OracleC()
-        run = lambda p, a, out: c.gemm(p, a, 1.0)  # noqa: E731
+    kind = "port"
+    c = refbind.OracleC()
+    run = lambda p, a, out: c.gemv_avx2(p, a, 1.0, out)  # noqa: E731
     rng = np.random.default_rng(1001)
     total_bytes, total_t, reps_done = 0, 0.0, []
     for n, k in GEMV_SHAPES:
@@ -602,7 +576,8 @@ def cpu_baseline(seconds: float):
         "kind": kind,
         "one_thread_GB/s": one_thread,
         "host_nproc": os.cpu_count(),
-        "sample": f"reference I2_S GEMV op (AVX2, OpenMP {threads} threads) on the 4 BitNet-2B decode shapes, "
+        "sample": f"AVX2 port of the reference I2_S GEMV op (OpenMP {threads} threads) on the 4 BitNet-2B "
+                  f"decode shapes, "
                   f"{'/'.join(map(str, reps_done))} calls each over {seconds:.0f} s, same byte formula; "
                   f"host CPU: {cpu_model}",
     }
@@ -668,9 +643,7 @@ def main():
 
     # ---- prefill GEMM, M in {512, 2048, 8192} ---------------------------------------
     # Beside each: the vendor library's plain int8 GEMM on the same M, N, K (torch._int_mm, hipBLASLt;
-    # int8 x int8 -> int32 with unpacked int8 weights, i.e. 4x the weight bytes and no unpack work), and
-    # the fraction of the measured MFMA rate with random operands (the practical ceiling).
-    mfma = mfma_ceiling(torch, dev, L)
+    # int8 x int8 -> int32 with unpacked int8 weights, i.e. 4x the weight bytes and no unpack work).
     prefill = []
     for n, k in PREFILL_SHAPES:
         syn = Synth(torch, dev, 3000 + n)
@@ -688,13 +661,12 @@ def main():
             prefill.append({"M": m, "N": n, "K": k, "activations": "uniform int8 [-127, 127]",
                             "us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
                             "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                            "frac_measured_mfma_rate": round(tops / mfma["random_operands_TOPS"], 4),
                             "library_int8_us": round(lib_ms * 1e3, 2),
                             "library_int8_frac_peak": round(2.0 * m * n * k / (lib_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)})
             del a, out
         # The path's own input distribution: per-token absmax int8 codes of configs[2]'s hidden states
         # (N(0, 1), 1% at +-20), as the fused RMSNorm + quant kernel hands them to the GEMM.  The
-        # matrix cores' rate depends on the operand bits (see int8_mfma_measured), so both are reported.
+        # matrix cores' rate depends on the operand bits (the bits that toggle set the matrix cores' power and clock), so both are reported.
         m = 2048
         x = syn.hidden(m, k)
         a = torch.round(x * (127.0 / x.abs().amax(dim=1, keepdim=True))).clamp_(-127, 127).to(torch.int8)
@@ -708,7 +680,6 @@ def main():
         prefill.append({"M": m, "N": n, "K": k, "activations": "per-token int8 codes of N(0,1) + 1% +-20",
                         "us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
                         "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                        "frac_measured_mfma_rate": round(tops / mfma["random_operands_TOPS"], 4),
                         "library_int8_us": round(lib_ms * 1e3, 2),
                         "library_int8_frac_peak": round(2.0 * m * n * k / (lib_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)})
         del a, out, w8t
@@ -783,7 +754,6 @@ def main():
         "device_copy_GB/s": round(copy_gbs, 1),
         "launch_context": launch,
         "gemv_per_shape": per_shape,
-        "int8_mfma_measured": mfma,
         "prefill_gemm": prefill,
         "rmsnorm_quant": normq,
         "decode_layer_2b": layer,

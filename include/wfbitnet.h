@@ -327,15 +327,6 @@ int wfb_linear_i2s_glu(const uint8_t* qweight, int64_t n, int64_t k, const int8_
                        const float* a_scale, const float* w_scales_dev, int act_kind, int mid_dtype, float* out,
                        int64_t ldo, void* stream);
 
-/* Diagnostic, with no counterpart in the reference: the rate of back-to-back int8 MFMA
- * (v_mfma_i32_32x32x32_i8, 8 independent accumulators per wave) on this device, the practical
- * ceiling to read the prefill GEMM's rate against, next to the nominal dense int8 peak.  Launches
- * `blocks` workgroups of 256 threads; each wave issues 8 * iters MFMAs (65536 int8 ops each) on
- * constant operands (random_operands = 0) or on distinct pseudo-random int8 operands per chain
- * (random_operands = 1, what a GEMM feeds).  sink: blocks * 256 ints of device memory, written so
- * the work is kept.  Time it with events on the stream: ops = 65536 * 8 * iters * blocks * 4. */
-int wfb_diag_mfma_i8(int random_operands, int64_t blocks, int64_t iters, int* sink, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,8 @@
 """ctypes access to the compiled CPU checkers -- TEST INFRASTRUCTURE ONLY.
 
-* ``oracle/c/liboracle_c.so``: our C restatement (oracle/c/i2s_oracle.c).
+* ``oracle/c/liboracle_c.so``: our C restatements -- the scalar checker (oracle/c/i2s_oracle.c) and
+  the AVX2 port of the reference CPU GEMV op (oracle/c/i2s_cpu_avx2.c), which bench.py times as
+  its CPU baseline.
 * ``oracle/_ref/libref_bitnet_avx2.so``: the reference's own bitnet_gemv.cpp compiled by
   oracle/Makefile (AVX2 path); ``libref_bitnet_avx512.so`` adds the reference CMake's AVX-512
   flags.  Both exist only where the reference tree was present at build time; callers skip
@@ -50,6 +52,35 @@ class OracleC:
         self.lib.orc_acc_i2_i8.argtypes = [_int, _int, _int, _vp, _vp, _vp]
         self.lib.orc_quantize_i8.restype = None
         self.lib.orc_quantize_i8.argtypes = [_int, _vp, _vp, _vp]
+        self.lib.cpu_gemv_i2s_avx2.restype = _int
+        self.lib.cpu_gemv_i2s_avx2.argtypes = [_int, _int, _vp, _vp, _vp, ctypes.c_float]
+        self.lib.cpu_gemm_i2s_avx2.restype = _int
+        self.lib.cpu_gemm_i2s_avx2.argtypes = [_int, _int, _int, _vp, _vp, _vp, ctypes.c_float]
+
+    def gemv_avx2(self, packed: np.ndarray, a: np.ndarray, scale: float, out: np.ndarray | None = None) -> np.ndarray:
+        """AVX2 port of the reference bitnet_gemv_cpu op: fp32 [N] = acc * scale."""
+        packed = np.ascontiguousarray(packed, np.uint8)
+        a = np.ascontiguousarray(a, np.int8).ravel()
+        n, k = packed.shape[0], packed.shape[1] * 4
+        if a.size != k:
+            raise ValueError("activations must hold packed_weights.shape[1] * 4 values")
+        if out is None:
+            out = np.empty(n, np.float32)
+        if self.lib.cpu_gemv_i2s_avx2(n, k, _ptr(out), _ptr(packed), _ptr(a), float(scale)) != 0:
+            raise ValueError("K must be a multiple of 128")
+        return out
+
+    def gemm_avx2(self, packed: np.ndarray, a: np.ndarray, scale: float) -> np.ndarray:
+        """AVX2 port of the reference bitnet_gemm_cpu op: fp32 in its [out, batch] layout (batch <= 64)."""
+        packed = np.ascontiguousarray(packed, np.uint8)
+        a2 = np.ascontiguousarray(np.atleast_2d(a), np.int8)
+        n, k = packed.shape[0], packed.shape[1] * 4
+        if a2.shape[1] != k:
+            raise ValueError("activations must hold packed_weights.shape[1] * 4 columns")
+        out = np.empty((n, a2.shape[0]), np.float32)
+        if self.lib.cpu_gemm_i2s_avx2(n, a2.shape[0], k, _ptr(out), _ptr(packed), _ptr(a2), float(scale)) != 0:
+            raise ValueError("K must be a multiple of 128 and the batch at most 64")
+        return out
 
     def acc(self, packed: np.ndarray, a: np.ndarray) -> np.ndarray:
         packed = np.ascontiguousarray(packed, np.uint8)

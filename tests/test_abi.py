@@ -204,14 +204,6 @@ def test_residual_argument_errors(pkg):
     assert st == -1 and "residual row stride" in pkg._lib.last_error()
 
 
-def test_diag_mfma_argument_errors(pkg):
-    vp = ctypes.c_void_p
-    assert pkg._lib.status("wfb_diag_mfma_i8", 1, 0, 10, vp(16), None) == -1
-    assert "blocks" in pkg._lib.last_error()
-    assert pkg._lib.status("wfb_diag_mfma_i8", 1, 4, 10, None, None) == -1
-    assert "null sink" in pkg._lib.last_error()
-
-
 def test_rmsnorm_linear_argument_errors(pkg):
     vp = ctypes.c_void_p
     seg = (ctypes.c_int64 * 2)(64, 64)

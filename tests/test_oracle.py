@@ -231,6 +231,31 @@ def test_c_oracle_matches_numpy():
     assert np.array_equal(q, q2) and s == s2[0]
 
 
+@pytest.mark.parametrize("k", [128, 384, 640, 2560, 6912, 14336])
+def test_avx2_port_matches_oracle(k):
+    """The AVX2 port of the reference GEMV op (bench.py's CPU baseline): exact integer dots, odd block
+    counts (the one-block tail), extreme activations (-128 and 127 in every field) and batches."""
+    c = refbind.OracleC()
+    rng = np.random.default_rng(100 + k)
+    packed = orc.pack_i2s(orc.random_ternary(rng, 37, k))
+    a = orc.random_int8(rng, 5, k)
+    a[1] = 127
+    a[2] = -128
+    want = orc.accumulate(packed, a)  # [batch, out]
+    for b in range(a.shape[0]):
+        assert np.array_equal(c.gemv_avx2(packed, a[b], 1.0).astype(np.int64), want[b])
+    got = c.gemm_avx2(packed, a, 1.0)  # [out, batch]
+    assert np.array_equal(got.T.astype(np.int64), want)
+    ws = np.float32(0.0371)
+    assert np.array_equal(c.gemv_avx2(packed, a[0], ws), (want[0].astype(np.float32) * ws).astype(np.float32))
+
+
+def test_avx2_port_rejects_bad_k():
+    c = refbind.OracleC()
+    with pytest.raises(ValueError):
+        c.gemv_avx2(np.zeros((4, 25), np.uint8), np.zeros(100, np.int8), 1.0)
+
+
 # ---- the reference's own kernels: golden fixtures and oracle/_ref ----------------------------------
 
 
@@ -276,6 +301,19 @@ def test_reference_build_matches_oracle(k):
     a = orc.random_int8(rng, 1, k)[0]
     got = ref.gemv(packed, a, 1.0)
     assert np.array_equal(got.astype(np.int64), orc.accumulate(packed, a)[0])
+
+
+@pytest.mark.parametrize("n,k", [(2560, 2560), (3200, 2560), (13824, 2560), (2560, 6912)])
+def test_avx2_port_equals_reference_build(n, k):
+    """bench.py's CPU baseline is our AVX2 port; on the four BitNet-2B decode shapes its fp32 outputs
+    equal the reference's own compiled bitnet_gemv op bit for bit (scale applied as float(acc) * s)."""
+    ref = _ref()
+    c = refbind.OracleC()
+    rng = np.random.default_rng(n + k)
+    packed = orc.pack_i2s(orc.random_ternary(rng, n, k))
+    a = orc.random_int8(rng, 1, k)[0]
+    s = float(orc.log_uniform(rng))
+    assert np.array_equal(c.gemv_avx2(packed, a, s), ref.gemv(packed, a, s))
 
 
 def test_reference_build_rejects_bad_k():

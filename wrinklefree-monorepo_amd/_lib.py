@@ -56,7 +56,6 @@ SIGNATURES = {
                                  _i64, _i64, _f32, _vp, _i64, _vp, _vp],
     "wfb_gqa_prefill_attention": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _i64, _f32, _vp, _i64, _vp],
-    "wfb_diag_mfma_i8": [_int, _i64, _i64, _vp, _vp],
     "wfb_linear_i2s_glu": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _int, _int, _vp, _i64, _vp],
     "wfb_rmsnorm_linear_i2s": [_vp, _int, _i64, _vp, _int, _f32, _i64, _i64, _vp, _i64, _i64, _int, _vp, _vp, _vp,
                                _int, _i64, _vp, _int, _i64, _vp],

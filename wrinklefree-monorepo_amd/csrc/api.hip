@@ -485,13 +485,4 @@ int wfb_linear_i2s_glu(const uint8_t* qweight, int64_t n, int64_t k, const int8_
                     name);
 }
 
-int wfb_diag_mfma_i8(int random_operands, int64_t blocks, int64_t iters, int* sink, void* stream) {
-  if (blocks <= 0 || blocks > 65535 || iters <= 0 || iters > (int64_t)1 << 24)
-    return fail(WFB_EINVAL, "wfb_diag_mfma_i8: blocks must be in 1..65535 and iters in 1..2^24 (got %lld, %lld)",
-                (long long)blocks, (long long)iters);
-  if (!sink) return fail(WFB_EINVAL, "wfb_diag_mfma_i8: null sink");
-  return hip_status(wfb::launch_mfma_rate(random_operands != 0, blocks, iters, sink, as_stream(stream)),
-                    "wfb_diag_mfma_i8");
-}
-
 }  // extern "C"

@@ -410,7 +410,6 @@ hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* 
                                   const Epilogue& e, hipStream_t s);
 hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                            const Epilogue& e, hipStream_t s);
-hipError_t launch_mfma_rate(bool random_operands, int64_t blocks, int64_t iters, int* sink, hipStream_t s);
 // gate|up linear with the gated activation in its epilogue (M <= 64; n = 2 * half, half % 32 == 0;
 // fp32 output [M, half] at e.out / e.ldo)
 hipError_t launch_gemm_i2s_glu(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, int act,
