@@ -254,8 +254,9 @@ int wfb_lm_head_argmax(const void* x, int x_dtype, int64_t ldx, const void* gamm
  * head_dim 64 or 128; G <= 8.  A position outside [0, max_len) writes NaN to that sequence's output
  * and leaves the cache untouched (positions live on the device and are not checked on the host).
  * workspace: WFB_ATTN_WS(batch, num_heads, head_dim, max_len) floats of device memory for the
- * split-context pass (keys cut into splits chosen from max_len and the grid size, merged by a second
- * kernel), or NULL for one workgroup per (kv head, sequence) over all keys.
+ * split-context pass (keys cut into 64-key splits, doubled only while splits x query heads per kv head
+ * would pass 4096, the combine's LDS staging; chosen from max_len alone; merged by a second kernel), or
+ * NULL for one workgroup per (kv head, sequence) over all keys.
  * Replaces attention_forward (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:381-441) with the
  * cache writes of kv_cache_update_key / kv_cache_update_value
  * (SGB/sgl-kernel/csrc/inference/kv_cache.h:81-101) and the rotary embedding of the stage-1 HF model

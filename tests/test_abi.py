@@ -56,6 +56,15 @@ def test_argument_errors(pkg):
     assert _linear_status(pkg, fn="wfb_gemv_i2s", m=4) == -1 and "GEMV" in pkg._lib.last_error()
 
 
+def test_prefill_gemm_rejects_row_stride_past_its_offsets(pkg):
+    """M > 64 runs the tile GEMM, which addresses up to 128 activation rows of a tile through 32-bit
+    offsets from the tile's first row: 127 * lda + K must stay below 2^31 (any M and N are fine)."""
+    assert _linear_status(pkg, m=256, lda=2**25) == -1
+    assert "too large for the prefill GEMM" in pkg._lib.last_error()
+    assert _linear_status(pkg, m=64, lda=2**25, w=8) == -1  # M <= 64 does not take that check
+    assert "aligned" in pkg._lib.last_error()
+
+
 def test_empty_batch_is_a_noop(pkg):
     # M == 0 returns before touching any pointer or the GPU
     assert _linear_status(pkg, m=0, w=0, a=0) == 0

@@ -97,17 +97,21 @@ CASES = [
     (2, 12, 2, 64, 520, [511, 512], torch.bfloat16, False),                            # G = 6, chunk edges
     (1, 7, 1, 128, 129, [127], torch.float32, True),                                   # G = 7
     (4, 2, 1, 64, 40, [3, 39, 0, 20], torch.bfloat16, True),                           # G = 2
-    (8, 16, 8, 128, 1100, [1099, 0, 63, 64, 255, 256, 700, 1023], torch.bfloat16, True),  # 256-key splits
-    (8, 8, 8, 64, 1100, [1099, 511, 512, 0, 128, 129, 1000, 7], torch.float32, True),    # fp32, 2 chunks/split
+    (8, 16, 8, 128, 1100, [1099, 0, 63, 64, 255, 256, 700, 1023], torch.bfloat16, True),  # split edges, G = 2
+    (8, 8, 8, 64, 1100, [1099, 511, 512, 0, 128, 129, 1000, 7], torch.float32, True),    # fp32, G = 1
+    # 513 64-key splits x G = 8 heads pass the combine's 4096 split-heads, so splits double to 128 keys
+    # while a bf16 chunk stays 256 keys: a chunk of a split that does not own pos reaches key pos
+    (4, 8, 1, 64, 32832, [200, 127, 128, 32831], torch.bfloat16, True),
+    (2, 8, 1, 128, 32832, [383, 32700], torch.float32, True),                           # fp32, 128-key splits
 ]
 
 
 @pytest.mark.parametrize("split", [True, False], ids=["split", "single"])
 @pytest.mark.parametrize("case", CASES, ids=[f"b{c[0]}_h{c[1]}x{c[2]}_d{c[3]}_L{c[4]}_{str(c[6])[6:]}" for c in CASES])
 def test_decode_attention_matches_torch(pkg, dev, case, split):
-    """Both forms: key splits on separate workgroups merged by the combine kernel (split; the split
-    length grows from 64 keys so the grid stays near 512 workgroups), and one workgroup per (kv head,
-    sequence) over all keys (single)."""
+    """Both forms: key splits on separate workgroups merged by the combine kernel (split; 64-key splits,
+    doubled only while splits x query heads would pass the combine's 4096), and one workgroup per
+    (kv head, sequence) over all keys (single)."""
     b, hq, hkv, d, max_len, pos, dtype, rope = case
     _run_case(pkg, dev, b, hq, hkv, d, max_len, pos, dtype, rope, seed=hq * 7 + max_len, split=split)
 

@@ -216,6 +216,47 @@ def test_prefill_gemm_8192_sampled(pkg, dev, n, k):
     assert np.array_equal(acc_g.sum(axis=1), a.astype(np.int64) @ w_col)
 
 
+def test_prefill_gemm_activation_offsets_past_4gib(pkg, dev):
+    """A strided activation view whose last row starts past 2^32 bytes: (M - 1) * lda + K > 2^32 while
+    127 * lda + K < 2^31 (the host's limit for the prefill GEMM), so every row must be read from its
+    own place -- a 32-bit offset from the start of A would wrap.  All 300 x 256 accumulators exact."""
+    m, n, k = 300, 256, 2560
+    lda = 16_777_088  # multiple of 16; 127 * lda + K < 2^31; (m - 1) * lda > 2^32
+    assert (m - 1) * lda + k > 2**32 and 127 * lda + k < 2**31
+    rng = np.random.default_rng(77)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    big = torch.empty((m, lda), dtype=torch.int8, device=dev)
+    big[:, :k].copy_(_t(a, dev))
+    y, acc = pkg.bitnet_linear(_t(packed, dev), big[:, :k], 1.0, return_acc=True)
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), _ref_acc(packed, a))
+    y2 = pkg.bitnet_linear(_t(packed, dev), big[:, :k], 1.0)  # the staged bf16 epilogue
+    assert torch.equal(y2, y)
+    del big
+
+
+def test_prefill_gemm_weight_offsets_past_4gib(pkg, dev):
+    """N * K / 4 > 2^32: weight rows past the first 4 GiB of the packed matrix (1,049,576 rows of
+    K = 16384, 4.3 GB) are read from their own place.  The matrix repeats 4096 random rows, so every
+    accumulator is checked against the oracle's product with the row it repeats."""
+    m, k, base_rows = 65, 16384, 4096
+    n = 2**32 // (k // 4) + 1000
+    rng = np.random.default_rng(78)
+    base = _packed(rng, base_rows, k)
+    a = orc.random_int8(rng, m, k)
+    reps = (n + base_rows - 1) // base_rows
+    w = _t(base, dev).repeat(reps, 1)[:n]
+    assert w.is_contiguous() and w.numel() > 2**32
+    _, acc = pkg.bitnet_linear(w, _t(a, dev), 1.0, return_acc=True)
+    ref = _ref_acc(base, a).astype(np.int32)  # [m, base_rows]
+    del w
+    got = acc.cpu().numpy()
+    del acc
+    full = (n // base_rows) * base_rows
+    assert np.array_equal(got[:, :full].reshape(m, -1, base_rows), np.broadcast_to(ref[:, None, :], (m, full // base_rows, base_rows)))
+    assert np.array_equal(got[:, full:], ref[:, :n - full])
+
+
 @pytest.mark.parametrize("m", [1, 2, 3, 17, 33, 300])
 @pytest.mark.parametrize("n,k", [(100, 128), (17, 640), (1, 256), (77, 14336), (130, 16384)])
 def test_ragged_shapes(pkg, dev, m, n, k):

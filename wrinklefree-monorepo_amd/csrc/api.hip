@@ -73,6 +73,11 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
   if (kind == Kernel::Gemv && !use_gemv(m, n, k, lda))
     return fail(WFB_EINVAL, "%s: the GEMV kernel takes M <= 2 tokens, K <= 32768 and N*K/4 < 2^31 (got M=%lld N=%lld K=%lld)",
                 name, (long long)m, (long long)n, (long long)k);
+  // The prefill GEMM (M > 64) addresses each tile of up to 128 activation rows through 32-bit offsets
+  // from the tile's first row; any M and N are fine, only a very long row stride is not.
+  if (m > 64 && 127 * lda + k > INT32_MAX)
+    return fail(WFB_EINVAL, "%s: activation row stride (%lld) too large for the prefill GEMM: 127 * lda + K must be "
+                "below 2^31", name, (long long)lda);
 
   wfb::Epilogue e;
   e.nseg = n_seg;

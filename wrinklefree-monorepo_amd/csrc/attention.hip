@@ -225,7 +225,9 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
       const int key = c0 + w * KW + r * KPW + kl;
       float kf[8];
       widen8<DT>(kr[r], kf);
-      if (key == pos) {
+      // only the split that owns pos wrote knew / vnew; a chunk longer than the split (CH > ks) can
+      // reach key pos in a split that does not own it, where the key is masked and must stay finite
+      if (owns_new && key == pos) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) kf[e] = knew[d0 + e];
       }
@@ -278,7 +280,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
       const int key = c0 + w * KW + r * KPW + kl;
       float vf[8];
       widen8<DT>(vr[r], vf);
-      if (key == pos) {
+      if (owns_new && key == pos) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) vf[e] = vnew[d0 + e];
       }

@@ -378,11 +378,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
   const int gm = min(kGroupM, tiles_m - grp * kGroupM);
   const int m0 = (grp * kGroupM + rr % gm) * BM, n0 = (rr / gm) * BN;
 
+  // The buffer descriptors start at the tile's first activation row and first weight row (64-bit
+  // pointer arithmetic), so the 32-bit offsets inside them stay below (BM - 1) * lda + K and
+  // 256 * K / 4 whatever M, N and the row stride (the host checks (BM - 1) * lda + K < 2^31).
   const int KS = (K + AROW - 1) / AROW;
   const uint32_t row_bytes = (uint32_t)K / 4;
-  const uint32_t a_end = (uint32_t)((int64_t)(M - 1) * lda + K), b_end = (uint32_t)N * row_bytes;
-  const buf_t ab = make_buf(A, a_end);
-  const buf_t wb = make_buf(W, b_end);
+  const int mrows = min(BM, M - m0), nrows = min(BN, N - n0);
+  const uint32_t a_end = (uint32_t)((int64_t)(mrows - 1) * lda + K), b_end = (uint32_t)nrows * row_bytes;
+  const buf_t ab = make_buf(A + (int64_t)m0 * lda, a_end);
+  const buf_t wb = make_buf(W + (int64_t)n0 * row_bytes, b_end);
 
   // LDS position p of activation row r holds chunk p ^ aswz(r); position q of weight row R holds
   // 16-byte piece q ^ bswz(R).  (16 consecutive rows then fall on 16 distinct 16-byte bank groups.)
@@ -391,18 +395,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 
   // Load descriptors: wave wn issues instructions AI*wn.. and BI*wn.. of each stage.  Rows past the
   // end of A or W are clamped to the last one (their results are never stored); bytes past K get an
-  // offset beyond the buffer and load as zeros without touching memory.
+  // offset beyond the buffer and load as zeros without touching memory.  Offsets are tile-relative.
   uint32_t a_row[AI], a_col[AI], b_row[BI], b_col[BI];
 #pragma unroll
   for (int jj = 0; jj < AI; ++jj) {
     const int r = ARPI * (AI * wn + jj) + l / CH;
-    a_row[jj] = (uint32_t)((int64_t)min(m0 + r, M - 1) * lda);
+    a_row[jj] = (uint32_t)((int64_t)min(r, mrows - 1) * lda);
     a_col[jj] = 16 * ((l % CH) ^ aswz(r));
   }
 #pragma unroll
   for (int jj = 0; jj < BI; ++jj) {
     const int R = (64 / BLPR) * (BI * wn + jj) + l / BLPR;
-    b_row[jj] = (uint32_t)min(n0 + R, N - 1) * row_bytes;
+    b_row[jj] = (uint32_t)min(R, nrows - 1) * row_bytes;
     b_col[jj] = 16 * ((l % BLPR) ^ bswz(R));
   }
   auto issue = [&](int kt, int8_t* la, uint8_t* lb) {
