@@ -270,6 +270,23 @@ int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int6
                              int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
                              float scale, void* out, int64_t ldo, float* workspace, void* stream);
 
+/* wfb_gqa_decode_attention without the workspace argument, allocating nothing.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The split partials go to a scratch array the
+ * library holds on each GPU for the life of the process: WFB_ATTN_SCRATCH_FLOATS floats (32 MiB);
+ * sizes whose partials would not fit are rejected with WFB_EINVAL (the exact need is
+ * batch * num_heads * (head_dim + 2) * splits, at most WFB_ATTN_WS(...)).  Same arguments, checks and
+ * results as wfb_gqa_decode_attention with a workspace.  Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (other streams, other threads) race; calls ordered on one
+ * stream do not.  Nothing in it needs clearing between calls (each split writes all it is read for). */
+#define WFB_ATTN_SCRATCH_FLOATS (8 * 1024 * 1024)
+int wfb_gqa_decode_attention_noalloc(const void* q, int64_t ldq, const void* k_new, int64_t ldk,
+                                     const void* v_new, int64_t ldv, int dtype,
+                                     const float* rope_cos, const float* rope_sin,
+                                     void* k_cache, void* v_cache, int64_t max_len, const int64_t* pos,
+                                     int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                     float scale, void* out, int64_t ldo, void* stream);
+
 /* Causal GQA attention of a prefill chunk: T new tokens per sequence at positions start .. start+T-1.
  * Rotary embedding of the new queries and keys (rope_cos / rope_sin fp32 [max_len, head_dim/2], or both
  * NULL for none), cache append of the T keys and values at their positions, then for token i of

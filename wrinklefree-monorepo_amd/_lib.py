@@ -54,6 +54,8 @@ SIGNATURES = {
                            _vp],
     "wfb_gqa_decode_attention": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
                                  _i64, _i64, _f32, _vp, _i64, _vp, _vp],
+    "wfb_gqa_decode_attention_noalloc": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
+                                         _i64, _i64, _i64, _f32, _vp, _i64, _vp],
     "wfb_gqa_prefill_attention": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _i64, _f32, _vp, _i64, _vp],
     "wfb_linear_i2s_glu": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _int, _int, _vp, _i64, _vp],

@@ -114,6 +114,37 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
   return hip_status(st, name);
 }
 
+
+// Host checks shared by the decode attention entry points; WFB_OK when the call may go ahead.
+int check_decode_attention(const char* name, const void* q, int64_t ldq, const void* k_new, int64_t ldk,
+                           const void* v_new, int64_t ldv, int dtype, const float* rope_cos, const float* rope_sin,
+                           void* k_cache, void* v_cache, int64_t max_len, const int64_t* pos, int64_t batch,
+                           int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, float scale, void* out,
+                           int64_t ldo) {
+  if (dtype != WFB_F32 && dtype != WFB_BF16) return fail(WFB_EINVAL, "%s: dtype must be WFB_F32 or WFB_BF16", name);
+  if (head_dim != 64 && head_dim != 128) return fail(WFB_EINVAL, "%s: head_dim (%lld) must be 64 or 128", name, (long long)head_dim);
+  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > 8)
+    return fail(WFB_EINVAL, "%s: num_heads (%lld) must be 1..8 times num_kv_heads (%lld)", name, (long long)num_heads,
+                (long long)num_kv_heads);
+  const int64_t esz = dtype == WFB_F32 ? 4 : 2;
+  if (batch < 0 || batch > 65535 || num_kv_heads > 65535)
+    return fail(WFB_EINVAL, "%s: batch (%lld) and num_kv_heads must be <= 65535", name, (long long)batch);
+  if (max_len <= 0 || max_len * head_dim * esz > INT32_MAX)
+    return fail(WFB_EINVAL, "%s: max_len (%lld) must be positive with max_len*head_dim*elem_size < 2^31", name,
+                (long long)max_len);
+  if (ldq < num_heads * head_dim || ldo < num_heads * head_dim || ldk < num_kv_heads * head_dim ||
+      ldv < num_kv_heads * head_dim)
+    return fail(WFB_EINVAL, "%s: row strides must cover num_heads*head_dim (q, out) and num_kv_heads*head_dim (k, v)",
+                name);
+  if ((rope_cos == nullptr) != (rope_sin == nullptr))
+    return fail(WFB_EINVAL, "%s: rope_cos and rope_sin must both be given or both be NULL", name);
+  if (!(scale == scale) || scale == __builtin_inff() || scale == -__builtin_inff())
+    return fail(WFB_EINVAL, "%s: scale must be finite", name);
+  if (batch == 0) return ok();
+  if (!q || !k_new || !v_new || !k_cache || !v_cache || !pos || !out) return fail(WFB_EINVAL, "%s: null pointer", name);
+  if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return fail(WFB_EINVAL, "%s: caches must be 16-byte aligned", name);
+  return WFB_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -333,31 +364,40 @@ int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int6
                              int64_t num_kv_heads, int64_t head_dim, float scale, void* out, int64_t ldo,
                              float* workspace, void* stream) {
   const char* name = "wfb_gqa_decode_attention";
-  if (dtype != WFB_F32 && dtype != WFB_BF16) return fail(WFB_EINVAL, "%s: dtype must be WFB_F32 or WFB_BF16", name);
-  if (head_dim != 64 && head_dim != 128) return fail(WFB_EINVAL, "%s: head_dim (%lld) must be 64 or 128", name, (long long)head_dim);
-  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > 8)
-    return fail(WFB_EINVAL, "%s: num_heads (%lld) must be 1..8 times num_kv_heads (%lld)", name, (long long)num_heads,
-                (long long)num_kv_heads);
-  const int64_t esz = dtype == WFB_F32 ? 4 : 2;
-  if (batch < 0 || batch > 65535 || num_kv_heads > 65535)
-    return fail(WFB_EINVAL, "%s: batch (%lld) and num_kv_heads must be <= 65535", name, (long long)batch);
-  if (max_len <= 0 || max_len * head_dim * esz > INT32_MAX)
-    return fail(WFB_EINVAL, "%s: max_len (%lld) must be positive with max_len*head_dim*elem_size < 2^31", name,
-                (long long)max_len);
-  if (ldq < num_heads * head_dim || ldo < num_heads * head_dim || ldk < num_kv_heads * head_dim ||
-      ldv < num_kv_heads * head_dim)
-    return fail(WFB_EINVAL, "%s: row strides must cover num_heads*head_dim (q, out) and num_kv_heads*head_dim (k, v)",
-                name);
-  if ((rope_cos == nullptr) != (rope_sin == nullptr))
-    return fail(WFB_EINVAL, "%s: rope_cos and rope_sin must both be given or both be NULL", name);
-  if (!(scale == scale) || scale == __builtin_inff() || scale == -__builtin_inff())
-    return fail(WFB_EINVAL, "%s: scale must be finite", name);
-  if (batch == 0) return ok();
-  if (!q || !k_new || !v_new || !k_cache || !v_cache || !pos || !out) return fail(WFB_EINVAL, "%s: null pointer", name);
-  if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return fail(WFB_EINVAL, "%s: caches must be 16-byte aligned", name);
+  const int st = check_decode_attention(name, q, ldq, k_new, ldk, v_new, ldv, dtype, rope_cos, rope_sin, k_cache,
+                                        v_cache, max_len, pos, batch, num_heads, num_kv_heads, head_dim, scale, out,
+                                        ldo);
+  if (st != WFB_OK || batch == 0) return st;
   return hip_status(wfb::launch_gqa_decode(dtype, (int)head_dim, (int)(num_heads / num_kv_heads), q, ldq, k_new, ldk,
                                            v_new, ldv, rope_cos, rope_sin, k_cache, v_cache, max_len, pos, (int)batch,
                                            (int)num_kv_heads, scale, out, ldo, workspace, as_stream(stream)),
+                    name);
+}
+
+int wfb_gqa_decode_attention_noalloc(const void* q, int64_t ldq, const void* k_new, int64_t ldk, const void* v_new,
+                                     int64_t ldv, int dtype, const float* rope_cos, const float* rope_sin,
+                                     void* k_cache, void* v_cache, int64_t max_len, const int64_t* pos, int64_t batch,
+                                     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, float scale,
+                                     void* out, int64_t ldo, void* stream) {
+  const char* name = "wfb_gqa_decode_attention_noalloc";
+  const int st = check_decode_attention(name, q, ldq, k_new, ldk, v_new, ldv, dtype, rope_cos, rope_sin, k_cache,
+                                        v_cache, max_len, pos, batch, num_heads, num_kv_heads, head_dim, scale, out,
+                                        ldo);
+  if (st != WFB_OK || batch == 0) return st;
+  const int g = (int)(num_heads / num_kv_heads);
+  const int64_t need = wfb::gqa_decode_workspace_floats(max_len, g, batch, num_kv_heads, (int)head_dim);
+  if (need > wfb::kAttnScratchFloats)
+    return fail(WFB_EINVAL, "%s: these sizes need %lld floats of split partials, more than the %lld (32 MiB) of the "
+                "library's scratch; pass a workspace to wfb_gqa_decode_attention instead", name, (long long)need,
+                (long long)wfb::kAttnScratchFloats);
+  float* part = nullptr;
+  if (need > 0) {
+    const hipError_t e = wfb::gqa_decode_scratch(&part);
+    if (e != hipSuccess) return hip_status(e, name);
+  }
+  return hip_status(wfb::launch_gqa_decode(dtype, (int)head_dim, g, q, ldq, k_new, ldk, v_new, ldv, rope_cos,
+                                           rope_sin, k_cache, v_cache, max_len, pos, (int)batch, (int)num_kv_heads,
+                                           scale, out, ldo, part, as_stream(stream)),
                     name);
 }
 

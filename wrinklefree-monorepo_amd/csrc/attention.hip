@@ -34,7 +34,15 @@
 // that owns the head; then each lane accumulates p * v for its keys and 8 elements.  At the end the
 // per-lane partial outputs are summed over the lanes of a wave sharing the same elements (xor
 // shuffles), then over the 4 waves in LDS, and divided by the softmax sum.
+#include <mutex>
+
 #include "wfb_common.h"
+
+// Split partials of wfb_gqa_decode_attention_noalloc, the entry point that allocates nothing: one copy
+// per GPU, held for the life of the process (a device global of the code object).  Host code never
+// passes this name to a kernel or a copy: it is a host-side stand-in, and the device address comes
+// from hipGetSymbolAddress (wfb::gqa_decode_scratch below).
+static __device__ __align__(256) float scratch[wfb::kAttnScratchFloats];
 
 namespace wfb {
 
@@ -42,6 +50,14 @@ namespace {
 
 constexpr int kAttnThreads = 256;
 constexpr int64_t kAttnMaxSplitHeads = 4096;  // splits x heads staged by the combine (32 KB of LDS)
+
+// Keys per split: 64, doubled only while the combine's LDS staging of the split weights (splits x
+// query heads per kv head) would pass kAttnMaxSplitHeads.
+int64_t split_keys(int64_t max_len, int g) {
+  int64_t ks = 64;
+  while (ks < max_len && ((max_len + ks - 1) / ks) * g > kAttnMaxSplitHeads) ks *= 2;
+  return ks;
+}
 
 template <int DT>
 __device__ __forceinline__ float round_to(float x) {
@@ -390,8 +406,7 @@ hipError_t launch_attn_g(const void* q, int64_t ldq, const void* kn, int64_t ldk
   // Measured at the Llama-3-8B batch-8 shape (split + combine, eager): 64-key splits are the fastest
   // or within 2% at every position of a 4096-slot cache (12.6 us at position 300, 20.7 at 1000,
   // 60.1 at 4000), where a grid-size target of 512 workgroups (512-key splits) gave 26.8 / 28.8 / 59.1.
-  int64_t ks = 64;
-  while (ks < max_len && ((max_len + ks - 1) / ks) * G > kAttnMaxSplitHeads) ks *= 2;
+  const int64_t ks = split_keys(max_len, G);
   const int64_t nsplit = (max_len + ks - 1) / ks;
   if (nsplit == 1 || part == nullptr) {
     constexpr int CH = DT == WFB_F32 ? 128 : 256;
@@ -450,6 +465,34 @@ hipError_t launch_gqa_decode(int dt, int d, int g, const void* q, int64_t ldq, c
   if (dt == WFB_BF16 && d == 128)
     return launch_attn_d<WFB_BF16, 128>(g, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo, part, s);
   return hipErrorInvalidValue;
+}
+
+int64_t gqa_decode_workspace_floats(int64_t max_len, int g, int64_t batch, int64_t hkv, int d) {
+  const int64_t ks = split_keys(max_len, g);
+  const int64_t nsplit = (max_len + ks - 1) / ks;
+  return nsplit == 1 ? 0 : batch * hkv * nsplit * g * (d + 2);
+}
+
+namespace {
+constexpr int kScratchDevices = 256;
+std::mutex g_scratch_mu;
+float* g_scratch_dev[kScratchDevices];  // device address of `scratch` on each GPU, looked up once
+}  // namespace
+
+hipError_t gqa_decode_scratch(float** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {  // first call on this device, with it current: its own copy's address
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  *ptr = g_scratch_dev[dev];
+  return hipSuccess;
 }
 
 }  // namespace wfb

@@ -390,6 +390,13 @@ hipError_t launch_glu_quant_rows(const void* gate, const void* up, int dt, int64
 hipError_t launch_quant_tensor(const void* x, int dt, int64_t numel, int8_t* q, float* a_scale, hipStream_t s);
 hipError_t launch_gemv_i2s(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                            const Epilogue& e, hipStream_t s);
+// Scratch of wfb_gqa_decode_attention_noalloc: 8 Mi floats (32 MiB) per GPU.
+constexpr int64_t kAttnScratchFloats = int64_t(8) << 20;
+static_assert(kAttnScratchFloats == WFB_ATTN_SCRATCH_FLOATS, "scratch size stated in the header");
+// floats of split partials launch_gqa_decode uses for these sizes (0: one split, no workspace pass)
+int64_t gqa_decode_workspace_floats(int64_t max_len, int g, int64_t batch, int64_t hkv, int d);
+// device address of this GPU's scratch array (looked up on the first call per device)
+hipError_t gqa_decode_scratch(float** ptr);
 hipError_t launch_gqa_decode(int dt, int d, int g, const void* q, int64_t ldq, const void* kn, int64_t ldk,
                              const void* vn, int64_t ldv, const float* rc, const float* rs, void* kc, void* vc,
                              int64_t max_len, const int64_t* pos, int b, int hkv, float scale, void* out, int64_t ldo,
