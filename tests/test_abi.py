@@ -65,6 +65,16 @@ def test_prefill_gemm_rejects_row_stride_past_its_offsets(pkg):
     assert "aligned" in pkg._lib.last_error()
 
 
+def test_bitlinear_lambda_below_one_raises_before_any_gpu_work(pkg):
+    mod = pkg.BitLinear(128, 64)
+    pkg.set_lambda_source(lambda: 0.5)
+    try:
+        with pytest.raises(RuntimeError, match="lambda"):
+            mod(torch.zeros(1, 128))
+    finally:
+        pkg.set_lambda_source(None)
+
+
 def test_empty_batch_is_a_noop(pkg):
     # M == 0 returns before touching any pointer or the GPU
     assert _linear_status(pkg, m=0, w=0, a=0) == 0

@@ -40,6 +40,7 @@ from .bitlinear import (
     SubLNBitLinear,
     convert_linear_to_bitlinear,
     patch_model_with_native_kernels,
+    set_lambda_source,
 )
 
 __all__ = [
@@ -49,5 +50,5 @@ __all__ = [
     "quantize_activations_i8", "quantize_activations_i8_per_token", "rmsnorm_linear", "rmsnorm_linear_preferred", "rmsnorm_linear_supported",
     "rmsnorm_quantize_i8", "unpack_i2s",
     "BitLinear", "BitNetLinearMethod", "BitNetLinearNative", "SubLNBitLinear", "convert_linear_to_bitlinear",
-    "patch_model_with_native_kernels", "model", "sglbitnt", "SGLBitNetFile", "write_sglbitnt",
+    "patch_model_with_native_kernels", "set_lambda_source", "model", "sglbitnt", "SGLBitNetFile", "write_sglbitnt",
 ]

@@ -10,13 +10,20 @@ Surfaces kept from the reference:
 
 The forward is the quantised serving forward of the reference CPU path (per-token absmax int8
 activations, I2_S ternary weights with a per-tensor absmean scale, exact int32 accumulation, then
-acc * w_scale * a_scale).  The float fake-quant QAT forward of the training module is not provided:
-this module is the inference hot path and has no CPU or eager-torch fallback.
+acc * w_scale * a_scale).  Under autograd (grad mode on and the weight or the input requiring grad)
+``BitLinear`` is the reference training module's straight-through estimator at lambda = 1
+(packages/training/src/wrinklefree/models/bitlinear.py:86-113: F.linear(x + (q(x) - x).detach(),
+w + (q(w) - w).detach())): the same forward value, computed by the kernels, and the gradients of
+F.linear at the quantised operands -- grad_x = grad_y @ q(w), grad_w = grad_y^T @ q(x).  A lambda
+warmup blend (lambda < 1) is a float product the ternary kernels do not compute; with a lambda source
+registered (:func:`set_lambda_source`) such a step raises.  The packed weight follows the float
+weight: any in-place change (optimizer step, ``copy_``, ``load_state_dict``) repacks on the next
+forward.  No CPU or eager-torch fallback for the forward.
 """
 
 from __future__ import annotations
 
-from typing import Iterable, List, Optional
+from typing import Callable, Iterable, List, Optional
 
 import torch
 import torch.nn as nn
@@ -28,7 +35,27 @@ from .ops import (
     quantize_activations_i8,
     quantize_activations_i8_per_token,
     rmsnorm_quantize_i8,
+    unpack_i2s,
 )
+
+_lambda_source: Optional[Callable[[], float]] = None
+
+
+def set_lambda_source(fn: Optional[Callable[[], float]]) -> None:
+    """Register the training loop's lambda-warmup value (the reference reads
+    ``wrinklefree.quantization.lambda_warmup.get_current_lambda``, lambda_warmup.py:131-135).  BitLinear
+    computes the fully quantised product only, so a forward while the source returns lambda != 1 raises
+    instead of silently training a different function."""
+    global _lambda_source
+    _lambda_source = fn
+
+
+def _check_lambda(name: str) -> None:
+    if _lambda_source is not None:
+        lam = float(_lambda_source())
+        if lam != 1.0:
+            raise RuntimeError(f"{name}: lambda warmup at {lam} (< 1) blends float and quantised operands; the "
+                               "ternary kernels compute lambda = 1 only")
 
 
 def _pad_k(k: int) -> int:
@@ -39,13 +66,88 @@ def _out_dtype(x: torch.Tensor) -> torch.dtype:
     return torch.float32 if x.dtype == torch.float32 else torch.bfloat16
 
 
+class _BitLinearSTE(torch.autograd.Function):
+    """Straight-through estimator of the reference training forward at lambda = 1
+    (WF/models/bitlinear.py:86-113).  Forward: the kernels' quantised product (per-token int8 codes of x,
+    the ternary pack of w, exact accumulators, rescale).  Backward: the gradients of F.linear at the
+    dequantised operands, identity through both quantisers -- grad_x = g @ (codes_w * s_w),
+    grad_w = g^T @ (codes_x * s_x), grad_b = sum g -- in fp32, cast to each input's dtype."""
+
+    @staticmethod
+    def forward(ctx, x2, weight, bias, mod):
+        q, a_scale = quantize_activations_i8_per_token(x2, k_pad=mod.k_pad)
+        y = bitnet_linear(mod.qweight, q, mod.weight_scale, a_scale=a_scale, bias=bias, out_dtype=_out_dtype(x2))
+        ctx.save_for_backward(q, a_scale, mod.qweight, mod.weight_scale)
+        ctx.meta = (x2.dtype, weight.dtype, None if bias is None else bias.dtype, mod.in_features)
+        return y if y.dtype == x2.dtype else y.to(x2.dtype)
+
+    @staticmethod
+    def backward(ctx, gy):
+        q, a_scale, qweight, wscale = ctx.saved_tensors
+        xdt, wdt, bdt, kin = ctx.meta
+        g = gy.to(torch.float32).contiguous()
+        gx = gw = gb = None
+        if ctx.needs_input_grad[0]:
+            w_deq = unpack_i2s(qweight)[:, :kin].to(torch.float32) * wscale  # [N, K]
+            gx = (g @ w_deq).to(xdt)
+        if ctx.needs_input_grad[1]:
+            x_deq = q[:, :kin].to(torch.float32) * a_scale[:, None]  # [M, K]
+            gw = (g.t().contiguous() @ x_deq).to(wdt)
+        if bdt is not None and ctx.needs_input_grad[2]:
+            gb = g.sum(0).to(bdt)
+        return gx, gw, gb, None
+
+
+class _SubLNBitLinearSTE(torch.autograd.Function):
+    """SubLN + BitLinear under autograd: the fused kernel's forward value (RMSNorm + per-token int8 codes
+    + the ternary product), the straight-through gradient of the linear as in :class:`_BitLinearSTE`,
+    and the RMSNorm's own gradient, from the float norm recomputed in fp32 in the backward (the
+    formula of WF/models/subln.py:42-59, x * rsqrt(mean(x^2) + eps) * weight)."""
+
+    @staticmethod
+    def forward(ctx, x2, gamma, weight, bias, mod, eps):
+        lin = mod.linear
+        q, a_scale = rmsnorm_quantize_i8(x2, gamma, eps=eps, k_pad=lin.k_pad)
+        y = bitnet_linear(lin.qweight, q, lin.weight_scale, a_scale=a_scale, bias=bias, out_dtype=_out_dtype(x2))
+        ctx.save_for_backward(x2, gamma, q, a_scale, lin.qweight, lin.weight_scale)
+        ctx.meta = (weight.dtype, None if bias is None else bias.dtype, lin.in_features, eps)
+        return y if y.dtype == x2.dtype else y.to(x2.dtype)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x2, gamma, q, a_scale, qweight, wscale = ctx.saved_tensors
+        wdt, bdt, kin, eps = ctx.meta
+        g = gy.to(torch.float32).contiguous()
+        gx = gg = gw = gb = None
+        if ctx.needs_input_grad[2]:
+            x_deq = q[:, :kin].to(torch.float32) * a_scale[:, None]
+            gw = (g.t().contiguous() @ x_deq).to(wdt)
+        if bdt is not None and ctx.needs_input_grad[3]:
+            gb = g.sum(0).to(bdt)
+        if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
+            w_deq = unpack_i2s(qweight)[:, :kin].to(torch.float32) * wscale
+            g_norm = g @ w_deq  # gradient at the norm's output (identity through the quantiser)
+            with torch.enable_grad():
+                xr = x2.detach().to(torch.float32).requires_grad_(ctx.needs_input_grad[0])
+                gr = gamma.detach().to(torch.float32).requires_grad_(ctx.needs_input_grad[1])
+                yn = xr * torch.rsqrt(xr.pow(2).mean(dim=-1, keepdim=True) + eps) * gr
+                wrt = [t for t in (xr, gr) if t.requires_grad]
+                grads = list(torch.autograd.grad(yn, wrt, g_norm))
+            if ctx.needs_input_grad[0]:
+                gx = grads.pop(0).to(x2.dtype)
+            if ctx.needs_input_grad[1]:
+                gg = grads.pop(0).to(gamma.dtype)
+        return gx, gg, gw, gb, None, None
+
+
 class BitLinear(nn.Linear):
     """Ternary-weight, int8-activation linear layer executed by libwfbitnet.
 
     ``in_features`` need not be a multiple of 128: K is zero-padded to ``k_pad`` inside the packed
     weight and the quantised activations (padded weights are 0, padded activations are 0, so the
-    accumulators are those of the unpadded product).  Call :meth:`pack` after changing ``weight``;
-    the first forward packs automatically.
+    accumulators are those of the unpadded product).  The packed weight is rebuilt whenever ``weight``
+    has changed since the last pack (its version counter or storage), so it never goes stale; under
+    autograd the forward is the reference's straight-through estimator (:class:`_BitLinearSTE`).
     """
 
     def __init__(self, in_features: int, out_features: int, bias: bool = False, eps: float = 1e-5,
@@ -53,12 +155,25 @@ class BitLinear(nn.Linear):
         super().__init__(in_features, out_features, bias=bias, device=device, dtype=dtype)
         self.eps = eps  # kept for signature parity; the int8 quantiser uses the kernel rule max < 1e-6 -> 1
         self.k_pad = _pad_k(in_features)
-        self.register_buffer("qweight", None, persistent=True)
-        self.register_buffer("weight_scale", None, persistent=True)
+        # derived from weight and rebuilt when it changes, so not part of the state dict: checkpoints hold
+        # weight (and bias) only, like the reference module's (modules from packed weights keep them)
+        self.register_buffer("qweight", None, persistent=False)
+        self.register_buffer("weight_scale", None, persistent=False)
 
     @torch.no_grad()
     def pack(self) -> "BitLinear":
         self.qweight, self.weight_scale = pack_ternary_i2s(self.weight.detach().contiguous(), k_pad=self.k_pad)
+        self._packed_from = self._weight_stamp()
+        return self
+
+    def _weight_stamp(self):
+        w = self.weight
+        return None if w is None else (w._version, w.data_ptr(), w.device)
+
+    def ensure_packed(self) -> "BitLinear":
+        """Pack if there is no packed weight yet or ``weight`` changed since the last pack."""
+        if self.weight is not None and (self.qweight is None or getattr(self, "_packed_from", None) != self._weight_stamp()):
+            self.pack()
         return self
 
     @classmethod
@@ -81,19 +196,25 @@ class BitLinear(nn.Linear):
 
     def forward_quantized(self, q: torch.Tensor, a_scale: torch.Tensor, out_dtype=torch.bfloat16,
                           return_acc: bool = False):
-        """Linear on already-quantised activations q [M, k_pad] with per-token scales a_scale [M]."""
-        if self.qweight is None:
-            self.pack()
+        """Linear on already-quantised activations q [M, k_pad] with per-token scales a_scale [M]
+        (inference only: no gradient flows to the weight)."""
+        self.ensure_packed()
         return bitnet_linear(self.qweight, q, self.weight_scale, a_scale=a_scale, bias=self.bias,
                              out_dtype=out_dtype, return_acc=return_acc)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.qweight is None:
-            self.pack()
+        _check_lambda("BitLinear")
+        self.ensure_packed()
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.in_features)
         if not x2.is_contiguous():
             x2 = x2.contiguous()
+        w, b = self.weight, self.bias
+        if torch.is_grad_enabled() and (x2.requires_grad or (w is not None and w.requires_grad)
+                                        or (b is not None and b.requires_grad)):
+            if w is None:
+                raise RuntimeError("BitLinear: a module built from packed weights has no float weight to train")
+            return _BitLinearSTE.apply(x2, w, b, self).view(*lead, self.out_features)
         q, a_scale = quantize_activations_i8_per_token(x2, k_pad=self.k_pad)
         y = bitnet_linear(self.qweight, q, self.weight_scale, a_scale=a_scale, bias=self.bias,
                           out_dtype=_out_dtype(x))
@@ -152,13 +273,20 @@ class SubLNBitLinear(nn.Module):
         self.linear = BitLinear(in_features, out_features, bias=bias, device=device, dtype=dtype)
 
     def forward(self, x: torch.Tensor, return_acc: bool = False):
+        """``return_acc`` (the int32 accumulators, a parity aid) gives a result without autograd."""
         lin = self.linear
-        if lin.qweight is None:
-            lin.pack()
+        _check_lambda("SubLNBitLinear")
+        lin.ensure_packed()
         lead = x.shape[:-1]
         x2 = x.reshape(-1, lin.in_features)
         if not x2.is_contiguous():
             x2 = x2.contiguous()
+        if not return_acc and torch.is_grad_enabled() and any(
+                t is not None and t.requires_grad for t in (x2, self.norm_weight, lin.weight, lin.bias)):
+            if lin.weight is None:
+                raise RuntimeError("SubLNBitLinear: a module built from packed weights has no float weight to train")
+            y = _SubLNBitLinearSTE.apply(x2, self.norm_weight, lin.weight, lin.bias, self, self.norm_eps)
+            return y.view(*lead, lin.out_features)
         q, a_scale = rmsnorm_quantize_i8(x2, self.norm_weight, eps=self.norm_eps, k_pad=lin.k_pad)
         res = bitnet_linear(lin.qweight, q, lin.weight_scale, a_scale=a_scale, bias=lin.bias,
                             out_dtype=_out_dtype(x), return_acc=return_acc)
