@@ -195,3 +195,80 @@ def test_host_copy_runs_the_same_model(pkg, dev):
     assert float((lg - lh).abs().max()) <= 2e-2 * float(lg.abs().max())
     toks = host.generate(prompt, 5)
     assert toks.shape == (2, 5) and toks.device.type == "cpu"
+
+
+def _ref_golden():
+    from pathlib import Path
+
+    return np.load(Path(__file__).resolve().parent / "golden" / "ref_e2e_smollm2.npz", allow_pickle=False)
+
+
+def _model_from_ref_state(pkg, dev, g):
+    M = pkg.model
+    cfg = M.SMOLLM2_135M
+    return M.BitNetDecoder.from_float_state(M.random_float_state(cfg, int(g["seed"][0])), cfg, device=dev,
+                                            backend=M.HipBackend(out_dtype=torch.float32, fused=True))
+
+
+def test_layers_match_reference_stage1_model(pkg, dev):
+    """configs[0] against the reference's OWN model, layer by layer: tests/golden/ref_e2e_smollm2.npz holds
+    the residual stream entering and leaving layers 0, 1, 10, 15, 20, 29 of transformers' LlamaForCausalLM
+    converted by the reference's convert_model_to_bitnet (stage1.py:169-214; reference BitLinear and SubLN
+    forwards, fp32, eager attention) on the 32-token prompt, written in the build container by
+    tests/golden/make_e2e_golden.py from the float weights random_float_state(seed).  The HIP model built
+    from the same floats (absmean-ternarised and packed on the device) maps each layer's input to its
+    output within 1e-2 normwise, and at least half the layers within 1e-6: the two float paths round
+    differently (dequantised fp32 F.linear there, exact integer accumulators here), which moves an int8
+    activation code across a rounding boundary only now and then (layers 0, 10 and 29 flip a few).  A wrong RoPE theta (1e4) or SubLN eps
+    (1e-5) gives 4.5e-3 / 9e-4 on layer 15 where this path gives about 1e-7 (measured on the CPU with the
+    oracle backend and the same float code)."""
+    g = _ref_golden()
+    model = _model_from_ref_state(pkg, dev, g)
+    errs = []
+    with torch.no_grad():
+        for li in g["layers"].tolist():
+            x_in = torch.from_numpy(g[f"layer{li}_in"])[None]
+            want = torch.from_numpy(g[f"layer{li}_out"]).double()
+            model.reset(1, x_in.shape[1])
+            got = model.forward_layers(x_in, 0, li, li + 1)[0].cpu().double()
+            errs.append(float((got - want).norm() / want.norm()))
+    print("per-layer normwise differences:", dict(zip(g["layers"].tolist(), [f"{e:.1e}" for e in errs])), flush=True)
+    assert max(errs) <= 1e-2, errs
+    assert sorted(errs)[len(errs) // 2 - 1] <= 1e-6, errs  # half the layers flip no code: fp32 rounding only
+
+
+def test_logits_match_reference_stage1_model_within_its_own_noise(pkg, dev):
+    """configs[0] end to end against the reference's OWN model (see the test above): prompt logits and
+    teacher-forced logits (at the reference's top-5 ids of each of its 128 greedy steps, fed its tokens)
+    differ from the reference's by no more than twice what the reference moves by itself when its input
+    embeddings get rounding-level noise (x (1 + 1e-7 N(0,1)), recorded in the fixture: 0.14 / 0.11 on
+    logits of range 2.0).  Code flips at rounding boundaries compound over 30 layers, so identical free-
+    running tokens are not a property of this random-init model: under that noise the reference's own
+    first greedy token already changes.  Where the reference's top-2 gap at a step exceeds twice its own
+    noise, the greedy pick must be the reference's."""
+    g = _ref_golden()
+    model = _model_from_ref_state(pkg, dev, g)
+    prompt = torch.from_numpy(g["prompt"])[None]
+    ref_toks = g["tokens"]
+    noise_prefill = float(np.abs(g["perturbed_prefill_logits"] - g["prefill_logits"]).max())
+    noise_tf = float(np.abs(g["perturbed_top5_logits"] - g["top5_logits"]).max())
+    with torch.no_grad():
+        model.reset(1, prompt.shape[1] + len(ref_toks))
+        logits = model.forward(prompt.to(dev), 0)
+        d_prefill = float(np.abs(logits[0].cpu().numpy() - g["prefill_logits"]).max())
+        pos = torch.full((1,), prompt.shape[1], dtype=torch.long, device=dev)
+        worst, robust = 0.0, 0
+        for t in range(len(ref_toks)):
+            row = logits[0].cpu().numpy()
+            worst = max(worst, float(np.abs(row[g["top5_ids"][t]] - g["top5_logits"][t]).max()))
+            gap = float(g["top5_logits"][t, 0] - g["top5_logits"][t, 1])
+            if gap > 2 * noise_tf:
+                robust += 1
+                assert int(row.argmax()) == int(ref_toks[t]), f"step {t}: greedy pick differs where the gap is {gap:.3f}"
+            if t + 1 < len(ref_toks):
+                logits = model.decode_step(torch.tensor([[int(ref_toks[t])]], device=dev), pos)
+                pos += 1
+    print(f"prompt logits: {d_prefill:.3e} (reference self-noise {noise_prefill:.3e}); teacher-forced top-5: "
+          f"{worst:.3e} (self-noise {noise_tf:.3e}); {robust} robust steps", flush=True)
+    assert d_prefill <= 2 * noise_prefill
+    assert worst <= 2 * noise_tf

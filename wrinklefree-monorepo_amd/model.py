@@ -313,6 +313,54 @@ class BitNetDecoder:
         write_sglbitnt(path, config, t)
 
     @classmethod
+    def from_float_state(cls, state: Dict[str, torch.Tensor], cfg: BitNetConfig, device="cuda",
+                         dtype: torch.dtype = torch.float32, backend=None, decode_attention: str = "hip",
+                         prefill_attention: str = "hip") -> "BitNetDecoder":
+        """Build the model from float weights under HuggingFace Llama names (``model.embed_tokens.weight``,
+        ``model.layers.{i}.self_attn.q_proj.weight`` ... ``model.norm.weight``, optional ``lm_head.weight``),
+        the names of the stage-1 source model (stage1.py:169-214).  Every projection is absmean-ternarised
+        and packed on the device.  SubLN weights are read from the converted model's names
+        (``self_attn.o_proj.0.weight``, ``mlp.down_proj.0.weight``) when present, else ones, as stage 1
+        creates them.  A ternary LM head (``cfg.ternary_lm_head``) is packed from ``lm_head.weight``; a
+        dense untied head keeps it as floats; a tied head uses the embedding."""
+        m = cls.__new__(cls)
+        m._setup(cfg, device, dtype, backend, decode_attention, prefill_attention)
+        dev = m.device
+
+        def get(name, shape=None, ones=False):
+            t = state.get(name)
+            if t is None:
+                if not ones:
+                    raise KeyError(f"from_float_state: missing {name}")
+                return torch.ones(shape, device=dev, dtype=dtype)
+            if shape is not None and tuple(t.shape) != tuple(shape):
+                raise ValueError(f"from_float_state: {name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+            return t
+
+        h, f = cfg.hidden_size, cfg.intermediate_size
+        qd, kvd = cfg.num_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+        shapes = {"q": (qd, h), "k": (kvd, h), "v": (kvd, h), "o": (h, qd), "gate": (f, h), "up": (f, h),
+                  "down": (h, f)}
+        m.embed = get("model.embed_tokens.weight", (cfg.vocab_size, h)).to(dev, dtype)
+        m.layers = []
+        for i in range(cfg.num_layers):
+            L = _Layer.__new__(_Layer)
+            pre = f"model.layers.{i}."
+            for attr, name in cls._LINEARS:
+                w = get(pre + name + ".weight", shapes[attr]).to(dev, torch.float32)
+                setattr(L, attr, PackedLinear(w))
+            L.input_norm = get(pre + "input_layernorm.weight", (h,)).to(dev, dtype)
+            L.post_attn_norm = get(pre + "post_attention_layernorm.weight", (h,)).to(dev, dtype)
+            L.attn_sub_norm = get(pre + "self_attn.o_proj.0.weight", (qd,), ones=True).to(dev, dtype)
+            L.ffn_sub_norm = get(pre + "mlp.down_proj.0.weight", (f,), ones=True).to(dev, dtype)
+            m.layers.append(L)
+        m.final_norm = get("model.norm.weight", (h,)).to(dev, dtype)
+        head = None if cfg.tie_embeddings else get("lm_head.weight", (cfg.vocab_size, h))
+        m.lm_head = PackedLinear(head.to(dev, torch.float32)) if cfg.ternary_lm_head else None
+        m.head_weight = m.embed if head is None or cfg.ternary_lm_head else head.to(dev, dtype)
+        return m
+
+    @classmethod
     def from_sglbitnt(cls, path, device="cuda", dtype: torch.dtype = torch.float32, backend=None,
                       decode_attention: str = "hip", prefill_attention: str = "hip") -> "BitNetDecoder":
         """Build the model from an SGLBITNT file (memory-mapped; tensors go to ``device`` one at a time).
@@ -458,10 +506,11 @@ class BitNetDecoder:
         freqs = self._key_pos.to(torch.float32)[:, None] * self.inv_freq[None, :]
         self._rope_cos, self._rope_sin = freqs.cos().contiguous(), freqs.sin().contiguous()
 
-    def _layers(self, x: torch.Tensor, attend) -> torch.Tensor:
+    def _layers(self, x: torch.Tensor, attend, first: int = 0, last: Optional[int] = None) -> torch.Tensor:
         cfg, be = self.cfg, self.backend
         b, t = x.shape[0], x.shape[1]
-        for li, L in enumerate(self.layers):
+        for li in range(first, len(self.layers) if last is None else last):
+            L = self.layers[li]
             h2 = x.reshape(b * t, cfg.hidden_size)
             q, k, v = be.norm_linears(h2, L.input_norm, cfg.rms_eps, [L.q, L.k, L.v])
             attn = attend(li, q.to(self.dtype), k.to(self.dtype), v.to(self.dtype)).reshape(b * t, -1)
@@ -523,10 +572,7 @@ class BitNetDecoder:
         m.kv, m._lm_t = [], None
         return m
 
-    def forward(self, ids: torch.Tensor, start: int, tokens: bool = False) -> torch.Tensor:
-        """ids [B, T] at positions start..start+T-1; returns fp32 logits of the last position [B, vocab], or
-        with ``tokens`` the greedy next ids [B]."""
-        b, t = ids.shape
+    def _prefill_attend(self, b: int, t: int, start: int):
         cfg = self.cfg
         pos = torch.arange(start, start + t, device=self.device)
 
@@ -539,8 +585,21 @@ class BitNetDecoder:
             k = self._rope(k.reshape(b, t, cfg.num_kv_heads, cfg.head_dim), pos)
             return self._attention(li, q, k, v.reshape(b, t, cfg.num_kv_heads, cfg.head_dim), start)
 
-        x = self._layers(self.embed[ids], attend)
+        return attend
+
+    def forward(self, ids: torch.Tensor, start: int, tokens: bool = False) -> torch.Tensor:
+        """ids [B, T] at positions start..start+T-1; returns fp32 logits of the last position [B, vocab], or
+        with ``tokens`` the greedy next ids [B]."""
+        b, t = ids.shape
+        x = self._layers(self.embed[ids], self._prefill_attend(b, t, start))
         return self._next_tokens(x[:, -1, :]) if tokens else self._logits(x[:, -1, :])
+
+    def forward_layers(self, hidden: torch.Tensor, start: int, first: int = 0, last: Optional[int] = None
+                       ) -> torch.Tensor:
+        """Hidden states [B, T, H] at positions start..start+T-1 through layers first..last-1 (the residual
+        stream a HuggingFace decoder layer takes and returns), appending to those layers' KV caches."""
+        b, t = hidden.shape[0], hidden.shape[1]
+        return self._layers(hidden.to(self.device, self.dtype), self._prefill_attend(b, t, start), first, last)
 
     def _hip_prefill(self) -> bool:
         cfg = self.cfg
@@ -593,6 +652,33 @@ class BitNetDecoder:
         for _ in range(steps - 1):
             g.replay()
         return out
+
+
+def random_float_state(cfg: BitNetConfig, seed: int) -> Dict[str, torch.Tensor]:
+    """Float32 CPU weights of a random-init model under HuggingFace Llama names: normal(0, 0.02) for the
+    embedding and every projection (and an untied LM head), ones for the RMSNorms (BitNetLlama._init_weights,
+    packages/training/src/wrinklefree/models/llama.py:58-65), drawn from torch.Generator(seed) in a fixed
+    order -- the same tensors on any host, for :meth:`BitNetDecoder.from_float_state` and for a
+    HuggingFace model built from the same state."""
+    gen = torch.Generator().manual_seed(seed)
+    h, f = cfg.hidden_size, cfg.intermediate_size
+    qd, kvd = cfg.num_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+
+    def normal(*shape):
+        return torch.randn(shape, generator=gen, dtype=torch.float32) * 0.02
+
+    st = {"model.embed_tokens.weight": normal(cfg.vocab_size, h)}
+    shapes = {"q": (qd, h), "k": (kvd, h), "v": (kvd, h), "o": (h, qd), "gate": (f, h), "up": (f, h), "down": (h, f)}
+    for i in range(cfg.num_layers):
+        pre = f"model.layers.{i}."
+        for attr, name in BitNetDecoder._LINEARS:
+            st[pre + name + ".weight"] = normal(*shapes[attr])
+        st[pre + "input_layernorm.weight"] = torch.ones(h)
+        st[pre + "post_attention_layernorm.weight"] = torch.ones(h)
+    st["model.norm.weight"] = torch.ones(h)
+    if not cfg.tie_embeddings:
+        st["lm_head.weight"] = normal(cfg.vocab_size, h)
+    return st
 
 
 def quantised_linears(model: BitNetDecoder) -> Dict[str, PackedLinear]:
