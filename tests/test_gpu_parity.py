@@ -175,6 +175,29 @@ def test_batched_sweep_mfma(pkg, dev, n, k, m):
         _check_linear(pkg, dev, packed, a, 1.0, np.ones(m, np.float32), kernel="auto", check_fp32=False)
 
 
+@pytest.mark.parametrize("m", [3, 4, 5, 8, 9, 12, 16])
+@pytest.mark.parametrize("n,k", SHAPES_2B)
+def test_batched_decode_outputs_without_accumulator_copy(pkg, dev, m, n, k):
+    """M <= 16 without an accumulator copy takes the LDS-staged kernel's whole-line epilogue: bf16 and fp32
+    outputs, a bias, and a residual in either dtype, all equal to the oracle's rescale bit for bit."""
+    rng = np.random.default_rng(7000 + m + n + k)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    ws, a_s = orc.log_uniform(rng), orc.log_uniform(rng, m)
+    acc = _ref_acc(packed, a)
+    pw, pa, ps = _t(packed, dev), _t(a, dev), _t(a_s, dev)
+    y = pkg.bitnet_linear(pw, pa, float(ws), a_scale=ps)
+    assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), orc.f32_to_bf16_bits(orc.rescale(acc, ws, a_s)))
+    bias = rng.standard_normal(n).astype(np.float32)
+    y32 = pkg.bitnet_linear(pw, pa, float(ws), a_scale=ps, bias=_t(bias, dev), out_dtype=torch.float32)
+    assert np.array_equal(y32.cpu().numpy(), orc.rescale(acc, ws, a_s, bias))
+    for rdt in (torch.float32, torch.bfloat16):
+        res = torch.from_numpy(rng.standard_normal((m, n)).astype(np.float32)).to(rdt)
+        want = torch.from_numpy(orc.rescale(acc, np.float32(ws), a_s) + res.float().numpy()).to(rdt)
+        got = pkg.bitnet_linear_residual(pw, pa, float(ws), res.to(dev), a_scale=ps)
+        assert torch.equal(got.cpu(), want)
+
+
 @pytest.mark.parametrize("m,n,k", [(12, 32800, 128), (24, 16400, 256), (64, 8200, 384), (9, 40, 8192),
                                    (24, 9216, 2560), (24, 9200, 2560), (40, 6144, 8192), (40, 6144, 8320),
                                    (40, 12000, 8320), (17, 18432, 256)])

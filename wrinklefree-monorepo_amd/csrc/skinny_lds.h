@@ -1,0 +1,334 @@
+// Batched-decode linear for M <= 16 tokens with both operands staged in LDS (included by the three
+// skinny_mr*.hip files, one per staged token-row count, so they compile in parallel).
+//
+// Replaces, like the other I2_S GEMM paths, bitnet_gemm_i2_i8 / bitnet_gemm_cpu
+// (SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:814-874, SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:370-406).
+//
+// v_mfma_i32_16x16x64_i8, one 16-token tile.  A workgroup owns NT tiles of 16 weight rows and all of K;
+// its S waves split K into step pairs of 512 weights (128 packed bytes per row), wave w taking pairs
+// w, w + S, ... (TP of them).  Measured on MI355X, what sets the time of this kernel is how its loads
+// cover cache lines, so both operands are brought in whole lines by 16-byte LDS-DMA loads
+// (buffer_load ... lds: lane l's 16 bytes land at LDS base + 16 l):
+//  * weights: one instruction = 8 rows x 128 bytes (lanes 8r .. 8r+7 read row r's pair); the 16-row tile
+//    of a pair takes two.  In LDS, 16-byte slot s of row r holds global chunk s ^ f(r),
+//    f(r) = (r & 7) ^ (r >> 3), so the MFMA-layout reads of 16 rows fall on 16 distinct bank groups.
+//    (Loading the MFMA layout directly -- 16 rows x 64 bytes per instruction, the other half line from
+//    another wave -- measured 0.6 us slower for 8.8 MB of weights.)
+//  * activations: per 256-weight step, MR token rows x 256 bytes, 4 rows per instruction; slot q of
+//    token row t holds chunk q ^ (t & 15).
+// MFMA operands: lane (nl, g) reads weight row nl, chunk 4 step + g (16 bytes = 64 weights; field f
+// covers k = 128 (c / 2) + 32 f + 16 (c % 2) + 0..15 of chunk c) and the 16 activation bytes of token nl
+// at the same k.  Fields enter masked but unshifted -- bits 1:0 (x1), 3:2 (x4), 5:4 and 7:6 >> 2 (x16) --
+// into three accumulators; the code offset is removed with each token's sum(a).  Partial tiles of the S
+// waves meet in LDS.
+// Epilogues: plain outputs go through LDS (y = (acc * ws) * as + bias in fp32 per element, then each
+// thread takes 4 consecutive outputs of a token row, adds the residual and stores them: whole-line
+// stores, 0.3-0.5 us faster than per-lane ones at M = 8-16); accumulator copies, the greedy-argmax
+// keys and the gated gate|up product are written from the MFMA layout.
+// Gated mode (GLUE = 1 SiLU, 2 relu^2): W is gate|up (N = 2 * half); tiles 0 .. NT/2 - 1 are gate rows
+// n0 + 16 j, the others the up rows half + n0 + 16 j; x = act(gate) * up is stored fp32 at [tok, n],
+// both products rounded to ep.mid_dtype first (what a plain linear would store).
+#pragma once
+
+#include "wfb_common.h"
+
+namespace wfb {
+namespace skinny_lds {
+
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void dma16(buf_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, 0, 0, 0);
+}
+
+constexpr size_t lds_bytes(int S, int NT, int TP, int MR) {
+  return (size_t)S * TP * (NT * 2048 + 2 * MR * 256) + (size_t)S * NT * 1024;
+}
+
+template <int S, int NT, int TP, int MR, int GLUE, bool STAGED>
+__global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, const int8_t* __restrict__ A,
+                                                 int64_t lda, int M, int N, int C, Epilogue ep) {
+  static_assert((GLUE ? NT / 2 : NT) <= S, "one wave per output row tile in the epilogue");
+  static_assert(GLUE == 0 || NT % 2 == 0, "gated mode pairs gate and up tiles");
+  static_assert(MR == 4 || MR == 8 || MR == 16, "staged token rows");
+  __shared__ __attribute__((aligned(16))) int8_t wl[S][TP][NT][2048];
+  __shared__ __attribute__((aligned(16))) int8_t al[S][TP][2][MR * 256];
+  __shared__ int red[S][NT][4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nl = lane & 15, g = lane >> 4;
+  const int half = N / 2;
+  const int n0 = GLUE ? blockIdx.x * 16 * (NT / 2) : blockIdx.x * 16 * NT;
+  const uint32_t row_bytes = (uint32_t)C * 16;
+  const uint32_t w_end = (uint32_t)N * row_bytes, a_end = (uint32_t)((int64_t)(M - 1) * lda + (int64_t)C * 64);
+  const buf_t wb = make_buf(W, w_end);
+  const buf_t ab = make_buf(A, a_end);
+  const int T = (C + 3) >> 2, T2 = (C + 7) >> 3;
+  auto tile_row = [&](int nt) {
+    return !GLUE ? n0 + 16 * nt : nt < NT / 2 ? n0 + 16 * nt : half + n0 + 16 * (nt - NT / 2);
+  };
+
+  // ---- operands into LDS (every load of the wave in flight before the first wait) --------------------
+#pragma unroll
+  for (int u = 0; u < TP; ++u) {
+    const int p = w + S * u;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = lane >> 3;
+        const int chunk = 8 * p + ((lane & 7) ^ (r ^ h));
+        const int row = tile_row(nt) + 8 * h + r;
+        const bool ok = p < T2 && chunk < C;
+        dma16(wb, wl[w][u][nt] + 1024 * h, ok ? (uint32_t)row * row_bytes + 16u * chunk : w_end);
+      }
+  }
+#pragma unroll
+  for (int u = 0; u < TP; ++u) {
+    const int p = w + S * u;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int i = 0; i < MR / 4; ++i) {
+        const int t = 2 * p + st;
+        const int tok = 4 * i + (lane >> 4);
+        const int q = (lane & 15) ^ (tok & 15);
+        const uint32_t kb = 256u * t + 16u * q;
+        const bool ok = p < T2 && t < T && tok < M && kb < (uint32_t)(64 * C);
+        dma16(ab, al[w][u][st] + 1024 * i, ok ? (uint32_t)((int64_t)tok * lda) + kb : a_end);
+      }
+  }
+  // epilogue operands of the column this lane owns in the MFMA layout (row n, tokens 4g + j)
+  int toks[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) toks[j] = 4 * g + j;
+  EpiCol<4> col;
+  if (!GLUE && w < NT) {
+    Epilogue e1 = ep;
+    if (STAGED) e1.res = nullptr;  // the staged path adds the residual with whole-line loads
+    col.load(e1, tile_row(w) + nl, N, toks, M);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS-DMA loads have landed
+
+  // ---- MFMA over the wave's step pairs -----------------------------------------------------------
+  v4i acc1[NT], acc4[NT], acc16[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc1[nt] = acc4[nt] = acc16[nt] = v4i{0, 0, 0, 0};
+  int sa = 0;
+  const int hh = nl >> 3, rr = nl & 7;
+  const int8_t* arow = nullptr;
+#pragma unroll
+  for (int u = 0; u < TP; ++u) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      arow = al[w][u][st] + 256 * (nl < MR ? nl : MR - 1);  // rows >= M hold zeros or unused codes
+      v4i av[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;  // step bytes 128 (g / 2) + 16 (g % 2) + 32 f
+        av[f] = *reinterpret_cast<const v4i*>(arow + 16 * (qg ^ nl));
+      }
+      const int slot = (4 * st + g) ^ (rr ^ hh);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const v4i wv = *reinterpret_cast<const v4i*>(wl[w][u][nt] + 1024 * hh + 128 * rr + 16 * slot);
+        v4i b0, b1, b2, b3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = wv[e];
+          b0[e] = (d >> 2) & 0x30303030;
+          b1[e] = d & 0x30303030;
+          b2[e] = d & 0x0C0C0C0C;
+          b3[e] = d & 0x03030303;
+        }
+        acc16[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[0], b0, acc16[nt], 0, 0, 0);
+        acc16[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[1], b1, acc16[nt], 0, 0, 0);
+        acc4[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[2], b2, acc4[nt], 0, 0, 0);
+        acc1[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[3], b3, acc1[nt], 0, 0, 0);
+      }
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sa = __builtin_amdgcn_sdot4(av[f][e], 0x01010101, sa, false);
+    }
+  }
+  // C layout of a 16x16 tile: lane (nl, g) holds tokens 4g + j of weight row nl.  sum(a) of token nl over
+  // this wave's K range: add the 4 lane groups, then fetch token 4g + j's from lane 4g + j.
+  {
+    int s = sa;
+    s += __shfl_xor(s, 16, 64);
+    s += __shfl_xor(s, 32, 64);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int sj = __shfl(s, 4 * g + j, 64);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) red[w][nt][j][lane] = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj;
+    }
+  }
+  __syncthreads();
+
+  // ---- epilogues -----------------------------------------------------------------------------------
+  if constexpr (GLUE != 0) {
+    if (w >= NT / 2) return;
+    const int n = n0 + 16 * w + nl;  // output column = gate row; its up row is half + n
+    if (n >= half) return;
+    const float wsg = epi_wscale(ep, n), wsu = epi_wscale(ep, half + n);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tok = 4 * g + j;
+      if (tok >= M) continue;
+      int tg = red[0][w][j][lane], tu = red[0][w + NT / 2][j][lane];
+#pragma unroll
+      for (int k = 1; k < S; ++k) {
+        tg += red[k][w][j][lane];
+        tu += red[k][w + NT / 2][j][lane];
+      }
+      const float as = epi_ascale(ep, tok);
+      float yg = __fmul_rn(__fmul_rn((float)tg, wsg), as), yu = __fmul_rn(__fmul_rn((float)tu, wsu), as);
+      if (ep.mid_dtype == WFB_BF16) {
+        yg = bf16_bits_to_f32(f32_to_bf16_rne(yg));
+        yu = bf16_bits_to_f32(f32_to_bf16_rne(yu));
+      }
+      reinterpret_cast<float*>(ep.out)[(int64_t)tok * ep.ldo + n] = glu<GLUE>(yg, yu);
+    }
+    return;
+  } else if constexpr (!STAGED) {
+    if (w >= NT) return;
+    const int nt = w;
+    const int n = n0 + 16 * nt + nl;
+    if (ep.amax) {  // greedy-argmax keys: the maximum over the 16 rows of each token, one slot per 16 rows
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tok = 4 * g + j;
+        int tot = red[0][nt][j][lane];
+#pragma unroll
+        for (int k = 1; k < S; ++k) tot += red[k][nt][j][lane];
+        const bool valid = tok < M && n < N;
+        uint64_t key = epi_store_key_r(ep, col.ws, col.as[j], col.bias, col.res[j], tok, n, tot, valid);
+        key = group_max_u64<16>(key);
+        const int slot = blockIdx.x * NT + nt;
+        if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
+      }
+      return;
+    }
+    if (n >= N) return;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tok = 4 * g + j;
+      int tot = red[0][nt][j][lane];
+#pragma unroll
+      for (int k = 1; k < S; ++k) tot += red[k][nt][j][lane];
+      if (tok < M) epi_store_r(ep, col.ws, col.as[j], col.bias, col.res[j], tok, n, tot);
+    }
+  } else {
+    // y (fp32, before the residual) of the [M tokens x 16 NT rows] tile into LDS -- the weight staging
+    // space, free after the barrier -- rows rotated by 4 per token to spread the banks
+    constexpr int RW = 16 * NT;
+    float* ys = reinterpret_cast<float*>(&wl[0][0][0][0]);
+    static_assert(sizeof(wl) >= 16 * RW * 4, "staging space");
+    if (w < NT) {
+      const int c = 16 * w + nl;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tok = 4 * g + j;
+        int tot = red[0][w][j][lane];
+#pragma unroll
+        for (int k = 1; k < S; ++k) tot += red[k][w][j][lane];
+        ys[tok * RW + ((c + 4 * tok) & (RW - 1))] = epi_y(ep, col.ws, col.as[j], col.bias, tot);
+      }
+    }
+    __syncthreads();
+    const bool out_vec = ep.ldo % 4 == 0 && (uintptr_t)ep.out % (ep.out_dtype == WFB_F32 ? 16 : 8) == 0;
+    const bool res_vec = !ep.res || (ep.ldr % 4 == 0 && (uintptr_t)ep.res % (ep.res_dtype == WFB_F32 ? 16 : 8) == 0);
+    for (int i = threadIdx.x; i < M * (RW / 4); i += 64 * S) {
+      const int tok = i / (RW / 4), q = i % (RW / 4);
+      const int n = n0 + 4 * q;
+      if (n >= N) continue;
+      const bool full = n + 3 < N;
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = ys[tok * RW + ((4 * q + e + 4 * tok) & (RW - 1))];
+      if (ep.res) {
+        float rv[4];
+        const int64_t ro = (int64_t)tok * ep.ldr + n;
+        if (full && res_vec) {
+          if (ep.res_dtype == WFB_F32) {
+            const float4 r4 = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ep.res) + ro);
+            rv[0] = r4.x; rv[1] = r4.y; rv[2] = r4.z; rv[3] = r4.w;
+          } else {
+            const uint2 r2 = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(ep.res) + ro);
+            rv[0] = __uint_as_float(r2.x << 16); rv[1] = __uint_as_float(r2.x & 0xffff0000u);
+            rv[2] = __uint_as_float(r2.y << 16); rv[3] = __uint_as_float(r2.y & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rv[e] = n + e < N ? epi_res(ep, tok, n + e) : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = __fadd_rn(y[e], rv[e]);
+      }
+      const int64_t off = (int64_t)tok * ep.ldo + n;
+      if (ep.out_dtype == WFB_F32) {
+        float* o = reinterpret_cast<float*>(ep.out) + off;
+        if (full && out_vec) *reinterpret_cast<float4*>(o) = make_float4(y[0], y[1], y[2], y[3]);
+        else
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) o[e] = y[e];
+      } else {
+        uint16_t* o = reinterpret_cast<uint16_t*>(ep.out) + off;
+        if (full && out_vec) {
+          const bf16x2_t lo = __builtin_convertvector((f32x2_t){y[0], y[1]}, bf16x2_t);
+          const bf16x2_t hi = __builtin_convertvector((f32x2_t){y[2], y[3]}, bf16x2_t);
+          *reinterpret_cast<uint2*>(o) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) o[e] = f32_to_bf16_rne(y[e]);
+        }
+      }
+    }
+  }
+}
+
+// (S, TP) by the number of 512-weight step pairs T2 = ceil(K / 512): S = T2 waves up to 8 (K = 2560: 5,
+// K = 4096: 8, from sweeps), two pairs per wave up to 16 pairs, then 14 x 2 (K <= 14336, LDS permitting).
+template <int MR, int GLUE>
+hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e, int nt_pref,
+                  hipStream_t s) {
+  const int T2 = (C + 7) / 8;
+  const bool staged = GLUE == 0 && e.out && !e.acc_out && !e.amax;
+#define WFB_SL_GO(S, NT, TP)                                                                                   \
+  do {                                                                                                         \
+    if constexpr (lds_bytes(S, NT, TP, MR) <= 163840 && (GLUE ? NT / 2 : NT) <= S) {                                                       \
+      const dim3 grid(GLUE ? (n / 2 + 8 * NT - 1) / (8 * NT) : (n + 16 * NT - 1) / (16 * NT));                 \
+      if (staged)                                                                                              \
+        hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, true>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, C, e); \
+      else                                                                                                     \
+        hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, false>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, C, e); \
+      return hipGetLastError();                                                                                \
+    }                                                                                                          \
+  } while (0)
+#define WFB_SL_NT(S, TP)                                 \
+  do {                                                   \
+    if constexpr (GLUE != 0) {                           \
+      if (nt_pref >= 4) WFB_SL_GO(S, 4, TP);             \
+      WFB_SL_GO(S, 2, TP);                               \
+    } else {                                             \
+      if (nt_pref >= 4) WFB_SL_GO(S, 4, TP);             \
+      WFB_SL_GO(S, 1, TP);                               \
+    }                                                    \
+    return hipErrorNotSupported;                         \
+  } while (0)
+  if (T2 <= 2) WFB_SL_NT(2, 1);
+  if (T2 <= 4) WFB_SL_NT(4, 1);
+  if (T2 <= 5) WFB_SL_NT(5, 1);
+  if (T2 <= 8) WFB_SL_NT(8, 1);
+  if (T2 <= 14) WFB_SL_NT(7, 2);
+  if (T2 <= 16) WFB_SL_NT(8, 2);
+  if (T2 <= 28) WFB_SL_NT(14, 2);
+#undef WFB_SL_NT
+#undef WFB_SL_GO
+  return hipErrorNotSupported;
+}
+
+}  // namespace skinny_lds
+}  // namespace wfb

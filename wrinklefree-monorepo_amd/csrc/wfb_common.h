@@ -411,6 +411,27 @@ hipError_t launch_argmax_finalize(const uint64_t* parts, int64_t n_parts, int64_
 hipError_t launch_lm_head_argmax(const void* x, int xdt, int64_t ldx, const void* gamma, int gdt, float eps,
                                  const void* w, int wdt, int64_t ldw, int64_t m, int64_t n, int64_t h, float* logits,
                                  int64_t ldo, uint64_t* parts, hipStream_t s);
+// M <= 16 tokens with both operands staged in LDS (skinny_lds.h); act 0 (plain) or a WFB_ACT_* gated
+// gate|up product; returns hipErrorNotSupported when the shape does not fit its LDS (the caller then
+// takes the register-operand kernels).  Needs N*K/4 and (M-1)*lda + K below 2^31.
+hipError_t launch_skinny_lds_mr4(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
+                                 const Epilogue& e, int act, int nt_pref, hipStream_t s);
+hipError_t launch_skinny_lds_mr8(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
+                                 const Epilogue& e, int act, int nt_pref, hipStream_t s);
+hipError_t launch_skinny_lds_mr16(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
+                                  const Epilogue& e, int act, int nt_pref, hipStream_t s);
+inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
+                                    const Epilogue& e, int act, hipStream_t s) {
+  const int C = k / 64;
+  // four 16-row tiles per workgroup on tall outputs, one on short ones (sweeps over the BitNet-2B shapes:
+  // N = 13824 fastest with 4, N = 2560 / 3200 with 1); gated: 2 + 2 tiles when half >= 4096
+  const int nt_pref = act ? (n / 2 >= 4096 ? 4 : 2) : (n >= 8192 ? 4 : 1);
+  if (m < 1) return hipErrorInvalidValue;
+  if (m <= 4) return launch_skinny_lds_mr4(W, n, C, A, m, lda, e, act, nt_pref, s);
+  if (m <= 8) return launch_skinny_lds_mr8(W, n, C, A, m, lda, e, act, nt_pref, s);
+  if (m <= 16) return launch_skinny_lds_mr16(W, n, C, A, m, lda, e, act, nt_pref, s);
+  return hipErrorNotSupported;
+}
 // 3 <= M <= 64 through the split-K skinny kernel (16, 32 or 64 rows per workgroup); needs
 // N*K/4 and (M-1)*lda + K below 2^31
 hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
