@@ -707,10 +707,12 @@ def main():
     if not args.no_sweep:
         print("[bench] batched M sweep (configs[2])", file=sys.stderr, flush=True)
         sweep = []
-        for n, k in ((2560, 2560), (2560, 6912), (13824, 2560)):
+        for n, k in GEMV_SHAPES:
             syn = Synth(torch, dev, 6000 + n + k)
             base = syn.packed(n, k)
-            copies = [base.clone() for _ in range(max(8, int(1.2e9 // (n * k // 4) // 4)))]
+            # cold weights, as the headline GEMV: >= 1.1 GB of distinct copies, so neither the L2 nor the
+            # 256 MB Infinity Cache serves a repeat
+            copies = [base.clone() for _ in range(max(8, int(1.1e9 // (n * k // 4))))]
             for m in (1, 2, 4, 8, 16, 32, 64):
                 a = syn.int8(m, k)
                 a_scale = torch.ones(m, dtype=torch.float32, device=dev)

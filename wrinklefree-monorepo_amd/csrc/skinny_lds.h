@@ -40,9 +40,9 @@ __device__ __forceinline__ void dma16(buf_t r, void* lds, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, 0, 0, 0);
 }
 
-constexpr size_t lds_bytes(int S, int NT, int TP, int MR) {
-  return (size_t)S * TP * (NT * 2048 + 2 * MR * 256) + (size_t)S * NT * 1024;
-}
+// The per-wave partial tiles of the K reduction overwrite the wave's own weight staging, and the staged
+// output tile the activation staging, so the LDS is the two operand stagings only.
+constexpr size_t lds_bytes(int S, int NT, int TP, int MR) { return (size_t)S * TP * (NT * 2048 + 2 * MR * 256); }
 
 template <int S, int NT, int TP, int MR, int GLUE, bool STAGED>
 __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, const int8_t* __restrict__ A,
@@ -52,7 +52,11 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   static_assert(MR == 4 || MR == 8 || MR == 16, "staged token rows");
   __shared__ __attribute__((aligned(16))) int8_t wl[S][TP][NT][2048];
   __shared__ __attribute__((aligned(16))) int8_t al[S][TP][2][MR * 256];
-  __shared__ int red[S][NT][4][64];
+  // partial tile (row tile nt, token slot j, lane) of wave w, in wave w's own weight staging (free once
+  // the wave has read it: its LDS reads and writes execute in order)
+  auto red = [&](int wv, int nt, int j, int l) -> int& {
+    return reinterpret_cast<int*>(&wl[wv][0][0][0])[(nt * 4 + j) * 64 + l];
+  };
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nl = lane & 15, g = lane >> 4;
   const int half = N / 2;
@@ -160,7 +164,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     for (int j = 0; j < 4; ++j) {
       const int sj = __shfl(s, 4 * g + j, 64);
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) red[w][nt][j][lane] = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj;
+      for (int nt = 0; nt < NT; ++nt) red(w, nt, j, lane) = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj;
     }
   }
   __syncthreads();
@@ -175,11 +179,11 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     for (int j = 0; j < 4; ++j) {
       const int tok = 4 * g + j;
       if (tok >= M) continue;
-      int tg = red[0][w][j][lane], tu = red[0][w + NT / 2][j][lane];
+      int tg = red(0, w, j, lane), tu = red(0, w + NT / 2, j, lane);
 #pragma unroll
       for (int k = 1; k < S; ++k) {
-        tg += red[k][w][j][lane];
-        tu += red[k][w + NT / 2][j][lane];
+        tg += red(k, w, j, lane);
+        tu += red(k, w + NT / 2, j, lane);
       }
       const float as = epi_ascale(ep, tok);
       float yg = __fmul_rn(__fmul_rn((float)tg, wsg), as), yu = __fmul_rn(__fmul_rn((float)tu, wsu), as);
@@ -198,9 +202,9 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int tok = 4 * g + j;
-        int tot = red[0][nt][j][lane];
+        int tot = red(0, nt, j, lane);
 #pragma unroll
-        for (int k = 1; k < S; ++k) tot += red[k][nt][j][lane];
+        for (int k = 1; k < S; ++k) tot += red(k, nt, j, lane);
         const bool valid = tok < M && n < N;
         uint64_t key = epi_store_key_r(ep, col.ws, col.as[j], col.bias, col.res[j], tok, n, tot, valid);
         key = group_max_u64<16>(key);
@@ -213,25 +217,25 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int tok = 4 * g + j;
-      int tot = red[0][nt][j][lane];
+      int tot = red(0, nt, j, lane);
 #pragma unroll
-      for (int k = 1; k < S; ++k) tot += red[k][nt][j][lane];
+      for (int k = 1; k < S; ++k) tot += red(k, nt, j, lane);
       if (tok < M) epi_store_r(ep, col.ws, col.as[j], col.bias, col.res[j], tok, n, tot);
     }
   } else {
-    // y (fp32, before the residual) of the [M tokens x 16 NT rows] tile into LDS -- the weight staging
-    // space, free after the barrier -- rows rotated by 4 per token to spread the banks
+    // y (fp32, before the residual) of the [M tokens x 16 NT rows] tile into LDS (the activation staging),
+    // rows rotated by 4 per token to spread the banks
     constexpr int RW = 16 * NT;
-    float* ys = reinterpret_cast<float*>(&wl[0][0][0][0]);
-    static_assert(sizeof(wl) >= 16 * RW * 4, "staging space");
+    float* ys = reinterpret_cast<float*>(&al[0][0][0][0]);  // free after the barrier above
+    static_assert(sizeof(al) >= 16 * RW * 4, "staging space");
     if (w < NT) {
       const int c = 16 * w + nl;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int tok = 4 * g + j;
-        int tot = red[0][w][j][lane];
+        int tot = red(0, w, j, lane);
 #pragma unroll
-        for (int k = 1; k < S; ++k) tot += red[k][w][j][lane];
+        for (int k = 1; k < S; ++k) tot += red(k, w, j, lane);
         ys[tok * RW + ((c + 4 * tok) & (RW - 1))] = epi_y(ep, col.ws, col.as[j], col.bias, tot);
       }
     }
@@ -298,7 +302,7 @@ hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_
   const bool staged = GLUE == 0 && e.out && !e.acc_out && !e.amax;
 #define WFB_SL_GO(S, NT, TP)                                                                                   \
   do {                                                                                                         \
-    if constexpr (lds_bytes(S, NT, TP, MR) <= 163840 && (GLUE ? NT / 2 : NT) <= S) {                                                       \
+    if constexpr (lds_bytes(S, NT, TP, MR) <= 163840 && (GLUE ? NT / 2 : NT) <= S) {                           \
       const dim3 grid(GLUE ? (n / 2 + 8 * NT - 1) / (8 * NT) : (n + 16 * NT - 1) / (16 * NT));                 \
       if (staged)                                                                                              \
         hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, true>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, C, e); \
@@ -309,13 +313,10 @@ hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_
   } while (0)
 #define WFB_SL_NT(S, TP)                                 \
   do {                                                   \
-    if constexpr (GLUE != 0) {                           \
-      if (nt_pref >= 4) WFB_SL_GO(S, 4, TP);             \
-      WFB_SL_GO(S, 2, TP);                               \
-    } else {                                             \
-      if (nt_pref >= 4) WFB_SL_GO(S, 4, TP);             \
-      WFB_SL_GO(S, 1, TP);                               \
-    }                                                    \
+    if (nt_pref >= 8) WFB_SL_GO(S, 8, TP);               \
+    if (nt_pref >= 4) WFB_SL_GO(S, 4, TP);               \
+    if constexpr (GLUE != 0) WFB_SL_GO(S, 2, TP);        \
+    else WFB_SL_GO(S, 1, TP);                            \
     return hipErrorNotSupported;                         \
   } while (0)
   if (T2 <= 2) WFB_SL_NT(2, 1);

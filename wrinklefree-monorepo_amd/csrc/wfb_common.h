@@ -423,9 +423,12 @@ hipError_t launch_skinny_lds_mr16(const uint8_t* W, int n, int C, const int8_t* 
 inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                                     const Epilogue& e, int act, hipStream_t s) {
   const int C = k / 64;
-  // four 16-row tiles per workgroup on tall outputs, one on short ones (sweeps over the BitNet-2B shapes:
-  // N = 13824 fastest with 4, N = 2560 / 3200 with 1); gated: 2 + 2 tiles when half >= 4096
-  const int nt_pref = act ? (n / 2 >= 4096 ? 4 : 2) : (n >= 8192 ? 4 : 1);
+  // 16-row tiles per workgroup, from sweeps on MI355X (rows n counts gate + up rows when gated):
+  //  * n >= 24576 (28672 gate|up, 128256 LM head): 4 for M <= 4, whose staging lets two such
+  //    workgroups share a CU, else 8 (one workgroup per CU either way, so fewer, larger ones);
+  //  * n >= 8192: 4; gated 2 up to M = 8 (13824 gate|up: 432 workgroups, all resident);
+  //  * shorter outputs: 1 (2 when gated, one gate and one up tile).
+  const int nt_pref = n >= 24576 ? (m <= 4 ? 4 : 8) : n >= 8192 ? (act && m <= 8 ? 2 : 4) : act ? 2 : 1;
   if (m < 1) return hipErrorInvalidValue;
   if (m <= 4) return launch_skinny_lds_mr4(W, n, C, A, m, lda, e, act, nt_pref, s);
   if (m <= 8) return launch_skinny_lds_mr8(W, n, C, A, m, lda, e, act, nt_pref, s);
