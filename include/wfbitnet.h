@@ -317,9 +317,8 @@ int wfb_gqa_prefill_attention(const void* q, int64_t ldq, const void* k_new, int
  *                                                         wfb_linear_i2s with a device scale)
  *         (+ residual, exactly as wfb_linear_i2s_residual when residual is not NULL)
  * x [M, H] (x_dtype WFB_F32 or WFB_BF16, row stride ldx elements, rows 16-byte aligned), gamma [H]
- * (WFB_F32 or WFB_BF16, 16-byte aligned) or NULL; 1 <= M <= 16, H % 8 == 0, H <= K <= 4096,
- * M * (K + 16) + H * sizeof(gamma) <= 49152 (codes and gamma live in LDS; larger calls take the
- * two-call path).  seg_rows /
+ * (WFB_F32 or WFB_BF16, 16-byte aligned) or NULL; 1 <= M <= 16, H % 8 == 0, H <= K <= 4096 (larger
+ * calls take the two-call path); N * K / 4 below 2^31.  seg_rows /
  * w_scales_dev as wfb_linear_i2s_segmented (n_seg = 1 with seg_rows NULL: one segment of N rows).
  * out [M, N] WFB_F32 or WFB_BF16 (row stride ldo); residual [M, N] WFB_F32 or WFB_BF16 (row stride ldr)
  * or NULL; out may alias residual.  Every workgroup recomputes the codes of the M rows in the
@@ -331,6 +330,20 @@ int wfb_rmsnorm_linear_i2s(const void* x, int x_dtype, int64_t ldx, const void* 
                            int64_t m, int64_t h, const uint8_t* qweight, int64_t n, int64_t k, int n_seg,
                            const int64_t* seg_rows, const float* w_scales_dev, const void* residual,
                            int residual_dtype, int64_t ldr, void* out, int out_dtype, int64_t ldo, void* stream);
+
+/* The MLP's first half for a decode batch in one launch: RMSNorm + per-token int8 quantisation of x in the
+ * prologue (exactly wfb_rmsnorm_quant_i8's codes and scales), the gate|up projection, and the gated
+ * product in the epilogue (exactly wfb_linear_i2s_glu on those codes):
+ *   out[m, j] = act(y[m, j]) * y[m, half + j],  y = linear_i2s_segmented(qweight, rmsnorm_quant(x, gamma, eps))
+ * x, gamma, M, H, K as wfb_rmsnorm_linear_i2s (M <= 16, H % 8 == 0, H <= K <= 4096); qweight gate|up
+ * (N = 2 * half rows, half % 32 == 0), w_scales_dev[2]; act_kind / mid_dtype / out [M, half] fp32 (row
+ * stride ldo) as wfb_linear_i2s_glu.  Replaces, per decode token, RMSNorm -> activation_quant -> gate and
+ * up BitLinears -> act(gate) * up of bitnet_mlp_fused (SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:289-375,
+ * 189-216). */
+int wfb_rmsnorm_linear_i2s_glu(const void* x, int x_dtype, int64_t ldx, const void* gamma, int gamma_dtype, float eps,
+                               int64_t m, int64_t h, const uint8_t* qweight, int64_t n, int64_t k,
+                               const float* w_scales_dev, int act_kind, int mid_dtype, float* out, int64_t ldo,
+                               void* stream);
 
 /* The gated MLP middle in the gate|up linear's epilogue (decode batches, M <= 64):
  *   out[m, j] = act(y[m, j]) * y[m, half + j],  j < half = N / 2,

@@ -235,12 +235,31 @@ def test_rmsnorm_linear_argument_errors(pkg):
     assert st(g_dt=2) == -1 and "gamma dtype" in pkg._lib.last_error()
     assert st(m=17) == -1 and "M (17)" in pkg._lib.last_error()
     assert st(h=4100, k=4224) == -1 and "H <= K <= 4096" in pkg._lib.last_error()
-    assert st(m=16) == -1 and "exceeds 49152" in pkg._lib.last_error()
     assert st(n_seg=2) == -1 and "seg_rows" in pkg._lib.last_error()
     assert st(n_seg=2, segp=ctypes.cast(seg, vp), n=136) == -1 and "sum to 128" in pkg._lib.last_error()
     assert st(res=vp(16), res_dt=2) == -1 and "residual dtype" in pkg._lib.last_error()
     assert st(out_dt=2) == -1 and "out must be" in pkg._lib.last_error()
     assert st(x=8) == -1 and "16-byte aligned" in pkg._lib.last_error()
+
+
+def test_rmsnorm_linear_glu_argument_errors(pkg):
+    vp = ctypes.c_void_p
+
+    def st(x_dt=1, g_dt=1, m=8, h=4096, n=128, k=4096, act=1, mid=1, ldo=64, x=16, out=16):
+        return pkg._lib.status("wfb_rmsnorm_linear_i2s_glu", vp(x) if x else None, x_dt, h, vp(16), g_dt, 1e-5, m, h,
+                               vp(16), n, k, vp(16), act, mid, vp(out) if out else None, ldo, None)
+
+    assert st(x_dt=2) == -1 and "x dtype" in pkg._lib.last_error()
+    assert st(g_dt=2) == -1 and "gamma dtype" in pkg._lib.last_error()
+    assert st(act=0) == -1 and "bad activation" in pkg._lib.last_error()
+    assert st(mid=2) == -1 and "mid dtype" in pkg._lib.last_error()
+    assert st(m=17) == -1 and "M (17)" in pkg._lib.last_error()
+    assert st(h=4100, k=4224) == -1 and "H <= K <= 4096" in pkg._lib.last_error()
+    assert st(n=96) == -1 and "multiple of 32" in pkg._lib.last_error()
+    assert st(ldo=63) == -1 and "row strides" in pkg._lib.last_error()
+    assert st(out=0) == -1 and "null pointer" in pkg._lib.last_error()
+    assert st(x=8) == -1 and "16-byte aligned" in pkg._lib.last_error()
+    assert st(m=0) == 0
 
 
 def test_linear_glu_argument_errors(pkg):

@@ -1,6 +1,7 @@
-"""wfb_rmsnorm_linear_i2s (RMSNorm + per-token quant in the prologue of the decode BitLinear): outputs
-bit-identical to the two-call path (wfb_rmsnorm_quant_i8, then the segmented / residual linear), which
-the parity tests pin against the oracle; one shape also checked against the oracle directly."""
+"""wfb_rmsnorm_linear_i2s and wfb_rmsnorm_linear_i2s_glu (RMSNorm + per-token quant in the prologue of the
+decode BitLinear, plain / residual / gated gate|up): outputs bit-identical to the two-call path
+(wfb_rmsnorm_quant_i8, then the segmented / residual / gated linear), which the parity tests pin against
+the oracle; one shape of each also checked against the oracle directly."""
 
 import numpy as np
 import pytest
@@ -30,6 +31,10 @@ CASES = [
     (3, 1536, [1000, 24], 1536, torch.bfloat16, None),                     # ragged tile, no gamma
     (16, 2560, [3200], 2560, torch.bfloat16, torch.bfloat16),              # M = 16
     (7, 4000, [136], 4096, torch.float32, torch.float32),                  # H < K, odd M
+    (16, 4096, [4096], 4096, torch.bfloat16, torch.float32),               # M = 16 at K = 4096
+    (16, 576, [576, 192, 192], 640, torch.bfloat16, torch.bfloat16),       # 8 rows per wave (2 waves)
+    (5, 1024, [2048], 1024, torch.float32, None),                          # K = 1024
+    (12, 3072, [128256], 3072, torch.bfloat16, torch.bfloat16),            # tall output, 12 rows
 ]
 
 
@@ -78,4 +83,42 @@ def test_fused_rejects_unsupported_sizes(pkg, dev):
         pkg.rmsnorm_linear(torch.zeros((17, 4096), device=dev), None, packed, sc)
     with pytest.raises(RuntimeError, match="fused path"):
         pkg.rmsnorm_linear(torch.zeros((2, 4100), device=dev), None, torch.zeros((64, 1280), dtype=torch.uint8, device=dev), sc)
-    assert not pkg.rmsnorm_linear_supported(16, 4096, 4096) and pkg.rmsnorm_linear_supported(8, 4096, 4096)
+    assert not pkg.rmsnorm_linear_supported(17, 4096, 4096) and pkg.rmsnorm_linear_supported(16, 4096, 4096)
+
+
+GLU_CASES = [
+    # m, h, half, k, x dtype, gamma dtype, act, mid dtype
+    (8, 4096, 14336, 4096, torch.bfloat16, torch.bfloat16, "silu", torch.bfloat16),   # Llama-3-8B gate|up
+    (4, 4096, 14336, 4096, torch.bfloat16, torch.float32, "silu", torch.bfloat16),
+    (16, 4096, 14336, 4096, torch.float32, torch.float32, "silu", torch.float32),
+    (1, 2560, 6912, 2560, torch.bfloat16, torch.bfloat16, "relu2", torch.bfloat16),   # BitNet-2B gate|up
+    (3, 2560, 6912, 2560, torch.float32, torch.bfloat16, "relu2", torch.float32),
+    (16, 2560, 6912, 2560, torch.bfloat16, None, "relu2", torch.bfloat16),
+    (1, 576, 1536, 640, torch.float32, torch.float32, "silu", torch.float32),         # SmolLM2, K padded
+    (9, 1000, 96, 1024, torch.bfloat16, torch.bfloat16, "silu", torch.bfloat16),      # H < K, ragged tiles
+]
+
+
+@pytest.mark.parametrize("case", GLU_CASES, ids=[f"m{c[0]}_h{c[1]}_half{c[2]}_{c[6]}_{str(c[4])[6:]}" for c in GLU_CASES])
+def test_fused_glu_equals_two_calls(pkg, dev, case):
+    m, h, half, k, xdt, gdt, act, mid = case
+    rng = np.random.default_rng(m * 17 + h + half)
+    packed, x, g, scales = (t.to(dev) if t is not None else None
+                            for t in _inputs(rng, m, h, [half, half], k, xdt, gdt))
+    y = pkg.rmsnorm_linear_glu(x, g, packed, scales, act, eps=1e-6, mid_dtype=mid)
+    q, a_scale = pkg.rmsnorm_quantize_i8(x, g, eps=1e-6, k_pad=k)
+    y_ref = pkg.bitnet_linear_glu(packed, scales, q, act, a_scale=a_scale, mid_dtype=mid)
+    assert torch.equal(y, y_ref)
+
+
+def test_fused_glu_matches_oracle(pkg, dev):
+    rng = np.random.default_rng(5)
+    m, h, half = 5, 2560, 640
+    packed, x, g, scales = _inputs(rng, m, h, [half, half], h, torch.float32, torch.float32)
+    y = pkg.rmsnorm_linear_glu(x.to(dev), g.to(dev), packed.to(dev), scales.to(dev), "relu2", eps=1e-6,
+                               mid_dtype=torch.float32)
+    q_ref, s_ref = orc.rmsnorm_quant(x.numpy(), g.numpy(), 1e-6)
+    acc = orc.accumulate(packed.numpy(), q_ref)
+    yy = orc.rescale_segmented(acc, [half, half], scales.numpy(), s_ref)
+    y_ref = orc.glu(yy[:, :half], yy[:, half:], orc.ACT_RELU2)
+    assert np.array_equal(y.cpu().numpy(), y_ref)

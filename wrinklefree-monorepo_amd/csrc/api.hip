@@ -452,11 +452,6 @@ int wfb_rmsnorm_linear_i2s(const void* x, int x_dtype, int64_t ldx, const void* 
   if (h <= 0 || h % 8 != 0 || h > k || k % WFB_QK_I2S != 0 || k > 4096)
     return fail(WFB_EINVAL, "%s: need H %% 8 == 0, H <= K <= 4096, K %% %d == 0 (got H=%lld K=%lld)", name, WFB_QK_I2S,
                 (long long)h, (long long)k);
-  const int64_t lds = m * (k + 16) + (gamma ? h * (gamma_dtype == WFB_F32 ? 4 : 2) : 0);
-  if (lds > 49152)
-    return fail(WFB_EINVAL,
-                "%s: M * (K + 16) + H * sizeof(gamma) = %lld exceeds 49152 (use wfb_rmsnorm_quant_i8 + wfb_linear_i2s)",
-                name, (long long)lds);
   if (n <= 0 || n > INT32_MAX / 2 || n * (k / 4) > INT32_MAX)
     return fail(WFB_EINVAL, "%s: bad N (%lld) for K %lld", name, (long long)n, (long long)k);
   if (ldx < h || ldo < n || (residual && ldr < n)) return fail(WFB_EINVAL, "%s: row strides too small", name);
@@ -494,8 +489,45 @@ int wfb_rmsnorm_linear_i2s(const void* x, int x_dtype, int64_t ldx, const void* 
   e.res = residual;
   e.res_dtype = residual_dtype;
   e.ldr = ldr;
-  return hip_status(wfb::launch_norm_linear(x, x_dtype, ldx, gamma, gamma_dtype, eps, (int)h, qweight, (int)m, (int)n,
-                                            (int)k, e, as_stream(stream)),
+  const wfb::NormSrc ns{x, x_dtype, ldx, gamma, gamma_dtype, eps, (int)h};
+  return hip_status(wfb::launch_skinny_lds(qweight, (int)n, (int)k, nullptr, (int)m, 0, e, 0, as_stream(stream), ns),
+                    name);
+}
+
+int wfb_rmsnorm_linear_i2s_glu(const void* x, int x_dtype, int64_t ldx, const void* gamma, int gamma_dtype, float eps,
+                               int64_t m, int64_t h, const uint8_t* qweight, int64_t n, int64_t k,
+                               const float* w_scales_dev, int act_kind, int mid_dtype, float* out, int64_t ldo,
+                               void* stream) {
+  const char* name = "wfb_rmsnorm_linear_i2s_glu";
+  if (x_dtype != WFB_F32 && x_dtype != WFB_BF16) return fail(WFB_EINVAL, "%s: x dtype must be WFB_F32 or WFB_BF16", name);
+  if (gamma && gamma_dtype != WFB_F32 && gamma_dtype != WFB_BF16)
+    return fail(WFB_EINVAL, "%s: gamma dtype must be WFB_F32 or WFB_BF16", name);
+  if (act_kind != WFB_ACT_SILU && act_kind != WFB_ACT_RELU2) return fail(WFB_EINVAL, "%s: bad activation %d", name, act_kind);
+  if (mid_dtype != WFB_F32 && mid_dtype != WFB_BF16)
+    return fail(WFB_EINVAL, "%s: mid dtype must be WFB_F32 or WFB_BF16", name);
+  if (m < 0 || m > 16) return fail(WFB_EINVAL, "%s: M (%lld) must be in 0..16", name, (long long)m);
+  if (h <= 0 || h % 8 != 0 || h > k || k % WFB_QK_I2S != 0 || k > 4096)
+    return fail(WFB_EINVAL, "%s: need H %% 8 == 0, H <= K <= 4096, K %% %d == 0 (got H=%lld K=%lld)", name, WFB_QK_I2S,
+                (long long)h, (long long)k);
+  if (n <= 0 || n % 64 != 0 || n * (k / 4) > INT32_MAX)
+    return fail(WFB_EINVAL, "%s: N (%lld) must be 2 x a multiple of 32 with N*K/4 below 2^31", name, (long long)n);
+  if (ldx < h || ldo < n / 2) return fail(WFB_EINVAL, "%s: row strides too small", name);
+  if (!(eps >= 0.0f)) return fail(WFB_EINVAL, "%s: eps must be >= 0", name);
+  if (m == 0) return ok();
+  if (!x || !qweight || !w_scales_dev || !out) return fail(WFB_EINVAL, "%s: null pointer", name);
+  const int esz = x_dtype == WFB_F32 ? 4 : 2;
+  if (!aligned(x, 16) || (ldx * esz) % 16 != 0 || (gamma && !aligned(gamma, 16)) || !aligned(qweight, 16))
+    return fail(WFB_EINVAL, "%s: x rows, gamma and qweight must be 16-byte aligned", name);
+  wfb::Epilogue e{};
+  e.nseg = 2;
+  e.seg_end[0] = (int)(n / 2);
+  e.ws_dev = w_scales_dev;
+  e.out = out;
+  e.out_dtype = WFB_F32;
+  e.ldo = ldo;
+  e.mid_dtype = mid_dtype;
+  const wfb::NormSrc ns{x, x_dtype, ldx, gamma, gamma_dtype, eps, (int)h};
+  return hip_status(wfb::launch_skinny_lds(qweight, (int)n, (int)k, nullptr, (int)m, 0, e, act_kind, as_stream(stream), ns),
                     name);
 }
 

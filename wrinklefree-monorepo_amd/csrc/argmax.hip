@@ -27,14 +27,23 @@ __device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
   return load_elem<WFB_F16>(p, i);
 }
 
-__global__ __launch_bounds__(256) void argmax_finalize_kernel(const uint64_t* __restrict__ parts, int64_t np, int m,
-                                                              int64_t* __restrict__ tokens) {
-  __shared__ uint64_t sb[4];
+// One workgroup per token; each thread keeps kFinLoads independent slot loads in flight per round (a
+// 128256-row head has 8016 slots: one round), then a wave and a workgroup maximum.
+constexpr int kFinThreads = 1024, kFinLoads = 8;
+__global__ __launch_bounds__(kFinThreads) void argmax_finalize_kernel(const uint64_t* __restrict__ parts, int64_t np,
+                                                                      int m, int64_t* __restrict__ tokens) {
+  __shared__ uint64_t sb[kFinThreads / 64];
   const int mm = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
   uint64_t best = 0;
-  for (int64_t p = t; p < np; p += 256) {
-    const uint64_t v = parts[p * m + mm];
-    best = v > best ? v : best;
+  for (int64_t p0 = 0; p0 < np; p0 += (int64_t)kFinThreads * kFinLoads) {
+    uint64_t v[kFinLoads];
+#pragma unroll
+    for (int i = 0; i < kFinLoads; ++i) {
+      const int64_t p = p0 + t + (int64_t)kFinThreads * i;
+      v[i] = p < np ? parts[p * m + mm] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < kFinLoads; ++i) best = v[i] > best ? v[i] : best;
   }
   best = group_max_u64<64>(best);
   if (lane == 0) sb[w] = best;
@@ -42,7 +51,7 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const uint64_t* __
   if (t == 0) {
     uint64_t b = sb[0];
 #pragma unroll
-    for (int i = 1; i < 4; ++i) b = sb[i] > b ? sb[i] : b;
+    for (int i = 1; i < kFinThreads / 64; ++i) b = sb[i] > b ? sb[i] : b;
     tokens[mm] = b ? (int64_t)(0xFFFFFFFFu - (uint32_t)b) : -1;
   }
 }
@@ -158,7 +167,7 @@ hipError_t launch_head_t(const void* x, int64_t ldx, const void* gamma, int gdt,
 }  // namespace
 
 hipError_t launch_argmax_finalize(const uint64_t* parts, int64_t n_parts, int64_t m, int64_t* tokens, hipStream_t s) {
-  hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)m), dim3(256), 0, s, parts, n_parts, (int)m, tokens);
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)m), dim3(kFinThreads), 0, s, parts, n_parts, (int)m, tokens);
   return hipGetLastError();
 }
 

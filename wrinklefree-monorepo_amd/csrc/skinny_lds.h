@@ -28,6 +28,18 @@
 // Gated mode (GLUE = 1 SiLU, 2 relu^2): W is gate|up (N = 2 * half); tiles 0 .. NT/2 - 1 are gate rows
 // n0 + 16 j, the others the up rows half + n0 + 16 j; x = act(gate) * up is stored fp32 at [tok, n],
 // both products rounded to ep.mid_dtype first (what a plain linear would store).
+// Norm prologue (XT = storage type of x, K <= 4096): instead of loading int8 codes, every workgroup
+// normalises and quantises the M float rows itself -- wave w takes rows w, w + S, ..., in the one-wave
+// summation order of the per-token quantiser (lane l adds the squares of elements (l + 64 j) * 8 + e,
+// j then e ascending, then a fixed xor butterfly), so the codes and scales are bit-identical to
+// wfb_rmsnorm_quant_i8's -- and writes the codes into the activation staging in its swizzled layout
+// (zeros from H to the staging's end).  A wave's first row and gamma are loaded before its weight
+// DMA, so their latency overlaps the weight stream; the token scales reach the epilogue through the
+// free half of the waves' weight staging, next to the partial tiles.
+// Replaces, for decode, SubLN/RMSNorm -> activation_quant -> BitLinear
+// (packages/training/src/wrinklefree/models/subln.py:42-59, 64-97,
+// packages/training/src/wrinklefree/models/bitlinear.py:66-113) as the reference's fused layer ops run
+// them per token (SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:150-231, 289-375).
 #pragma once
 
 #include "wfb_common.h"
@@ -44,9 +56,137 @@ __device__ __forceinline__ void dma16(buf_t r, void* lds, uint32_t voff) {
 // output tile the activation staging, so the LDS is the two operand stagings only.
 constexpr size_t lds_bytes(int S, int NT, int TP, int MR) { return (size_t)S * TP * (NT * 2048 + 2 * MR * 256); }
 
-template <int S, int NT, int TP, int MR, int GLUE, bool STAGED>
+// ---- norm prologue helpers ---------------------------------------------------------------------------
+// Storage-type tags of the prologue's x and gamma (kNone: no prologue / no gamma).  Distinct from the
+// WFB_* dtype codes, where WFB_F32 is 0.
+constexpr int kNone = 0, kBf16 = 1, kF32 = 2;
+inline int src_tag(int wfb_dtype) { return wfb_dtype == WFB_F32 ? kF32 : kBf16; }
+
+// 8 consecutive elements of a row (storage tag DT), as raw 16-byte words (fp32: two), zero when not loaded
+template <int DT>
+struct Raw8 {
+  v4i r[DT == kF32 ? 2 : 1] = {};
+};
+template <int DT>
+__device__ __forceinline__ Raw8<DT> load_raw8(const void* p, int e0) {
+  Raw8<DT> v;
+  const v4i* q = reinterpret_cast<const v4i*>(reinterpret_cast<const char*>(p) + (int64_t)e0 * (DT == kF32 ? 4 : 2));
+  v.r[0] = q[0];
+  if constexpr (DT == kF32) v.r[1] = q[1];
+  return v;
+}
+template <int DT>
+__device__ __forceinline__ void widen8(const Raw8<DT>& v, float (&f)[8]) {
+  if constexpr (DT == kF32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = __int_as_float(v.r[0][e]);
+      f[4 + e] = __int_as_float(v.r[1][e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t u = (uint32_t)v.r[0][e];
+      f[2 * e] = __uint_as_float(u << 16);
+      f[2 * e + 1] = __uint_as_float(u & 0xffff0000u);
+    }
+  }
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_fixed_f32(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// The M rows of x through the norm and the quantiser into the activation staging.  XT: x's storage tag;
+// GT: gamma's (kNone: no gamma).  between() issues the weight DMA after the first row's loads.  Codes go
+// to put() for k < H, zeros for H <= k < lim.  Returns the token scales of the wave's rows w, w + S, ...
+// in sc[].
+template <int S, int MR, int XT, int GT, class Put, class Between>
+__device__ __forceinline__ void norm_prologue(const NormSrc& ns, int M, int w, int lane, int lim, Put put,
+                                              Between between, float (&sc)[(MR + S - 1) / S]) {
+  constexpr int RPW = (MR + S - 1) / S;
+  const int H = ns.h;
+  constexpr int GS = GT == kF32 ? kF32 : kBf16;
+  Raw8<GS> gv[8];
+  Raw8<XT> xv[8];
+  auto load_row = [&](int r) {
+    const void* xr = reinterpret_cast<const char*>(ns.x) + (int64_t)r * ns.ldx * (XT == kF32 ? 4 : 2);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e0 = (lane + 64 * j) * 8;
+      xv[j] = e0 < H ? load_raw8<XT>(xr, e0) : Raw8<XT>{};
+    }
+  };
+  if (w < M) load_row(w);
+  if constexpr (GT != kNone) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e0 = (lane + 64 * j) * 8;
+      gv[j] = e0 < H ? load_raw8<GS>(ns.gamma, e0) : Raw8<GS>{};
+    }
+  }
+  between();
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int r = w + S * i;
+    sc[i] = 1.0f;
+    if (r >= M) break;
+    if (i > 0) load_row(r);
+    // x widened once; y = (x * rs) * gamma then replaces it
+    float y[8][8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) widen8<XT>(xv[j], y[j]);
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __fadd_rn(ss, __fmul_rn(y[j][e], y[j][e]));
+    ss = wave_sum_fixed_f32(ss);
+    const float rs = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(ss, (float)H), ns.eps)));
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float gm[8];
+      if constexpr (GT != kNone) {
+        widen8<GS>(gv[j], gm);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gm[e] = 1.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        y[j][e] = __fmul_rn(__fmul_rn(y[j][e], rs), gm[e]);
+        mx = fmaxf(mx, fabsf(y[j][e]));
+      }
+    }
+    mx = wave_max_f32(mx);
+    if (mx < 1e-6f) mx = 1.0f;
+    const float inv = __fdiv_rn(127.0f, mx);
+    sc[i] = __fdiv_rn(mx, 127.0f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e0 = (lane + 64 * j) * 8;
+      if (e0 < lim) {  // codes up to H, zeros to the end of the staging
+        uint32_t lo = 0, hi = 0;
+        if (e0 < H) {
+          lo = quant4_i8(&y[j][0], inv);
+          hi = quant4_i8(&y[j][4], inv);
+        }
+        put(r, e0, lo, hi);
+      }
+    }
+  }
+}
+
+template <int S, int NT, int TP, int MR, int GLUE, bool STAGED, int XT>
 __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, const int8_t* __restrict__ A,
-                                                 int64_t lda, int M, int N, int C, Epilogue ep) {
+                                                 int64_t lda, int M, int N, int C, Epilogue ep, NormSrc ns) {
   static_assert((GLUE ? NT / 2 : NT) <= S, "one wave per output row tile in the epilogue");
   static_assert(GLUE == 0 || NT % 2 == 0, "gated mode pairs gate and up tiles");
   static_assert(MR == 4 || MR == 8 || MR == 16, "staged token rows");
@@ -56,6 +196,11 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   // the wave has read it: its LDS reads and writes execute in order)
   auto red = [&](int wv, int nt, int j, int l) -> int& {
     return reinterpret_cast<int*>(&wl[wv][0][0][0])[(nt * 4 + j) * 64 + l];
+  };
+  // norm prologue: scale of token tok, written by its wave (tok % S) after that wave's partial tiles
+  constexpr int RPW = (MR + S - 1) / S;
+  auto tok_scale = [&](int tok) -> float& {
+    return reinterpret_cast<float*>(&wl[tok % S][0][0][0] + NT * 1024)[tok / S];
   };
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nl = lane & 15, g = lane >> 4;
@@ -71,44 +216,75 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   };
 
   // ---- operands into LDS (every load of the wave in flight before the first wait) --------------------
+  auto dma_weights = [&]() {
 #pragma unroll
-  for (int u = 0; u < TP; ++u) {
-    const int p = w + S * u;
+    for (int u = 0; u < TP; ++u) {
+      const int p = w + S * u;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+      for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int r = lane >> 3;
-        const int chunk = 8 * p + ((lane & 7) ^ (r ^ h));
-        const int row = tile_row(nt) + 8 * h + r;
-        const bool ok = p < T2 && chunk < C;
-        dma16(wb, wl[w][u][nt] + 1024 * h, ok ? (uint32_t)row * row_bytes + 16u * chunk : w_end);
-      }
-  }
-#pragma unroll
-  for (int u = 0; u < TP; ++u) {
-    const int p = w + S * u;
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int i = 0; i < MR / 4; ++i) {
-        const int t = 2 * p + st;
-        const int tok = 4 * i + (lane >> 4);
-        const int q = (lane & 15) ^ (tok & 15);
-        const uint32_t kb = 256u * t + 16u * q;
-        const bool ok = p < T2 && t < T && tok < M && kb < (uint32_t)(64 * C);
-        dma16(ab, al[w][u][st] + 1024 * i, ok ? (uint32_t)((int64_t)tok * lda) + kb : a_end);
-      }
-  }
+        for (int h = 0; h < 2; ++h) {
+          const int r = lane >> 3;
+          const int chunk = 8 * p + ((lane & 7) ^ (r ^ h));
+          const int row = tile_row(nt) + 8 * h + r;
+          const bool ok = p < T2 && chunk < C;
+          dma16(wb, wl[w][u][nt] + 1024 * h, ok ? (uint32_t)row * row_bytes + 16u * chunk : w_end);
+        }
+    }
+  };
   // epilogue operands of the column this lane owns in the MFMA layout (row n, tokens 4g + j)
   int toks[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) toks[j] = 4 * g + j;
   EpiCol<4> col;
-  if (!GLUE && w < NT) {
-    Epilogue e1 = ep;
-    if (STAGED) e1.res = nullptr;  // the staged path adds the residual with whole-line loads
-    col.load(e1, tile_row(w) + nl, N, toks, M);
+  auto col_loads = [&]() {
+    if (!GLUE && w < NT) {
+      Epilogue e1 = ep;
+      if (STAGED) e1.res = nullptr;  // the staged path adds the residual with whole-line loads
+      col.load(e1, tile_row(w) + nl, N, toks, M);
+    }
+  };
+  float my_scale[RPW];
+  if constexpr (XT == kNone) {
+    dma_weights();
+#pragma unroll
+    for (int u = 0; u < TP; ++u) {
+      const int p = w + S * u;
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int i = 0; i < MR / 4; ++i) {
+          const int t = 2 * p + st;
+          const int tok = 4 * i + (lane >> 4);
+          const int q = (lane & 15) ^ (tok & 15);
+          const uint32_t kb = 256u * t + 16u * q;
+          const bool ok = p < T2 && t < T && tok < M && kb < (uint32_t)(64 * C);
+          dma16(ab, al[w][u][st] + 1024 * i, ok ? (uint32_t)((int64_t)tok * lda) + kb : a_end);
+        }
+    }
+    col_loads();
+  } else {
+    // 8 codes of token row r at k = e0 .. e0 + 7 into the staging: step t = e0 / 256 of pair t / 2, which
+    // wave (t / 2) % S stages as its pair (t / 2) / S; 16-byte slot q of the step at q ^ (r & 15)
+    auto put = [&](int r, int e0, uint32_t lo, uint32_t hi) {
+      const int t = e0 >> 8, p = t >> 1, b = e0 & 255;
+      int8_t* dst = al[p % S][p / S][t & 1] + 256 * r + 16 * ((b >> 4) ^ (r & 15)) + (b & 15);
+      *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+    };
+    auto between = [&]() {
+      dma_weights();
+      col_loads();
+    };
+    // the whole staging: waves whose pairs lie past K read zeros (their sum(a) stays 0), as after the DMA
+    constexpr int lim = 512 * S * TP;
+    static_assert(lim <= 64 * 8 * 8, "the prologue's lanes cover 4096 elements");
+    if (ns.gamma == nullptr)
+      norm_prologue<S, MR, XT, kNone>(ns, M, w, lane, lim, put, between, my_scale);
+    else if (ns.gdt == WFB_F32)
+      norm_prologue<S, MR, XT, kF32>(ns, M, w, lane, lim, put, between, my_scale);
+    else
+      norm_prologue<S, MR, XT, kBf16>(ns, M, w, lane, lim, put, between, my_scale);
+    __syncthreads();  // every wave's codes are in the staging
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS-DMA loads have landed
 
@@ -167,7 +343,18 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
       for (int nt = 0; nt < NT; ++nt) red(w, nt, j, lane) = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj;
     }
   }
+  if constexpr (XT != kNone) {
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < RPW; ++i)
+        if (w + S * i < M) tok_scale(w + S * i) = my_scale[i];
+    }
+  }
   __syncthreads();
+  if constexpr (XT != kNone) {  // token scales from the prologue (ep.a_scale is not used)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) col.as[j] = toks[j] < M ? tok_scale(toks[j]) : 0.0f;
+  }
 
   // ---- epilogues -----------------------------------------------------------------------------------
   if constexpr (GLUE != 0) {
@@ -185,7 +372,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
         tg += red(k, w, j, lane);
         tu += red(k, w + NT / 2, j, lane);
       }
-      const float as = epi_ascale(ep, tok);
+      const float as = XT != kNone ? col.as[j] : epi_ascale(ep, tok);
       float yg = __fmul_rn(__fmul_rn((float)tg, wsg), as), yu = __fmul_rn(__fmul_rn((float)tu, wsu), as);
       if (ep.mid_dtype == WFB_BF16) {
         yg = bf16_bits_to_f32(f32_to_bf16_rne(yg));
@@ -295,40 +482,62 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
 
 // (S, TP) by the number of 512-weight step pairs T2 = ceil(K / 512): S = T2 waves up to 8 (K = 2560: 5,
 // K = 4096: 8, from sweeps), two pairs per wave up to 16 pairs, then 14 x 2 (K <= 14336, LDS permitting).
-template <int MR, int GLUE>
+// XT != kNone: the norm prologue on x of that storage tag (K <= 4096).
+template <int MR, int GLUE, int XT>
 hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e, int nt_pref,
-                  hipStream_t s) {
+                  const NormSrc& ns, hipStream_t s) {
   const int T2 = (C + 7) / 8;
   const bool staged = GLUE == 0 && e.out && !e.acc_out && !e.amax;
 #define WFB_SL_GO(S, NT, TP)                                                                                   \
   do {                                                                                                         \
     if constexpr (lds_bytes(S, NT, TP, MR) <= 163840 && (GLUE ? NT / 2 : NT) <= S) {                           \
       const dim3 grid(GLUE ? (n / 2 + 8 * NT - 1) / (8 * NT) : (n + 16 * NT - 1) / (16 * NT));                 \
-      if (staged)                                                                                              \
-        hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, true>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, C, e); \
+      if (GLUE == 0 && staged)                                                                                 \
+        hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, GLUE == 0, XT>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, \
+                           C, e, ns);                                                                          \
       else                                                                                                     \
-        hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, false>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, C, e); \
+        hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, false, XT>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, \
+                           C, e, ns);                                                                          \
       return hipGetLastError();                                                                                \
     }                                                                                                          \
   } while (0)
-#define WFB_SL_NT(S, TP)                                 \
-  do {                                                   \
-    if (nt_pref >= 8) WFB_SL_GO(S, 8, TP);               \
-    if (nt_pref >= 4) WFB_SL_GO(S, 4, TP);               \
-    if constexpr (GLUE != 0) WFB_SL_GO(S, 2, TP);        \
-    else WFB_SL_GO(S, 1, TP);                            \
-    return hipErrorNotSupported;                         \
+#define WFB_SL_NT(S, TP)                                         \
+  do {                                                           \
+    if (nt_pref >= 8) WFB_SL_GO(S, 8, TP);                       \
+    if (nt_pref >= 4) WFB_SL_GO(S, 4, TP);                       \
+    if constexpr (GLUE != 0) {                                   \
+      WFB_SL_GO(S, 2, TP);                                       \
+    } else {                                                     \
+      if constexpr (XT != kNone) if (nt_pref >= 2) WFB_SL_GO(S, 2, TP); \
+      WFB_SL_GO(S, 1, TP);                                       \
+    }                                                            \
+    return hipErrorNotSupported;                                 \
   } while (0)
   if (T2 <= 2) WFB_SL_NT(2, 1);
   if (T2 <= 4) WFB_SL_NT(4, 1);
   if (T2 <= 5) WFB_SL_NT(5, 1);
   if (T2 <= 8) WFB_SL_NT(8, 1);
-  if (T2 <= 14) WFB_SL_NT(7, 2);
-  if (T2 <= 16) WFB_SL_NT(8, 2);
-  if (T2 <= 28) WFB_SL_NT(14, 2);
+  if constexpr (XT == kNone) {
+    if (T2 <= 14) WFB_SL_NT(7, 2);
+    if (T2 <= 16) WFB_SL_NT(8, 2);
+    if (T2 <= 28) WFB_SL_NT(14, 2);
+  }
 #undef WFB_SL_NT
 #undef WFB_SL_GO
   return hipErrorNotSupported;
+}
+
+// The three modes of one staged token-row count: codes A (x null), or the norm prologue on bf16 / fp32 x.
+template <int MR, int GLUE>
+hipError_t launch_modes(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
+                        int nt_pref, const NormSrc& ns, hipStream_t s) {
+  if (ns.x == nullptr) {
+    if (A == nullptr) return hipErrorInvalidValue;
+    return launch<MR, GLUE, kNone>(W, n, C, A, m, lda, e, nt_pref, ns, s);
+  }
+  if (C > 64 || ns.h > 64 * C || (ns.xdt != WFB_F32 && ns.xdt != WFB_BF16)) return hipErrorInvalidValue;
+  if (src_tag(ns.xdt) == kF32) return launch<MR, GLUE, kF32>(W, n, C, A, m, lda, e, nt_pref, ns, s);
+  return launch<MR, GLUE, kBf16>(W, n, C, A, m, lda, e, nt_pref, ns, s);
 }
 
 }  // namespace skinny_lds

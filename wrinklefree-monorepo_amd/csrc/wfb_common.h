@@ -103,6 +103,23 @@ __device__ __forceinline__ int quant_i8(float v, float inv) {
   return (int)r;
 }
 
+// Four codes quant_i8(v[e], inv), e = 0..3, packed little-endian into one word.  Clamping first and
+// rounding after gives the same integer for every finite input (a value clamped to +-127/-128 is already
+// integral; one inside rounds as before), and NaN clamps to -128 as in quant_i8.  The rounding adds
+// 1.5 * 2^23: below 2^22 in magnitude the sum is rounded to an integer, half to even, and its low byte is
+// that integer's two's-complement byte; v_perm_b32 then gathers the four low bytes.
+__device__ __forceinline__ uint32_t quant4_i8(const float* v, float inv) {
+  uint32_t b[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float c = fminf(fmaxf(__fmul_rn(v[e], inv), -128.0f), 127.0f);
+    b[e] = __float_as_uint(__fadd_rn(c, 12582912.0f));
+  }
+  const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u);  // bytes: b0.0, b1.0, 0, 0
+  const uint32_t hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);  // bytes: b2.0, b3.0, 0, 0
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);                   // lo.0, lo.1, hi.0, hi.1
+}
+
 // ---- raw buffer access (out-of-range reads return 0) --------------------------------------
 
 typedef __amdgpu_buffer_rsrc_t buf_t;
@@ -411,28 +428,48 @@ hipError_t launch_argmax_finalize(const uint64_t* parts, int64_t n_parts, int64_
 hipError_t launch_lm_head_argmax(const void* x, int xdt, int64_t ldx, const void* gamma, int gdt, float eps,
                                  const void* w, int wdt, int64_t ldw, int64_t m, int64_t n, int64_t h, float* logits,
                                  int64_t ldo, uint64_t* parts, hipStream_t s);
+// Activation rows that the batched-decode kernel normalises and quantises itself (its RMSNorm prologue):
+// x [M, H] (x_dtype WFB_F32 / WFB_BF16, row stride ldx elements, rows 16-byte aligned), gamma [H]
+// (gdt WFB_F32 / WFB_BF16, 16-byte aligned) or null, H % 8 == 0, H <= K <= 4096.  x == null: the
+// activations are int8 codes A with per-token scales ep.a_scale, as for wfb_linear_i2s.
+struct NormSrc {
+  const void* x;
+  int xdt;
+  int64_t ldx;
+  const void* gamma;
+  int gdt;
+  float eps;
+  int h;
+};
 // M <= 16 tokens with both operands staged in LDS (skinny_lds.h); act 0 (plain) or a WFB_ACT_* gated
 // gate|up product; returns hipErrorNotSupported when the shape does not fit its LDS (the caller then
 // takes the register-operand kernels).  Needs N*K/4 and (M-1)*lda + K below 2^31.
 hipError_t launch_skinny_lds_mr4(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
-                                 const Epilogue& e, int act, int nt_pref, hipStream_t s);
+                                 const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
 hipError_t launch_skinny_lds_mr8(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
-                                 const Epilogue& e, int act, int nt_pref, hipStream_t s);
+                                 const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
 hipError_t launch_skinny_lds_mr16(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
-                                  const Epilogue& e, int act, int nt_pref, hipStream_t s);
+                                  const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
 inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
-                                    const Epilogue& e, int act, hipStream_t s) {
+                                    const Epilogue& e, int act, hipStream_t s, const NormSrc& ns = NormSrc{}) {
   const int C = k / 64;
   // 16-row tiles per workgroup, from sweeps on MI355X (rows n counts gate + up rows when gated):
   //  * n >= 24576 (28672 gate|up, 128256 LM head): 4 for M <= 4, whose staging lets two such
   //    workgroups share a CU, else 8 (one workgroup per CU either way, so fewer, larger ones);
   //  * n >= 8192: 4; gated 2 up to M = 8 (13824 gate|up: 432 workgroups, all resident);
   //  * shorter outputs: 1 (2 when gated, one gate and one up tile).
-  const int nt_pref = n >= 24576 ? (m <= 4 ? 4 : 8) : n >= 8192 ? (act && m <= 8 ? 2 : 4) : act ? 2 : 1;
+  int nt_pref = n >= 24576 ? (m <= 4 ? 4 : 8) : n >= 8192 ? (act && m <= 8 ? 2 : 4) : act ? 2 : 1;
+  // with the norm prologue every workgroup repeats the M x H normalisation, so the grid is kept to one
+  // round of at most 256 workgroups (one per CU)
+  if (ns.x) {
+    const int tiles = (n + 15) / 16;
+    nt_pref = tiles <= 256 ? 1 : tiles <= 512 ? 2 : tiles <= 1024 ? 4 : 8;
+    if (act && nt_pref < 2) nt_pref = 2;
+  }
   if (m < 1) return hipErrorInvalidValue;
-  if (m <= 4) return launch_skinny_lds_mr4(W, n, C, A, m, lda, e, act, nt_pref, s);
-  if (m <= 8) return launch_skinny_lds_mr8(W, n, C, A, m, lda, e, act, nt_pref, s);
-  if (m <= 16) return launch_skinny_lds_mr16(W, n, C, A, m, lda, e, act, nt_pref, s);
+  if (m <= 4) return launch_skinny_lds_mr4(W, n, C, A, m, lda, e, act, nt_pref, ns, s);
+  if (m <= 8) return launch_skinny_lds_mr8(W, n, C, A, m, lda, e, act, nt_pref, ns, s);
+  if (m <= 16) return launch_skinny_lds_mr16(W, n, C, A, m, lda, e, act, nt_pref, ns, s);
   return hipErrorNotSupported;
 }
 // 3 <= M <= 64 through the split-K skinny kernel (16, 32 or 64 rows per workgroup); needs
@@ -445,8 +482,5 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
 // fp32 output [M, half] at e.out / e.ldo)
 hipError_t launch_gemm_i2s_glu(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, int act,
                                const Epilogue& e, hipStream_t s);
-// RMSNorm + quant in the prologue of the batched-decode linear (M <= 16, H <= K <= 4096)
-hipError_t launch_norm_linear(const void* x, int xdt, int64_t ldx, const void* gamma, int gdt, float eps, int h,
-                              const uint8_t* W, int m, int n, int k, const Epilogue& e, hipStream_t s);
 
 }  // namespace wfb

@@ -35,7 +35,8 @@ from .sglbitnt import SGLBitNetFile, write_sglbitnt
 from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_glu,
                   bitnet_linear_residual, bitnet_linear_segmented, glu_rmsnorm_quantize_i8, gqa_decode_attention,
                   gqa_prefill_attention,
-                  lm_head_argmax, pack_ternary_i2s, rmsnorm_linear, rmsnorm_linear_preferred, rmsnorm_quantize_i8)
+                  lm_head_argmax, pack_ternary_i2s, rmsnorm_linear, rmsnorm_linear_glu, rmsnorm_linear_preferred,
+                  rmsnorm_quantize_i8)
 
 
 @dataclass(frozen=True)
@@ -194,9 +195,12 @@ class HipBackend:
         half = gate.out_features
         if (self.fused and not self.keep_acc and x.dim() == 2 and x.shape[0] <= 64 and up.out_features == half
                 and half % 32 == 0 and act in ("silu", "relu2")):
-            q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=gate.k_pad)
             qw, sc, _ = self._group([gate, up])
-            mid = bitnet_linear_glu(qw, sc, q, act, a_scale=a_scale, mid_dtype=self.out_dtype)
+            if self._fused_norm(x, norm_weight, 2 * half, gate.k_pad):
+                mid = rmsnorm_linear_glu(x, norm_weight, qw, sc, act, eps=eps, mid_dtype=self.out_dtype)
+            else:
+                q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=gate.k_pad)
+                mid = bitnet_linear_glu(qw, sc, q, act, a_scale=a_scale, mid_dtype=self.out_dtype)
             return self.norm_linear_residual(mid, sub_norm, sub_eps, down, residual)
         g, u = self.norm_linears(x, norm_weight, eps, [gate, up])
         return self.glu_norm_linear_residual(g, u, act, sub_norm, sub_eps, down, residual)

@@ -468,17 +468,16 @@ def bitnet_linear_residual(
 
 
 def rmsnorm_linear_supported(m: int, h: int, k: int, gamma_bytes: int = 2) -> bool:
-    """Whether rmsnorm_linear takes these sizes (decode batches: the codes of the M rows and gamma live in
-    LDS; ``gamma_bytes`` per gamma element, 0 without gamma)."""
-    return (1 <= m <= 16 and h % 8 == 0 and 0 < h <= k <= 4096 and k % QK_I2_S == 0
-            and m * (k + 16) + h * gamma_bytes <= 49152)
+    """Whether rmsnorm_linear / rmsnorm_linear_glu take these sizes (decode batches of up to 16 rows, rows of
+    up to 4096 elements; ``gamma_bytes`` is kept for callers and no longer limits the size)."""
+    return 1 <= m <= 16 and h % 8 == 0 and 0 < h <= k <= 4096 and k % QK_I2_S == 0
 
 
 def rmsnorm_linear_preferred(m: int, h: int, n: int, k: int, gamma_bytes: int = 2) -> bool:
-    """Whether the fused launch is the faster choice (measured on MI355X): supported sizes whose grid of
-    16-row tiles fits one workgroup per CU (256)."""
-    nt = 4 if n >= 24576 else (2 if n >= 6144 and k <= 8192 else 1)
-    return rmsnorm_linear_supported(m, h, k, gamma_bytes) and (n + 16 * nt - 1) // (16 * nt) <= 256
+    """Whether the fused launch is the faster choice: every supported size (measured on MI355X, the prologue
+    costs less than the separate quantiser launch it replaces at the Llama-3-8B, BitNet-2B and SmolLM2
+    decode shapes)."""
+    return rmsnorm_linear_supported(m, h, k, gamma_bytes)
 
 
 def rmsnorm_linear(
@@ -510,7 +509,7 @@ def rmsnorm_linear(
     gbytes = 0 if weight is None else weight.element_size()
     if not rmsnorm_linear_supported(m, h, k, gbytes):
         raise RuntimeError(f"{name}: M={m}, H={h}, K={k} outside the fused path (M <= 16, H % 8 == 0, "
-                           f"H <= K <= 4096, M*(K+16) + H*{gbytes} <= 49152)")
+                           f"H <= K <= 4096)")
     dev = _require_gpu(name, x, weight, packed_weights, scales, residual)
     if weight is not None and (weight.numel() != h or weight.dtype not in (torch.float32, torch.bfloat16)):
         raise RuntimeError(f"{name}: weight must be float32/bfloat16 with {h} elements")
@@ -534,6 +533,53 @@ def rmsnorm_linear(
                   _DT[residual.dtype] if residual is not None else WFB_F32,
                   residual.stride(0) if residual is not None else n, _p(out), _DT[out.dtype], out.stride(0),
                   _stream(dev))
+    return out
+
+
+def rmsnorm_linear_glu(
+    x: torch.Tensor, weight: Optional[torch.Tensor], packed_weights: torch.Tensor, scales: torch.Tensor,
+    act: str = "silu", eps: float = 1e-6, mid_dtype: torch.dtype = torch.bfloat16, out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """RMSNorm + per-token int8 quantisation + gate|up BitLinear + act(gate) * up in one launch (decode
+    batches, ``rmsnorm_linear_supported``): fp32 [M, half], equal, bit for bit, to ``rmsnorm_quantize_i8``
+    followed by ``bitnet_linear_glu``.
+
+    x: float32/bfloat16 [M, H]; weight: [H] or None; packed_weights: uint8 gate|up [2 * half, K/4] (half %
+    32 == 0, K >= H); scales: fp32 [2] on the device."""
+    name = "rmsnorm_linear_glu"
+    if act not in _ACTS:
+        raise ValueError(f"{name}: act must be one of {sorted(_ACTS)}")
+    if x.dim() != 2 or x.dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError(f"{name}: x must be float32/bfloat16 [batch, hidden]")
+    if packed_weights.dtype != torch.uint8 or packed_weights.dim() != 2:
+        raise RuntimeError(f"{name}: packed_weights must be uint8 2D [2 * half, in_features/4]")
+    if mid_dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError(f"{name}: mid_dtype must be float32 or bfloat16")
+    m, h = x.shape
+    n, kb = packed_weights.shape
+    k = kb * 4
+    if n % 64 != 0:
+        raise ValueError(f"{name}: gate|up rows ({n}) must be 2 x a multiple of 32")
+    if scales.dtype != torch.float32 or scales.numel() != 2:
+        raise RuntimeError(f"{name}: scales must be fp32 [2] (gate, up)")
+    if not rmsnorm_linear_supported(m, h, k):
+        raise RuntimeError(f"{name}: M={m}, H={h}, K={k} outside the fused path (M <= 16, H % 8 == 0, H <= K <= 4096)")
+    dev = _require_gpu(name, x, weight, packed_weights, scales)
+    if weight is not None and (weight.numel() != h or weight.dtype not in (torch.float32, torch.bfloat16)):
+        raise RuntimeError(f"{name}: weight must be float32/bfloat16 with {h} elements")
+    if x.stride(1) != 1 or (x.stride(0) * x.element_size()) % 16 != 0 or x.data_ptr() % 16 != 0:
+        x = x.contiguous()
+    if weight is not None:
+        weight = weight.contiguous()
+    half = n // 2
+    if out is None:
+        out = torch.empty((m, half), dtype=torch.float32, device=dev)
+    elif out.dtype != torch.float32 or out.shape != (m, half) or out.stride(-1) != 1:
+        raise RuntimeError(f"{name}: out must be float32 [{m}, {half}] with contiguous rows")
+    with torch.cuda.device(dev):
+        _lib.call("wfb_rmsnorm_linear_i2s_glu", _p(x), _DT[x.dtype], x.stride(0), _p(weight),
+                  _DT[weight.dtype] if weight is not None else WFB_F32, float(eps), m, h, _p(packed_weights), n, k,
+                  _p(scales), _ACTS[act], _DT[mid_dtype], _p(out), out.stride(0), _stream(dev))
     return out
 
 
