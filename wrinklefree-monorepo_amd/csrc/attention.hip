@@ -369,6 +369,20 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_combine_kernel(const float* 
   float* sm = cw;                // [ns * G]: m, then the split weights e^(m_s - M)
   float* sl = cw + nsplit * G;   // [ns * G]: l
   float* sden = sl + nsplit * G; // [G]
+  // Up to kPre splits: the accumulators of the thread's output elements are requested together with m
+  // and l (one round trip to the partials instead of two).
+  constexpr int kPre = 16, EPT = (G * D + kAttnThreads - 1) / kAttnThreads;
+  const bool pre = ns <= kPre;  // uniform
+  float pa[EPT][kPre];
+  if (pre) {
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int i = t + kAttnThreads * k;
+      const int g = i / D, d = i % D;
+#pragma unroll
+      for (int s = 0; s < kPre; ++s) pa[k][s] = (i < G * D && s < ns) ? pp[(s * G + g) * (D + 2) + d] : 0.0f;
+    }
+  }
   for (int i = t; i < ns * G; i += kAttnThreads) {
     sm[i] = pp[i * (D + 2) + D];
     sl[i] = pp[i * (D + 2) + D + 1];
@@ -386,6 +400,20 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_combine_kernel(const float* 
     sden[t] = den;
   }
   __syncthreads();
+  if (pre) {
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int i = t + kAttnThreads * k;
+      if (i >= G * D) break;
+      const int g = i / D;
+      float num = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kPre; ++s)
+        if (s < ns) num += pa[k][s] * sm[s * G + g];
+      store_elem<DT>(out, obase + i, num / sden[g]);
+    }
+    return;
+  }
   for (int i = t; i < G * D; i += kAttnThreads) {
     const int g = i / D, d = i % D;
     float num = 0.0f;
