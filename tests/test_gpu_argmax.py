@@ -18,7 +18,11 @@ def _first_argmax(x):
     return np.argmax(x, axis=-1)  # numpy returns the first maximum, as std::max_element
 
 
+# (8, 128256, 4096), (3, 40000, 2560), (5, 33000, 1024), (12, 65543, 2560), (16, 49152, 4096): the
+# persistent head kernel
+# (>= 32768 rows, up to 16 tokens), one-shot elsewhere
 @pytest.mark.parametrize("m,n,k", [(1, 1000, 256), (2, 5000, 640), (3, 4099, 2560), (8, 128256, 4096),
+                                   (3, 40000, 2560), (5, 33000, 1024), (12, 65543, 2560), (16, 49152, 4096),
                                    (17, 3000, 512), (64, 2048, 384)])
 @pytest.mark.parametrize("ldt", [torch.float32, torch.bfloat16])
 def test_ternary_head_argmax_matches_oracle(pkg, dev, m, n, k, ldt):
@@ -40,6 +44,21 @@ def test_ternary_head_argmax_matches_oracle(pkg, dev, m, n, k, ldt):
     assert np.array_equal(tok.cpu().numpy(), _first_argmax(yt.numpy()))
     # without stored logits, same tokens
     assert torch.equal(pkg.bitnet_linear_argmax(pw, at, float(ws), a_scale=st, logits_dtype=ldt), tok)
+
+
+@pytest.mark.parametrize("m,n,k", [(4, 36000, 4096), (8, 33011, 2560), (16, 40000, 1024)])
+def test_persistent_head_accumulators(pkg, dev, m, n, k):
+    """The persistent form of the batched-decode kernel with an accumulator copy (>= 32768 rows): every
+    int32 accumulator and fp32 output equal the oracle's."""
+    rng = np.random.default_rng(m + n + k)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    ws, a_scale = orc.log_uniform(rng), orc.log_uniform(rng, m)
+    y, acc = pkg.bitnet_linear(torch.from_numpy(packed).to(dev), torch.from_numpy(a).to(dev), float(ws),
+                               a_scale=torch.from_numpy(a_scale).to(dev), out_dtype=torch.float32, return_acc=True)
+    acc_ref = (a.astype(np.float32) @ orc.unpack_i2s(packed).astype(np.float32).T).astype(np.int64)
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), acc_ref)
+    assert np.array_equal(y.cpu().numpy(), orc.rescale(acc_ref, np.float32(ws), a_scale))
 
 
 def test_ternary_head_argmax_ties_pick_first(pkg, dev):

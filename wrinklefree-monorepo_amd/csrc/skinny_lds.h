@@ -480,6 +480,198 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   }
 }
 
+// Persistent form for outputs of many row tiles (the LM head: 128256 rows = 4008 tiles of 32), codes
+// path, one weight scale, no bias or residual, per-lane epilogues (greedy-argmax keys, accumulator copies,
+// per-lane stores).  One workgroup per CU loops over tiles t = blockIdx.x, + gridDim.x, ...  The
+// activation fragments and token scales are loaded once into registers (they are the same for every
+// tile), so the LDS holds only weights: a ring of DEPTH tile buffers, DEPTH - 1 tiles' weight DMA in
+// flight while one tile is multiplied, reduced and stored -- about 128 KB per CU at K = 4096, what the M = 1
+// GEMV keeps in flight to stream at ~6.4 TB/s.  A tile's wait is vmcnt(ops of the tiles issued after it)
+// (loads complete in issue order; the epilogue's stores sit between those tiles, so the wait can only be
+// longer, never short).  TP = 1 (K <= 4096).  Same operand layouts and arithmetic as the one-shot kernel.
+template <int OPS>
+__device__ __forceinline__ void wait_tiles_after(int later) {
+  // vmcnt(n) with expcnt / lgkmcnt at their maxima (gfx9: vmcnt bits 3:0 and 15:14)
+#define WFB_VMCNT(nn) __builtin_amdgcn_s_waitcnt(((nn) & 15) | (((nn) >> 4) << 14) | (7 << 4) | (15 << 8))
+  switch (later) {
+    case 0: WFB_VMCNT(0); break;
+    case 1: WFB_VMCNT(OPS); break;
+    case 2: WFB_VMCNT(2 * OPS); break;
+    case 3: WFB_VMCNT(3 * OPS); break;
+    case 4: WFB_VMCNT(4 * OPS); break;
+    case 5: WFB_VMCNT(5 * OPS); break;
+    case 6: WFB_VMCNT(6 * OPS); break;
+    default: WFB_VMCNT(7 * OPS); break;
+  }
+#undef WFB_VMCNT
+}
+
+template <int S, int NT, int DEPTH>
+__global__ __launch_bounds__(64 * S) void kernel_persist(const uint8_t* __restrict__ W, const int8_t* __restrict__ A,
+                                                         int64_t lda, int M, int N, int C, int ntiles, Epilogue ep) {
+  static_assert(NT <= S, "one wave per output row tile in the epilogue");
+  static_assert(DEPTH >= 2 && DEPTH <= 8 && 7 * 2 * NT < 64, "ring depth and vmcnt range");
+  constexpr int OPS = 2 * NT;  // LDS-DMA instructions of one tile's weights (per wave)
+  __shared__ __attribute__((aligned(16))) int8_t wl[DEPTH][S][NT][2048];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nl = lane & 15, g = lane >> 4;
+  const uint32_t row_bytes = (uint32_t)C * 16;
+  const uint32_t w_end = (uint32_t)N * row_bytes, a_end = (uint32_t)((int64_t)(M - 1) * lda + (int64_t)C * 64);
+  const buf_t wb = make_buf(W, w_end);
+  const buf_t ab = make_buf(A, a_end);
+  const int T = (C + 3) >> 2, T2 = (C + 7) >> 3;
+  const int p = w;  // this wave's step pair (TP = 1)
+
+  // activation fragments of token nl over this wave's pair: the 16 bytes the MFMA takes from lane (nl, g)
+  // (step bytes 128 (g / 2) + 16 (g % 2) + 32 f); tokens past M and bytes past K read as zeros
+  v4i av[2][4];
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int t = 2 * p + st;
+      const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;
+      const uint32_t kb = 256u * t + 16u * qg;
+      const bool ok = p < T2 && t < T && nl < M && kb < (uint32_t)(64 * C);
+      av[st][f] = buf_load16(ab, ok ? (uint32_t)((int64_t)nl * lda) + kb : a_end);
+    }
+  // token scales of the four tokens this lane stores, and the weight scale (one segment)
+  float as[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) as[j] = 4 * g + j < M ? epi_ascale(ep, 4 * g + j) : 0.0f;
+  const float ws = ep.ws_dev ? ep.ws_dev[0] : ep.ws;
+
+  auto dma = [&](int tile, int buf) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = lane >> 3;
+        const int chunk = 8 * p + ((lane & 7) ^ (r ^ h));
+        const int row = tile * 16 * NT + 16 * nt + 8 * h + r;
+        const bool ok = p < T2 && chunk < C;
+        dma16(wb, wl[buf][w][nt] + 1024 * h, ok ? (uint32_t)row * row_bytes + 16u * chunk : w_end);
+      }
+  };
+#pragma unroll
+  for (int i = 0; i < DEPTH - 1; ++i) {
+    const int t = blockIdx.x + i * gridDim.x;
+    if (t < ntiles) dma(t, i);
+  }
+
+  // sum(a) of token 4g + j over this wave's K range (the same for every tile)
+  int sj[4];
+  {
+    int sa = 0;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sa = __builtin_amdgcn_sdot4(av[st][f][e], 0x01010101, sa, false);
+    sa += __shfl_xor(sa, 16, 64);
+    sa += __shfl_xor(sa, 32, 64);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sj[j] = __shfl(sa, 4 * g + j, 64);
+  }
+  const int hh = nl >> 3, rr = nl & 7;
+
+  for (int it = 0;; ++it) {
+    const int tile = blockIdx.x + it * gridDim.x;
+    if (tile >= ntiles) break;
+    const int buf = it % DEPTH;
+    const int ahead = blockIdx.x + (it + DEPTH - 1) * gridDim.x;
+    if (ahead < ntiles) dma(ahead, (it + DEPTH - 1) % DEPTH);  // buffer freed by the previous tile's last barrier
+    const int later = min(DEPTH - 1, (ntiles - 1 - tile) / (int)gridDim.x);
+    wait_tiles_after<OPS>(later);
+
+    v4i acc1[NT], acc4[NT], acc16[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc1[nt] = acc4[nt] = acc16[nt] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int slot = (4 * st + g) ^ (rr ^ hh);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const v4i wv = *reinterpret_cast<const v4i*>(wl[buf][w][nt] + 1024 * hh + 128 * rr + 16 * slot);
+        v4i b0, b1, b2, b3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = wv[e];
+          b0[e] = (d >> 2) & 0x30303030;
+          b1[e] = d & 0x30303030;
+          b2[e] = d & 0x0C0C0C0C;
+          b3[e] = d & 0x03030303;
+        }
+        acc16[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[st][0], b0, acc16[nt], 0, 0, 0);
+        acc16[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[st][1], b1, acc16[nt], 0, 0, 0);
+        acc4[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[st][2], b2, acc4[nt], 0, 0, 0);
+        acc1[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[st][3], b3, acc1[nt], 0, 0, 0);
+      }
+    }
+    // partial tiles into this wave's consumed weight buffer (its LDS reads and writes execute in order)
+    auto red = [&](int wv, int nt, int j, int l) -> int& {
+      return reinterpret_cast<int*>(&wl[buf][wv][0][0])[(nt * 4 + j) * 64 + l];
+    };
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) red(w, nt, j, lane) = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj[j];
+    __syncthreads();
+    if (w < NT) {
+      const int nt = w;
+      const int n = tile * 16 * NT + 16 * nt + nl;
+      if (ep.amax) {  // greedy-argmax keys: the maximum over the 16 rows of each token, one slot per 16 rows
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tok = 4 * g + j;
+          int tot = red(0, nt, j, lane);
+#pragma unroll
+          for (int k = 1; k < S; ++k) tot += red(k, nt, j, lane);
+          const bool valid = tok < M && n < N;
+          uint64_t key = epi_store_key_r(ep, ws, as[j], 0.0f, 0.0f, tok, n, tot, valid);
+          key = group_max_u64<16>(key);
+          const int slot = tile * NT + nt;
+          if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
+        }
+      } else if (n < N) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tok = 4 * g + j;
+          int tot = red(0, nt, j, lane);
+#pragma unroll
+          for (int k = 1; k < S; ++k) tot += red(k, nt, j, lane);
+          if (tok < M) epi_store_r(ep, ws, as[j], 0.0f, 0.0f, tok, n, tot);
+        }
+      }
+    }
+    __syncthreads();  // buffer `buf` (partial tiles) is refilled by the DMA issued at the next iteration's top
+  }
+}
+
+// Persistent launch for grids of many tiles: two 16-row tiles per workgroup step, the ring as deep as the
+// LDS allows (at most 8); hipErrorNotSupported where it does not apply (the caller then takes the one-shot
+// kernel).
+inline hipError_t launch_persist(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
+                                 const Epilogue& e, int cus, hipStream_t s) {
+  constexpr int NT = 2;
+  const int T2 = (C + 7) / 8;
+  const int ntiles = (n + 16 * NT - 1) / (16 * NT);
+  const int grid = ntiles < cus ? ntiles : cus;
+#define WFB_SL_P(S)                                                                                    \
+  do {                                                                                                 \
+    constexpr int D = 163840 / (S * NT * 2048) > 8 ? 8 : 163840 / (S * NT * 2048);                   \
+    hipLaunchKernelGGL((kernel_persist<S, NT, D>), dim3(grid), dim3(64 * S), 0, s, W, A, lda, m, n, C, ntiles, e); \
+    return hipGetLastError();                                                                          \
+  } while (0)
+  if (T2 <= 2) WFB_SL_P(2);
+  if (T2 <= 4) WFB_SL_P(4);
+  if (T2 <= 5) WFB_SL_P(5);
+  if (T2 <= 8) WFB_SL_P(8);
+#undef WFB_SL_P
+  return hipErrorNotSupported;
+}
+
 // (S, TP) by the number of 512-weight step pairs T2 = ceil(K / 512): S = T2 waves up to 8 (K = 2560: 5,
 // K = 4096: 8, from sweeps), two pairs per wave up to 16 pairs, then 14 x 2 (K <= 14336, LDS permitting).
 // XT != kNone: the norm prologue on x of that storage tag (K <= 4096).
@@ -527,12 +719,35 @@ hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_
   return hipErrorNotSupported;
 }
 
+// Rows from which the persistent form is used: 2048 tiles of 16 rows (8 per CU at NT = 4, four
+// one-workgroup-per-CU rounds of the one-shot kernel).
+constexpr int kPersistMinRows = 32768;
+
+// Compute units of the current device (cached per device).
+inline int cu_count() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev] = v;
+  }
+  return cache[dev];
+}
+
 // The three modes of one staged token-row count: codes A (x null), or the norm prologue on bf16 / fp32 x.
 template <int MR, int GLUE>
 hipError_t launch_modes(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
                         int nt_pref, const NormSrc& ns, hipStream_t s) {
   if (ns.x == nullptr) {
     if (A == nullptr) return hipErrorInvalidValue;
+    // many row tiles with a per-lane epilogue (the greedy LM head): the persistent form
+    if (GLUE == 0 && (e.amax || e.acc_out || !e.out) && !e.bias && !e.res && e.nseg == 1 &&
+        n >= kPersistMinRows) {
+      const hipError_t st = launch_persist(W, n, C, A, m, lda, e, cu_count(), s);
+      if (st != hipErrorNotSupported) return st;
+    }
     return launch<MR, GLUE, kNone>(W, n, C, A, m, lda, e, nt_pref, ns, s);
   }
   if (C > 64 || ns.h > 64 * C || (ns.xdt != WFB_F32 && ns.xdt != WFB_BF16)) return hipErrorInvalidValue;
