@@ -509,10 +509,13 @@ __device__ __forceinline__ void wait_tiles_after(int later) {
 template <int S, int NT, int DEPTH>
 __global__ __launch_bounds__(64 * S) void kernel_persist(const uint8_t* __restrict__ W, const int8_t* __restrict__ A,
                                                          int64_t lda, int M, int N, int C, int ntiles, Epilogue ep) {
-  static_assert(NT <= S, "one wave per output row tile in the epilogue");
   static_assert(DEPTH >= 2 && DEPTH <= 8 && 7 * 2 * NT < 64, "ring depth and vmcnt range");
   constexpr int OPS = 2 * NT;  // LDS-DMA instructions of one tile's weights (per wave)
   __shared__ __attribute__((aligned(16))) int8_t wl[DEPTH][S][NT][2048];
+  // partial tiles, double-buffered by tile parity: a wave only ever refills its own weight slot (program
+  // order protects it), and a parity buffer is rewritten two tiles later, after a barrier every wave
+  // passes only once done with the epilogue that read it -- one barrier per tile
+  __shared__ int redb[2][S][NT * 4][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nl = lane & 15, g = lane >> 4;
   const uint32_t row_bytes = (uint32_t)C * 16;
@@ -609,43 +612,36 @@ __global__ __launch_bounds__(64 * S) void kernel_persist(const uint8_t* __restri
         acc1[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[st][3], b3, acc1[nt], 0, 0, 0);
       }
     }
-    // partial tiles into this wave's consumed weight buffer (its LDS reads and writes execute in order)
-    auto red = [&](int wv, int nt, int j, int l) -> int& {
-      return reinterpret_cast<int*>(&wl[buf][wv][0][0])[(nt * 4 + j) * 64 + l];
-    };
+    const int par = it & 1;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) red(w, nt, j, lane) = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj[j];
+      for (int nt = 0; nt < NT; ++nt)
+        redb[par][w][nt * 4 + j][lane] = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj[j];
     __syncthreads();
-    if (w < NT) {
-      const int nt = w;
+    // epilogue spread over the waves: (row tile nt, token slot j) pairs c = w, w + S, ...; lane (nl, g)
+    // finishes row 16 nt + nl of token 4g + j
+    for (int c = w; c < NT * 4; c += S) {
+      const int nt = c >> 2, j = c & 3;
+      const int tok = 4 * g + j;
       const int n = tile * 16 * NT + 16 * nt + nl;
+      int tot = redb[par][0][c][lane];
+#pragma unroll
+      for (int k = 1; k < S; ++k) tot += redb[par][k][c][lane];
+      float a = as[0];
+#pragma unroll
+      for (int jj = 1; jj < 4; ++jj)
+        if (j == jj) a = as[jj];
       if (ep.amax) {  // greedy-argmax keys: the maximum over the 16 rows of each token, one slot per 16 rows
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int tok = 4 * g + j;
-          int tot = red(0, nt, j, lane);
-#pragma unroll
-          for (int k = 1; k < S; ++k) tot += red(k, nt, j, lane);
-          const bool valid = tok < M && n < N;
-          uint64_t key = epi_store_key_r(ep, ws, as[j], 0.0f, 0.0f, tok, n, tot, valid);
-          key = group_max_u64<16>(key);
-          const int slot = tile * NT + nt;
-          if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
-        }
-      } else if (n < N) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int tok = 4 * g + j;
-          int tot = red(0, nt, j, lane);
-#pragma unroll
-          for (int k = 1; k < S; ++k) tot += red(k, nt, j, lane);
-          if (tok < M) epi_store_r(ep, ws, as[j], 0.0f, 0.0f, tok, n, tot);
-        }
+        const bool valid = tok < M && n < N;
+        uint64_t key = epi_store_key_r(ep, ws, a, 0.0f, 0.0f, tok, n, tot, valid);
+        key = group_max_u64<16>(key);
+        const int slot = tile * NT + nt;
+        if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
+      } else if (n < N && tok < M) {
+        epi_store_r(ep, ws, a, 0.0f, 0.0f, tok, n, tot);
       }
     }
-    __syncthreads();  // buffer `buf` (partial tiles) is refilled by the DMA issued at the next iteration's top
   }
 }
 
@@ -660,7 +656,8 @@ inline hipError_t launch_persist(const uint8_t* W, int n, int C, const int8_t* A
   const int grid = ntiles < cus ? ntiles : cus;
 #define WFB_SL_P(S)                                                                                    \
   do {                                                                                                 \
-    constexpr int D = 163840 / (S * NT * 2048) > 8 ? 8 : 163840 / (S * NT * 2048);                   \
+    constexpr int D = (163840 - 2 * S * NT * 1024) / (S * NT * 2048) > 8 ? 8                          \
+                                                                        : (163840 - 2 * S * NT * 1024) / (S * NT * 2048); \
     hipLaunchKernelGGL((kernel_persist<S, NT, D>), dim3(grid), dim3(64 * S), 0, s, W, A, lda, m, n, C, ntiles, e); \
     return hipGetLastError();                                                                          \
   } while (0)
