@@ -198,6 +198,28 @@ def test_batched_decode_outputs_without_accumulator_copy(pkg, dev, m, n, k):
         assert torch.equal(got.cpu(), want)
 
 
+@pytest.mark.parametrize("m,n,k", [(5, 4096, 14336), (8, 4096, 14336), (16, 4096, 14336), (9, 1000, 14208),
+                                   (12, 100, 8448), (7, 2600, 10240), (16, 33, 12800)])
+def test_batched_long_rows_register_activations(pkg, dev, m, n, k):
+    """5 <= M <= 16 with 8192 < K <= 14336 (the Llama-3-8B down projection): the activations do not fit the
+    LDS beside the weights, so the staged kernel holds them in registers.  Accumulators (per-lane
+    epilogue), bf16 / fp32 outputs and a residual in either dtype (whole-line epilogue) equal the oracle's."""
+    rng = np.random.default_rng(8100 + m + n + k)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    ws, a_s = orc.log_uniform(rng), orc.log_uniform(rng, m)
+    _check_linear(pkg, dev, packed, a, ws, a_s, kernel="gemm")
+    acc = _ref_acc(packed, a)
+    pw, pa, ps = _t(packed, dev), _t(a, dev), _t(a_s, dev)
+    y = pkg.bitnet_linear(pw, pa, float(ws), a_scale=ps)
+    assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), orc.f32_to_bf16_bits(orc.rescale(acc, ws, a_s)))
+    for rdt in (torch.float32, torch.bfloat16):
+        res = torch.from_numpy(rng.standard_normal((m, n)).astype(np.float32)).to(rdt)
+        want = torch.from_numpy(orc.rescale(acc, np.float32(ws), a_s) + res.float().numpy()).to(rdt)
+        got = pkg.bitnet_linear_residual(pw, pa, float(ws), res.to(dev), a_scale=ps)
+        assert torch.equal(got.cpu(), want)
+
+
 @pytest.mark.parametrize("m,n,k", [(12, 32800, 128), (24, 16400, 256), (64, 8200, 384), (9, 40, 8192),
                                    (24, 9216, 2560), (24, 9200, 2560), (40, 6144, 8192), (40, 6144, 8320),
                                    (40, 12000, 8320), (17, 18432, 256)])

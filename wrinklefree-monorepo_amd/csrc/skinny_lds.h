@@ -55,11 +55,17 @@ __device__ __forceinline__ void dma16(buf_t r, void* lds, uint32_t voff) {
 // The per-wave partial tiles of the K reduction overwrite the wave's own weight staging, and the staged
 // output tile the activation staging, so the LDS is the two operand stagings only.
 constexpr size_t lds_bytes(int S, int NT, int TP, int MR) { return (size_t)S * TP * (NT * 2048 + 2 * MR * 256); }
+// with the activations in registers (kAreg): the weight staging and the staged output tile
+constexpr size_t lds_bytes_areg(int S, int NT, int TP) { return (size_t)S * TP * NT * 2048 + 16 * 16 * NT * 4 + 64; }
 
 // ---- norm prologue helpers ---------------------------------------------------------------------------
 // Storage-type tags of the prologue's x and gamma (kNone: no prologue / no gamma).  Distinct from the
 // WFB_* dtype codes, where WFB_F32 is 0.
 constexpr int kNone = 0, kBf16 = 1, kF32 = 2;
+// Codes path with the activation fragments loaded straight into registers in MFMA layout instead of the
+// LDS staging: for shapes whose M x K activation bytes do not fit the LDS beside the weights (the
+// Llama-3-8B down projection, K = 14336, at M > 4).
+constexpr int kAreg = 3;
 inline int src_tag(int wfb_dtype) { return wfb_dtype == WFB_F32 ? kF32 : kBf16; }
 
 // 8 consecutive elements of a row (storage tag DT), as raw 16-byte words (fp32: two), zero when not loaded
@@ -190,8 +196,11 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   static_assert((GLUE ? NT / 2 : NT) <= S, "one wave per output row tile in the epilogue");
   static_assert(GLUE == 0 || NT % 2 == 0, "gated mode pairs gate and up tiles");
   static_assert(MR == 4 || MR == 8 || MR == 16, "staged token rows");
+  constexpr bool NORM = XT == kF32 || XT == kBf16;  // codes formed in the prologue, token scales with them
   __shared__ __attribute__((aligned(16))) int8_t wl[S][TP][NT][2048];
-  __shared__ __attribute__((aligned(16))) int8_t al[S][TP][2][MR * 256];
+  __shared__ __attribute__((aligned(16))) int8_t al[XT == kAreg ? 1 : S][XT == kAreg ? 1 : TP][2][XT == kAreg ? 16 : MR * 256];
+  // staged output tile of the register-activation mode (the others use the activation staging)
+  __shared__ __attribute__((aligned(16))) float ysb[XT == kAreg && STAGED ? 16 * 16 * NT : 1];
   // partial tile (row tile nt, token slot j, lane) of wave w, in wave w's own weight staging (free once
   // the wave has read it: its LDS reads and writes execute in order)
   auto red = [&](int wv, int nt, int j, int l) -> int& {
@@ -245,7 +254,26 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     }
   };
   float my_scale[RPW];
-  if constexpr (XT == kNone) {
+  // register-activation mode: lane (nl, g)'s 16 activation bytes of step pair u, step st, field f -- step
+  // bytes 128 (g / 2) + 16 (g % 2) + 32 f of token nl (zeros past M and past K)
+  v4i avr[XT == kAreg ? TP : 1][2][4];
+  if constexpr (XT == kAreg) {
+    dma_weights();
+#pragma unroll
+    for (int u = 0; u < TP; ++u)
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          const int p = w + S * u;
+          const int t = 2 * p + st;
+          const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;
+          const uint32_t kb = 256u * t + 16u * qg;
+          const bool ok = p < T2 && t < T && nl < M && kb < (uint32_t)(64 * C);
+          avr[u][st][f] = buf_load16(ab, ok ? (uint32_t)((int64_t)nl * lda) + kb : a_end);
+        }
+    col_loads();
+  } else if constexpr (XT == kNone) {
     dma_weights();
 #pragma unroll
     for (int u = 0; u < TP; ++u) {
@@ -299,12 +327,17 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   for (int u = 0; u < TP; ++u) {
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      arow = al[w][u][st] + 256 * (nl < MR ? nl : MR - 1);  // rows >= M hold zeros or unused codes
       v4i av[4];
+      if constexpr (XT == kAreg) {
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;  // step bytes 128 (g / 2) + 16 (g % 2) + 32 f
-        av[f] = *reinterpret_cast<const v4i*>(arow + 16 * (qg ^ nl));
+        for (int f = 0; f < 4; ++f) av[f] = avr[u][st][f];
+      } else {
+        arow = al[w][u][st] + 256 * (nl < MR ? nl : MR - 1);  // rows >= M hold zeros or unused codes
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;  // step bytes 128 (g / 2) + 16 (g % 2) + 32 f
+          av[f] = *reinterpret_cast<const v4i*>(arow + 16 * (qg ^ nl));
+        }
       }
       const int slot = (4 * st + g) ^ (rr ^ hh);
 #pragma unroll
@@ -343,7 +376,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
       for (int nt = 0; nt < NT; ++nt) red(w, nt, j, lane) = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj;
     }
   }
-  if constexpr (XT != kNone) {
+  if constexpr (NORM) {
     if (lane == 0) {
 #pragma unroll
       for (int i = 0; i < RPW; ++i)
@@ -351,7 +384,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     }
   }
   __syncthreads();
-  if constexpr (XT != kNone) {  // token scales from the prologue (ep.a_scale is not used)
+  if constexpr (NORM) {  // token scales from the prologue (ep.a_scale is not used)
 #pragma unroll
     for (int j = 0; j < 4; ++j) col.as[j] = toks[j] < M ? tok_scale(toks[j]) : 0.0f;
   }
@@ -372,7 +405,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
         tg += red(k, w, j, lane);
         tu += red(k, w + NT / 2, j, lane);
       }
-      const float as = XT != kNone ? col.as[j] : epi_ascale(ep, tok);
+      const float as = NORM ? col.as[j] : epi_ascale(ep, tok);
       float yg = __fmul_rn(__fmul_rn((float)tg, wsg), as), yu = __fmul_rn(__fmul_rn((float)tu, wsu), as);
       if (ep.mid_dtype == WFB_BF16) {
         yg = bf16_bits_to_f32(f32_to_bf16_rne(yg));
@@ -413,8 +446,8 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     // y (fp32, before the residual) of the [M tokens x 16 NT rows] tile into LDS (the activation staging),
     // rows rotated by 4 per token to spread the banks
     constexpr int RW = 16 * NT;
-    float* ys = reinterpret_cast<float*>(&al[0][0][0][0]);  // free after the barrier above
-    static_assert(sizeof(al) >= 16 * RW * 4, "staging space");
+    float* ys = XT == kAreg ? ysb : reinterpret_cast<float*>(&al[0][0][0][0]);  // free after the barrier above
+    static_assert(XT == kAreg || sizeof(al) >= 16 * RW * 4, "staging space");
     if (w < NT) {
       const int c = 16 * w + nl;
 #pragma unroll
@@ -671,7 +704,8 @@ inline hipError_t launch_persist(const uint8_t* W, int n, int C, const int8_t* A
 
 // (S, TP) by the number of 512-weight step pairs T2 = ceil(K / 512): S = T2 waves up to 8 (K = 2560: 5,
 // K = 4096: 8, from sweeps), two pairs per wave up to 16 pairs, then 14 x 2 (K <= 14336, LDS permitting).
-// XT != kNone: the norm prologue on x of that storage tag (K <= 4096).
+// XT = kF32 / kBf16: the norm prologue on x of that storage tag (K <= 4096); kAreg: codes A held in
+// registers (rows whose activations do not fit the LDS beside the weights).
 template <int MR, int GLUE, int XT>
 hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e, int nt_pref,
                   const NormSrc& ns, hipStream_t s) {
@@ -679,7 +713,8 @@ hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_
   const bool staged = GLUE == 0 && e.out && !e.acc_out && !e.amax;
 #define WFB_SL_GO(S, NT, TP)                                                                                   \
   do {                                                                                                         \
-    if constexpr (lds_bytes(S, NT, TP, MR) <= 163840 && (GLUE ? NT / 2 : NT) <= S) {                           \
+    if constexpr ((XT == kAreg ? lds_bytes_areg(S, NT, TP) : lds_bytes(S, NT, TP, MR)) <= 163840 &&          \
+                  (GLUE ? NT / 2 : NT) <= S) {                                                                \
       const dim3 grid(GLUE ? (n / 2 + 8 * NT - 1) / (8 * NT) : (n + 16 * NT - 1) / (16 * NT));                 \
       if (GLUE == 0 && staged)                                                                                 \
         hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, GLUE == 0, XT>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, \
@@ -702,11 +737,13 @@ hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_
     }                                                            \
     return hipErrorNotSupported;                                 \
   } while (0)
-  if (T2 <= 2) WFB_SL_NT(2, 1);
-  if (T2 <= 4) WFB_SL_NT(4, 1);
-  if (T2 <= 5) WFB_SL_NT(5, 1);
-  if (T2 <= 8) WFB_SL_NT(8, 1);
-  if constexpr (XT == kNone) {
+  if constexpr (XT != kAreg) {  // the register-activation mode only serves the long rows below
+    if (T2 <= 2) WFB_SL_NT(2, 1);
+    if (T2 <= 4) WFB_SL_NT(4, 1);
+    if (T2 <= 5) WFB_SL_NT(5, 1);
+    if (T2 <= 8) WFB_SL_NT(8, 1);
+  }
+  if constexpr (XT == kNone || XT == kAreg) {
     if (T2 <= 14) WFB_SL_NT(7, 2);
     if (T2 <= 16) WFB_SL_NT(8, 2);
     if (T2 <= 28) WFB_SL_NT(14, 2);
@@ -745,7 +782,11 @@ hipError_t launch_modes(const uint8_t* W, int n, int C, const int8_t* A, int m, 
       const hipError_t st = launch_persist(W, n, C, A, m, lda, e, cu_count(), s);
       if (st != hipErrorNotSupported) return st;
     }
-    return launch<MR, GLUE, kNone>(W, n, C, A, m, lda, e, nt_pref, ns, s);
+    const hipError_t st = launch<MR, GLUE, kNone>(W, n, C, A, m, lda, e, nt_pref, ns, s);
+    if constexpr (GLUE == 0) {  // activations too long for the LDS beside the weights: in registers
+      if (st == hipErrorNotSupported) return launch<MR, GLUE, kAreg>(W, n, C, A, m, lda, e, nt_pref, ns, s);
+    }
+    return st;
   }
   if (C > 64 || ns.h > 64 * C || (ns.xdt != WFB_F32 && ns.xdt != WFB_BF16)) return hipErrorInvalidValue;
   if (src_tag(ns.xdt) == kF32) return launch<MR, GLUE, kF32>(W, n, C, A, m, lda, e, nt_pref, ns, s);
