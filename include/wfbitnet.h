@@ -239,6 +239,16 @@ int wfb_lm_head_argmax(const void* x, int x_dtype, int64_t ldx, const void* gamm
                        int64_t h, float* logits, int64_t ldo, uint64_t* workspace, int64_t* token_out,
                        void* stream);
 
+/* ---- rotary tables ------------------------------------------------------------------------- */
+
+/* Host buffers cos_out / sin_out fp32 [max_len, head_dim/2] of the HF rotate-half rotary embedding:
+ * angle(p, i) = p * theta^(-2i / head_dim), evaluated in double precision (pow, product, cos / sin of
+ * the C library) and rounded once to float, so every caller that takes its tables from here uses the
+ * same values.  Host memory only; touches no GPU.  head_dim even and >= 2, max_len >= 1, theta > 0.
+ * The angles of the stage-1 HF model's rotary embedding (WF/training/stage1.py:169-214; the reference
+ * C engine has none, SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:381-441). */
+int wfb_rope_tables(double theta, int64_t head_dim, int64_t max_len, float* cos_out, float* sin_out);
+
 /* ---- GQA decode attention over a KV cache (one new token per sequence) --------------------- */
 
 /* For each sequence b < batch at position p = pos[b] (device int64 [batch]):

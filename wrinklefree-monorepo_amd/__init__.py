@@ -30,9 +30,11 @@ from .ops import (
     rmsnorm_linear_preferred,
     rmsnorm_linear_supported,
     rmsnorm_quantize_i8,
+    rope_tables,
     unpack_i2s,
 )
-from . import model, sglbitnt
+from . import engine, model, sglbitnt
+from .engine import NativeEngine
 from .sglbitnt import SGLBitNetFile, write_sglbitnt
 from .bitlinear import (
     BitLinear,
@@ -49,7 +51,7 @@ __all__ = [
     "bitnet_linear_argmax", "bitnet_linear_glu", "bitnet_linear_residual", "bitnet_linear_segmented", "check_kernel_available", "convert_hf_offline_i2s",
     "glu_rmsnorm_quantize_i8", "gqa_decode_attention", "gqa_prefill_attention", "lm_head_argmax", "pack_ternary_i2s",
     "quantize_activations_i8", "quantize_activations_i8_per_token", "rmsnorm_linear", "rmsnorm_linear_glu", "rmsnorm_linear_preferred", "rmsnorm_linear_supported",
-    "rmsnorm_quantize_i8", "unpack_i2s",
+    "rmsnorm_quantize_i8", "rope_tables", "unpack_i2s",
     "BitLinear", "BitNetLinearMethod", "BitNetLinearNative", "SubLNBitLinear", "convert_linear_to_bitlinear",
-    "patch_model_with_native_kernels", "set_lambda_source", "model", "sglbitnt", "SGLBitNetFile", "write_sglbitnt",
+    "patch_model_with_native_kernels", "set_lambda_source", "engine", "NativeEngine", "model", "sglbitnt", "SGLBitNetFile", "write_sglbitnt",
 ]

@@ -61,6 +61,7 @@ SIGNATURES = {
     "wfb_linear_i2s_glu": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _int, _int, _vp, _i64, _vp],
     "wfb_rmsnorm_linear_i2s": [_vp, _int, _i64, _vp, _int, _f32, _i64, _i64, _vp, _i64, _i64, _int, _vp, _vp, _vp,
                                _int, _i64, _vp, _int, _i64, _vp],
+    "wfb_rope_tables": [ctypes.c_double, _i64, _i64, _vp, _vp],
     "wfb_rmsnorm_linear_i2s_glu": [_vp, _int, _i64, _vp, _int, _f32, _i64, _i64, _vp, _i64, _i64, _vp, _int, _int, _vp,
                                    _i64, _vp],
 }

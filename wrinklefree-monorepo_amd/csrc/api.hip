@@ -4,6 +4,7 @@
 // SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:336-346, 375-386, 410 and the K % 128 check of
 // SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:331-336, 824-829) and adds the alignment the 128-bit
 // loads need.  Every check runs on the host before anything touches the GPU.
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -560,6 +561,23 @@ int wfb_linear_i2s_glu(const uint8_t* qweight, int64_t n, int64_t k, const int8_
   e.mid_dtype = mid_dtype;
   return hip_status(wfb::launch_gemm_i2s_glu(qweight, (int)n, (int)k, act, (int)m, lda, act_kind, e, as_stream(stream)),
                     name);
+}
+
+int wfb_rope_tables(double theta, int64_t head_dim, int64_t max_len, float* cos_out, float* sin_out) {
+  const char* name = "wfb_rope_tables";
+  if (!(theta > 0.0) || head_dim < 2 || head_dim % 2 != 0 || max_len < 1)
+    return fail(WFB_EINVAL, "%s: bad theta / head_dim / max_len", name);
+  if (!cos_out || !sin_out) return fail(WFB_EINVAL, "%s: null output", name);
+  const int64_t half = head_dim / 2;
+  for (int64_t i = 0; i < half; ++i) {
+    const double inv = 1.0 / std::pow(theta, (double)(2 * i) / (double)head_dim);
+    for (int64_t p = 0; p < max_len; ++p) {
+      const double a = (double)p * inv;
+      cos_out[p * half + i] = (float)std::cos(a);
+      sin_out[p * half + i] = (float)std::sin(a);
+    }
+  }
+  return ok();
 }
 
 }  // extern "C"

@@ -36,7 +36,7 @@ from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_gl
                   bitnet_linear_residual, bitnet_linear_segmented, glu_rmsnorm_quantize_i8, gqa_decode_attention,
                   gqa_prefill_attention,
                   lm_head_argmax, pack_ternary_i2s, rmsnorm_linear, rmsnorm_linear_glu, rmsnorm_linear_preferred,
-                  rmsnorm_quantize_i8)
+                  rmsnorm_quantize_i8, rope_tables)
 
 
 @dataclass(frozen=True)
@@ -279,8 +279,6 @@ class BitNetDecoder:
         self.dtype = dtype
         self.backend = backend if backend is not None else HipBackend(out_dtype=dtype if dtype == torch.float32
                                                                        else torch.bfloat16)
-        inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, dtype=torch.float32) / cfg.head_dim))
-        self.inv_freq = inv.to(self.device)
         self.kv: List[Optional[List[torch.Tensor]]] = []
         self._lm_t = None
 
@@ -292,10 +290,12 @@ class BitNetDecoder:
     _NORMS = (("input_norm", "input_layernorm"), ("post_attn_norm", "post_attention_layernorm"),
               ("attn_sub_norm", "self_attn.attn_sub_norm"), ("ffn_sub_norm", "mlp.ffn_sub_norm"))
 
-    def save_sglbitnt(self, path) -> None:
+    def save_sglbitnt(self, path, config_overrides: Optional[Dict] = None) -> None:
         """Write the model as an SGLBITNT file with the tensor names the reference engine loads
         (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:622-668): packed linears uint8 [out, k_pad/4] with
-        their scale, embedding and norms as float32, a ternary LM head as lm_head.weight."""
+        their scale, embedding and norms as float32, a ternary LM head (uint8) or an untied dense head
+        (float32) as lm_head.weight, none for a head tied to the embedding.  ``config_overrides``: extra or
+        replaced keys of the config JSON (e.g. ``eos_token_id``)."""
         cfg = self.cfg
         config = {"vocab_size": cfg.vocab_size, "hidden_size": cfg.hidden_size,
                   "intermediate_size": cfg.intermediate_size, "num_hidden_layers": cfg.num_layers,
@@ -314,6 +314,10 @@ class BitNetDecoder:
         t["model.norm.weight"] = (self.final_norm.float(), None)
         if self.lm_head is not None:
             t["lm_head.weight"] = (self.lm_head.qweight, float(self.lm_head.scale.item()))
+        elif self.head_weight is not self.embed:
+            t["lm_head.weight"] = (self.head_weight.float(), None)
+        config["tie_word_embeddings"] = self.lm_head is None and self.head_weight is self.embed
+        config.update(config_overrides or {})
         write_sglbitnt(path, config, t)
 
     @classmethod
@@ -423,10 +427,11 @@ class BitNetDecoder:
     # ---- float glue --------------------------------------------------------------------------
 
     def _rope(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-        """HF rotate-half rotary embedding; x [B, T, H, D], pos [T]."""
-        freqs = pos.to(torch.float32)[:, None] * self.inv_freq[None, :]
-        emb = torch.cat([freqs, freqs], dim=-1)
-        cos, sin = emb.cos()[None, :, None, :], emb.sin()[None, :, None, :]
+        """HF rotate-half rotary embedding; x [B, T, H, D], pos [T] (rows of the tables set by reset, the values
+        the attention kernels use)."""
+        c = self._rope_cos.index_select(0, pos.to(self._rope_cos.device))
+        s = self._rope_sin.index_select(0, pos.to(self._rope_sin.device))
+        cos, sin = torch.cat([c, c], dim=-1)[None, :, None, :], torch.cat([s, s], dim=-1)[None, :, None, :]
         x32 = x.to(torch.float32)
         half = x32.shape[-1] // 2
         rot = torch.cat([-x32[..., half:], x32[..., :half]], dim=-1)
@@ -506,9 +511,9 @@ class BitNetDecoder:
         self._max_len = max_len
         self.kv = [None] * self.cfg.num_layers
         self._key_pos = torch.arange(max_len, device=self.device)
-        # cos/sin of pos * inv_freq for every cache position (the values _rope computes per call)
-        freqs = self._key_pos.to(torch.float32)[:, None] * self.inv_freq[None, :]
-        self._rope_cos, self._rope_sin = freqs.cos().contiguous(), freqs.sin().contiguous()
+        # cos / sin of every cache position from libwfbitnet's tables (the native engine's values)
+        cos, sin = _rope_tables_cpu(self.cfg.rope_theta, self.cfg.head_dim, max_len)
+        self._rope_cos, self._rope_sin = cos.to(self.device), sin.to(self.device)
 
     def _layers(self, x: torch.Tensor, attend, first: int = 0, last: Optional[int] = None) -> torch.Tensor:
         cfg, be = self.cfg, self.backend
@@ -565,7 +570,7 @@ class BitNetDecoder:
         cpu = torch.device("cpu")
         m = copy.copy(self)
         m.device, m.backend, m.decode_attention, m.prefill_attention = cpu, backend, "torch", "torch"
-        m.embed, m.final_norm, m.inv_freq = self.embed.to(cpu), self.final_norm.to(cpu), self.inv_freq.to(cpu)
+        m.embed, m.final_norm = self.embed.to(cpu), self.final_norm.to(cpu)
         m.head_weight = m.embed if self.head_weight is self.embed else self.head_weight.to(cpu)
         m.layers = []
         for L in self.layers:
@@ -620,12 +625,17 @@ class BitNetDecoder:
         return self._next_tokens(x[:, -1, :]) if tokens else self._logits(x[:, -1, :])
 
     @torch.no_grad()
-    def generate(self, prompt: torch.Tensor, new_tokens: int, graph: bool = False) -> torch.Tensor:
+    def generate(self, prompt: torch.Tensor, new_tokens: int, graph: bool = False,
+                 max_len: Optional[int] = None) -> torch.Tensor:
         """Greedy decoding: prompt [B, T0] -> generated ids [B, new_tokens].  The prompt is one
         forward; every further token is decode_step, run directly or (graph=True) replayed from one
-        HIP graph capture, the next ids, position and output column updated on the device."""
+        HIP graph capture, the next ids, position and output column updated on the device.  ``max_len``:
+        KV cache positions (default T0 + new_tokens; the split decode attention's key splits follow it)."""
         b, t0 = prompt.shape
-        self.reset(b, t0 + new_tokens)
+        max_len = t0 + new_tokens if max_len is None else int(max_len)
+        if max_len < t0 + new_tokens:
+            raise ValueError(f"generate: max_len {max_len} < prompt + new tokens ({t0 + new_tokens})")
+        self.reset(b, max_len)
         nxt = self.forward(prompt.to(self.device), 0, tokens=True)
         out = torch.empty((b, new_tokens), dtype=torch.long, device=self.device)
         out[:, 0] = nxt
@@ -656,6 +666,20 @@ class BitNetDecoder:
         for _ in range(steps - 1):
             g.replay()
         return out
+
+
+_ROPE_CACHE: Dict[tuple, tuple] = {}
+
+
+def _rope_tables_cpu(theta: float, head_dim: int, max_len: int):
+    """rope_tables rows 0..max_len-1 (a row depends on its position only, so a longer table computed once
+    per (theta, head_dim) is sliced)."""
+    key = (float(theta), int(head_dim))
+    hit = _ROPE_CACHE.get(key)
+    if hit is None or hit[0].shape[0] < max_len:
+        hit = rope_tables(theta, head_dim, max(max_len, 4096))
+        _ROPE_CACHE[key] = hit
+    return hit[0][:max_len], hit[1][:max_len]
 
 
 def random_float_state(cfg: BitNetConfig, seed: int) -> Dict[str, torch.Tensor]:

@@ -724,6 +724,19 @@ def _rows2d(name: str, t: torch.Tensor, b: int, width: int) -> Tuple[torch.Tenso
     return t2, (t2.stride(0) if b > 1 else width)
 
 
+def rope_tables(theta: float, head_dim: int, max_len: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """cos / sin fp32 CPU tensors [max_len, head_dim/2] of the HF rotate-half rotary embedding at positions
+    0..max_len-1 (angle p * theta^(-2i/head_dim) in double precision, rounded once to float): the tables
+    the decode / prefill attention kernels take, the same values the native engine computes."""
+    name = "rope_tables"
+    if head_dim < 2 or head_dim % 2 != 0 or max_len < 1 or not theta > 0:
+        raise ValueError(f"{name}: bad theta / head_dim / max_len")
+    cos = torch.empty((max_len, head_dim // 2), dtype=torch.float32)
+    sin = torch.empty_like(cos)
+    _lib.call("wfb_rope_tables", float(theta), head_dim, max_len, _p(cos), _p(sin))
+    return cos, sin
+
+
 def gqa_decode_attention(
     q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     pos: torch.Tensor, rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None,
