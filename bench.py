@@ -15,9 +15,11 @@ RMSNorm+quant kernel, one BitNet-2B decode layer's quantised path with separate 
 (decode_layer_2b), and the reference CPU kernel timed on this host (cpu_baseline).  Context for the
 roofline fractions: launch_context (an empty kernel's per-launch time, a plain copy moving the same
 bytes as the dominant GEMV, the GEMV on a 131 MB matrix) and, per prefill entry, the vendor library's
-plain int8 GEMM (torch._int_mm on hipBLASLt) on the same M, N, K.
+plain int8 GEMM (torch._int_mm on hipBLASLt) on the same M, N, K.  e2e: greedy decoding of the configs[0]
+/ configs[4] models through the Python model on the HIP kernels; engine: the same shapes through the
+native engine's C ABI (include/wfbitnet_engine.h), batch 1.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-e2e] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-e2e] [--no-engine] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -93,6 +95,7 @@ def parse():
     p.add_argument("--no-sweep", action="store_true", help="skip the batched M sweep (configs[2])")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--no-engine", action="store_true", help="skip the native engine section")
     p.add_argument("--no-e2e", action="store_true",
                    help="skip the end-to-end models (configs[4] Llama-3-8B shape, configs[0] SmolLM2 shape)")
     return p.parse_args()
@@ -424,6 +427,56 @@ def e2e_bench(pkg, torch, dev, cpu: bool = True):
     return res
 
 
+def engine_bench(pkg, torch, dev):
+    """The native engine (include/wfbitnet_engine.h, the reference engine's C ABI) on SGLBITNT files of the
+    configs[0] / configs[4] shapes (bf16 glue, random init on the device, written to /dev/shm): load time,
+    the prompt as one batched pass (mean of 3), greedy decoding in bitnet_generate (graph replays, one host
+    synchronisation per 32 tokens; generate's time minus the prompt's), and the latency of one
+    bitnet_decode_step call (one replay plus the token's copy to the host).  Batch 1, as the reference
+    engine."""
+    import tempfile
+
+    M = pkg.model
+    res = {}
+    tmpdir = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    for name, cfg, t0, new in (("smollm2_135m", M.SMOLLM2_135M, 32, 128), ("llama3_8b", M.LLAMA3_8B, 256, 256)):
+        print(f"[engine] {name}: writing the model file", file=sys.stderr, flush=True)
+        model = M.BitNetDecoder(cfg, seed=0, device=dev, dtype=torch.bfloat16, init_on_device=True)
+        with tempfile.NamedTemporaryFile(dir=tmpdir, suffix=".sglbitnt") as f:
+            model.save_sglbitnt(f.name)
+            del model
+            torch.cuda.empty_cache()
+            t = time.perf_counter()
+            eng = pkg.NativeEngine(f.name, max_seq_len=t0 + new)
+            load_s = time.perf_counter() - t
+        prompt = torch.randint(0, cfg.vocab_size, (t0,), generator=torch.Generator().manual_seed(5)).tolist()
+        with eng:
+            eng.generate(prompt[:8], max_tokens=4)  # warm-up
+            eng.prefill(prompt)
+            reps = 3
+            t = time.perf_counter()
+            for _ in range(reps):
+                eng.prefill(prompt)
+            prefill_s = (time.perf_counter() - t) / reps
+            t = time.perf_counter()
+            out = eng.generate(prompt, max_tokens=new)
+            decode_s = time.perf_counter() - t - prefill_s
+            eng.prefill(prompt)
+            calls = 64
+            t = time.perf_counter()
+            for i in range(calls):
+                eng.decode_step(t0 + i)
+            step_s = (time.perf_counter() - t) / calls
+        print(f"[engine] {name}: load {load_s:.2f} s, prefill {prefill_s * 1e3:.2f} ms, "
+              f"decode {decode_s / new * 1e3:.3f} ms/token", file=sys.stderr, flush=True)
+        res[name] = {"load_s": round(load_s, 2), "prefill_tokens": t0, "prefill_ms": round(prefill_s * 1e3, 3),
+                     "prefill_tok_s": round(t0 / prefill_s, 1), "decode_tokens": new,
+                     "decode_ms_per_token": round(decode_s / new * 1e3, 4),
+                     "decode_tok_s": round(new / decode_s, 1),
+                     "decode_step_call_ms": round(step_s * 1e3, 4), "distinct_tokens": len(set(out))}
+    return res
+
+
 def e2e_cpu_baseline(M, model, prompt, torch, new_tokens: int = 12):
     """The same model decoded on the host: float glue as torch CPU ops, quantised groups on the numpy
     oracle (oracle/model_backend.py).  Bounded sample: the prompt plus ``new_tokens`` greedy tokens."""
@@ -730,6 +783,7 @@ def main():
     nxt = next_rows_bench(torch, L, dev, min(args.steps, 100), 5)
 
     e2e = None if args.no_e2e else e2e_bench(__graft_entry__.load_package(), torch, dev, cpu=not args.no_cpu)
+    engine = None if args.no_e2e or args.no_engine else engine_bench(pkg, torch, dev)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
@@ -765,6 +819,8 @@ def main():
         line["batched_sweep"] = sweep
     if e2e is not None:
         line["e2e"] = e2e
+    if engine is not None:
+        line["engine"] = engine
     print(json.dumps(line), flush=True)
 
 
