@@ -429,25 +429,28 @@ def e2e_bench(pkg, torch, dev, cpu: bool = True):
 
 def engine_bench(pkg, torch, dev):
     """The native engine (include/wfbitnet_engine.h, the reference engine's C ABI) on SGLBITNT files of the
-    configs[0] / configs[4] shapes (bf16 glue, random init on the device, written to /dev/shm): load time,
+    configs[0] / BitNet-2B / configs[4] shapes (bf16 glue, random init on the device, written to /dev/shm): load time,
     the prompt as one batched pass (mean of 3), greedy decoding in bitnet_generate (graph replays, one host
     synchronisation per 32 tokens; generate's time minus the prompt's), and the latency of one
-    bitnet_decode_step call (one replay plus the token's copy to the host).  Batch 1, as the reference
-    engine."""
+    bitnet_decode_step call (one replay plus the token's copy to the host); for BitNet-2B also the whole
+    bitnet_generate latency on the input / output lengths of the MS BitNet GPU table
+    (packages/inference/extern/BitNet/gpu/README.md:91-105, A100).  Batch 1, as the reference engine."""
     import tempfile
 
     M = pkg.model
     res = {}
     tmpdir = "/dev/shm" if os.path.isdir("/dev/shm") else None
-    for name, cfg, t0, new in (("smollm2_135m", M.SMOLLM2_135M, 32, 128), ("llama3_8b", M.LLAMA3_8B, 256, 256)):
+    for name, cfg, t0, new in (("smollm2_135m", M.SMOLLM2_135M, 32, 128), ("bitnet_2b", M.BITNET_2B, 64, 64),
+                               ("llama3_8b", M.LLAMA3_8B, 256, 256)):
         print(f"[engine] {name}: writing the model file", file=sys.stderr, flush=True)
         model = M.BitNetDecoder(cfg, seed=0, device=dev, dtype=torch.bfloat16, init_on_device=True)
+        max_len = 576 if name == "bitnet_2b" else t0 + new
         with tempfile.NamedTemporaryFile(dir=tmpdir, suffix=".sglbitnt") as f:
             model.save_sglbitnt(f.name)
             del model
             torch.cuda.empty_cache()
             t = time.perf_counter()
-            eng = pkg.NativeEngine(f.name, max_seq_len=t0 + new)
+            eng = pkg.NativeEngine(f.name, max_seq_len=max_len)
             load_s = time.perf_counter() - t
         prompt = torch.randint(0, cfg.vocab_size, (t0,), generator=torch.Generator().manual_seed(5)).tolist()
         with eng:
@@ -467,6 +470,14 @@ def engine_bench(pkg, torch, dev):
             for i in range(calls):
                 eng.decode_step(t0 + i)
             step_s = (time.perf_counter() - t) / calls
+            latency = {}
+            if name == "bitnet_2b":  # the input / output grid of the MS BitNet A100 end-to-end table
+                for tin, tout in ((64, 16), (64, 64), (256, 32), (512, 64)):
+                    ids = torch.randint(0, cfg.vocab_size, (tin,), generator=torch.Generator().manual_seed(tin)).tolist()
+                    eng.generate(ids, max_tokens=tout)
+                    t = time.perf_counter()
+                    eng.generate(ids, max_tokens=tout)
+                    latency[f"{tin}_in_{tout}_out_ms"] = round((time.perf_counter() - t) * 1e3, 2)
         print(f"[engine] {name}: load {load_s:.2f} s, prefill {prefill_s * 1e3:.2f} ms, "
               f"decode {decode_s / new * 1e3:.3f} ms/token", file=sys.stderr, flush=True)
         res[name] = {"load_s": round(load_s, 2), "prefill_tokens": t0, "prefill_ms": round(prefill_s * 1e3, 3),
@@ -474,6 +485,8 @@ def engine_bench(pkg, torch, dev):
                      "decode_ms_per_token": round(decode_s / new * 1e3, 4),
                      "decode_tok_s": round(new / decode_s, 1),
                      "decode_step_call_ms": round(step_s * 1e3, 4), "distinct_tokens": len(set(out))}
+        if latency:
+            res[name]["generate_latency"] = latency
     return res
 
 

@@ -59,6 +59,11 @@ class BitNetConfig:
 # SmolLM2-135M architecture (packages/training/configs/model/smollm2_135m.yaml)
 SMOLLM2_135M = BitNetConfig(vocab_size=49152, hidden_size=576, intermediate_size=1536, num_layers=30, num_heads=9,
                             num_kv_heads=3, head_dim=64, rope_theta=100000.0)
+# BitNet b1.58 2B4T architecture (the BitNet-2B shapes of configs[1]; the model of the MS BitNet GPU
+# end-to-end latency table, packages/inference/extern/BitNet/gpu/README.md:91-105): relu^2 MLP, GQA 20/5,
+# tied bf16 embedding head
+BITNET_2B = BitNetConfig(vocab_size=128256, hidden_size=2560, intermediate_size=6912, num_layers=30, num_heads=20,
+                         num_kv_heads=5, head_dim=128, rope_theta=500000.0, hidden_act="relu2")
 # Llama-3-8B architecture, every linear ternary (incl. the LM head)
 LLAMA3_8B = BitNetConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_layers=32, num_heads=32,
                          num_kv_heads=8, head_dim=128, rope_theta=500000.0, tie_embeddings=False,
