@@ -70,6 +70,48 @@ def build(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+ASAN_DIR = OBJ_DIR / "asan"
+ASAN_DRIVER_SRC = PKG_DIR.parent / "tests" / "asan" / "abi_driver.cpp"
+
+
+# Sources with host code only (no kernels): the entry points' validation and dispatch, the native engine.
+HOST_ONLY_SOURCES = ("api.hip", "engine.hip")
+
+
+def build_asan(verbose: bool = False) -> Path:
+    """Host-code AddressSanitizer build for the CPU tests of the C ABI: the host-only sources (argument
+    validation, dispatch, the engine's loader and state) compiled with ASan, linked with the kernel objects
+    of the product build (run build() first) into _build/asan/libwfbitnet_asan.so, and the driver
+    tests/asan/abi_driver.cpp linked against it.  Returns the driver's path."""
+    hipcc = _hipcc()
+    ASAN_DIR.mkdir(parents=True, exist_ok=True)
+    host = ["--offload-host-only", "-O1", "-g", "-fPIC", "-std=c++17", "-Wno-unused-command-line-argument"]
+    san = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+    objs = []
+    for src in sorted(CSRC.glob("*.hip")):
+        if src.name in HOST_ONLY_SOURCES:
+            obj = ASAN_DIR / (src.stem + ".o")
+            cmd = [hipcc, *host, *san, "-c", str(src), "-o", str(obj)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            _run(cmd)
+        else:
+            obj = OBJ_DIR / (src.stem + ".o")
+            if not obj.exists():
+                raise RuntimeError(f"{obj} missing: build() the library first")
+        objs.append(obj)
+    lib = ASAN_DIR / "libwfbitnet_asan.so"
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *san, *map(str, objs), "-o", str(lib)])
+    driver = ASAN_DIR / "abi_driver"
+    dobj = ASAN_DIR / "abi_driver.o"
+    _run([hipcc, *host, *san, f"-I{PKG_DIR.parent / 'include'}", "-c", str(ASAN_DRIVER_SRC), "-o", str(dobj)])
+    _run([hipcc, "--offload-host-only", *san, str(dobj), f"-L{ASAN_DIR}", "-lwfbitnet_asan",
+          f"-Wl,-rpath,{ASAN_DIR}", "-o", str(driver)])
+    return driver
+
+
 if __name__ == "__main__":
     path = build(verbose="-v" in sys.argv)
     print(path)
+    if "--asan" in sys.argv:
+        print(build_asan(verbose="-v" in sys.argv))

@@ -16,7 +16,8 @@
 //    with the reference's algorithm (bitnet_engine.cpp:208-253, 782-788) and replays the rest.
 // Every layer step issues exactly the calls the Python model's fused HIP backend issues for the same
 // rows (wrinklefree-monorepo_amd/model.py, HipBackend(fused=True) with bf16 glue), so both produce the
-// same tokens bit for bit.
+// same tokens bit for bit.  This file is host code only; the engine's own small kernels (embedding rows,
+// bf16 conversion at load, the decode step's commit, the hidden-state restore) are in engine_kernels.hip.
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -32,6 +33,7 @@
 #include <vector>
 
 #include "../../include/wfbitnet_engine.h"
+#include "engine_kernels.h"
 #include "wfb_common.h"
 
 namespace {
@@ -43,60 +45,6 @@ int efail(const std::string& msg) {
   return -1;
 }
 
-// ---- kernels ------------------------------------------------------------------------------------
-
-// out[r, :] = table[ids[r], :] (bf16 rows of h elements, h % 8 == 0).  Ids are checked on the host
-// (prompt) or come from the argmax (decode); the clamp keeps every read inside the table regardless.
-// One workgroup per row.
-__global__ void embed_rows_kernel(const uint16_t* __restrict__ table, int64_t vocab, int h,
-                                  const int64_t* __restrict__ ids, uint16_t* __restrict__ out) {
-  int64_t id = ids[blockIdx.x];
-  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
-  const uint4* src = reinterpret_cast<const uint4*>(table + id * h);
-  uint4* dst = reinterpret_cast<uint4*>(out + (int64_t)blockIdx.x * h);
-  for (int i = threadIdx.x; i < h / 8; i += blockDim.x) dst[i] = src[i];
-}
-
-// dst = bf16(src) for a float32 / float16 / bfloat16 source (SGLBITNT dtype ids 1 / 2 / 3);
-// round to nearest even, as torch's conversion.
-__global__ void to_bf16_kernel(const void* __restrict__ src, int dtype_id, int64_t n, uint16_t* __restrict__ dst) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    if (dtype_id == 3) {
-      dst[i] = reinterpret_cast<const uint16_t*>(src)[i];
-    } else {
-      const float v = dtype_id == 1 ? reinterpret_cast<const float*>(src)[i]
-                                    : wfb::f16_bits_to_f32(reinterpret_cast<const uint16_t*>(src)[i]);
-      dst[i] = wfb::f32_to_bf16_rne(v);
-    }
-  }
-}
-
-// End of a decode step: ctl = {token, position, count}.  The hidden state after the step (the token run
-// through every layer) goes to ring slot count % ring, the token to tokens[count] (when count < cap) and
-// to *last; then position and count advance.  One workgroup.
-__global__ void commit_kernel(int64_t* __restrict__ ctl, int32_t* __restrict__ tokens, int64_t cap,
-                              int32_t* __restrict__ last, const uint16_t* __restrict__ x, uint16_t* __restrict__ ring,
-                              int nring, int h) {
-  const int64_t count = ctl[2];
-  const uint4* src = reinterpret_cast<const uint4*>(x);
-  uint4* dst = reinterpret_cast<uint4*>(ring + (count % nring) * h);
-  for (int i = threadIdx.x; i < h / 8; i += blockDim.x) dst[i] = src[i];
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int32_t tok = (int32_t)ctl[0];
-    if (count >= 0 && count < cap) tokens[count] = tok;
-    *last = tok;
-    ctl[1] = ctl[1] + 1;
-    ctl[2] = count + 1;
-  }
-}
-
-// dst = src (h bf16 elements, h % 8 == 0): a ring slot back to the hidden state.
-__global__ void copy_row_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int h) {
-  for (int i = threadIdx.x; i < h / 8; i += blockDim.x)
-    reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
-}
-
 // ---- SGLBITNT file (format of SGB/sgl-kernel/csrc/inference/sglkernel_loader.h:1-20) -------------
 
 struct TensorRec {
@@ -105,9 +53,11 @@ struct TensorRec {
   bool has_scale = false;
   float scale = 1.0f;
   size_t offset = 0, nbytes = 0;
+  // element count, or -1 when it does not fit in 62 bits (a corrupt header)
   int64_t numel() const {
     int64_t n = 1;
-    for (int64_t d : shape) n *= d;
+    for (int64_t d : shape)
+      if (__builtin_mul_overflow(n, d, &n) || n > ((int64_t)1 << 62)) return -1;
     return n;
   }
 };
@@ -174,7 +124,8 @@ int open_model(const char* path, ModelFile& f) {
     if (t.has_scale && !take(&t.scale, 4)) return efail("Bad tensor header: " + name);
     if (!take(&nbytes, 8) || nbytes > f.size - at) return efail("Truncated tensor data: " + name);
     const int64_t esize = t.dtype == 0 ? 1 : t.dtype == 1 ? 4 : 2;
-    if ((uint64_t)(t.numel() * esize) != nbytes) return efail("Tensor size does not match its shape: " + name);
+    if (t.numel() < 0 || (uint64_t)(t.numel() * esize) != nbytes)
+      return efail("Tensor size does not match its shape: " + name);
     t.offset = at;
     t.nbytes = nbytes;
     at += nbytes;
@@ -443,9 +394,7 @@ int load_floats(Engine& e, Uploader& up, const ModelFile& f, const std::string& 
   for (int64_t off = 0; off < numel; off += per) {
     const int64_t len = std::min(per, numel - off);
     ECHECK(up.put(scratch, f.base + t->offset + off * esize, (size_t)(len * esize)));
-    hipLaunchKernelGGL(to_bf16_kernel, dim3((unsigned)std::min<int64_t>((len + 255) / 256, 4096)), dim3(256), 0, e.s,
-                       scratch, (int)t->dtype, len, dst + off);
-    HCHECK(hipGetLastError(), "to_bf16");
+    HCHECK(wfb::launch_to_bf16(scratch, (int)t->dtype, len, dst + off, e.s), "to_bf16");
   }
   return 0;
 }
@@ -589,13 +538,9 @@ int head(Engine& e, bool logits) {
 int body(Engine& e) {
   const Cfg& c = e.c;
   Acts& a = e.dec;
-  hipLaunchKernelGGL(embed_rows_kernel, dim3(1), dim3(256), 0, e.s, e.embed, c.vocab, (int)c.hidden,
-                     (const int64_t*)e.ctl, a.x);
-  HCHECK(hipGetLastError(), "embedding");
+  HCHECK(wfb::launch_embed_rows(e.embed, c.vocab, (int)c.hidden, e.ctl, 1, a.x, e.s), "embedding");
   for (const Layer& Ly : e.L) ECHECK(layer(e, Ly, a, 1, false));
-  hipLaunchKernelGGL(commit_kernel, dim3(1), dim3(256), 0, e.s, e.ctl, e.tokens, c.max_len, e.last_tok,
-                     (const uint16_t*)a.x, e.ring, kRing, (int)c.hidden);
-  HCHECK(hipGetLastError(), "commit");
+  HCHECK(wfb::launch_commit(e.ctl, e.tokens, c.max_len, e.last_tok, a.x, e.ring, kRing, (int)c.hidden, e.s), "commit");
   return 0;
 }
 
@@ -655,9 +600,7 @@ int prefill(Engine& e, const int32_t* ids, int64_t n) {
   Acts& a = e.pre;
   for (int64_t i = 0; i < n; ++i) e.ids_h[i] = ids[i];
   HCHECK(hipMemcpyAsync(a.ids, e.ids_h, n * sizeof(int64_t), hipMemcpyHostToDevice, e.s), "prompt upload");
-  hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)n), dim3(256), 0, e.s, e.embed, c.vocab, (int)c.hidden,
-                     (const int64_t*)a.ids, a.x);
-  HCHECK(hipGetLastError(), "embedding");
+  HCHECK(wfb::launch_embed_rows(e.embed, c.vocab, (int)c.hidden, a.ids, n, a.x, e.s), "embedding");
   for (const Layer& Ly : e.L) ECHECK(layer(e, Ly, a, n, true));
   HCHECK(hipMemcpyAsync(e.dec.x, a.x + (n - 1) * c.hidden, c.hidden * 2, hipMemcpyDeviceToDevice, e.s), "hidden copy");
   ECHECK(sync(e, "prefill"));
@@ -754,8 +697,11 @@ int create(Engine& e, const char* path, const BitNetConfig* user) {
   Cfg& c = e.c;
   const std::string& js = f.json;
   double v = 0;
+  // every size of the config is a positive integer well inside 32 bits (products of them stay in 64)
+  auto in_range = [](double x) { return x >= 1.0 && x <= (double)(1 << 30); };
   auto req = [&](const char* key, int64_t& out) -> int {
-    if (!json_num(js, key, v) || v <= 0) return efail(std::string("Invalid config: ") + key + " missing or 0");
+    if (!json_num(js, key, v) || !in_range(v))
+      return efail(std::string("Invalid config: ") + key + " missing, 0 or out of range");
     out = (int64_t)v;
     return 0;
   };
@@ -766,13 +712,14 @@ int create(Engine& e, const char* path, const BitNetConfig* user) {
   ECHECK(req("intermediate_size", c.inter));
   ECHECK(req("num_hidden_layers", c.layers));
   ECHECK(req("num_attention_heads", c.heads));
-  c.kv_heads = json_num(js, "num_key_value_heads", v) && v > 0 ? (int64_t)v : c.heads;
-  c.head_dim = json_num(js, "head_dim", v) && v > 0 ? (int64_t)v : c.hidden / c.heads;
-  if (json_num(js, "rope_theta", v) && v > 0) c.theta = v;
-  if (json_num(js, "rms_norm_eps", v)) c.rms_eps = (float)v;
-  if (json_num(js, "subln_eps", v)) c.subln_eps = (float)v;
-  c.max_len = json_num(js, "max_position_embeddings", v) && v > 0 ? (int64_t)v : 4096;
+  c.kv_heads = json_num(js, "num_key_value_heads", v) && in_range(v) ? (int64_t)v : c.heads;
+  c.head_dim = json_num(js, "head_dim", v) && in_range(v) ? (int64_t)v : c.hidden / c.heads;
+  if (json_num(js, "rope_theta", v) && v > 0 && std::isfinite(v)) c.theta = v;
+  if (json_num(js, "rms_norm_eps", v) && v >= 0 && v < 1) c.rms_eps = (float)v;
+  if (json_num(js, "subln_eps", v) && v >= 0 && v < 1) c.subln_eps = (float)v;
+  c.max_len = json_num(js, "max_position_embeddings", v) && in_range(v) ? (int64_t)v : 4096;
   if (user && user->max_seq_len > 0) c.max_len = user->max_seq_len;
+  if (c.vocab > (1 << 26) || c.layers > 4096) return efail("Invalid config: vocab_size or num_hidden_layers too large");
   const std::string act = json_raw(js, "hidden_act");
   if (act.empty() || act == "\"silu\"") {
     c.act = WFB_ACT_SILU;
@@ -787,6 +734,10 @@ int create(Engine& e, const char* path, const BitNetConfig* user) {
     if (p >= eos.size()) break;
     char* end = nullptr;
     const long long id = std::strtoll(eos.c_str() + p, &end, 10);
+    if (end == eos.c_str() + p) {  // a lone '-'
+      ++p;
+      continue;
+    }
     c.eos.push_back(id);
     p = (size_t)(end - eos.c_str());
   }
@@ -797,7 +748,7 @@ int create(Engine& e, const char* path, const BitNetConfig* user) {
   if (c.hidden % 8 != 0 || c.inter % 8 != 0 || c.hidden > WFB_NORM_MAX_H || c.inter > WFB_NORM_MAX_H ||
       c.qd() > WFB_NORM_MAX_H)
     return efail("hidden_size, intermediate_size and heads x head_dim must be multiples of 8 up to 16384");
-  if (c.max_len < 1 || c.max_len > (1 << 24)) return efail("max_seq_len out of range");
+  if (c.max_len < 1 || c.max_len > (1 << 20)) return efail("max_seq_len out of range (1 .. 1048576)");
   e.kpad_h = (c.hidden + WFB_QK_I2S - 1) / WFB_QK_I2S * WFB_QK_I2S;
   e.kpad_qd = (c.qd() + WFB_QK_I2S - 1) / WFB_QK_I2S * WFB_QK_I2S;
   e.kpad_f = (c.inter + WFB_QK_I2S - 1) / WFB_QK_I2S * WFB_QK_I2S;
@@ -941,8 +892,7 @@ int generate(Engine& e, const int32_t* ids, int32_t n, const SamplingParams* p, 
     if (eos_at >= 0) {
       // the reference stops before running the EOS token: state after token eos_at - 1
       const uint16_t* src = eos_at == 0 ? e.x_start : e.ring + ((eos_at - 1) % kRing) * e.c.hidden;
-      hipLaunchKernelGGL(copy_row_kernel, dim3(1), dim3(256), 0, e.s, src, e.dec.x, (int)e.c.hidden);
-      HCHECK(hipGetLastError(), "hidden restore");
+      HCHECK(wfb::launch_copy_row(src, e.dec.x, (int)e.c.hidden, e.s), "hidden restore");
       ECHECK(sync(e, "decode"));
       e.seq_len = n + eos_at;
     } else {
