@@ -104,7 +104,8 @@ int bitnet_prefill(BitNetEngine* engine, const int32_t* input_ids, int32_t num_t
 /* Pick the next token from the logits of the last token run (greedy or sampled per params), store it
  * in *output_id, and run it through the model at `position` (bitnet_engine.h:114-119;
  * bitnet_engine.cpp:851-893).  0 / -1 (no prompt run since creation or the last reset, position
- * outside [0, max_seq_len)). */
+ * outside [0, max_seq_len)).  A failure of the GPU work of a step or of a generation leaves no pending
+ * state: the next decode step needs a new prompt. */
 int bitnet_decode_step(BitNetEngine* engine, int32_t position, const SamplingParams* params, int32_t* output_id);
 
 /* Forget the sequence (bitnet_engine.h:124; bitnet_engine.cpp:895-900). */

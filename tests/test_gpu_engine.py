@@ -88,6 +88,23 @@ def test_engine_llama3_width_matches_the_model(pkg, dev, tmp_path):
         assert eng.generate(prompt[0].tolist(), max_tokens=40) == want
 
 
+def test_engine_bitnet_2b_full_size_matches_the_model(pkg, dev, tmp_path):
+    """The BitNet b1.58 2B4T shape at full size (30 layers, relu^2, GQA 20/5, 128256-row tied bf16 head): 64-token
+    prompt, 16 tokens -- the first row of the published A100 latency table -- equal to the Python model's."""
+    M = pkg.model
+    cfg = M.BITNET_2B
+    model = M.BitNetDecoder(cfg, seed=4, device=dev, dtype=torch.bfloat16, init_on_device=True,
+                            backend=M.HipBackend(out_dtype=torch.bfloat16, fused=True))
+    path = tmp_path / "bitnet2b.bin"
+    model.save_sglbitnt(path)
+    prompt = _prompt(cfg, 64, 12)
+    want = model.generate(prompt, 16, max_len=128)[0].tolist()
+    del model
+    torch.cuda.empty_cache()
+    with pkg.NativeEngine(str(path), max_seq_len=128) as eng:
+        assert eng.generate(prompt[0].tolist(), max_tokens=16) == want
+
+
 def test_prefill_and_decode_steps_equal_generate(pkg, dev, tmp_path):
     """bitnet_prefill then bitnet_decode_step(position = prompt + i): the reference's step contract (pick from
     the logits of the last token run, run the pick at `position`) gives generate's tokens."""

@@ -867,6 +867,7 @@ int generate(Engine& e, const int32_t* ids, int32_t n, const SamplingParams* p, 
     return efail("num_input_tokens + max_tokens (" + std::to_string((int64_t)n + max_new) + ") exceeds max_seq_len " +
                  std::to_string(e.c.max_len));
   ECHECK(prefill(e, ids, n));
+  e.have_hidden = false;  // until the steps below complete: a failure leaves no pending state
   std::vector<int32_t> out;
   out.reserve((size_t)max_new);
   if (p->temperature <= 0.0f) {
@@ -908,6 +909,7 @@ int generate(Engine& e, const int32_t* ids, int32_t n, const SamplingParams* p, 
       e.seq_len += 1;
     }
   }
+  e.have_hidden = true;
   res->num_tokens = (int32_t)out.size();
   res->output_ids = static_cast<int32_t*>(std::malloc(std::max<size_t>(out.size(), 1) * sizeof(int32_t)));
   if (!res->output_ids) return efail("out of host memory");
@@ -922,6 +924,7 @@ int decode_step(Engine& e, int32_t position, const SamplingParams* p, int32_t* o
   if (position < 0 || position >= e.c.max_len)
     return efail("position " + std::to_string(position) + " outside [0, max_seq_len " + std::to_string(e.c.max_len) +
                  ")");
+  e.have_hidden = false;  // until the step completes: a failure leaves no pending state
   if (p->temperature <= 0.0f) {
     ECHECK(set_ctl(e, 1, position));
     ECHECK(set_ctl(e, 2, 0));
@@ -936,6 +939,7 @@ int decode_step(Engine& e, int32_t position, const SamplingParams* p, int32_t* o
     *output_id = tok;
   }
   e.seq_len = (int64_t)position + 1;
+  e.have_hidden = true;
   return 0;
 }
 
