@@ -165,3 +165,40 @@ def test_tile_epilogue_out_types_match_oracle(pkg, dev, m, n, k, odt):
     pw, at, st = (torch.from_numpy(x).to(dev) for x in (packed, a, a_s))
     got = pkg.bitnet_linear(pw, at, float(ws), a_scale=st, out_dtype=odt)
     assert torch.equal(got.cpu(), want)
+
+
+@pytest.mark.parametrize("h,f,qn,kvn", [(2560, 6912, 2560, 640), (1024, 2816, 1024, 256)])
+def test_reference_fused_mlp_and_qkv_ops(pkg, dev, h, f, qn, kvn):
+    """bitnet_mlp_forward / bitnet_qkv_forward (the reference's batch-1 fused ops,
+    SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:150-375, schemas torch_extension_cpu.cpp:921-926) equal the
+    oracle chain bit for bit: per-token quantisation, exact accumulators, rescale by each projection's own
+    weight scale, relu(gate)^2 * up -> SubLN -> re-quantisation -> down.  Also through torch.ops.wfbitnet."""
+    rng = np.random.default_rng(h + f)
+    x = orc.outlier_hidden(rng, 1, h)[0]
+    xt = torch.from_numpy(x).to(dev)
+    # qkv
+    ws = [orc.pack_i2s(orc.random_ternary(rng, n, h)) for n in (qn, kvn, kvn)]
+    sc = [float(orc.log_uniform(rng)) for _ in range(3)]
+    q_ref, s_ref = orc.quantize_per_token(x[None, :])
+    outs = pkg.bitnet_qkv_forward(xt, *[torch.from_numpy(w).to(dev) for w in ws], *sc)
+    for o, w, s_w in zip(outs, ws, sc):
+        want = orc.rescale(orc.accumulate(w, q_ref), s_w, s_ref)[0]
+        assert o.dtype == torch.float32 and np.array_equal(o.cpu().numpy(), want)
+    outs2 = torch.ops.wfbitnet.bitnet_qkv_forward(xt[None, :], *[torch.from_numpy(w).to(dev) for w in ws], *sc)
+    assert all(torch.equal(a, b) for a, b in zip(outs, outs2))
+    # mlp
+    gw, uw = (orc.pack_i2s(orc.random_ternary(rng, f, h)) for _ in range(2))
+    dw = orc.pack_i2s(orc.random_ternary(rng, h, f))
+    gs, us, ds = (float(orc.log_uniform(rng)) for _ in range(3))
+    gamma = (1.0 + 0.1 * rng.standard_normal(f)).astype(np.float32)
+    gate = orc.rescale(orc.accumulate(gw, q_ref), gs, s_ref)
+    up = orc.rescale(orc.accumulate(uw, q_ref), us, s_ref)
+    h8, hs = orc.glu_rmsnorm_quant(gate, up, orc.ACT_RELU2, gamma, 1e-5)
+    want = orc.rescale(orc.accumulate(dw, h8), ds, hs)[0]
+    args = [torch.from_numpy(w).to(dev) for w in (gw, uw, dw)]
+    y = pkg.bitnet_mlp_forward(xt, *args, gs, us, ds, torch.from_numpy(gamma).to(dev), 1e-5)
+    assert y.shape == (h,) and np.array_equal(y.cpu().numpy(), want)
+    y2 = torch.ops.wfbitnet.bitnet_mlp_forward(xt, *args, gs, us, ds, torch.from_numpy(gamma).to(dev), 1e-5)
+    assert torch.equal(y, y2)
+    with pytest.raises(RuntimeError, match="1D or"):
+        pkg.bitnet_mlp_forward(xt.reshape(2, -1), *args, gs, us, ds, torch.from_numpy(gamma).to(dev), 1e-5)

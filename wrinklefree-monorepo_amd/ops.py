@@ -877,15 +877,67 @@ def bitnet_gemm(packed_weights: torch.Tensor, activations: torch.Tensor, scale: 
     return bitnet_linear(packed_weights, activations, scale, out_dtype=torch.float32)
 
 
-# ---- torch.ops.wfbitnet registrations (reference schemas, torch_extension_cpu.cpp:913-920) ------
+def _fused_input(name: str, x: torch.Tensor, packed: torch.Tensor) -> torch.Tensor:
+    """One token: a 1-D or [1, hidden] float input as a contiguous [1, hidden] row matching the weights."""
+    if not (x.dim() == 1 or (x.dim() == 2 and x.shape[0] == 1)):
+        raise RuntimeError(f"{name}: Input must be 1D or [1, hidden_size]")
+    h = x.numel()
+    if h % QK_I2_S != 0 or packed.dim() != 2 or packed.shape[1] * 4 != h:
+        raise ValueError(f"{name}: hidden size ({h}) must be a multiple of {QK_I2_S} and match the weights")
+    x = x.reshape(1, h)
+    return x if x.dtype in (torch.float32, torch.bfloat16, torch.float16) else x.float()
+
+
+def bitnet_qkv_forward(input: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor, v_weight: torch.Tensor,
+                       q_scale: float, k_scale: float, v_scale: float
+                       ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fused QKV of one token: the input quantised once (per-token absmax int8), then q / k / v = acc * a_scale *
+    w_scale, fp32 1-D outputs.  The op of SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:289-375 (schema
+    torch_extension_cpu.cpp:924-926) without its double sum(a) subtraction (anomaly ii): q = acc(q_weight) *
+    a_scale * q_scale exactly as bitnet_linear gives it."""
+    name = "bitnet_qkv_forward"
+    x = _fused_input(name, input, q_weight)
+    q8, a_s = quantize_activations_i8_per_token(x)
+    return tuple(bitnet_linear(w, q8, float(sc), a_scale=a_s, out_dtype=torch.float32).reshape(-1)
+                 for w, sc in ((q_weight, q_scale), (k_weight, k_scale), (v_weight, v_scale)))
+
+
+def bitnet_mlp_forward(input: torch.Tensor, gate_weight: torch.Tensor, up_weight: torch.Tensor,
+                       down_weight: torch.Tensor, gate_scale: float, up_scale: float, down_scale: float,
+                       ffn_sub_norm: torch.Tensor, eps: float) -> torch.Tensor:
+    """Fused BitNet MLP of one token: quantise the input once, gate / up = acc * a_scale * w_scale (fp32),
+    relu(gate)^2 * up, SubLN (ffn_sub_norm, eps), re-quantise, down = acc * h_scale * down_scale; fp32 [hidden].
+    The op of SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:150-287 (schema torch_extension_cpu.cpp:921-923)
+    with every projection scaled by its weight scale and sum(a) removed once (anomaly ii not copied)."""
+    name = "bitnet_mlp_forward"
+    x = _fused_input(name, input, gate_weight)
+    f = gate_weight.shape[0]
+    if up_weight.shape != gate_weight.shape or down_weight.dim() != 2 or down_weight.shape[1] * 4 != f:
+        raise ValueError(f"{name}: gate/up must be [intermediate, hidden/4] and down [hidden, intermediate/4]")
+    if ffn_sub_norm.numel() != f:
+        raise ValueError(f"{name}: ffn_sub_norm must have {f} elements")
+    q8, a_s = quantize_activations_i8_per_token(x)
+    gate = bitnet_linear(gate_weight, q8, float(gate_scale), a_scale=a_s, out_dtype=torch.float32)
+    up = bitnet_linear(up_weight, q8, float(up_scale), a_scale=a_s, out_dtype=torch.float32)
+    h8, h_s = glu_rmsnorm_quantize_i8(gate, up, "relu2", ffn_sub_norm.to(torch.float32).contiguous(), eps=float(eps))
+    return bitnet_linear(down_weight, h8, float(down_scale), a_scale=h_s, out_dtype=torch.float32).reshape(-1)
+
+
+# ---- torch.ops.wfbitnet registrations (reference schemas, torch_extension_cpu.cpp:913-926) ------
 
 _LIB_DEF = torch.library.Library("wfbitnet", "DEF")
 _LIB_DEF.define("bitnet_gemv(Tensor packed_weights, Tensor activations, float scale) -> Tensor")
 _LIB_DEF.define("bitnet_gemm(Tensor packed_weights, Tensor activations, float scale) -> Tensor")
 _LIB_DEF.define("bitnet_quantize_activations(Tensor input) -> (Tensor, Tensor)")
+_LIB_DEF.define("bitnet_mlp_forward(Tensor input, Tensor gate_weight, Tensor up_weight, Tensor down_weight, "
+                "float gate_scale, float up_scale, float down_scale, Tensor ffn_sub_norm, float eps) -> Tensor")
+_LIB_DEF.define("bitnet_qkv_forward(Tensor input, Tensor q_weight, Tensor k_weight, Tensor v_weight, "
+                "float q_scale, float k_scale, float v_scale) -> (Tensor, Tensor, Tensor)")
 _LIB_DEF.impl("bitnet_gemv", bitnet_gemv, "CUDA")
 _LIB_DEF.impl("bitnet_gemm", bitnet_gemm, "CUDA")
 _LIB_DEF.impl("bitnet_quantize_activations", quantize_activations_i8, "CUDA")
+_LIB_DEF.impl("bitnet_mlp_forward", bitnet_mlp_forward, "CUDA")
+_LIB_DEF.impl("bitnet_qkv_forward", bitnet_qkv_forward, "CUDA")
 
 
 def _gemv_meta(packed_weights, activations, scale):
@@ -900,6 +952,16 @@ def _quant_meta(x):
     return x.new_empty(x.shape, dtype=torch.int8), x.new_empty((1,), dtype=torch.float32)
 
 
+def _mlp_meta(input, gate_weight, up_weight, down_weight, gate_scale, up_scale, down_scale, ffn_sub_norm, eps):
+    return input.new_empty((input.numel(),), dtype=torch.float32)
+
+
+def _qkv_meta(input, q_weight, k_weight, v_weight, q_scale, k_scale, v_scale):
+    return tuple(input.new_empty((w.shape[0],), dtype=torch.float32) for w in (q_weight, k_weight, v_weight))
+
+
+_LIB_DEF.impl("bitnet_mlp_forward", _mlp_meta, "Meta")
+_LIB_DEF.impl("bitnet_qkv_forward", _qkv_meta, "Meta")
 _LIB_DEF.impl("bitnet_gemv", _gemv_meta, "Meta")
 _LIB_DEF.impl("bitnet_gemm", _gemm_meta, "Meta")
 _LIB_DEF.impl("bitnet_quantize_activations", _quant_meta, "Meta")
