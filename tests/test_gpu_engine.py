@@ -44,16 +44,17 @@ def _cases(M):
     }
 
 
-@pytest.mark.parametrize("case", ["smollm2", "relu2_ternary_head", "dense_head", "ffn_648"])
-@pytest.mark.parametrize("plen", [5, 40, 100])
+# the small models at every prompt path, the SmolLM2 shape at one
+_GREEDY_CASES = [("smollm2", 40)] + [(c, p) for c in ("relu2_ternary_head", "dense_head", "ffn_648") for p in (5, 40, 100)]
+
+
+@pytest.mark.parametrize("case,plen", _GREEDY_CASES)
 def test_engine_greedy_tokens_equal_the_model(pkg, dev, tmp_path, case, plen):
     """Prompt lengths 5 / 40 / 100 take the three prompt paths (norm fused into the linear for <= 16 rows,
     the gated gate|up epilogue for <= 64, the prefill GEMMs beyond); 70 decode steps cross two 32-step
     chunks."""
     M = pkg.model
     cfg, dense = _cases(M)[case]
-    if case == "smollm2" and plen != 40:
-        pytest.skip("SmolLM2 shape at one prompt length (the small models cover the paths)")
     model = _model(M, dev, cfg, seed=11, dense_head=dense)
     path = tmp_path / "m.bin"
     model.save_sglbitnt(path)
