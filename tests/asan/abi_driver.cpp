@@ -85,9 +85,13 @@ static void op_validation() {
   refused(wfb_rmsnorm_linear_i2s(fake(0x5000), WFB_BF16, 256, nullptr, WFB_F32, 1e-6f, 17, 256, W, 256, 256, 1, rows1,
                                  static_cast<const float*>(fake(0x4000)), nullptr, WFB_F32, 256, O, WFB_BF16, 256, nullptr),
           "fused norm rows");
-  refused(wfb_rmsnorm_linear_i2s(fake(0x5000), WFB_BF16, 8192, nullptr, WFB_F32, 1e-6f, 1, 8192, W, 256, 8192, 1, rows1,
+  refused(wfb_rmsnorm_linear_i2s(fake(0x5000), WFB_BF16, 8192, nullptr, WFB_F32, 1e-6f, 2, 8192, W, 256, 8192, 1, rows1,
                                  static_cast<const float*>(fake(0x4000)), nullptr, WFB_F32, 256, O, WFB_BF16, 256, nullptr),
-          "fused norm length");
+          "fused norm length at M 2");
+  refused(wfb_rmsnorm_linear_i2s(fake(0x5000), WFB_BF16, 16392, nullptr, WFB_F32, 1e-6f, 1, 16392, W, 256, 16512, 1,
+                                 rows1, static_cast<const float*>(fake(0x4000)), nullptr, WFB_F32, 256, O, WFB_BF16, 256,
+                                 nullptr),
+          "fused norm length past 16384");
   refused(wfb_linear_i2s_glu(W, 96, 256, A, 1, 256, nullptr, static_cast<const float*>(fake(0x4000)), WFB_ACT_SILU,
                              WFB_BF16, static_cast<float*>(fake(0x8000)), 48, nullptr),
           "gated half % 32");

@@ -76,6 +76,41 @@ def test_fused_matches_oracle(pkg, dev):
     assert np.array_equal(y.cpu().numpy(), y_ref)
 
 
+LONG_CASES = [
+    # h, rows, k, x dtype, gamma dtype, residual dtype: one token, 4096 < H <= K <= 16384 (the GEMV prologue)
+    (14336, [4096], 14336, torch.float32, torch.bfloat16, torch.bfloat16),    # Llama-3-8B down (fp32 gated row)
+    (6912, [2560], 6912, torch.float32, torch.bfloat16, torch.bfloat16),      # BitNet-2B down
+    (5000, [296, 40], 5120, torch.bfloat16, torch.float32, None),             # H < K, two segments, ragged rows
+    (16384, [256], 16384, torch.bfloat16, None, torch.float32),               # longest rows, no gamma
+    (4104, [1000], 4224, torch.float32, torch.float32, None),                 # shortest long rows
+]
+
+
+@pytest.mark.parametrize("case", LONG_CASES, ids=[f"h{c[0]}_n{sum(c[1])}_k{c[2]}_{str(c[3])[6:]}" for c in LONG_CASES])
+def test_fused_long_rows_equal_two_calls_and_oracle(pkg, dev, case):
+    """One token with rows longer than 4096: codes formed in the decode GEMV's prologue in the 256-thread
+    quantiser's order, so outputs equal wfb_rmsnorm_quant_i8 + the linear bit for bit, and the oracle."""
+    h, rows, k, xdt, gdt, rdt = case
+    rng = np.random.default_rng(h + k + sum(rows))
+    packed, x, g, scales = (t.to(dev) if t is not None else None for t in _inputs(rng, 1, h, rows, k, xdt, gdt))
+    assert pkg.rmsnorm_linear_supported(1, h, k) and not pkg.rmsnorm_linear_supported(2, h, k)
+    q, a_scale = pkg.rmsnorm_quantize_i8(x, g, eps=1e-6, k_pad=k)
+    if rdt is None:
+        y = pkg.rmsnorm_linear(x, g, packed, scales, rows, eps=1e-6, out_dtype=torch.float32)
+        y_ref = pkg.bitnet_linear_segmented(packed, rows, scales, q, a_scale=a_scale, out_dtype=torch.float32)
+    else:
+        res = torch.from_numpy(rng.standard_normal((1, sum(rows))).astype(np.float32)).to(rdt).to(dev)
+        y = pkg.rmsnorm_linear(x, g, packed, scales, eps=1e-6, residual=res.clone())
+        y_ref = pkg.bitnet_linear_residual(packed, q, scales, res.clone(), a_scale=a_scale)
+    assert torch.equal(y, y_ref)
+    q_ref, s_ref = orc.rmsnorm_quant(x.float().cpu().numpy(), None if g is None else g.float().cpu().numpy(), 1e-6,
+                                     k_pad=k)
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(a_scale.cpu().numpy(), s_ref)
+    if rdt is None:
+        acc = (q_ref.astype(np.float32) @ orc.unpack_i2s(packed.cpu().numpy()).astype(np.float32).T).astype(np.int64)
+        assert np.array_equal(y.cpu().numpy(), orc.rescale_segmented(acc, rows, scales.cpu().numpy(), s_ref))
+
+
 def test_fused_rejects_unsupported_sizes(pkg, dev):
     packed = torch.zeros((64, 1024), dtype=torch.uint8, device=dev)
     sc = torch.ones(1, device=dev)

@@ -420,9 +420,15 @@ void free_acts(Engine& e, Acts& a) {
   a = Acts{};
 }
 
-// The fused norm + linear launch takes these sizes (the Python backend's rmsnorm_linear_supported).
-bool fused_norm_ok(int64_t m, int64_t h, int64_t k) {
+// The fused norm + linear launches take these sizes (the Python backend's rmsnorm_linear_supported and
+// rmsnorm_linear_glu_supported): up to 16 rows of up to 4096 elements; the plain linear also one row of
+// 4097 .. 16384 elements.
+bool fused_glu_ok(int64_t m, int64_t h, int64_t k) {
   return m >= 1 && m <= 16 && h % 8 == 0 && h > 0 && h <= k && k <= 4096 && k % WFB_QK_I2S == 0;
+}
+bool fused_norm_ok(int64_t m, int64_t h, int64_t k) {
+  if (h % 8 != 0 || h <= 0 || h > k || k % WFB_QK_I2S != 0) return false;
+  return (m >= 1 && m <= 16 && k <= 4096) || (m == 1 && h > 4096 && k <= WFB_NORM_MAX_H);
 }
 
 // residual + linear(quantise(norm(x))) into the residual stream x (in place), one projection.
@@ -479,7 +485,7 @@ int layer(Engine& e, const Layer& Ly, Acts& a, int64_t m, bool prompt) {
   ECHECK(norm_linear_residual(e, a, m, a.att, WFB_BF16, qd, Ly.attn_sub, c.subln_eps, Ly.o, e.kpad_qd, Ly.scales + 3));
   // RMSNorm -> gate|up -> act(gate) * up -> SubLN -> down + residual
   if (m <= 64 && F % 32 == 0) {
-    if (fused_norm_ok(m, H, e.kpad_h)) {
+    if (fused_glu_ok(m, H, e.kpad_h)) {
       ECHECK(wcheck(wfb_rmsnorm_linear_i2s_glu(a.x, WFB_BF16, H, Ly.post_norm, WFB_BF16, c.rms_eps, m, H, Ly.gu, 2 * F,
                                                e.kpad_h, Ly.scales + 4, c.act, WFB_BF16, a.mid, F, st),
                     "rmsnorm_linear_glu"));

@@ -16,7 +16,12 @@
 // and acc = acc_a + acc_b / 4 + acc_c / 16 (all exact), then minus sum(a) of the lane's chunks.
 // Row totals are reduced over the L lanes of a group with DPP (quad_perm, row_half_mirror,
 // row_mirror) and, above 16 lanes, xor shuffles.
-#include "wfb_common.h"
+//
+// Norm prologue (XDT >= 0, rows longer than 4096): the workgroup forms the int8 codes of its M rows
+// itself from the float rows x (RMSNorm/SubLN + per-token absmax quantisation) into LDS and reads its
+// activation fragments from there -- bit for bit wfb_rmsnorm_quant_i8's codes and scales, because
+// threads 0..255 run that quantiser's own 256-thread path (quant_rows.h) on each row.
+#include "quant_rows.h"
 
 namespace wfb {
 
@@ -42,53 +47,75 @@ __device__ __forceinline__ int wave_sum(int v) {
   return v;
 }
 
-template <int M, int L, int CPL, int RP, int S, bool EXACT, bool PRE>
+template <int M, int L, int CPL, int RP, int S, bool EXACT, bool PRE, int XDT = -1>
 __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restrict__ W,
                                                           const int8_t* __restrict__ A, int64_t lda, int N,
-                                                          int C, Epilogue ep) {
+                                                          int C, Epilogue ep, NormSrc ns) {
   constexpr int RPG = 64 / L;  // rows per pass
   constexpr int RB = RP * RPG; // rows per workgroup
+  constexpr bool NORM = XDT >= 0;
+  constexpr int KMAX = 64 * L * CPL * S;  // the longest row the launch shape covers
   static_assert(RB <= 64 * S, "one thread per row in the epilogue");
+  static_assert(!NORM || S >= kTPB / 64, "the norm prologue runs on 256 threads");
   __shared__ int red[S][M][RB];
+  // norm prologue (one row): the row's elements, its codes and scale, the per-wave partials
+  static_assert(!NORM || M == 1, "the norm prologue takes one row");
+  __shared__ __attribute__((aligned(16))) float xs[NORM ? KMAX : 4];
+  __shared__ __attribute__((aligned(16))) int8_t codes[1][NORM ? KMAX : 16];
+  __shared__ float nscale[1], nred[kTPB / 64], mred[S];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int r_in = lane / L, s = lane % L;
+  const int t = threadIdx.x;
   const uint32_t row_bytes = (uint32_t)C * 16;
   const int row0 = blockIdx.x * RB;
   const int kc0 = w * (L * CPL);
   const buf_t wb = make_buf(W, (uint32_t)N * row_bytes);
-  const buf_t ab = make_buf(A, (uint32_t)((M - 1) * lda + (int64_t)C * 64));
+  const buf_t ab = make_buf(A, NORM ? 0u : (uint32_t)((M - 1) * lda + (int64_t)C * 64));
+
+  // norm prologue, first part: every thread loads two 8-element chunks of the row (chunks t and
+  // t + 64*S; zeros past h), issued before the weights
+  constexpr int PCH = NORM ? KMAX / (kVec * 64 * S) : 1;  // chunks per thread (2 for 16 lanes x 1 chunk)
+  static_assert(!NORM || PCH * kVec * 64 * S == KMAX, "chunks tile the row");
+  float xv[PCH][kVec];
+  if constexpr (NORM) {
+    const buf_t xb = row_buf<XDT>(ns.x, ns.h);
+#pragma unroll
+    for (int j = 0; j < PCH; ++j) load_row8_full<XDT, 0>(xb, xb, (t + j * 64 * S) * kVec, xv[j]);
+  }
 
   // a[m][i][q] = a_m[128b + 32q + j0 .. +15] for chunk c (b = c/2, j0 = 16*(c%2))
   v4i a[M][CPL][4];
-#pragma unroll
-  for (int m = 0; m < M; ++m)
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = kc0 + s + L * i;
-      const uint32_t off = (uint32_t)(m * lda) + 128 * (c >> 1) + 16 * (c & 1);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        a[m][i][q] = buf_load16(ab, off + 32 * q);
-        if (!EXACT && c >= C) a[m][i][q] = v4i{0, 0, 0, 0};
-      }
-    }
-
-  // sum(a) over the wave's K range: bytes loaded here, summed after the weight loads are issued
   constexpr int SB = (L * CPL + 15) / 16;  // 16-byte pieces per lane (L*CPL = 8: one 8-byte piece)
   v4i sv[M][SB];
+  if constexpr (!NORM) {
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    const uint32_t boff = (uint32_t)(64 * kc0 + lane * (L * CPL));
-    const bool in = EXACT || boff < (uint32_t)(64 * C);
-    const uint32_t off = (uint32_t)(m * lda) + boff;
+    for (int m = 0; m < M; ++m)
 #pragma unroll
-    for (int b = 0; b < SB; ++b) {
-      if constexpr (L * CPL == 8) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(ab, in ? (int)off : 0x7FFFFFF0, 0, 0);
-        sv[m][b] = v4i{(int)v[0], (int)v[1], 0, 0};
-      } else {
-        sv[m][b] = buf_load16(ab, in ? off + 16 * b : 0xFFFFFFF0u);
+      for (int i = 0; i < CPL; ++i) {
+        const int c = kc0 + s + L * i;
+        const uint32_t off = (uint32_t)(m * lda) + 128 * (c >> 1) + 16 * (c & 1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          a[m][i][q] = buf_load16(ab, off + 32 * q);
+          if (!EXACT && c >= C) a[m][i][q] = v4i{0, 0, 0, 0};
+        }
+      }
+
+    // sum(a) over the wave's K range: bytes loaded here, summed after the weight loads are issued
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint32_t boff = (uint32_t)(64 * kc0 + lane * (L * CPL));
+      const bool in = EXACT || boff < (uint32_t)(64 * C);
+      const uint32_t off = (uint32_t)(m * lda) + boff;
+#pragma unroll
+      for (int b = 0; b < SB; ++b) {
+        if constexpr (L * CPL == 8) {
+          const auto v = __builtin_amdgcn_raw_buffer_load_b64(ab, in ? (int)off : 0x7FFFFFF0, 0, 0);
+          sv[m][b] = v4i{(int)v[0], (int)v[1], 0, 0};
+        } else {
+          sv[m][b] = buf_load16(ab, in ? off + 16 * b : 0xFFFFFFF0u);
+        }
       }
     }
   }
@@ -108,13 +135,118 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   // Epilogue operands of the row this thread stores (thread t < RB stores row row0 + t): loaded here
   // (PRE) or after the final barrier.  With the activation-first load order, loading them here measured
   // faster on every BitNet-2B and Llama-3-8B shape (13824x2560 4.39 -> 4.23 us, 28672x4096 7.30 -> 7.08).
-  const int t = threadIdx.x;
   const int n = row0 + t;
   int toks[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) toks[m] = m;
   EpiCol<M> col;
   if (PRE && t < RB) col.load(ep, n, N, toks, M);
+
+  if constexpr (NORM) {
+    // norm prologue, second part: wfb_rmsnorm_quant_i8's 256-thread path (sum of squares of thread t < 256
+    // sequential over elements (it*256 + t)*8 + e, fixed butterfly, the 4 wave sums in wave order; then
+    // y = (x * r) * gamma, absmax scale, round-half-even codes; the element-wise part spread over all
+    // threads), codes into LDS with zeros from h to the end of the row
+    const int h = ns.h;
+    const int kpad = 64 * C;
+    float g[PCH][kVec];
+#pragma unroll
+    for (int j = 0; j < PCH; ++j) {
+      const int e0 = (t + j * 64 * S) * kVec;
+      if (ns.gamma == nullptr || e0 >= h) {
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) g[j][e] = 1.0f;
+      } else if (ns.gdt == WFB_F32) {
+        load8_buf<WFB_F32>(row_buf<WFB_F32>(ns.gamma, h), e0, g[j]);
+      } else {
+        load8_buf<WFB_BF16>(row_buf<WFB_BF16>(ns.gamma, h), e0, g[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < PCH; ++j) {
+      float* dst = &xs[(t + j * 64 * S) * kVec];
+      *reinterpret_cast<float4*>(dst) = make_float4(xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(xv[j][4], xv[j][5], xv[j][6], xv[j][7]);
+    }
+    __syncthreads();
+    if (t < kTPB) {
+      float ss = 0.0f;
+      // elements past h are zeros in the quantiser's sum (adding +0 to a sum of squares changes nothing), so
+      // only whole 8-element chunks below h are read: the last step may reach past the staged row
+      for (int it = 0; it * kTPB * kVec < h; ++it) {
+        const int e0 = (it * kTPB + t) * kVec;
+        if (e0 >= h) break;
+        const float4 p = *reinterpret_cast<const float4*>(&xs[e0]);
+        const float4 q = *reinterpret_cast<const float4*>(&xs[e0 + 4]);
+        const float v[kVec] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) ss = __fadd_rn(ss, __fmul_rn(v[e], v[e]));
+      }
+      ss = wave_sum_fixed(ss);
+      if (lane == 0) nred[w] = ss;
+    }
+    __syncthreads();
+    float tot = nred[0];
+#pragma unroll
+    for (int k = 1; k < kTPB / 64; ++k) tot = __fadd_rn(tot, nred[k]);
+    const float r = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)h), ns.eps)));
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PCH; ++j)
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) {
+        xv[j][e] = __fmul_rn(__fmul_rn(xv[j][e], r), g[j][e]);
+        mx = fmaxf(mx, fabsf(xv[j][e]));
+      }
+    mx = wave_max(mx);
+    if (lane == 0) mred[w] = mx;
+    __syncthreads();
+    mx = mred[0];
+#pragma unroll
+    for (int k = 1; k < S; ++k) mx = fmaxf(mx, mred[k]);
+    if (mx < 1e-6f) mx = 1.0f;
+    const float inv = __fdiv_rn(127.0f, mx);
+    if (t == 0) nscale[0] = __fdiv_rn(mx, 127.0f);
+#pragma unroll
+    for (int j = 0; j < PCH; ++j) {
+      const int e0 = (t + j * 64 * S) * kVec;
+      if (e0 < kpad) {
+        uint32_t lo = 0, hi = 0;  // zeros past h
+        if (e0 < h) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) lo |= (uint32_t)(quant_i8(xv[j][e], inv) & 0xff) << (8 * e);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) hi |= (uint32_t)(quant_i8(xv[j][4 + e], inv) & 0xff) << (8 * e);
+        }
+        *reinterpret_cast<uint2*>(&codes[0][e0]) = make_uint2(lo, hi);
+      }
+    }
+    __syncthreads();  // codes and the scale complete
+    // the activation fragments and sum(a) pieces from the LDS codes (same offsets as the global loads)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = kc0 + s + L * i;
+        const int off = 128 * (c >> 1) + 16 * (c & 1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          a[m][i][q] = (EXACT || c < C) ? *reinterpret_cast<const v4i*>(&codes[m][off + 32 * q]) : v4i{0, 0, 0, 0};
+      }
+      const int boff = 64 * kc0 + lane * (L * CPL);
+      const bool in = EXACT || boff < 64 * C;
+#pragma unroll
+      for (int b = 0; b < SB; ++b) {
+        if constexpr (L * CPL == 8) {
+          const uint2 v = in ? *reinterpret_cast<const uint2*>(&codes[m][boff]) : make_uint2(0, 0);
+          sv[m][b] = v4i{(int)v.x, (int)v.y, 0, 0};
+        } else {
+          sv[m][b] = in ? *reinterpret_cast<const v4i*>(&codes[m][boff + 16 * b]) : v4i{0, 0, 0, 0};
+        }
+      }
+      if (PRE && t < RB) col.as[m] = nscale[0];
+    }
+  }
 
   int suma[M];
 #pragma unroll
@@ -162,7 +294,7 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
       }
       uint64_t key;
       if constexpr (PRE) key = epi_store_key_r(ep, ws, col.as[m], bias, col.res[m], m, n, tot, valid);
-      else key = epi_store_key(ep, ws, epi_ascale(ep, m), bias, m, n, tot, valid);
+      else key = epi_store_key(ep, ws, NORM ? nscale[0] : epi_ascale(ep, m), bias, m, n, tot, valid);
       key = group_max_u64<64>(key);
       // slots are per 16 rows: the workgroup's first slot takes its maximum, the others key 0
       const int slot = row0 / 16 + t;
@@ -180,20 +312,31 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
 #pragma unroll
     for (int k = 1; k < S; ++k) tot += red[k][m][t];
     if constexpr (PRE) epi_store_r(ep, ws, col.as[m], bias, col.res[m], m, n, tot);
-    else epi_store(ep, ws, epi_ascale(ep, m), bias, m, n, tot);
+    else epi_store(ep, ws, NORM ? nscale[0] : epi_ascale(ep, m), bias, m, n, tot);
   }
 }
 
-template <int M, int L, int CPL, int RP, int S, bool PRE = true>
+template <int M, int L, int CPL, int RP, int S, bool PRE = true, int XDT = -1>
 hipError_t launch_cfg(const uint8_t* W, int n, int C, const int8_t* A, int64_t lda, const Epilogue& e,
-                      hipStream_t st) {
+                      hipStream_t st, const NormSrc& ns = NormSrc{}) {
   constexpr int RB = RP * (64 / L);
   const dim3 grid((n + RB - 1) / RB), block(64 * S);
   if (C == L * CPL * S)
-    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true, PRE>), grid, block, 0, st, W, A, lda, n, C, e);
+    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true, PRE, XDT>), grid, block, 0, st, W, A, lda, n, C, e, ns);
   else
-    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, false, PRE>), grid, block, 0, st, W, A, lda, n, C, e);
+    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, false, PRE, XDT>), grid, block, 0, st, W, A, lda, n, C, e, ns);
   return hipGetLastError();
+}
+
+// Norm prologue launches (rows of 4097 .. 16384 elements, the quantiser's 256-thread path): the launch
+// shapes of the codes GEMV at those K.
+template <int M, int XDT>
+hipError_t launch_norm_m(const uint8_t* W, int n, int C, const Epilogue& e, const NormSrc& ns, hipStream_t s) {
+  if (C <= 64) return hipErrorNotSupported;  // K <= 4096: the wave-order quantiser, not this path
+  if (C <= 112) return launch_cfg<M, 16, 1, 4, 7, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 224) return launch_cfg<M, 16, 1, 4, 14, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 256) return launch_cfg<M, 16, 1, 4, 16, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
+  return hipErrorNotSupported;
 }
 
 // Launch shape by K (C = K/64 chunks), from cold-HBM sweeps on MI355X at the BitNet-2B and Llama-3-8B
@@ -221,6 +364,15 @@ hipError_t launch_gemv_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   if (m == 1) return launch_m<1>(W, n, C, A, lda, e, s);
   if (m == 2) return launch_m<2>(W, n, C, A, lda, e, s);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv_i2s_norm(const uint8_t* W, int n, int k, int m, const Epilogue& e, const NormSrc& ns,
+                                hipStream_t s) {
+  const int C = k / 64;
+  if (m != 1) return hipErrorNotSupported;  // one row: the prologue keeps the row's elements in registers
+  if (ns.xdt == WFB_F32) return launch_norm_m<1, WFB_F32>(W, n, C, e, ns, s);
+  if (ns.xdt == WFB_BF16) return launch_norm_m<1, WFB_BF16>(W, n, C, e, ns, s);
+  return hipErrorNotSupported;
 }
 
 }  // namespace wfb

@@ -441,6 +441,11 @@ struct NormSrc {
   float eps;
   int h;
 };
+// One token (m == 1) whose RMSNorm/SubLN + quantisation runs in the decode GEMV's prologue (codes in
+// LDS, the quantiser's 256-thread order): 4096 < H <= K <= 16384, rows 16-byte aligned; ep.a_scale unused.
+// hipErrorNotSupported for other sizes.
+hipError_t launch_gemv_i2s_norm(const uint8_t* W, int n, int k, int m, const Epilogue& e, const NormSrc& ns,
+                                hipStream_t s);
 // M <= 16 tokens with both operands staged in LDS (skinny_lds.h); act 0 (plain) or a WFB_ACT_* gated
 // gate|up product; returns hipErrorNotSupported when the shape does not fit its LDS (the caller then
 // takes the register-operand kernels).  Needs N*K/4 and (M-1)*lda + K below 2^31.

@@ -35,8 +35,8 @@ from .sglbitnt import SGLBitNetFile, write_sglbitnt
 from .ops import (QK_I2_S, bitnet_linear, bitnet_linear_argmax, bitnet_linear_glu,
                   bitnet_linear_residual, bitnet_linear_segmented, glu_rmsnorm_quantize_i8, gqa_decode_attention,
                   gqa_prefill_attention,
-                  lm_head_argmax, pack_ternary_i2s, rmsnorm_linear, rmsnorm_linear_glu, rmsnorm_linear_preferred,
-                  rmsnorm_quantize_i8, rope_tables)
+                  lm_head_argmax, pack_ternary_i2s, rmsnorm_linear, rmsnorm_linear_glu, rmsnorm_linear_glu_supported,
+                  rmsnorm_linear_preferred, rmsnorm_quantize_i8, rope_tables)
 
 
 @dataclass(frozen=True)
@@ -143,12 +143,16 @@ class HipBackend:
             outs.append(y)
         return outs
 
-    def _fused_norm(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], n: int, k: int) -> bool:
-        """Norm + quant in the linear's prologue (one launch) where that is the faster choice."""
+    def _fused_norm(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], n: int, k: int,
+                    glu: bool = False) -> bool:
+        """Norm + quant in the linear's prologue (one launch) where that is the faster choice (``glu``: the
+        gated gate|up form, rmsnorm_linear_glu)."""
         if not self.fused or self.keep_acc or x.dim() != 2 or x.dtype not in (torch.float32, torch.bfloat16):
             return False
         if norm_weight is not None and norm_weight.dtype not in (torch.float32, torch.bfloat16):
             return False
+        if glu:
+            return rmsnorm_linear_glu_supported(x.shape[0], x.shape[1], k)
         gb = 0 if norm_weight is None else norm_weight.element_size()
         return rmsnorm_linear_preferred(x.shape[0], x.shape[1], n, k, gb)
 
@@ -201,7 +205,7 @@ class HipBackend:
         if (self.fused and not self.keep_acc and x.dim() == 2 and x.shape[0] <= 64 and up.out_features == half
                 and half % 32 == 0 and act in ("silu", "relu2")):
             qw, sc, _ = self._group([gate, up])
-            if self._fused_norm(x, norm_weight, 2 * half, gate.k_pad):
+            if self._fused_norm(x, norm_weight, 2 * half, gate.k_pad, glu=True):
                 mid = rmsnorm_linear_glu(x, norm_weight, qw, sc, act, eps=eps, mid_dtype=self.out_dtype)
             else:
                 q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=gate.k_pad)

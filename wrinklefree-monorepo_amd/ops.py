@@ -468,8 +468,17 @@ def bitnet_linear_residual(
 
 
 def rmsnorm_linear_supported(m: int, h: int, k: int, gamma_bytes: int = 2) -> bool:
-    """Whether rmsnorm_linear / rmsnorm_linear_glu take these sizes (decode batches of up to 16 rows, rows of
-    up to 4096 elements; ``gamma_bytes`` is kept for callers and no longer limits the size)."""
+    """Whether rmsnorm_linear takes these sizes: decode batches of up to 16 rows of up to 4096 elements (the
+    LDS-staged kernel's prologue), or one row of 4097 .. 16384 elements (the decode GEMV's prologue; the
+    gated rmsnorm_linear_glu keeps the first form).  ``gamma_bytes`` is kept for callers and no longer limits
+    the size."""
+    if h % 8 != 0 or not 0 < h <= k or k % QK_I2_S != 0:
+        return False
+    return (1 <= m <= 16 and k <= 4096) or (m == 1 and 4096 < h and k <= 16384)
+
+
+def rmsnorm_linear_glu_supported(m: int, h: int, k: int) -> bool:
+    """Whether rmsnorm_linear_glu takes these sizes (decode batches of up to 16 rows of up to 4096 elements)."""
     return 1 <= m <= 16 and h % 8 == 0 and 0 < h <= k <= 4096 and k % QK_I2_S == 0
 
 
@@ -508,8 +517,8 @@ def rmsnorm_linear(
         raise RuntimeError(f"{name}: scales must be fp32 with one element per segment")
     gbytes = 0 if weight is None else weight.element_size()
     if not rmsnorm_linear_supported(m, h, k, gbytes):
-        raise RuntimeError(f"{name}: M={m}, H={h}, K={k} outside the fused path (M <= 16, H % 8 == 0, "
-                           f"H <= K <= 4096)")
+        raise RuntimeError(f"{name}: M={m}, H={h}, K={k} outside the fused path (H % 8 == 0 and either M <= 16 with "
+                           f"H <= K <= 4096, or M == 1 with 4096 < H <= K <= 16384)")
     dev = _require_gpu(name, x, weight, packed_weights, scales, residual)
     if weight is not None and (weight.numel() != h or weight.dtype not in (torch.float32, torch.bfloat16)):
         raise RuntimeError(f"{name}: weight must be float32/bfloat16 with {h} elements")
@@ -541,7 +550,7 @@ def rmsnorm_linear_glu(
     act: str = "silu", eps: float = 1e-6, mid_dtype: torch.dtype = torch.bfloat16, out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """RMSNorm + per-token int8 quantisation + gate|up BitLinear + act(gate) * up in one launch (decode
-    batches, ``rmsnorm_linear_supported``): fp32 [M, half], equal, bit for bit, to ``rmsnorm_quantize_i8``
+    batches, ``rmsnorm_linear_glu_supported``): fp32 [M, half], equal, bit for bit, to ``rmsnorm_quantize_i8``
     followed by ``bitnet_linear_glu``.
 
     x: float32/bfloat16 [M, H]; weight: [H] or None; packed_weights: uint8 gate|up [2 * half, K/4] (half %
@@ -562,7 +571,7 @@ def rmsnorm_linear_glu(
         raise ValueError(f"{name}: gate|up rows ({n}) must be 2 x a multiple of 32")
     if scales.dtype != torch.float32 or scales.numel() != 2:
         raise RuntimeError(f"{name}: scales must be fp32 [2] (gate, up)")
-    if not rmsnorm_linear_supported(m, h, k):
+    if not rmsnorm_linear_glu_supported(m, h, k):
         raise RuntimeError(f"{name}: M={m}, H={h}, K={k} outside the fused path (M <= 16, H % 8 == 0, H <= K <= 4096)")
     dev = _require_gpu(name, x, weight, packed_weights, scales)
     if weight is not None and (weight.numel() != h or weight.dtype not in (torch.float32, torch.bfloat16)):
