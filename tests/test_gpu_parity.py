@@ -164,6 +164,34 @@ def test_decode_gemv_2b_shapes(pkg, dev, n, k, m):
     _check_linear(pkg, dev, packed, a, orc.log_uniform(rng), orc.log_uniform(rng, m), kernel="gemv")
 
 
+# (n, k): grids of 2048 workgroups or fewer stage each wave's activation slice in LDS; above that (70000 x
+# 4096: 2188 workgroups of 32 rows, 40000 x 2560: 2500, 36000 x 640: 2250 with masked chunks, 33000 x 1024:
+# 2063) the fragments come straight from global memory
+@pytest.mark.parametrize("n,k", [(2560, 2560), (4099, 640), (70000, 4096), (40000, 2560), (36000, 640), (33000, 1024)])
+@pytest.mark.parametrize("m", [1, 2])
+def test_decode_gemv_epilogue_operands_and_grid_sizes(pkg, dev, n, k, m):
+    """The M <= 2 GEMV on both activation paths: accumulators and bf16 outputs exact, a bias in each float
+    dtype and a residual in either dtype (operands loaded as raw bits at kernel entry, converted at the
+    epilogue) equal to the oracle's rescale."""
+    rng = np.random.default_rng(9000 + m + n + k)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    ws, a_s = orc.log_uniform(rng), orc.log_uniform(rng, m)
+    _check_linear(pkg, dev, packed, a, ws, a_s, kernel="gemv", check_fp32=False)
+    acc = _ref_acc(packed, a)
+    pw, pa, ps = _t(packed, dev), _t(a, dev), _t(a_s, dev)
+    for bdt in (torch.float32, torch.bfloat16, torch.float16):
+        bias = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(bdt)
+        y32 = pkg.bitnet_linear(pw, pa, float(ws), a_scale=ps, bias=bias.to(dev), out_dtype=torch.float32,
+                                kernel="gemv")
+        assert np.array_equal(y32.cpu().numpy(), orc.rescale(acc, ws, a_s, bias.float().numpy())), bdt
+    for rdt in (torch.float32, torch.bfloat16):
+        res = torch.from_numpy(rng.standard_normal((m, n)).astype(np.float32)).to(rdt)
+        want = torch.from_numpy(orc.rescale(acc, np.float32(ws), a_s) + res.float().numpy()).to(rdt)
+        got = pkg.bitnet_linear_residual(pw, pa, float(ws), res.to(dev), a_scale=ps)
+        assert torch.equal(got.cpu(), want), rdt
+
+
 @pytest.mark.parametrize("n,k", [(2560, 2560), (2560, 6912), (13824, 2560)])
 @pytest.mark.parametrize("m", [1, 2, 4, 8, 16, 32, 64])
 def test_batched_sweep_mfma(pkg, dev, n, k, m):

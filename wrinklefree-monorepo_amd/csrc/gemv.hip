@@ -47,7 +47,7 @@ __device__ __forceinline__ int wave_sum(int v) {
   return v;
 }
 
-template <int M, int L, int CPL, int RP, int S, bool EXACT, bool PRE, int XDT = -1>
+template <int M, int L, int CPL, int RP, int S, bool EXACT, bool PRE, int XDT = -1, bool STAGE = true>
 __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restrict__ W,
                                                           const int8_t* __restrict__ A, int64_t lda, int N,
                                                           int C, Epilogue ep, NormSrc ns) {
@@ -63,6 +63,9 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   __shared__ __attribute__((aligned(16))) float xs[NORM ? KMAX : 4];
   __shared__ __attribute__((aligned(16))) int8_t codes[1][NORM ? KMAX : 16];
   __shared__ float nscale[1], nred[kTPB / 64], mred[S];
+  constexpr int XA = 64 * L * CPL;  // activation bytes of a wave's K range, per token
+  constexpr bool XS = !NORM && STAGE;
+  __shared__ __attribute__((aligned(16))) int8_t xa[XS ? S : 1][XS ? M : 1][XS ? XA : 16];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int r_in = lane / L, s = lane % L;
@@ -88,7 +91,8 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   v4i a[M][CPL][4];
   constexpr int SB = (L * CPL + 15) / 16;  // 16-byte pieces per lane (L*CPL = 8: one 8-byte piece)
   v4i sv[M][SB];
-  if constexpr (!NORM) {
+  if constexpr (!NORM && !STAGE) {
+    // grids of many rounds: the fragments of the lane's chunks straight from global memory
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
@@ -101,8 +105,13 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
           if (!EXACT && c >= C) a[m][i][q] = v4i{0, 0, 0, 0};
         }
       }
-
-    // sum(a) over the wave's K range: bytes loaded here, summed after the weight loads are issued
+  }
+  if constexpr (!NORM) {
+    // the wave's activation slice (bytes 64*kc0 .. 64*(kc0 + L*CPL) of each token row), one piece per
+    // lane: summed for sum(a) and (STAGE) copied into the wave's LDS slice, from which the chunk fragments
+    // are read.  Loading the fragments from global memory instead -- every lane of a row group 4 x 16
+    // bytes of the same few lines, in every workgroup -- measured 0.5 us slower at 13824x2560 (864
+    // workgroups) on MI355X, the staging 5% slower at 128256x4096 (4008 workgroups, many rounds).
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const uint32_t boff = (uint32_t)(64 * kc0 + lane * (L * CPL));
@@ -132,15 +141,44 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
       if (!EXACT && c >= C) wv[p][i] = v4i{0, 0, 0, 0};
     }
   }
-  // Epilogue operands of the row this thread stores (thread t < RB stores row row0 + t): loaded here
-  // (PRE) or after the final barrier.  With the activation-first load order, loading them here measured
-  // faster on every BitNet-2B and Llama-3-8B shape (13824x2560 4.39 -> 4.23 us, 28672x4096 7.30 -> 7.08).
+  // Epilogue operands of the row this thread stores (thread t < RB stores row row0 + t): loaded below,
+  // behind the weight loads (PRE), or after the final barrier.  With the activation-first load order,
+  // loading them early measured faster on every BitNet-2B and Llama-3-8B shape (13824x2560 4.39 -> 4.23 us,
+  // 28672x4096 7.30 -> 7.08).
   const int n = row0 + t;
   int toks[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) toks[m] = m;
   EpiCol<M> col;
-  if (PRE && t < RB) col.load(ep, n, N, toks, M);
+
+  if constexpr (!NORM && STAGE) {
+    // the slice into the wave's LDS (waits only for the slice loads, issued before the weights), then the
+    // fragments of the lane's chunks; writer and readers are lanes of one wave
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int b = 0; b < SB; ++b) {
+        if constexpr (L * CPL == 8)
+          *reinterpret_cast<uint2*>(&xa[w][m][lane * 8]) = make_uint2((uint32_t)sv[m][b][0], (uint32_t)sv[m][b][1]);
+        else
+          *reinterpret_cast<v4i*>(&xa[w][m][lane * (L * CPL) + 16 * b]) = sv[m][b];
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = kc0 + s + L * i;
+        const int off = 128 * ((c - kc0) >> 1) + 16 * (c & 1);  // kc0 is even
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[m][i][q] = *reinterpret_cast<const v4i*>(&xa[w][m][off + 32 * q]);
+      }
+  }
+  // issued after the slice copy: issued before it, the copy's wait for the slice also covered the first
+  // weight load in the storing wave (its counter holds these loads too)
+  if (PRE && t < RB) col.load_raw(ep, n, N, toks, M);
 
   if constexpr (NORM) {
     // norm prologue, second part: wfb_rmsnorm_quant_i8's 256-thread path (sum of squares of thread t < 256
@@ -279,6 +317,7 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
     }
   }
   __syncthreads();
+  if constexpr (PRE) col.finish(ep);
   if (ep.amax) {  // argmax epilogue: the RB <= 64 rows sit in wave 0
     if (t >= 64) return;
     const bool valid = t < RB && n < N;
@@ -316,11 +355,26 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   }
 }
 
-template <int M, int L, int CPL, int RP, int S, bool PRE = true, int XDT = -1>
+// Grids above this many workgroups (many rounds over the 256 CUs: the LM-head shapes) load the activation
+// fragments directly (STAGE = false) where the launch shape has that variant (WIDE).
+constexpr int kStageMaxGrid = 2048;
+
+template <int M, int L, int CPL, int RP, int S, bool PRE = true, int XDT = -1, bool WIDE = false>
 hipError_t launch_cfg(const uint8_t* W, int n, int C, const int8_t* A, int64_t lda, const Epilogue& e,
                       hipStream_t st, const NormSrc& ns = NormSrc{}) {
   constexpr int RB = RP * (64 / L);
   const dim3 grid((n + RB - 1) / RB), block(64 * S);
+  if constexpr (WIDE && XDT < 0) {
+    if ((int)grid.x > kStageMaxGrid) {
+      if (C == L * CPL * S)
+        hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true, PRE, XDT, false>), grid, block, 0, st, W, A, lda, n,
+                           C, e, ns);
+      else
+        hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, false, PRE, XDT, false>), grid, block, 0, st, W, A, lda,
+                           n, C, e, ns);
+      return hipGetLastError();
+    }
+  }
   if (C == L * CPL * S)
     hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true, PRE, XDT>), grid, block, 0, st, W, A, lda, n, C, e, ns);
   else
@@ -344,11 +398,11 @@ hipError_t launch_norm_m(const uint8_t* W, int n, int C, const Epilogue& e, cons
 // 4.23 us against 4; 4 at K = 4096), 16 lanes for longer rows.  Other K take the nearest shape with masking.
 template <int M>
 hipError_t launch_m(const uint8_t* W, int n, int C, const int8_t* A, int64_t lda, const Epilogue& e, hipStream_t s) {
-  if (C <= 8) return launch_cfg<M, 8, 1, 2, 1>(W, n, C, A, lda, e, s);
-  if (C <= 16) return launch_cfg<M, 8, 1, 2, 2>(W, n, C, A, lda, e, s);
-  if (C <= 24) return launch_cfg<M, 8, 1, 2, 3>(W, n, C, A, lda, e, s);
-  if (C <= 40) return launch_cfg<M, 8, 1, 2, 5>(W, n, C, A, lda, e, s);
-  if (C <= 64) return launch_cfg<M, 8, 1, 4, 8>(W, n, C, A, lda, e, s);
+  if (C <= 8) return launch_cfg<M, 8, 1, 2, 1, true, -1, true>(W, n, C, A, lda, e, s);
+  if (C <= 16) return launch_cfg<M, 8, 1, 2, 2, true, -1, true>(W, n, C, A, lda, e, s);
+  if (C <= 24) return launch_cfg<M, 8, 1, 2, 3, true, -1, true>(W, n, C, A, lda, e, s);
+  if (C <= 40) return launch_cfg<M, 8, 1, 2, 5, true, -1, true>(W, n, C, A, lda, e, s);
+  if (C <= 64) return launch_cfg<M, 8, 1, 4, 8, true, -1, true>(W, n, C, A, lda, e, s);
   if (C <= 112) return launch_cfg<M, 16, 1, 4, 7>(W, n, C, A, lda, e, s);
   if (C <= 224) return launch_cfg<M, 16, 1, 4, 14>(W, n, C, A, lda, e, s);
   if (C <= 256) return launch_cfg<M, 16, 1, 4, 16>(W, n, C, A, lda, e, s);

@@ -341,6 +341,45 @@ struct EpiCol {
       load_res_col<T>(e, tok, ok, n, res);
     }
   }
+  // load() with the bias and the residuals kept as the bits loaded, converted by finish() at the
+  // epilogue: a conversion right after a load inside a dtype branch makes the wave wait for every load
+  // in flight at that point (the weight stream included, in the GEMV's storing wave)
+  uint32_t braw = 0, rraw[T], okm = 0;
+  __device__ __forceinline__ void load_raw(const Epilogue& e, int n, int N, const int (&tok)[T], int M) {
+#pragma unroll
+    for (int j = 0; j < T; ++j) as[j] = res[j] = 0.0f, rraw[j] = 0;
+    if (n >= N) return;
+    ws = epi_wscale(e, n);
+    if (e.bias) {
+      if (e.bias_dtype == WFB_F32) braw = reinterpret_cast<const uint32_t*>(e.bias)[n];
+      else braw = reinterpret_cast<const uint16_t*>(e.bias)[n];
+    }
+#pragma unroll
+    for (int j = 0; j < T; ++j)
+      if (tok[j] < M) as[j] = epi_ascale(e, tok[j]);
+    if (e.res) {
+      // every load issued before the first use; entries not wanted load element 0 (in bounds whenever a
+      // residual is given) and are zeroed by finish()
+#pragma unroll
+      for (int j = 0; j < T; ++j) {
+        const int64_t off = tok[j] < M ? (int64_t)tok[j] * e.ldr + n : 0;
+        if (e.res_dtype == WFB_F32) rraw[j] = reinterpret_cast<const uint32_t*>(e.res)[off];
+        else rraw[j] = reinterpret_cast<const uint16_t*>(e.res)[off];
+        okm |= tok[j] < M ? 1u << j : 0u;
+      }
+    }
+  }
+  __device__ __forceinline__ void finish(const Epilogue& e) {
+    if (e.bias)
+      bias = e.bias_dtype == WFB_F32    ? __uint_as_float(braw)
+             : e.bias_dtype == WFB_BF16 ? bf16_bits_to_f32((uint16_t)braw)
+                                        : f16_bits_to_f32((uint16_t)braw);
+#pragma unroll
+    for (int j = 0; j < T; ++j) {
+      const float v = e.res_dtype == WFB_F32 ? __uint_as_float(rraw[j]) : bf16_bits_to_f32((uint16_t)rraw[j]);
+      res[j] = (okm >> j) & 1u ? v : 0.0f;
+    }
+  }
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
