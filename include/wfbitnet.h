@@ -327,9 +327,9 @@ int wfb_gqa_prefill_attention(const void* q, int64_t ldq, const void* k_new, int
  *                                                         wfb_linear_i2s with a device scale)
  *         (+ residual, exactly as wfb_linear_i2s_residual when residual is not NULL)
  * x [M, H] (x_dtype WFB_F32 or WFB_BF16, row stride ldx elements, rows 16-byte aligned), gamma [H]
- * (WFB_F32 or WFB_BF16, 16-byte aligned) or NULL; H % 8 == 0 and either 1 <= M <= 16 with H <= K <= 4096
- * (the LDS-staged batched kernel's prologue) or M == 1 with 4096 < H <= K <= 16384 (the decode GEMV's
- * prologue: every workgroup forms the row's codes in LDS in the quantiser's 256-thread order); N * K / 4
+ * (WFB_F32 or WFB_BF16, 16-byte aligned) or NULL; H % 8 == 0, H <= K and either M == 1 with K <= 16384
+ * (the decode GEMV's prologue: every workgroup forms the row's codes in LDS in the quantiser's order for
+ * the row length) or 2 <= M <= 16 with K <= 4096 (the LDS-staged batched kernel's prologue); N * K / 4
  * below 2^31; other sizes take the two-call path.  seg_rows /
  * w_scales_dev as wfb_linear_i2s_segmented (n_seg = 1 with seg_rows NULL: one segment of N rows).
  * out [M, N] WFB_F32 or WFB_BF16 (row stride ldo); residual [M, N] WFB_F32 or WFB_BF16 (row stride ldr)

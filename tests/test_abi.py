@@ -235,8 +235,8 @@ def test_rmsnorm_linear_argument_errors(pkg):
     assert st(g_dt=2) == -1 and "gamma dtype" in pkg._lib.last_error()
     assert st(m=17) == -1 and "M (17)" in pkg._lib.last_error()
     assert st(h=4104, k=4224) == -1 and "needs M == 1" in pkg._lib.last_error()  # long rows: one token only
-    assert st(m=1, h=4096, k=4224) == -1 and "needs M == 1" in pkg._lib.last_error()  # ... with H > 4096
-    assert st(m=1, h=16392, k=16512) == -1 and "needs M == 1" in pkg._lib.last_error()
+    assert st(m=2, h=4096, k=4224) == -1 and "needs M == 1" in pkg._lib.last_error()  # ... whatever H
+    assert st(m=1, h=16392, k=16512) == -1 and "needs M == 1" in pkg._lib.last_error()  # ... up to 16384
     assert st(h=4100, k=4224) == -1 and "H % 8 == 0" in pkg._lib.last_error()
     assert st(n_seg=2) == -1 and "seg_rows" in pkg._lib.last_error()
     assert st(n_seg=2, segp=ctypes.cast(seg, vp), n=136) == -1 and "sum to 128" in pkg._lib.last_error()

@@ -76,8 +76,16 @@ def test_fused_matches_oracle(pkg, dev):
     assert np.array_equal(y.cpu().numpy(), y_ref)
 
 
-LONG_CASES = [
-    # h, rows, k, x dtype, gamma dtype, residual dtype: one token, 4096 < H <= K <= 16384 (the GEMV prologue)
+ONE_TOKEN_CASES = [
+    # h, rows, k, x dtype, gamma dtype, residual dtype: one token (the GEMV prologue; the quantiser's
+    # one-wave order up to 4096 elements, its 256-thread order beyond)
+    (4096, [4096, 1024, 1024], 4096, torch.bfloat16, torch.bfloat16, None),   # Llama-3-8B q|k|v (8 waves)
+    (4096, [4096], 4096, torch.bfloat16, torch.bfloat16, torch.bfloat16),     # Llama-3-8B o + residual
+    (2560, [2560, 640, 640], 2560, torch.bfloat16, torch.bfloat16, None),     # BitNet-2B q|k|v (5 waves)
+    (576, [576], 640, torch.float32, None, torch.float32),                    # SmolLM2 o, K padded (2 waves)
+    (1536, [576], 1536, torch.bfloat16, torch.float32, torch.bfloat16),       # SmolLM2 down (3 waves)
+    (256, [104, 24], 256, torch.bfloat16, torch.bfloat16, None),              # one wave, two segments
+    (4000, [136], 4224, torch.float32, torch.bfloat16, None),                 # H <= 4096 < K: one-wave order, 16 lanes
     (14336, [4096], 14336, torch.float32, torch.bfloat16, torch.bfloat16),    # Llama-3-8B down (fp32 gated row)
     (6912, [2560], 6912, torch.float32, torch.bfloat16, torch.bfloat16),      # BitNet-2B down
     (5000, [296, 40], 5120, torch.bfloat16, torch.float32, None),             # H < K, two segments, ragged rows
@@ -86,14 +94,15 @@ LONG_CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", LONG_CASES, ids=[f"h{c[0]}_n{sum(c[1])}_k{c[2]}_{str(c[3])[6:]}" for c in LONG_CASES])
-def test_fused_long_rows_equal_two_calls_and_oracle(pkg, dev, case):
-    """One token with rows longer than 4096: codes formed in the decode GEMV's prologue in the 256-thread
-    quantiser's order, so outputs equal wfb_rmsnorm_quant_i8 + the linear bit for bit, and the oracle."""
+@pytest.mark.parametrize("case", ONE_TOKEN_CASES,
+                         ids=[f"h{c[0]}_n{sum(c[1])}_k{c[2]}_{str(c[3])[6:]}" for c in ONE_TOKEN_CASES])
+def test_fused_one_token_equals_two_calls_and_oracle(pkg, dev, case):
+    """One token: codes formed in the decode GEMV's prologue in the quantiser's order for the row length,
+    so outputs equal wfb_rmsnorm_quant_i8 + the linear bit for bit, and the oracle."""
     h, rows, k, xdt, gdt, rdt = case
     rng = np.random.default_rng(h + k + sum(rows))
     packed, x, g, scales = (t.to(dev) if t is not None else None for t in _inputs(rng, 1, h, rows, k, xdt, gdt))
-    assert pkg.rmsnorm_linear_supported(1, h, k) and not pkg.rmsnorm_linear_supported(2, h, k)
+    assert pkg.rmsnorm_linear_supported(1, h, k) and pkg.rmsnorm_linear_supported(2, h, k) == (k <= 4096)
     q, a_scale = pkg.rmsnorm_quantize_i8(x, g, eps=1e-6, k_pad=k)
     if rdt is None:
         y = pkg.rmsnorm_linear(x, g, packed, scales, rows, eps=1e-6, out_dtype=torch.float32)

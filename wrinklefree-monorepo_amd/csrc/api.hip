@@ -453,11 +453,10 @@ int wfb_rmsnorm_linear_i2s(const void* x, int x_dtype, int64_t ldx, const void* 
   if (h <= 0 || h % 8 != 0 || h > k || k % WFB_QK_I2S != 0)
     return fail(WFB_EINVAL, "%s: need H %% 8 == 0, H <= K, K %% %d == 0 (got H=%lld K=%lld)", name, WFB_QK_I2S,
                 (long long)h, (long long)k);
-  // K <= 4096: the LDS-staged batched kernel's prologue (the quantiser's one-wave-per-row order);
-  // longer rows: one token through the GEMV's prologue (the quantiser's 256-thread order, used for H > 4096)
-  const bool long_rows = k > 4096;
-  if (long_rows && !(m <= 1 && h > 4096 && k <= WFB_NORM_MAX_H))
-    return fail(WFB_EINVAL, "%s: K > 4096 needs M == 1 and 4096 < H <= K <= %d (got M=%lld H=%lld K=%lld)", name,
+  // one token: the GEMV's prologue (rows up to WFB_NORM_MAX_H; the quantiser's one-wave order for H <= 4096,
+  // its 256-thread order beyond); 2..16 tokens with K <= 4096: the LDS-staged batched kernel's prologue
+  if (k > 4096 && !(m <= 1 && k <= WFB_NORM_MAX_H))
+    return fail(WFB_EINVAL, "%s: K > 4096 needs M == 1 and K <= %d (got M=%lld H=%lld K=%lld)", name,
                 WFB_NORM_MAX_H, (long long)m, (long long)h, (long long)k);
   if (n <= 0 || n > INT32_MAX / 2 || n * (k / 4) > INT32_MAX)
     return fail(WFB_EINVAL, "%s: bad N (%lld) for K %lld", name, (long long)n, (long long)k);
@@ -497,7 +496,7 @@ int wfb_rmsnorm_linear_i2s(const void* x, int x_dtype, int64_t ldx, const void* 
   e.res_dtype = residual_dtype;
   e.ldr = ldr;
   const wfb::NormSrc ns{x, x_dtype, ldx, gamma, gamma_dtype, eps, (int)h};
-  if (long_rows)
+  if (m == 1)
     return hip_status(wfb::launch_gemv_i2s_norm(qweight, (int)n, (int)k, (int)m, e, ns, as_stream(stream)), name);
   return hip_status(wfb::launch_skinny_lds(qweight, (int)n, (int)k, nullptr, (int)m, 0, e, 0, as_stream(stream), ns),
                     name);

@@ -428,7 +428,7 @@ bool fused_glu_ok(int64_t m, int64_t h, int64_t k) {
 }
 bool fused_norm_ok(int64_t m, int64_t h, int64_t k) {
   if (h % 8 != 0 || h <= 0 || h > k || k % WFB_QK_I2S != 0) return false;
-  return (m >= 1 && m <= 16 && k <= 4096) || (m == 1 && h > 4096 && k <= WFB_NORM_MAX_H);
+  return (m >= 1 && m <= 16 && k <= 4096) || (m == 1 && k <= WFB_NORM_MAX_H);
 }
 
 // residual + linear(quantise(norm(x))) into the residual stream x (in place), one projection.

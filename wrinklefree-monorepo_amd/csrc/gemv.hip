@@ -56,7 +56,7 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   constexpr bool NORM = XDT >= 0;
   constexpr int KMAX = 64 * L * CPL * S;  // the longest row the launch shape covers
   static_assert(RB <= 64 * S, "one thread per row in the epilogue");
-  static_assert(!NORM || S >= kTPB / 64, "the norm prologue runs on 256 threads");
+  static_assert(!NORM || S >= kTPB / 64 || KMAX <= kWaveMaxH, "rows past 4096 elements take the 256-thread order");
   __shared__ int red[S][M][RB];
   // norm prologue (one row): the row's elements, its codes and scale, the per-wave partials
   static_assert(!NORM || M == 1, "the norm prologue takes one row");
@@ -181,10 +181,12 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   if (PRE && t < RB) col.load_raw(ep, n, N, toks, M);
 
   if constexpr (NORM) {
-    // norm prologue, second part: wfb_rmsnorm_quant_i8's 256-thread path (sum of squares of thread t < 256
-    // sequential over elements (it*256 + t)*8 + e, fixed butterfly, the 4 wave sums in wave order; then
-    // y = (x * r) * gamma, absmax scale, round-half-even codes; the element-wise part spread over all
-    // threads), codes into LDS with zeros from h to the end of the row
+    // norm prologue, second part: wfb_rmsnorm_quant_i8's summation order for the row length -- rows of up
+    // to 4096 elements its one-wave path (lane l of wave 0 sequential over elements (j*64 + l)*8 + e, fixed
+    // butterfly), longer rows its 256-thread path (thread t < 256 sequential over elements (it*256 + t)*8
+    // + e, fixed butterfly, the 4 wave sums in wave order); then y = (x * r) * gamma, absmax scale,
+    // round-half-even codes (the element-wise part spread over all threads), codes into LDS with zeros
+    // from h to the end of the row
     const int h = ns.h;
     const int kpad = 64 * C;
     float g[PCH][kVec];
@@ -207,12 +209,14 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
       *reinterpret_cast<float4*>(dst + 4) = make_float4(xv[j][4], xv[j][5], xv[j][6], xv[j][7]);
     }
     __syncthreads();
-    if (t < kTPB) {
+    const bool wave_order = h <= kWaveMaxH;
+    const int nsum = wave_order ? 64 : kTPB;  // threads of the sum
+    if (t < nsum) {
       float ss = 0.0f;
       // elements past h are zeros in the quantiser's sum (adding +0 to a sum of squares changes nothing), so
       // only whole 8-element chunks below h are read: the last step may reach past the staged row
-      for (int it = 0; it * kTPB * kVec < h; ++it) {
-        const int e0 = (it * kTPB + t) * kVec;
+      for (int it = 0; it * nsum * kVec < h; ++it) {
+        const int e0 = (it * nsum + t) * kVec;
         if (e0 >= h) break;
         const float4 p = *reinterpret_cast<const float4*>(&xs[e0]);
         const float4 q = *reinterpret_cast<const float4*>(&xs[e0 + 4]);
@@ -225,8 +229,10 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
     }
     __syncthreads();
     float tot = nred[0];
+    if (!wave_order) {
 #pragma unroll
-    for (int k = 1; k < kTPB / 64; ++k) tot = __fadd_rn(tot, nred[k]);
+      for (int k = 1; k < kTPB / 64; ++k) tot = __fadd_rn(tot, nred[k]);
+    }
     const float r = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)h), ns.eps)));
     float mx = 0.0f;
 #pragma unroll
@@ -382,11 +388,14 @@ hipError_t launch_cfg(const uint8_t* W, int n, int C, const int8_t* A, int64_t l
   return hipGetLastError();
 }
 
-// Norm prologue launches (rows of 4097 .. 16384 elements, the quantiser's 256-thread path): the launch
-// shapes of the codes GEMV at those K.
+// Norm prologue launches (rows up to 16384 elements): the launch shapes of the codes GEMV at those K.
 template <int M, int XDT>
 hipError_t launch_norm_m(const uint8_t* W, int n, int C, const Epilogue& e, const NormSrc& ns, hipStream_t s) {
-  if (C <= 64) return hipErrorNotSupported;  // K <= 4096: the wave-order quantiser, not this path
+  if (C <= 8) return launch_cfg<M, 8, 1, 2, 1, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 16) return launch_cfg<M, 8, 1, 2, 2, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 24) return launch_cfg<M, 8, 1, 2, 3, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 40) return launch_cfg<M, 8, 1, 2, 5, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 64) return launch_cfg<M, 8, 1, 4, 8, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 112) return launch_cfg<M, 16, 1, 4, 7, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 224) return launch_cfg<M, 16, 1, 4, 14, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 256) return launch_cfg<M, 16, 1, 4, 16, true, XDT>(W, n, C, nullptr, 0, e, s, ns);

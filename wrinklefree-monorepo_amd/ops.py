@@ -468,13 +468,13 @@ def bitnet_linear_residual(
 
 
 def rmsnorm_linear_supported(m: int, h: int, k: int, gamma_bytes: int = 2) -> bool:
-    """Whether rmsnorm_linear takes these sizes: decode batches of up to 16 rows of up to 4096 elements (the
-    LDS-staged kernel's prologue), or one row of 4097 .. 16384 elements (the decode GEMV's prologue; the
-    gated rmsnorm_linear_glu keeps the first form).  ``gamma_bytes`` is kept for callers and no longer limits
-    the size."""
+    """Whether rmsnorm_linear takes these sizes: one row of up to 16384 elements (the decode GEMV's
+    prologue), or decode batches of 2 .. 16 rows of up to 4096 elements (the LDS-staged kernel's prologue;
+    the gated rmsnorm_linear_glu takes only this form, also for one row).  ``gamma_bytes`` is kept for
+    callers and no longer limits the size."""
     if h % 8 != 0 or not 0 < h <= k or k % QK_I2_S != 0:
         return False
-    return (1 <= m <= 16 and k <= 4096) or (m == 1 and 4096 < h and k <= 16384)
+    return (1 <= m <= 16 and k <= 4096) or (m == 1 and k <= 16384)
 
 
 def rmsnorm_linear_glu_supported(m: int, h: int, k: int) -> bool:
@@ -517,8 +517,8 @@ def rmsnorm_linear(
         raise RuntimeError(f"{name}: scales must be fp32 with one element per segment")
     gbytes = 0 if weight is None else weight.element_size()
     if not rmsnorm_linear_supported(m, h, k, gbytes):
-        raise RuntimeError(f"{name}: M={m}, H={h}, K={k} outside the fused path (H % 8 == 0 and either M <= 16 with "
-                           f"H <= K <= 4096, or M == 1 with 4096 < H <= K <= 16384)")
+        raise RuntimeError(f"{name}: M={m}, H={h}, K={k} outside the fused path (H % 8 == 0, H <= K and either "
+                           f"M == 1 with K <= 16384, or M <= 16 with K <= 4096)")
     dev = _require_gpu(name, x, weight, packed_weights, scales, residual)
     if weight is not None and (weight.numel() != h or weight.dtype not in (torch.float32, torch.bfloat16)):
         raise RuntimeError(f"{name}: weight must be float32/bfloat16 with {h} elements")
