@@ -140,6 +140,10 @@ GLU_CASES = [
     (16, 2560, 6912, 2560, torch.bfloat16, None, "relu2", torch.bfloat16),
     (1, 576, 1536, 640, torch.float32, torch.float32, "silu", torch.float32),         # SmolLM2, K padded
     (9, 1000, 96, 1024, torch.bfloat16, torch.bfloat16, "silu", torch.bfloat16),      # H < K, ragged tiles
+    # one token: the GEMV's gated form (gate rows and their up rows in one workgroup)
+    (1, 4096, 14336, 4096, torch.bfloat16, torch.bfloat16, "silu", torch.bfloat16),   # Llama-3-8B, 16 + 16 rows
+    (1, 1000, 96, 1024, torch.float32, None, "relu2", torch.float32),                 # H < K, 6 workgroups
+    (1, 256, 32, 256, torch.bfloat16, torch.bfloat16, "silu", torch.bfloat16),        # one wave, one workgroup
 ]
 
 
@@ -155,9 +159,10 @@ def test_fused_glu_equals_two_calls(pkg, dev, case):
     assert torch.equal(y, y_ref)
 
 
-def test_fused_glu_matches_oracle(pkg, dev):
-    rng = np.random.default_rng(5)
-    m, h, half = 5, 2560, 640
+@pytest.mark.parametrize("m", [5, 1])
+def test_fused_glu_matches_oracle(pkg, dev, m):
+    rng = np.random.default_rng(5 + m)
+    h, half = 2560, 640
     packed, x, g, scales = _inputs(rng, m, h, [half, half], h, torch.float32, torch.float32)
     y = pkg.rmsnorm_linear_glu(x.to(dev), g.to(dev), packed.to(dev), scales.to(dev), "relu2", eps=1e-6,
                                mid_dtype=torch.float32)

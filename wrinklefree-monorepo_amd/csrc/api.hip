@@ -535,6 +535,8 @@ int wfb_rmsnorm_linear_i2s_glu(const void* x, int x_dtype, int64_t ldx, const vo
   e.ldo = ldo;
   e.mid_dtype = mid_dtype;
   const wfb::NormSrc ns{x, x_dtype, ldx, gamma, gamma_dtype, eps, (int)h};
+  if (m == 1)  // one token: the GEMV with gate and up rows side by side in each workgroup
+    return hip_status(wfb::launch_gemv_i2s_norm_glu(qweight, (int)n, (int)k, e, ns, act_kind, as_stream(stream)), name);
   return hip_status(wfb::launch_skinny_lds(qweight, (int)n, (int)k, nullptr, (int)m, 0, e, act_kind, as_stream(stream), ns),
                     name);
 }

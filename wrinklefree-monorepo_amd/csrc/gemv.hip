@@ -47,7 +47,7 @@ __device__ __forceinline__ int wave_sum(int v) {
   return v;
 }
 
-template <int M, int L, int CPL, int RP, int S, bool EXACT, bool PRE, int XDT = -1, bool STAGE = true>
+template <int M, int L, int CPL, int RP, int S, bool EXACT, bool PRE, int XDT = -1, bool STAGE = true, int GLU = 0>
 __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restrict__ W,
                                                           const int8_t* __restrict__ A, int64_t lda, int N,
                                                           int C, Epilogue ep, NormSrc ns) {
@@ -56,6 +56,7 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   constexpr bool NORM = XDT >= 0;
   constexpr int KMAX = 64 * L * CPL * S;  // the longest row the launch shape covers
   static_assert(RB <= 64 * S, "one thread per row in the epilogue");
+  static_assert(GLU == 0 || (!PRE && RB % 2 == 0), "gated rows load their epilogue operands late");
   static_assert(!NORM || S >= kTPB / 64 || KMAX <= kWaveMaxH, "rows past 4096 elements take the 256-thread order");
   __shared__ int red[S][M][RB];
   // norm prologue (one row): the row's elements, its codes and scale, the per-wave partials
@@ -76,15 +77,28 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   const buf_t wb = make_buf(W, (uint32_t)N * row_bytes);
   const buf_t ab = make_buf(A, NORM ? 0u : (uint32_t)((M - 1) * lda + (int64_t)C * 64));
 
-  // norm prologue, first part: every thread loads two 8-element chunks of the row (chunks t and
-  // t + 64*S; zeros past h), issued before the weights
+  // norm prologue, first part: every thread loads its 8-element chunks of the row (chunks t + 64*S*j;
+  // zeros past h) and the same elements of gamma, all issued before the weights: loads complete in issue
+  // order, so a gamma load issued after the weights would hold the whole prologue until they arrived.
+  // gamma is read as 32 raw bytes per chunk whatever its dtype (a bf16 chunk uses the first 16; a null
+  // gamma reads zeros from an empty descriptor), so every path issues the same loads.
   constexpr int PCH = NORM ? KMAX / (kVec * 64 * S) : 1;  // chunks per thread (2 for 16 lanes x 1 chunk)
   static_assert(!NORM || PCH * kVec * 64 * S == KMAX, "chunks tile the row");
   float xv[PCH][kVec];
+  v4i graw[PCH][2];
   if constexpr (NORM) {
     const buf_t xb = row_buf<XDT>(ns.x, ns.h);
 #pragma unroll
     for (int j = 0; j < PCH; ++j) load_row8_full<XDT, 0>(xb, xb, (t + j * 64 * S) * kVec, xv[j]);
+    const uint32_t gsz = ns.gdt == WFB_F32 ? 4u : 2u;
+    const buf_t gb = make_buf(ns.gamma, ns.gamma ? (uint32_t)ns.h * gsz : 0u);
+#pragma unroll
+    for (int j = 0; j < PCH; ++j) {
+      const uint32_t off = (uint32_t)((t + j * 64 * S) * kVec) * gsz;
+      graw[j][0] = buf_load16(gb, off);
+      graw[j][1] = buf_load16(gb, off + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weight loads
   }
 
   // a[m][i][q] = a_m[128b + 32q + j0 .. +15] for chunk c (b = c/2, j0 = 16*(c%2))
@@ -133,7 +147,10 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   v4i wv[RP][CPL];
 #pragma unroll
   for (int p = 0; p < RP; ++p) {
-    const uint32_t rowoff = (uint32_t)(row0 + p * RPG + r_in) * row_bytes;
+    // GLU: local rows 0 .. RB/2-1 are gate rows b*RB/2 + i, the others their up rows N/2 + b*RB/2 + i
+    const int lr = p * RPG + r_in;
+    const int wr = GLU == 0 ? row0 + lr : lr < RB / 2 ? blockIdx.x * (RB / 2) + lr : N / 2 + blockIdx.x * (RB / 2) + lr - RB / 2;
+    const uint32_t rowoff = (uint32_t)wr * row_bytes;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = kc0 + s + L * i;
@@ -176,9 +193,10 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
         for (int q = 0; q < 4; ++q) a[m][i][q] = *reinterpret_cast<const v4i*>(&xa[w][m][off + 32 * q]);
       }
   }
-  // issued after the slice copy: issued before it, the copy's wait for the slice also covered the first
-  // weight load in the storing wave (its counter holds these loads too)
-  if (PRE && t < RB) col.load_raw(ep, n, N, toks, M);
+  // issued after the slice copy (or after the norm prologue): issued before it, the copy's or the
+  // prologue's wait for its own loads also covered weight loads in the storing wave (its counter holds
+  // these loads too), and the prologue's barriers pass that wait on to every wave
+  if (!NORM && PRE && t < RB) col.load_raw(ep, n, N, toks, M);
 
   if constexpr (NORM) {
     // norm prologue, second part: wfb_rmsnorm_quant_i8's summation order for the row length -- rows of up
@@ -189,17 +207,25 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
     // from h to the end of the row
     const int h = ns.h;
     const int kpad = 64 * C;
-    float g[PCH][kVec];
+    float g[PCH][kVec];  // gamma of the thread's elements (1 without gamma; past h the elements are 0)
 #pragma unroll
     for (int j = 0; j < PCH; ++j) {
-      const int e0 = (t + j * 64 * S) * kVec;
-      if (ns.gamma == nullptr || e0 >= h) {
+      if (ns.gamma == nullptr) {
 #pragma unroll
         for (int e = 0; e < kVec; ++e) g[j][e] = 1.0f;
       } else if (ns.gdt == WFB_F32) {
-        load8_buf<WFB_F32>(row_buf<WFB_F32>(ns.gamma, h), e0, g[j]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          g[j][e] = __int_as_float(graw[j][0][e]);
+          g[j][4 + e] = __int_as_float(graw[j][1][e]);
+        }
       } else {
-        load8_buf<WFB_BF16>(row_buf<WFB_BF16>(ns.gamma, h), e0, g[j]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t w2 = (uint32_t)graw[j][0][e];
+          g[j][2 * e] = __uint_as_float(w2 << 16);
+          g[j][2 * e + 1] = __uint_as_float(w2 & 0xFFFF0000u);
+        }
       }
     }
 #pragma unroll
@@ -288,7 +314,11 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
           sv[m][b] = in ? *reinterpret_cast<const v4i*>(&codes[m][boff + 16 * b]) : v4i{0, 0, 0, 0};
         }
       }
-      if (PRE && t < RB) col.as[m] = nscale[0];
+    }
+    if (PRE && t < RB) {
+      col.load_raw(ep, n, N, toks, M);
+#pragma unroll
+      for (int m = 0; m < M; ++m) col.as[m] = nscale[0];
     }
   }
 
@@ -324,6 +354,31 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
   }
   __syncthreads();
   if constexpr (PRE) col.finish(ep);
+  if constexpr (GLU != 0) {
+    // gated epilogue (the arithmetic of the batched kernels' gated epilogue): out[m, j] =
+    // act(y_gate) * y_up with y = (acc * ws) * as per half, each rounded to mid_dtype, fp32 out
+    constexpr int HB = RB / 2;
+    const int half = N / 2, j = blockIdx.x * HB + t;
+    if (t >= HB || j >= half) return;
+    const float wsg = epi_wscale(ep, j), wsu = epi_wscale(ep, half + j);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      int tg = red[0][m][t], tu = red[0][m][t + HB];
+#pragma unroll
+      for (int k = 1; k < S; ++k) {
+        tg += red[k][m][t];
+        tu += red[k][m][t + HB];
+      }
+      const float as = NORM ? nscale[0] : epi_ascale(ep, m);
+      float yg = __fmul_rn(__fmul_rn((float)tg, wsg), as), yu = __fmul_rn(__fmul_rn((float)tu, wsu), as);
+      if (ep.mid_dtype == WFB_BF16) {
+        yg = bf16_bits_to_f32(f32_to_bf16_rne(yg));
+        yu = bf16_bits_to_f32(f32_to_bf16_rne(yu));
+      }
+      reinterpret_cast<float*>(ep.out)[(int64_t)m * ep.ldo + j] = glu<GLU>(yg, yu);
+    }
+    return;
+  }
   if (ep.amax) {  // argmax epilogue: the RB <= 64 rows sit in wave 0
     if (t >= 64) return;
     const bool valid = t < RB && n < N;
@@ -365,7 +420,7 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
 // fragments directly (STAGE = false) where the launch shape has that variant (WIDE).
 constexpr int kStageMaxGrid = 2048;
 
-template <int M, int L, int CPL, int RP, int S, bool PRE = true, int XDT = -1, bool WIDE = false>
+template <int M, int L, int CPL, int RP, int S, bool PRE = true, int XDT = -1, bool WIDE = false, int GLU = 0>
 hipError_t launch_cfg(const uint8_t* W, int n, int C, const int8_t* A, int64_t lda, const Epilogue& e,
                       hipStream_t st, const NormSrc& ns = NormSrc{}) {
   constexpr int RB = RP * (64 / L);
@@ -373,18 +428,18 @@ hipError_t launch_cfg(const uint8_t* W, int n, int C, const int8_t* A, int64_t l
   if constexpr (WIDE && XDT < 0) {
     if ((int)grid.x > kStageMaxGrid) {
       if (C == L * CPL * S)
-        hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true, PRE, XDT, false>), grid, block, 0, st, W, A, lda, n,
+        hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true, PRE, XDT, false, GLU>), grid, block, 0, st, W, A, lda, n,
                            C, e, ns);
       else
-        hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, false, PRE, XDT, false>), grid, block, 0, st, W, A, lda,
+        hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, false, PRE, XDT, false, GLU>), grid, block, 0, st, W, A, lda,
                            n, C, e, ns);
       return hipGetLastError();
     }
   }
   if (C == L * CPL * S)
-    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true, PRE, XDT>), grid, block, 0, st, W, A, lda, n, C, e, ns);
+    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, true, PRE, XDT, true, GLU>), grid, block, 0, st, W, A, lda, n, C, e, ns);
   else
-    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, false, PRE, XDT>), grid, block, 0, st, W, A, lda, n, C, e, ns);
+    hipLaunchKernelGGL((gemv_i2s_kernel<M, L, CPL, RP, S, false, PRE, XDT, true, GLU>), grid, block, 0, st, W, A, lda, n, C, e, ns);
   return hipGetLastError();
 }
 
@@ -435,6 +490,30 @@ hipError_t launch_gemv_i2s_norm(const uint8_t* W, int n, int k, int m, const Epi
   if (m != 1) return hipErrorNotSupported;  // one row: the prologue keeps the row's elements in registers
   if (ns.xdt == WFB_F32) return launch_norm_m<1, WFB_F32>(W, n, C, e, ns, s);
   if (ns.xdt == WFB_BF16) return launch_norm_m<1, WFB_BF16>(W, n, C, e, ns, s);
+  return hipErrorNotSupported;
+}
+
+// Gated gate|up with the norm prologue, one token, K <= 4096: workgroups of RB/2 gate rows and their up rows.
+template <int XDT, int GLU>
+hipError_t launch_norm_glu(const uint8_t* W, int n, int C, const Epilogue& e, const NormSrc& ns, hipStream_t s) {
+  if (C <= 8) return launch_cfg<1, 8, 1, 2, 1, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 16) return launch_cfg<1, 8, 1, 2, 2, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 24) return launch_cfg<1, 8, 1, 2, 3, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 40) return launch_cfg<1, 8, 1, 2, 5, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 64) return launch_cfg<1, 8, 1, 4, 8, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
+  return hipErrorNotSupported;
+}
+
+hipError_t launch_gemv_i2s_norm_glu(const uint8_t* W, int n, int k, const Epilogue& e, const NormSrc& ns, int act,
+                                    hipStream_t s) {
+  const int C = k / 64;
+  if (n % 64 != 0) return hipErrorNotSupported;  // whole gate/up row groups per workgroup
+  const bool silu = act == WFB_ACT_SILU;
+  if (ns.xdt == WFB_F32)
+    return silu ? launch_norm_glu<WFB_F32, WFB_ACT_SILU>(W, n, C, e, ns, s) : launch_norm_glu<WFB_F32, WFB_ACT_RELU2>(W, n, C, e, ns, s);
+  if (ns.xdt == WFB_BF16)
+    return silu ? launch_norm_glu<WFB_BF16, WFB_ACT_SILU>(W, n, C, e, ns, s)
+                : launch_norm_glu<WFB_BF16, WFB_ACT_RELU2>(W, n, C, e, ns, s);
   return hipErrorNotSupported;
 }
 

@@ -485,6 +485,10 @@ struct NormSrc {
 // hipErrorNotSupported for other sizes.
 hipError_t launch_gemv_i2s_norm(const uint8_t* W, int n, int k, int m, const Epilogue& e, const NormSrc& ns,
                                 hipStream_t s);
+// One token, norm prologue + gate|up + act(gate) * up into fp32 out (e.out, e.ldo, e.mid_dtype, two
+// weight-scale segments), K <= 4096, n % 64 == 0; act WFB_ACT_SILU or WFB_ACT_RELU2.
+hipError_t launch_gemv_i2s_norm_glu(const uint8_t* W, int n, int k, const Epilogue& e, const NormSrc& ns, int act,
+                                    hipStream_t s);
 // M <= 16 tokens with both operands staged in LDS (skinny_lds.h); act 0 (plain) or a WFB_ACT_* gated
 // gate|up product; returns hipErrorNotSupported when the shape does not fit its LDS (the caller then
 // takes the register-operand kernels).  Needs N*K/4 and (M-1)*lda + K below 2^31.
