@@ -41,10 +41,7 @@ namespace {
 // barrier the first RB threads add the S partials of their row and store it (one coalesced store
 // per token).
 __device__ __forceinline__ int wave_sum(int v) {
-  v = group_sum<16>(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  return group_sum<64>(v);
 }
 
 template <int M, int L, int CPL, int RP, int S, bool EXACT, bool PRE, int XDT = -1, bool STAGE = true, int GLU = 0>
@@ -239,14 +236,25 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
     const int nsum = wave_order ? 64 : kTPB;  // threads of the sum
     if (t < nsum) {
       float ss = 0.0f;
-      // elements past h are zeros in the quantiser's sum (adding +0 to a sum of squares changes nothing), so
-      // only whole 8-element chunks below h are read: the last step may reach past the staged row
-      for (int it = 0; it * nsum * kVec < h; ++it) {
+      // the staged row is zero from h to KMAX and adding +0 to a sum of squares changes nothing, so every
+      // step the launch shape allows is read, all reads issued before the first add (the adds keep the
+      // quantiser's order; a step past h reads zeros)
+      // steps: the one-wave order covers at most kWaveMaxH elements, the 256-thread order at most KMAX
+      constexpr int WMAX = KMAX < kWaveMaxH ? KMAX : kWaveMaxH;
+      constexpr int NIT_W = (WMAX + 64 * kVec - 1) / (64 * kVec), NIT_B = (KMAX + kTPB * kVec - 1) / (kTPB * kVec);
+      constexpr int NIT = NIT_W > NIT_B ? NIT_W : NIT_B;
+      float4 p[NIT][2];
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
         const int e0 = (it * nsum + t) * kVec;
-        if (e0 >= h) break;
-        const float4 p = *reinterpret_cast<const float4*>(&xs[e0]);
-        const float4 q = *reinterpret_cast<const float4*>(&xs[e0 + 4]);
-        const float v[kVec] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+        const bool in = (wave_order ? it < NIT_W : it < NIT_B) && e0 < KMAX;
+        p[it][0] = in ? *reinterpret_cast<const float4*>(&xs[e0]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        p[it][1] = in ? *reinterpret_cast<const float4*>(&xs[e0 + 4]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const float v[kVec] = {p[it][0].x, p[it][0].y, p[it][0].z, p[it][0].w,
+                               p[it][1].x, p[it][1].y, p[it][1].z, p[it][1].w};
 #pragma unroll
         for (int e = 0; e < kVec; ++e) ss = __fadd_rn(ss, __fmul_rn(v[e], v[e]));
       }
@@ -443,14 +451,16 @@ hipError_t launch_cfg(const uint8_t* W, int n, int C, const int8_t* A, int64_t l
   return hipGetLastError();
 }
 
-// Norm prologue launches (rows up to 16384 elements): the launch shapes of the codes GEMV at those K.
+// Norm prologue launches (rows up to 16384 elements): the launch shapes of the codes GEMV at those K, except
+// K 2561..4096: 4 waves of 2 chunks per lane (Llama-3-8B q|k|v 6.09 -> 5.79 us, o 5.93 -> 5.64 against 8 waves
+// of one chunk, cold weights on MI355X).
 template <int M, int XDT>
 hipError_t launch_norm_m(const uint8_t* W, int n, int C, const Epilogue& e, const NormSrc& ns, hipStream_t s) {
   if (C <= 8) return launch_cfg<M, 8, 1, 2, 1, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 16) return launch_cfg<M, 8, 1, 2, 2, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 24) return launch_cfg<M, 8, 1, 2, 3, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 40) return launch_cfg<M, 8, 1, 2, 5, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
-  if (C <= 64) return launch_cfg<M, 8, 1, 4, 8, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 64) return launch_cfg<M, 8, 2, 4, 4, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 112) return launch_cfg<M, 16, 1, 4, 7, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 224) return launch_cfg<M, 16, 1, 4, 14, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 256) return launch_cfg<M, 16, 1, 4, 16, true, XDT>(W, n, C, nullptr, 0, e, s, ns);
@@ -493,14 +503,16 @@ hipError_t launch_gemv_i2s_norm(const uint8_t* W, int n, int k, int m, const Epi
   return hipErrorNotSupported;
 }
 
-// Gated gate|up with the norm prologue, one token, K <= 4096: workgroups of RB/2 gate rows and their up rows.
+// Gated gate|up with the norm prologue, one token, K <= 4096: workgroups of RB/2 gate rows and their up rows;
+// 64-row workgroups from K 2049 (fewer workgroups repeating the norm: Llama-3-8B 28672 x 4096 11.74 -> 10.46 us,
+// BitNet-2B 13824 x 2560 7.26 -> 6.33 us against 32 and 16 rows, cold weights on MI355X).
 template <int XDT, int GLU>
 hipError_t launch_norm_glu(const uint8_t* W, int n, int C, const Epilogue& e, const NormSrc& ns, hipStream_t s) {
   if (C <= 8) return launch_cfg<1, 8, 1, 2, 1, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 16) return launch_cfg<1, 8, 1, 2, 2, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
   if (C <= 24) return launch_cfg<1, 8, 1, 2, 3, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
-  if (C <= 40) return launch_cfg<1, 8, 1, 2, 5, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
-  if (C <= 64) return launch_cfg<1, 8, 1, 4, 8, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 40) return launch_cfg<1, 8, 1, 8, 5, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
+  if (C <= 64) return launch_cfg<1, 8, 2, 8, 4, false, XDT, false, GLU>(W, n, C, nullptr, 0, e, s, ns);
   return hipErrorNotSupported;
 }
 

@@ -20,16 +20,22 @@ constexpr int kVec = 8;        // elements per thread per iteration
 constexpr int kMaxIt = WFB_NORM_MAX_H / (kTPB * kVec);
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, xor_lanes_f32<32>(v));
+  v = fmaxf(v, xor_lanes_f32<16>(v));
+  v = fmaxf(v, xor_lanes_f32<8>(v));
+  v = fmaxf(v, xor_lanes_f32<4>(v));
+  v = fmaxf(v, xor_lanes_f32<2>(v));
+  return fmaxf(v, xor_lanes_f32<1>(v));
 }
 
-// Sum in a fixed xor-butterfly order; every lane ends with the same value.
+// Sum in a fixed xor-butterfly order (partners 32, 16, 8, 4, 2, 1); every lane ends with the same value.
 __device__ __forceinline__ float wave_sum_fixed(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o, 64));
-  return v;
+  v = __fadd_rn(v, xor_lanes_f32<32>(v));
+  v = __fadd_rn(v, xor_lanes_f32<16>(v));
+  v = __fadd_rn(v, xor_lanes_f32<8>(v));
+  v = __fadd_rn(v, xor_lanes_f32<4>(v));
+  v = __fadd_rn(v, xor_lanes_f32<2>(v));
+  return __fadd_rn(v, xor_lanes_f32<1>(v));
 }
 
 // 8 consecutive row elements from element e0 (h = row length): x itself (GLU = 0) or the gated

@@ -99,14 +99,21 @@ __device__ __forceinline__ void widen8(const Raw8<DT>& v, float (&f)[8]) {
   }
 }
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, xor_lanes_f32<32>(v));
+  v = fmaxf(v, xor_lanes_f32<16>(v));
+  v = fmaxf(v, xor_lanes_f32<8>(v));
+  v = fmaxf(v, xor_lanes_f32<4>(v));
+  v = fmaxf(v, xor_lanes_f32<2>(v));
+  return fmaxf(v, xor_lanes_f32<1>(v));
 }
+// the quantiser's fixed xor-butterfly order (partners 32, 16, 8, 4, 2, 1)
 __device__ __forceinline__ float wave_sum_fixed_f32(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o, 64));
-  return v;
+  v = __fadd_rn(v, xor_lanes_f32<32>(v));
+  v = __fadd_rn(v, xor_lanes_f32<16>(v));
+  v = __fadd_rn(v, xor_lanes_f32<8>(v));
+  v = __fadd_rn(v, xor_lanes_f32<4>(v));
+  v = __fadd_rn(v, xor_lanes_f32<2>(v));
+  return __fadd_rn(v, xor_lanes_f32<1>(v));
 }
 
 // The M rows of x through the norm and the quantiser into the activation staging.  XT: x's storage tag;
@@ -367,8 +374,8 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   // this wave's K range: add the 4 lane groups, then fetch token 4g + j's from lane 4g + j.
   {
     int s = sa;
-    s += __shfl_xor(s, 16, 64);
-    s += __shfl_xor(s, 32, 64);
+    s += xor_lanes<16>(s);
+    s += xor_lanes<32>(s);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int sj = __shfl(s, 4 * g + j, 64);
@@ -605,8 +612,8 @@ __global__ __launch_bounds__(64 * S) void kernel_persist(const uint8_t* __restri
       for (int f = 0; f < 4; ++f)
 #pragma unroll
         for (int e = 0; e < 4; ++e) sa = __builtin_amdgcn_sdot4(av[st][f][e], 0x01010101, sa, false);
-    sa += __shfl_xor(sa, 16, 64);
-    sa += __shfl_xor(sa, 32, 64);
+    sa += xor_lanes<16>(sa);
+    sa += xor_lanes<32>(sa);
 #pragma unroll
     for (int j = 0; j < 4; ++j) sj[j] = __shfl(sa, 4 * g + j, 64);
   }

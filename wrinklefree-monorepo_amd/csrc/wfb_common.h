@@ -66,6 +66,37 @@ __device__ __forceinline__ void load8(const void* p, int64_t i, float (&v)[8]) {
 
 // ---- lane-group reductions ------------------------------------------------------------------
 
+// The value of lane (lane ^ O) -- what __shfl_xor(v, O, 64) returns -- by VALU lane moves instead of the
+// LDS permute (whose latency sits on every reduction's critical path): gfx950's v_permlane32_swap /
+// v_permlane16_swap for O = 32 / 16, DPP row_ror:8, row_shl:4 / row_shr:4 and quad permutes below; all
+// 64 lanes must be active.  Checked against __shfl_xor for every lane and offset on MI355X.
+template <int O>
+__device__ __forceinline__ int xor_lanes(int v) {
+  const int lane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  if constexpr (O == 32) {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);  // p[0]: halves swapped up, p[1]: down
+    return lane < 32 ? (int)p[1] : (int)p[0];
+  } else if constexpr (O == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? (int)p[0] : (int)p[1];
+  } else if constexpr (O == 8) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (O == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, false);  // row_shl:4: lane + 4
+    const int dn = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4: lane - 4
+    return (lane & 4) ? dn : up;
+  } else if constexpr (O == 2) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+  } else {
+    static_assert(O == 1, "O is a power of two below 64");
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+  }
+}
+template <int O>
+__device__ __forceinline__ float xor_lanes_f32(float v) {
+  return __int_as_float(xor_lanes<O>(__float_as_int(v)));
+}
+
 // Sum over aligned groups of L consecutive lanes (L = 2..64, a power of two); every lane of a group
 // ends with the group total.  DPP quad_perm / row_half_mirror / row_mirror below 32 lanes.
 template <int L>
@@ -74,8 +105,8 @@ __device__ __forceinline__ int group_sum(int v) {
   if constexpr (L >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
   if constexpr (L >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
   if constexpr (L >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false); // row_mirror
-  if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
+  if constexpr (L >= 32) v += xor_lanes<16>(v);
+  if constexpr (L >= 64) v += xor_lanes<32>(v);
   return v;
 }
 
@@ -90,8 +121,8 @@ __device__ __forceinline__ float group_sum_f32(float v) {
   if constexpr (L >= 4) v += dpp_f32<0x4E>(v);
   if constexpr (L >= 8) v += dpp_f32<0x141>(v);
   if constexpr (L >= 16) v += dpp_f32<0x140>(v);
-  if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
+  if constexpr (L >= 32) v += xor_lanes_f32<16>(v);
+  if constexpr (L >= 64) v += xor_lanes_f32<32>(v);
   return v;
 }
 
