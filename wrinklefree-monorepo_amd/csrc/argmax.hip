@@ -74,8 +74,12 @@ __global__ __launch_bounds__(256) void lm_head_kernel(const void* __restrict__ x
       const float v = load_elem<XT>(x, (int64_t)mm * ldx + k);
       ss += v * v;
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    ss += xor_lanes_f32<32>(ss);
+    ss += xor_lanes_f32<16>(ss);
+    ss += xor_lanes_f32<8>(ss);
+    ss += xor_lanes_f32<4>(ss);
+    ss += xor_lanes_f32<2>(ss);
+    ss += xor_lanes_f32<1>(ss);
     if (lane == 0) rs[mm] = 1.0f / sqrtf(ss / (float)h + eps);
   }
   __syncthreads();

@@ -104,14 +104,32 @@ __device__ __forceinline__ void widen8(const Raw8<CT>& x, float (&v)[8]) {
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, xor_lanes_f32<32>(v));
+  v = fmaxf(v, xor_lanes_f32<16>(v));
+  v = fmaxf(v, xor_lanes_f32<8>(v));
+  v = fmaxf(v, xor_lanes_f32<4>(v));
+  v = fmaxf(v, xor_lanes_f32<2>(v));
+  return fmaxf(v, xor_lanes_f32<1>(v));
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  v += xor_lanes_f32<32>(v);
+  v += xor_lanes_f32<16>(v);
+  v += xor_lanes_f32<8>(v);
+  v += xor_lanes_f32<4>(v);
+  v += xor_lanes_f32<2>(v);
+  return v + xor_lanes_f32<1>(v);
+}
+
+// sum over the lanes l, l ^ LPK, l ^ 2 LPK, ... (partners LPK, 2 LPK, .., 32 in that order)
+template <int LPK>
+__device__ __forceinline__ float sum_across_keys(float v) {
+  if constexpr (LPK <= 1) v += xor_lanes_f32<1>(v);
+  if constexpr (LPK <= 2) v += xor_lanes_f32<2>(v);
+  if constexpr (LPK <= 4) v += xor_lanes_f32<4>(v);
+  if constexpr (LPK <= 8) v += xor_lanes_f32<8>(v);
+  if constexpr (LPK <= 16) v += xor_lanes_f32<16>(v);
+  if constexpr (LPK <= 32) v += xor_lanes_f32<32>(v);
   return v;
 }
 
@@ -322,9 +340,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float v = acc[g][e];
-#pragma unroll
-      for (int o = LPK; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+      const float v = sum_across_keys<LPK>(acc[g][e]);
       if (kl == 0) red[w][g][d0 + e] = v;
     }
   __syncthreads();

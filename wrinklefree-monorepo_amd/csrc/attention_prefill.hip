@@ -285,8 +285,8 @@ __global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(D == 128
         s[nb][i] = v;
         bmax = fmaxf(bmax, v);
       }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    bmax = fmaxf(bmax, xor_lanes_f32<16>(bmax));
+    bmax = fmaxf(bmax, xor_lanes_f32<32>(bmax));
     const float m_new = fmaxf(m_run, bmax);  // finite: key 0 <= qpos is in block 0
     const float alpha = __expf(m_run - m_new);
     float psum = 0.0f;
