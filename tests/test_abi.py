@@ -245,6 +245,34 @@ def test_rmsnorm_linear_argument_errors(pkg):
     assert st(x=8) == -1 and "16-byte aligned" in pkg._lib.last_error()
 
 
+def test_fusion_predicates_match_the_entry_points(pkg):
+    """rmsnorm_linear_supported / rmsnorm_linear_glu_supported accept exactly the sizes the C entry points'
+    argument checks accept.  Every call also carries one bad argument checked after the size rules (an
+    output dtype / a null output), so an accepted size stops there and nothing is launched."""
+    vp = ctypes.c_void_p
+    size_rules = ("must be in 0..16", "needs M == 1", "H % 8 == 0")
+
+    def refused(fn, m, h, k, n=128):
+        if fn == "wfb_rmsnorm_linear_i2s":
+            st = pkg._lib.status(fn, vp(16), 1, h, vp(16), 1, 1e-5, m, h, vp(16), n, k, 1, None, vp(16), None, 1, n,
+                                 vp(16), 2, n, None)
+            later = "out must be"
+        else:
+            st = pkg._lib.status(fn, vp(16), 1, h, vp(16), 1, 1e-5, m, h, vp(16), n, k, vp(16), 1, 1, None, n, None)
+            later = "null pointer"
+        err = pkg._lib.last_error()
+        assert st == -1 and (later in err or any(r in err for r in size_rules)), err
+        return any(r in err for r in size_rules)
+
+    sizes = [(576, 640), (640, 576), (2560, 2560), (4096, 4096), (4000, 4096), (4096, 4224), (4104, 4224),
+             (4100, 4224), (6912, 6912), (14336, 14336), (16384, 16384), (16392, 16512)]
+    for m in (1, 2, 8, 16, 17):
+        for h, k in sizes:
+            assert pkg.rmsnorm_linear_supported(m, h, k) == (not refused("wfb_rmsnorm_linear_i2s", m, h, k)), (m, h, k)
+            assert pkg.rmsnorm_linear_glu_supported(m, h, k) == (not refused("wfb_rmsnorm_linear_i2s_glu", m, h, k)), (
+                m, h, k)
+
+
 def test_rmsnorm_linear_glu_argument_errors(pkg):
     vp = ctypes.c_void_p
 
