@@ -171,8 +171,8 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   const int64_t cbase = ((int64_t)b * hkv + kvh) * max_len * D;  // element offset of this cache slice
 
   // keys k0..min(pos, k1)-1 come from the cache (loads past them read zeros); key pos from knew / vnew.
-  // The first chunk's K and V rows are requested before the rotary / append phase: the range never
-  // includes pos, so they do not wait for this workgroup's own append.
+  // The first chunk's K and V rows are requested before the rotary arithmetic and the append: the range
+  // never includes pos, so they do not wait for this workgroup's own append.
   const int kl = lane / LPK;        // key slot of the lane within a wave instruction
   const int d0 = 8 * (lane % LPK);  // first of the lane's 8 elements
   const int kend = owns_new ? (int)pos : k1;
@@ -192,19 +192,40 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
       vr[r] = load_raw8<DT>(vb, (uint32_t)(key * D + d0) * ESZ);
     }
   };
-  load_chunk(k0);
-
   // ---- rotary embedding of the new query heads and key; append key and value ------------------
+  // This phase's loads are issued before the first chunk's K and V rows: loads complete in issue order,
+  // so a load issued after them would make its use wait for the chunk as well.  Indices are clamped
+  // into range instead of guarding the loads, so every wave issues the same loads.
   const float* cs = rope_cos ? rope_cos + pos * HD : nullptr;
   const float* sn = rope_sin ? rope_sin + pos * HD : nullptr;
-  for (int i = t; i < G * HD; i += kAttnThreads) {
+  constexpr int NQ = (G * HD + kAttnThreads - 1) / kAttnThreads;
+  float qx1[NQ], qx2[NQ], qc[NQ], qsi[NQ];
+#pragma unroll
+  for (int it = 0; it < NQ; ++it) {
+    const int i = t + it * kAttnThreads < G * HD ? t + it * kAttnThreads : G * HD - 1;
     const int g = i / HD, j = i % HD;
     const int64_t qo = (int64_t)b * ldq + (int64_t)(kvh * G + g) * D;
-    float x1 = load_elem<DT>(q, qo + j), x2 = load_elem<DT>(q, qo + j + HD);
+    qx1[it] = load_elem<DT>(q, qo + j);
+    qx2[it] = load_elem<DT>(q, qo + j + HD);
+    qc[it] = cs ? cs[j] : 1.0f;
+    qsi[it] = cs ? sn[j] : 0.0f;
+  }
+  const int tk = t < HD ? t : HD - 1, tv = t < 64 ? 0 : t < 64 + D ? t - 64 : D - 1;
+  const int64_t ko = (int64_t)b * ldk + (int64_t)kvh * D;
+  const float kx1 = load_elem<DT>(kn, ko + tk), kx2 = load_elem<DT>(kn, ko + tk + HD);
+  const float kcs = cs ? cs[tk] : 1.0f, ksn = cs ? sn[tk] : 0.0f;
+  const float vx = load_elem<DT>(vn, (int64_t)b * ldv + (int64_t)kvh * D + tv);
+  load_chunk(k0);
+
+#pragma unroll
+  for (int it = 0; it < NQ; ++it) {
+    const int i = t + it * kAttnThreads;
+    if (i >= G * HD) break;
+    const int g = i / HD, j = i % HD;
+    float x1 = qx1[it], x2 = qx2[it];
     if (cs) {
-      const float c = cs[j], s = sn[j];
-      const float y1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(-x2, s));
-      const float y2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+      const float y1 = __fadd_rn(__fmul_rn(x1, qc[it]), __fmul_rn(-x2, qsi[it]));
+      const float y2 = __fadd_rn(__fmul_rn(x2, qc[it]), __fmul_rn(x1, qsi[it]));
       x1 = round_to<DT>(y1);
       x2 = round_to<DT>(y2);
     }
@@ -213,12 +234,10 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   }
   if (!owns_new) {
   } else if (t < HD) {
-    const int64_t ko = (int64_t)b * ldk + (int64_t)kvh * D;
-    float x1 = load_elem<DT>(kn, ko + t), x2 = load_elem<DT>(kn, ko + t + HD);
+    float x1 = kx1, x2 = kx2;
     if (cs) {
-      const float c = cs[t], s = sn[t];
-      const float y1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(-x2, s));
-      const float y2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+      const float y1 = __fadd_rn(__fmul_rn(x1, kcs), __fmul_rn(-x2, ksn));
+      const float y2 = __fadd_rn(__fmul_rn(x2, kcs), __fmul_rn(x1, ksn));
       x1 = round_to<DT>(y1);
       x2 = round_to<DT>(y2);
     }
@@ -228,9 +247,8 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
     store_elem<DT>(kc, cbase + pos * D + t + HD, x2);
   } else if (t >= 64 && t < 64 + D) {
     const int j = t - 64;
-    const float x = load_elem<DT>(vn, (int64_t)b * ldv + (int64_t)kvh * D + j);
-    vnew[j] = x;
-    store_elem<DT>(vc, cbase + pos * D + j, x);
+    vnew[j] = vx;
+    store_elem<DT>(vc, cbase + pos * D + j, vx);
   }
   __syncthreads();
 
