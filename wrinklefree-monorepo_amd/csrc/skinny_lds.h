@@ -306,10 +306,11 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
       int8_t* dst = al[p % S][p / S][t & 1] + 256 * r + 16 * ((b >> 4) ^ (r & 15)) + (b & 15);
       *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
     };
-    auto between = [&]() {
-      dma_weights();
-      col_loads();
-    };
+    auto between = [&]() { dma_weights(); };
+    // the epilogue operands first: issued after the weight DMA (they load in waves w < NT only), the
+    // prologue's wait for its row and gamma also covered DMA loads in those waves (loads complete in
+    // issue order), and the prologue's barrier passed that wait on to every wave
+    col_loads();
     // the whole staging: waves whose pairs lie past K read zeros (their sum(a) stays 0), as after the DMA
     constexpr int lim = 512 * S * TP;
     static_assert(lim <= 64 * 8 * 8, "the prologue's lanes cover 4096 elements");
