@@ -64,31 +64,91 @@ __global__ __launch_bounds__(256) void lm_head_kernel(const void* __restrict__ x
                                                       uint64_t* __restrict__ parts) {
   extern __shared__ float xn[];  // [m][h]
   __shared__ float rs[16];
+  __shared__ float red[4][MM];
   constexpr int ESZ = WT == WFB_F32 ? 4 : 2;
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
 
-  for (int mm = w; mm < m; mm += 4) {
-    float ss = 0.0f;
-    for (int k = lane; k < h; k += 64) {
-      const float v = load_elem<XT>(x, (int64_t)mm * ldx + k);
-      ss += v * v;
+  // The final norm of the m rows: 8-element chunks of the rows spread over all 256 threads, each batch's
+  // loads issued before any is used (a load-then-add loop waits one cache round trip per element).
+  // Pass 1: each row's sum of squares (per-thread partials per row, then the wave and the 4 waves).
+  const int C8 = h >> 3, nch = m * C8;
+  float ssr[MM];
+#pragma unroll
+  for (int mm = 0; mm < MM; ++mm) ssr[mm] = 0.0f;
+  for (int j0 = 0; j0 * 256 < nch; j0 += 2) {
+    float v[2][8];
+    int mrow[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = (j0 + u) * 256 + t;
+      const int ic = i < nch ? i : 0;
+      const int mm = ic / C8, c = ic - mm * C8;
+      mrow[u] = i < nch ? mm : -1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[u][e] = load_elem<XT>(x, (int64_t)mm * ldx + 8 * c + e);
     }
-    ss += xor_lanes_f32<32>(ss);
-    ss += xor_lanes_f32<16>(ss);
-    ss += xor_lanes_f32<8>(ss);
-    ss += xor_lanes_f32<4>(ss);
-    ss += xor_lanes_f32<2>(ss);
-    ss += xor_lanes_f32<1>(ss);
-    if (lane == 0) rs[mm] = 1.0f / sqrtf(ss / (float)h + eps);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      float sq = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sq += v[u][e] * v[u][e];
+#pragma unroll
+      for (int mm = 0; mm < MM; ++mm) ssr[mm] += mrow[u] == mm ? sq : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int mm = 0; mm < MM; ++mm) {
+    float v = ssr[mm];
+    v += xor_lanes_f32<32>(v);
+    v += xor_lanes_f32<16>(v);
+    v += xor_lanes_f32<8>(v);
+    v += xor_lanes_f32<4>(v);
+    v += xor_lanes_f32<2>(v);
+    v += xor_lanes_f32<1>(v);
+    if (lane == 0) red[w][mm] = v;
   }
   __syncthreads();
-  for (int i = t; i < m * h; i += 256) {
-    const int mm = i / h, k = i - mm * h;
-    float v = load_elem<XT>(x, (int64_t)mm * ldx + k) * rs[mm];
-    if (gamma) v = v * load_any(gamma, gdt, k);
-    if constexpr (XT == WFB_BF16) v = bf16_bits_to_f32(f32_to_bf16_rne(v));
-    xn[i] = v;
+  if (t < m) rs[t] = 1.0f / sqrtf((((red[0][t] + red[1][t]) + red[2][t]) + red[3][t]) / (float)h + eps);
+  __syncthreads();
+  // Pass 2: y = x * rs * gamma, rounded to x's dtype as the torch glue does, into LDS.
+  for (int j0 = 0; j0 * 256 < nch; j0 += 2) {
+    float v[2][8], gv[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = (j0 + u) * 256 + t;
+      const int ic = i < nch ? i : 0;
+      const int mm = ic / C8, c = ic - mm * C8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[u][e] = load_elem<XT>(x, (int64_t)mm * ldx + 8 * c + e);
+      // gamma's dtype tested once per chunk, so the 8 loads of a chunk go out together
+      if (gamma == nullptr) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gv[u][e] = 1.0f;
+      } else if (gdt == WFB_F32) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gv[u][e] = load_elem<WFB_F32>(gamma, 8 * c + e);
+      } else if (gdt == WFB_BF16) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gv[u][e] = load_elem<WFB_BF16>(gamma, 8 * c + e);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gv[u][e] = load_elem<WFB_F16>(gamma, 8 * c + e);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = (j0 + u) * 256 + t;
+      if (i >= nch) break;
+      const int mm = i / C8, c = i - mm * C8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float y = v[u][e] * rs[mm];
+        if (gamma) y = y * gv[u][e];
+        if constexpr (XT == WFB_BF16) y = bf16_bits_to_f32(f32_to_bf16_rne(y));
+        xn[mm * h + 8 * c + e] = y;
+      }
+    }
   }
   __syncthreads();
 
@@ -104,31 +164,44 @@ __global__ __launch_bounds__(256) void lm_head_kernel(const void* __restrict__ x
     float acc[MM];
 #pragma unroll
     for (int mm = 0; mm < MM; ++mm) acc[mm] = 0.0f;
-#pragma unroll 4
-    for (int c = s; c < C; c += 8) {
-      float wv[8];
-      const v4i r0 = buf_load16(wb, roff + (uint32_t)(8 * c * ESZ));
-      if constexpr (WT == WFB_F32) {
-        const v4i r1 = buf_load16(wb, roff + (uint32_t)(8 * c * ESZ) + 16);
+    // U chunks' loads in flight per lane, then their arithmetic in chunk order (a one-load-then-wait loop
+    // kept a single 16-byte load in flight per lane); chunks past the row read zeros from an out-of-range
+    // offset (below 2^31, so offset + 16 cannot wrap) and add exactly +0
+    constexpr int U = 4;
+    for (int c0 = s; c0 < C; c0 += 8 * U) {
+      v4i r0[U], r1[U];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          wv[e] = __int_as_float(r0[e]);
-          wv[4 + e] = __int_as_float(r1[e]);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          wv[2 * e] = __uint_as_float((uint32_t)r0[e] << 16);
-          wv[2 * e + 1] = __uint_as_float((uint32_t)r0[e] & 0xffff0000u);
-        }
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + 8 * u;
+        const uint32_t off = c < C ? roff + (uint32_t)(8 * c * ESZ) : 0x7FFFFF00u;
+        r0[u] = buf_load16(wb, off);
+        if constexpr (WT == WFB_F32) r1[u] = buf_load16(wb, off + 16);
       }
 #pragma unroll
-      for (int mm = 0; mm < MM; ++mm) {
-        if (mm < m) {
-          const float4* xp = reinterpret_cast<const float4*>(xn + mm * h + 8 * c);
-          const float4 a = xp[0], b = xp[1];
-          acc[mm] += wv[0] * a.x + wv[1] * a.y + wv[2] * a.z + wv[3] * a.w + wv[4] * b.x + wv[5] * b.y +
-                     wv[6] * b.z + wv[7] * b.w;
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + 8 * u < C ? c0 + 8 * u : 0;  // the LDS index stays in range (its weights are 0)
+        float wv[8];
+        if constexpr (WT == WFB_F32) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            wv[e] = __int_as_float(r0[u][e]);
+            wv[4 + e] = __int_as_float(r1[u][e]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            wv[2 * e] = __uint_as_float((uint32_t)r0[u][e] << 16);
+            wv[2 * e + 1] = __uint_as_float((uint32_t)r0[u][e] & 0xffff0000u);
+          }
+        }
+#pragma unroll
+        for (int mm = 0; mm < MM; ++mm) {
+          if (mm < m) {
+            const float4* xp = reinterpret_cast<const float4*>(xn + mm * h + 8 * c);
+            const float4 a = xp[0], b = xp[1];
+            acc[mm] += wv[0] * a.x + wv[1] * a.y + wv[2] * a.z + wv[3] * a.w + wv[4] * b.x + wv[5] * b.y +
+                       wv[6] * b.z + wv[7] * b.w;
+          }
         }
       }
     }
