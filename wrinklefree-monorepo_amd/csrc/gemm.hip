@@ -147,19 +147,20 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) sa[mt] = 0;
   const int T = (C + 3) >> 2;
-#pragma unroll 2
-  for (int t = w; t < T; t += S) {
+  // operands of step t: the weight chunk of each row tile and the activation fragments (steps past T read
+  // zeros from out-of-range offsets)
+  auto load_step = [&](int t, v4i (&wv)[NT], v4i (&av)[MT][4]) {
     const int c = 4 * t + g;
-    const bool ok = c < C;
-    v4i wv[NT];
+    const bool ok = t < T && c < C;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) wv[nt] = buf_load16(wb, ok ? woff[nt] + 64u * t : w_end);
     const uint32_t ab0 = 128u * (c >> 1) + 16u * (c & 1);
-    v4i av[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int f = 0; f < 4; ++f) av[mt][f] = buf_load16(ab, (ok && tok_ok[mt]) ? aoff[mt] + ab0 + 32 * f : a_end);
+  };
+  auto compute_step = [&](const v4i (&wv)[NT], const v4i (&av)[MT][4]) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       v4i b0, b1, b2, b3;
@@ -185,14 +186,21 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
       for (int f = 0; f < 4; ++f)
 #pragma unroll
         for (int e = 0; e < 4; ++e) sa[mt] = __builtin_amdgcn_sdot4(av[mt][f][e], 0x01010101, sa[mt], false);
+  };
+  // (a form with two operand sets, the next step's loads issued before this step's MFMAs, measured no
+  // faster at M = 17..32 on MI355X: the activation fragments' cache traffic, not the round trip, bounds it)
+  for (int t = w; t < T; t += S) {
+    v4i wv[NT], av[MT][4];
+    load_step(t, wv, av);
+    compute_step(wv, av);
   }
   // C layout of a 16x16 tile: lane (nl, g) holds tokens 4g + j (j < 4) of weight row nl.  sum(a) of
   // token nl over this wave's K range: add the 4 lane groups, then fetch token 4g + j's from lane 4g + j.
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     int s = sa[mt];
-    s += __shfl_xor(s, 16, 64);
-    s += __shfl_xor(s, 32, 64);
+    s += xor_lanes<16>(s);
+    s += xor_lanes<32>(s);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int sj = __shfl(s, 4 * g + j, 64);
