@@ -238,20 +238,28 @@ __device__ __forceinline__ uint64_t amax_key(float y, int n) {
   return ((uint64_t)k << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)n);
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
+template <int O>
+__device__ __forceinline__ uint64_t xor_lanes_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)xor_lanes<O>((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)xor_lanes<O>((int)(uint32_t)(v >> 32));
   return ((uint64_t)hi << 32) | lo;
 }
+template <int O>
+__device__ __forceinline__ uint64_t max_xor_u64(uint64_t v) {
+  const uint64_t x = xor_lanes_u64<O>(v);
+  return x > v ? x : v;
+}
 
-// max over aligned groups of L lanes (xor butterfly); every lane of a group ends with the maximum
+// max over aligned groups of L lanes (xor butterfly by lane moves; all 64 lanes active); every lane of a
+// group ends with the maximum
 template <int L>
 __device__ __forceinline__ uint64_t group_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 1; o < L; o <<= 1) {
-    const uint64_t x = shfl_xor_u64(v, o);
-    v = x > v ? x : v;
-  }
+  if constexpr (L > 1) v = max_xor_u64<1>(v);
+  if constexpr (L > 2) v = max_xor_u64<2>(v);
+  if constexpr (L > 4) v = max_xor_u64<4>(v);
+  if constexpr (L > 8) v = max_xor_u64<8>(v);
+  if constexpr (L > 16) v = max_xor_u64<16>(v);
+  if constexpr (L > 32) v = max_xor_u64<32>(v);
   return v;
 }
 
