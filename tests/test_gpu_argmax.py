@@ -21,11 +21,12 @@ def _first_argmax(x):
 # (1, 70000, 4096), (2, 40000, 2560): the GEMV with activation fragments from global memory (grids above
 # 2048 workgroups); (8, 128256, 4096), (3, 40000, 2560), (5, 33000, 1024), (12, 65543, 2560), (16, 49152, 4096):
 # the persistent head kernel
-# (>= 32768 rows, up to 16 tokens), one-shot elsewhere
+# (>= 32768 rows, up to 16 tokens), one-shot elsewhere; (17, 3000, 512), (32, 20000, 2560), (24, 4096, 4096):
+# two token tiles per weight fragment
 @pytest.mark.parametrize("m,n,k", [(1, 1000, 256), (2, 5000, 640), (1, 70000, 4096), (2, 40000, 2560),
                                    (3, 4099, 2560), (8, 128256, 4096),
                                    (3, 40000, 2560), (5, 33000, 1024), (12, 65543, 2560), (16, 49152, 4096),
-                                   (17, 3000, 512), (64, 2048, 384)])
+                                   (17, 3000, 512), (32, 20000, 2560), (24, 4096, 4096), (64, 2048, 384)])
 @pytest.mark.parametrize("ldt", [torch.float32, torch.bfloat16])
 def test_ternary_head_argmax_matches_oracle(pkg, dev, m, n, k, ldt):
     rng = np.random.default_rng(m * 1000 + n + k)

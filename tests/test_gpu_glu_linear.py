@@ -16,6 +16,8 @@ CASES = [
     (1, 6912, 2560, torch.bfloat16),    # BitNet-2B
     (3, 1536, 640, torch.float32),      # SmolLM2 (fp32 model), K padded
     (17, 2048, 1024, torch.bfloat16),   # two token tiles
+    (32, 6912, 2560, torch.bfloat16),   # BitNet-2B gate|up at 32 tokens (LDS-staged, two token tiles)
+    (24, 2048, 4096, torch.float32),    # 4096-long rows, one round of workgroups
     (64, 4096, 512, torch.float32),     # four token tiles
 ]
 

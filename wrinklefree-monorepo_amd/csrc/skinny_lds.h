@@ -1,10 +1,11 @@
-// Batched-decode linear for M <= 16 tokens with both operands staged in LDS (included by the three
+// Batched-decode linear for M <= 32 tokens with both operands staged in LDS (included by the four
 // skinny_mr*.hip files, one per staged token-row count, so they compile in parallel).
 //
 // Replaces, like the other I2_S GEMM paths, bitnet_gemm_i2_i8 / bitnet_gemm_cpu
 // (SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:814-874, SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:370-406).
 //
-// v_mfma_i32_16x16x64_i8, one 16-token tile.  A workgroup owns NT tiles of 16 weight rows and all of K;
+// v_mfma_i32_16x16x64_i8, one 16-token tile (two for 17..32 tokens, MR = 32: each weight fragment read
+// from LDS and unpacked once feeds both tiles' MFMAs).  A workgroup owns NT tiles of 16 weight rows and all of K;
 // its S waves split K into step pairs of 512 weights (128 packed bytes per row), wave w taking pairs
 // w, w + S, ... (TP of them).  Measured on MI355X, what sets the time of this kernel is how its loads
 // cover cache lines, so both operands are brought in whole lines by 16-byte LDS-DMA loads
@@ -56,7 +57,7 @@ __device__ __forceinline__ void dma16(buf_t r, void* lds, uint32_t voff) {
 // output tile the activation staging, so the LDS is the two operand stagings only.
 constexpr size_t lds_bytes(int S, int NT, int TP, int MR) { return (size_t)S * TP * (NT * 2048 + 2 * MR * 256); }
 // with the activations in registers (kAreg): the weight staging and the staged output tile
-constexpr size_t lds_bytes_areg(int S, int NT, int TP) { return (size_t)S * TP * NT * 2048 + 16 * 16 * NT * 4 + 64; }
+constexpr size_t lds_bytes_areg(int S, int NT, int TP, int MT) { return (size_t)S * TP * NT * 2048 + 16 * MT * 16 * NT * 4 + 64; }
 
 // ---- norm prologue helpers ---------------------------------------------------------------------------
 // Storage-type tags of the prologue's x and gamma (kNone: no prologue / no gamma).  Distinct from the
@@ -202,16 +203,20 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
                                                  int64_t lda, int M, int N, int C, Epilogue ep, NormSrc ns) {
   static_assert((GLUE ? NT / 2 : NT) <= S, "one wave per output row tile in the epilogue");
   static_assert(GLUE == 0 || NT % 2 == 0, "gated mode pairs gate and up tiles");
-  static_assert(MR == 4 || MR == 8 || MR == 16, "staged token rows");
+  static_assert(MR == 4 || MR == 8 || MR == 16 || MR == 32, "staged token rows");
   constexpr bool NORM = XT == kF32 || XT == kBf16;  // codes formed in the prologue, token scales with them
+  // 16-token tiles: MR = 32 runs two, each weight fragment feeding both
+  constexpr int MT = MR > 16 ? 2 : 1;
+  static_assert(MT == 1 || !NORM, "the norm prologue serves up to 16 tokens");
+  static_assert(MT <= 2 * TP, "partial tiles fit the wave's weight staging");
   __shared__ __attribute__((aligned(16))) int8_t wl[S][TP][NT][2048];
   __shared__ __attribute__((aligned(16))) int8_t al[XT == kAreg ? 1 : S][XT == kAreg ? 1 : TP][2][XT == kAreg ? 16 : MR * 256];
   // staged output tile of the register-activation mode (the others use the activation staging)
-  __shared__ __attribute__((aligned(16))) float ysb[XT == kAreg && STAGED ? 16 * 16 * NT : 1];
-  // partial tile (row tile nt, token slot j, lane) of wave w, in wave w's own weight staging (free once
-  // the wave has read it: its LDS reads and writes execute in order)
-  auto red = [&](int wv, int nt, int j, int l) -> int& {
-    return reinterpret_cast<int*>(&wl[wv][0][0][0])[(nt * 4 + j) * 64 + l];
+  __shared__ __attribute__((aligned(16))) float ysb[XT == kAreg && STAGED ? 16 * MT * 16 * NT : 1];
+  // partial tile (token tile mt, row tile nt, token slot j, lane) of wave w, in wave w's own weight
+  // staging (free once the wave has read it: its LDS reads and writes execute in order)
+  auto red = [&](int wv, int mt, int nt, int j, int l) -> int& {
+    return reinterpret_cast<int*>(&wl[wv][0][0][0])[((mt * NT + nt) * 4 + j) * 64 + l];
   };
   // norm prologue: scale of token tok, written by its wave (tok % S) after that wave's partial tiles
   constexpr int RPW = (MR + S - 1) / S;
@@ -248,11 +253,13 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
         }
     }
   };
-  // epilogue operands of the column this lane owns in the MFMA layout (row n, tokens 4g + j)
-  int toks[4];
+  // epilogue operands of the column this lane owns in the MFMA layout (row n, tokens 16 mt + 4g + j at
+  // slot 4 mt + j)
+  constexpr int JT = 4 * MT;
+  int toks[JT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) toks[j] = 4 * g + j;
-  EpiCol<4> col;
+  for (int jj = 0; jj < JT; ++jj) toks[jj] = 16 * (jj >> 2) + 4 * g + (jj & 3);
+  EpiCol<JT> col;
   auto col_loads = [&]() {
     if (!GLUE && w < NT) {
       Epilogue e1 = ep;
@@ -261,24 +268,27 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     }
   };
   float my_scale[RPW];
-  // register-activation mode: lane (nl, g)'s 16 activation bytes of step pair u, step st, field f -- step
-  // bytes 128 (g / 2) + 16 (g % 2) + 32 f of token nl (zeros past M and past K)
-  v4i avr[XT == kAreg ? TP : 1][2][4];
+  // register-activation mode: lane (nl, g)'s 16 activation bytes of token tile mt, step pair u, step st,
+  // field f -- step bytes 128 (g / 2) + 16 (g % 2) + 32 f of token 16 mt + nl (zeros past M and past K)
+  v4i avr[XT == kAreg ? MT : 1][XT == kAreg ? TP : 1][2][4];
   if constexpr (XT == kAreg) {
     dma_weights();
 #pragma unroll
-    for (int u = 0; u < TP; ++u)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+      for (int u = 0; u < TP; ++u)
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
-          const int p = w + S * u;
-          const int t = 2 * p + st;
-          const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;
-          const uint32_t kb = 256u * t + 16u * qg;
-          const bool ok = p < T2 && t < T && nl < M && kb < (uint32_t)(64 * C);
-          avr[u][st][f] = buf_load16(ab, ok ? (uint32_t)((int64_t)nl * lda) + kb : a_end);
-        }
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int f = 0; f < 4; ++f) {
+            const int p = w + S * u;
+            const int t = 2 * p + st;
+            const int tr = 16 * mt + nl;
+            const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;
+            const uint32_t kb = 256u * t + 16u * qg;
+            const bool ok = p < T2 && t < T && tr < M && kb < (uint32_t)(64 * C);
+            avr[mt][u][st][f] = buf_load16(ab, ok ? (uint32_t)((int64_t)tr * lda) + kb : a_end);
+          }
     col_loads();
   } else if constexpr (XT == kNone) {
     dma_weights();
@@ -325,26 +335,34 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS-DMA loads have landed
 
   // ---- MFMA over the wave's step pairs -----------------------------------------------------------
-  v4i acc1[NT], acc4[NT], acc16[NT];
+  v4i acc1[MT][NT], acc4[MT][NT], acc16[MT][NT];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) acc1[nt] = acc4[nt] = acc16[nt] = v4i{0, 0, 0, 0};
-  int sa = 0;
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc1[mt][nt] = acc4[mt][nt] = acc16[mt][nt] = v4i{0, 0, 0, 0};
+  int sa[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) sa[mt] = 0;
   const int hh = nl >> 3, rr = nl & 7;
-  const int8_t* arow = nullptr;
 #pragma unroll
   for (int u = 0; u < TP; ++u) {
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      v4i av[4];
-      if constexpr (XT == kAreg) {
+      v4i av[MT][4];
 #pragma unroll
-        for (int f = 0; f < 4; ++f) av[f] = avr[u][st][f];
-      } else {
-        arow = al[w][u][st] + 256 * (nl < MR ? nl : MR - 1);  // rows >= M hold zeros or unused codes
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (XT == kAreg) {
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
-          const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;  // step bytes 128 (g / 2) + 16 (g % 2) + 32 f
-          av[f] = *reinterpret_cast<const v4i*>(arow + 16 * (qg ^ nl));
+          for (int f = 0; f < 4; ++f) av[mt][f] = avr[mt][u][st][f];
+        } else {
+          // token row 16 mt + nl (its slots swizzled by nl); rows >= M hold zeros or unused codes
+          const int tr = 16 * mt + nl;
+          const int8_t* arow = al[w][u][st] + 256 * (tr < MR ? tr : MR - 1);
+#pragma unroll
+          for (int f = 0; f < 4; ++f) {
+            const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;  // step bytes 128 (g / 2) + 16 (g % 2) + 32 f
+            av[mt][f] = *reinterpret_cast<const v4i*>(arow + 16 * (qg ^ nl));
+          }
         }
       }
       const int slot = (4 * st + g) ^ (rr ^ hh);
@@ -360,28 +378,35 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
           b2[e] = d & 0x0C0C0C0C;
           b3[e] = d & 0x03030303;
         }
-        acc16[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[0], b0, acc16[nt], 0, 0, 0);
-        acc16[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[1], b1, acc16[nt], 0, 0, 0);
-        acc4[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[2], b2, acc4[nt], 0, 0, 0);
-        acc1[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[3], b3, acc1[nt], 0, 0, 0);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc16[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][0], b0, acc16[mt][nt], 0, 0, 0);
+          acc16[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][1], b1, acc16[mt][nt], 0, 0, 0);
+          acc4[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][2], b2, acc4[mt][nt], 0, 0, 0);
+          acc1[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt][3], b3, acc1[mt][nt], 0, 0, 0);
+        }
       }
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sa = __builtin_amdgcn_sdot4(av[f][e], 0x01010101, sa, false);
+        for (int f = 0; f < 4; ++f)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sa[mt] = __builtin_amdgcn_sdot4(av[mt][f][e], 0x01010101, sa[mt], false);
     }
   }
   // C layout of a 16x16 tile: lane (nl, g) holds tokens 4g + j of weight row nl.  sum(a) of token nl over
   // this wave's K range: add the 4 lane groups, then fetch token 4g + j's from lane 4g + j.
-  {
-    int s = sa;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    int s = sa[mt];
     s += xor_lanes<16>(s);
     s += xor_lanes<32>(s);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int sj = __shfl(s, 4 * g + j, 64);
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) red(w, nt, j, lane) = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj;
+      for (int nt = 0; nt < NT; ++nt)
+        red(w, mt, nt, j, lane) = acc1[mt][nt][j] + (acc4[mt][nt][j] >> 2) + (acc16[mt][nt][j] >> 4) - sj;
     }
   }
   if constexpr (NORM) {
@@ -394,7 +419,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   __syncthreads();
   if constexpr (NORM) {  // token scales from the prologue (ep.a_scale is not used)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) col.as[j] = toks[j] < M ? tok_scale(toks[j]) : 0.0f;
+    for (int jj = 0; jj < JT; ++jj) col.as[jj] = toks[jj] < M ? tok_scale(toks[jj]) : 0.0f;
   }
 
   // ---- epilogues -----------------------------------------------------------------------------------
@@ -404,16 +429,16 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     if (n >= half) return;
     const float wsg = epi_wscale(ep, n), wsu = epi_wscale(ep, half + n);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int tok = 4 * g + j;
+    for (int jj = 0; jj < JT; ++jj) {
+      const int tok = toks[jj], mt = jj >> 2, j = jj & 3;
       if (tok >= M) continue;
-      int tg = red(0, w, j, lane), tu = red(0, w + NT / 2, j, lane);
+      int tg = red(0, mt, w, j, lane), tu = red(0, mt, w + NT / 2, j, lane);
 #pragma unroll
       for (int k = 1; k < S; ++k) {
-        tg += red(k, w, j, lane);
-        tu += red(k, w + NT / 2, j, lane);
+        tg += red(k, mt, w, j, lane);
+        tu += red(k, mt, w + NT / 2, j, lane);
       }
-      const float as = NORM ? col.as[j] : epi_ascale(ep, tok);
+      const float as = NORM ? col.as[jj] : epi_ascale(ep, tok);
       float yg = __fmul_rn(__fmul_rn((float)tg, wsg), as), yu = __fmul_rn(__fmul_rn((float)tu, wsu), as);
       if (ep.mid_dtype == WFB_BF16) {
         yg = bf16_bits_to_f32(f32_to_bf16_rne(yg));
@@ -428,13 +453,13 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     const int n = n0 + 16 * nt + nl;
     if (ep.amax) {  // greedy-argmax keys: the maximum over the 16 rows of each token, one slot per 16 rows
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tok = 4 * g + j;
-        int tot = red(0, nt, j, lane);
+      for (int jj = 0; jj < JT; ++jj) {
+        const int tok = toks[jj], mt = jj >> 2, j = jj & 3;
+        int tot = red(0, mt, nt, j, lane);
 #pragma unroll
-        for (int k = 1; k < S; ++k) tot += red(k, nt, j, lane);
+        for (int k = 1; k < S; ++k) tot += red(k, mt, nt, j, lane);
         const bool valid = tok < M && n < N;
-        uint64_t key = epi_store_key_r(ep, col.ws, col.as[j], col.bias, col.res[j], tok, n, tot, valid);
+        uint64_t key = epi_store_key_r(ep, col.ws, col.as[jj], col.bias, col.res[jj], tok, n, tot, valid);
         key = group_max_u64<16>(key);
         const int slot = blockIdx.x * NT + nt;
         if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
@@ -443,28 +468,28 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     }
     if (n >= N) return;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int tok = 4 * g + j;
-      int tot = red(0, nt, j, lane);
+    for (int jj = 0; jj < JT; ++jj) {
+      const int tok = toks[jj], mt = jj >> 2, j = jj & 3;
+      int tot = red(0, mt, nt, j, lane);
 #pragma unroll
-      for (int k = 1; k < S; ++k) tot += red(k, nt, j, lane);
-      if (tok < M) epi_store_r(ep, col.ws, col.as[j], col.bias, col.res[j], tok, n, tot);
+      for (int k = 1; k < S; ++k) tot += red(k, mt, nt, j, lane);
+      if (tok < M) epi_store_r(ep, col.ws, col.as[jj], col.bias, col.res[jj], tok, n, tot);
     }
   } else {
     // y (fp32, before the residual) of the [M tokens x 16 NT rows] tile into LDS (the activation staging),
     // rows rotated by 4 per token to spread the banks
     constexpr int RW = 16 * NT;
     float* ys = XT == kAreg ? ysb : reinterpret_cast<float*>(&al[0][0][0][0]);  // free after the barrier above
-    static_assert(XT == kAreg || sizeof(al) >= 16 * RW * 4, "staging space");
+    static_assert(XT == kAreg || sizeof(al) >= 16 * MT * RW * 4, "staging space");
     if (w < NT) {
       const int c = 16 * w + nl;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tok = 4 * g + j;
-        int tot = red(0, w, j, lane);
+      for (int jj = 0; jj < JT; ++jj) {
+        const int tok = toks[jj], mt = jj >> 2, j = jj & 3;
+        int tot = red(0, mt, w, j, lane);
 #pragma unroll
-        for (int k = 1; k < S; ++k) tot += red(k, w, j, lane);
-        ys[tok * RW + ((c + 4 * tok) & (RW - 1))] = epi_y(ep, col.ws, col.as[j], col.bias, tot);
+        for (int k = 1; k < S; ++k) tot += red(k, mt, w, j, lane);
+        ys[tok * RW + ((c + 4 * tok) & (RW - 1))] = epi_y(ep, col.ws, col.as[jj], col.bias, tot);
       }
     }
     __syncthreads();
@@ -710,6 +735,10 @@ inline hipError_t launch_persist(const uint8_t* W, int n, int C, const int8_t* A
   return hipErrorNotSupported;
 }
 
+// Shapes whose two-token-tile form (MR = 32) stays within the registers of its occupancy (more row
+// tiles per wave spill).
+constexpr bool fits_two_tiles(int S, int NT) { return NT * S <= 20; }
+
 // (S, TP) by the number of 512-weight step pairs T2 = ceil(K / 512): S = T2 waves up to 8 (K = 2560: 5,
 // K = 4096: 8, from sweeps), two pairs per wave up to 16 pairs, then 14 x 2 (K <= 14336, LDS permitting).
 // XT = kF32 / kBf16: the norm prologue on x of that storage tag (K <= 4096); kAreg: codes A held in
@@ -721,8 +750,8 @@ hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_
   const bool staged = GLUE == 0 && e.out && !e.acc_out && !e.amax;
 #define WFB_SL_GO(S, NT, TP)                                                                                   \
   do {                                                                                                         \
-    if constexpr ((XT == kAreg ? lds_bytes_areg(S, NT, TP) : lds_bytes(S, NT, TP, MR)) <= 163840 &&          \
-                  (GLUE ? NT / 2 : NT) <= S) {                                                                \
+    if constexpr ((XT == kAreg ? lds_bytes_areg(S, NT, TP, (MR + 15) / 16) : lds_bytes(S, NT, TP, MR)) <= 163840 && \
+                  (GLUE ? NT / 2 : NT) <= S && (MR <= 16 || fits_two_tiles(S, NT))) {         \
       const dim3 grid(GLUE ? (n / 2 + 8 * NT - 1) / (8 * NT) : (n + 16 * NT - 1) / (16 * NT));                 \
       if (GLUE == 0 && staged)                                                                                 \
         hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, GLUE == 0, XT>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, \
@@ -784,21 +813,26 @@ hipError_t launch_modes(const uint8_t* W, int n, int C, const int8_t* A, int m, 
                         int nt_pref, const NormSrc& ns, hipStream_t s) {
   if (ns.x == nullptr) {
     if (A == nullptr) return hipErrorInvalidValue;
-    // many row tiles with a per-lane epilogue (the greedy LM head): the persistent form
-    if (GLUE == 0 && (e.amax || e.acc_out || !e.out) && !e.bias && !e.res && e.nseg == 1 &&
-        n >= kPersistMinRows) {
-      const hipError_t st = launch_persist(W, n, C, A, m, lda, e, cu_count(), s);
-      if (st != hipErrorNotSupported) return st;
+    // many row tiles with a per-lane epilogue (the greedy LM head): the persistent form (one token tile)
+    if constexpr (MR <= 16) {
+      if (GLUE == 0 && (e.amax || e.acc_out || !e.out) && !e.bias && !e.res && e.nseg == 1 && n >= kPersistMinRows) {
+        const hipError_t st = launch_persist(W, n, C, A, m, lda, e, cu_count(), s);
+        if (st != hipErrorNotSupported) return st;
+      }
     }
     const hipError_t st = launch<MR, GLUE, kNone>(W, n, C, A, m, lda, e, nt_pref, ns, s);
-    if constexpr (GLUE == 0) {  // activations too long for the LDS beside the weights: in registers
+    if constexpr (GLUE == 0 && MR <= 16) {  // activations too long for the LDS beside the weights: in registers
       if (st == hipErrorNotSupported) return launch<MR, GLUE, kAreg>(W, n, C, A, m, lda, e, nt_pref, ns, s);
     }
     return st;
   }
-  if (C > 64 || ns.h > 64 * C || (ns.xdt != WFB_F32 && ns.xdt != WFB_BF16)) return hipErrorInvalidValue;
-  if (src_tag(ns.xdt) == kF32) return launch<MR, GLUE, kF32>(W, n, C, A, m, lda, e, nt_pref, ns, s);
-  return launch<MR, GLUE, kBf16>(W, n, C, A, m, lda, e, nt_pref, ns, s);
+  if constexpr (MR > 16) {  // the norm prologue serves one token tile
+    return hipErrorNotSupported;
+  } else {
+    if (C > 64 || ns.h > 64 * C || (ns.xdt != WFB_F32 && ns.xdt != WFB_BF16)) return hipErrorInvalidValue;
+    if (src_tag(ns.xdt) == kF32) return launch<MR, GLUE, kF32>(W, n, C, A, m, lda, e, nt_pref, ns, s);
+    return launch<MR, GLUE, kBf16>(W, n, C, A, m, lda, e, nt_pref, ns, s);
+  }
 }
 
 }  // namespace skinny_lds

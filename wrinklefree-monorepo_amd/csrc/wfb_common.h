@@ -528,7 +528,7 @@ hipError_t launch_gemv_i2s_norm(const uint8_t* W, int n, int k, int m, const Epi
 // weight-scale segments), K <= 4096, n % 64 == 0; act WFB_ACT_SILU or WFB_ACT_RELU2.
 hipError_t launch_gemv_i2s_norm_glu(const uint8_t* W, int n, int k, const Epilogue& e, const NormSrc& ns, int act,
                                     hipStream_t s);
-// M <= 16 tokens with both operands staged in LDS (skinny_lds.h); act 0 (plain) or a WFB_ACT_* gated
+// M <= 32 tokens (16 with the norm prologue) with both operands staged in LDS (skinny_lds.h); act 0 (plain) or a WFB_ACT_* gated
 // gate|up product; returns hipErrorNotSupported when the shape does not fit its LDS (the caller then
 // takes the register-operand kernels).  Needs N*K/4 and (M-1)*lda + K below 2^31.
 hipError_t launch_skinny_lds_mr4(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
@@ -536,6 +536,9 @@ hipError_t launch_skinny_lds_mr4(const uint8_t* W, int n, int C, const int8_t* A
 hipError_t launch_skinny_lds_mr8(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
                                  const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
 hipError_t launch_skinny_lds_mr16(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
+                                  const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
+// 17..32 tokens as two 16-token tiles (no norm prologue)
+hipError_t launch_skinny_lds_mr32(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
                                   const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
 inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                                     const Epilogue& e, int act, hipStream_t s, const NormSrc& ns = NormSrc{}) {
@@ -557,6 +560,15 @@ inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t
   if (m <= 4) return launch_skinny_lds_mr4(W, n, C, A, m, lda, e, act, nt_pref, ns, s);
   if (m <= 8) return launch_skinny_lds_mr8(W, n, C, A, m, lda, e, act, nt_pref, ns, s);
   if (m <= 16) return launch_skinny_lds_mr16(W, n, C, A, m, lda, e, act, nt_pref, ns, s);
+  // 17..32 tokens: two token tiles per weight fragment where the staging of 32 activation rows still
+  // leaves room for a full grid -- rows up to 2560 on outputs up to 32768 rows (gate|up rows when
+  // gated), rows up to 4096 on outputs of one round (4096 rows).  Measured on MI355X against the
+  // split-K and 32-row tile kernels at M = 17 / 24 / 32: 13824 x 2560 12.7 -> 7.3-7.7 us, 2560 x 2560
+  // 5.1-6.4 -> 4.4, gated 13824 x 2560 8.9-11.8 -> 8.1-9.0, 4096 x 4096 6.3-8.0 -> 5.5-5.8; with 4096-long
+  // rows on taller outputs (6144 x 4096: 7.4 -> 9.4 at M = 17, 28672 x 4096: 17.4 -> 29.8) and rows
+  // held in registers (2560 x 6912) it is slower or even, and those keep the other kernels.
+  if (m <= 32 && !ns.x && ((k <= 2560 && n <= 32768) || (k <= 4096 && n <= 4096)))
+    return launch_skinny_lds_mr32(W, n, C, A, m, lda, e, act, nt_pref, ns, s);
   return hipErrorNotSupported;
 }
 // 3 <= M <= 64 through the split-K skinny kernel (16, 32 or 64 rows per workgroup); needs
