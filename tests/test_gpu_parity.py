@@ -203,12 +203,12 @@ def test_batched_sweep_mfma(pkg, dev, n, k, m):
         _check_linear(pkg, dev, packed, a, 1.0, np.ones(m, np.float32), kernel="auto", check_fp32=False)
 
 
-@pytest.mark.parametrize("m", [3, 4, 5, 8, 9, 12, 16, 17, 31, 32])
+@pytest.mark.parametrize("m", [3, 4, 5, 8, 9, 12, 16, 17, 31, 32, 40, 64])
 @pytest.mark.parametrize("n,k", SHAPES_2B)
 def test_batched_decode_outputs_without_accumulator_copy(pkg, dev, m, n, k):
     """M <= 16 without an accumulator copy takes the LDS-staged kernel's whole-line epilogue (17..32 tokens
-    too, as two token tiles, on the K = 2560 shapes): bf16 and fp32 outputs, a bias, and a residual in
-    either dtype, all equal to the oracle's rescale bit for bit."""
+    too, as two token tiles, on the K = 2560 shapes, and 33..64 as four on the narrow ones): bf16 and fp32
+    outputs, a bias, and a residual in either dtype, all equal to the oracle's rescale bit for bit."""
     rng = np.random.default_rng(7000 + m + n + k)
     packed = _packed(rng, n, k)
     a = orc.random_int8(rng, m, k)
@@ -252,10 +252,13 @@ def test_batched_long_rows_register_activations(pkg, dev, m, n, k):
 @pytest.mark.parametrize("m,n,k", [(12, 32800, 128), (24, 16400, 256), (64, 8200, 384), (9, 40, 8192),
                                    (24, 9216, 2560), (24, 9200, 2560), (40, 6144, 8192), (40, 6144, 8320),
                                    (40, 12000, 8320), (17, 18432, 256), (24, 9216, 4096), (24, 9200, 4096),
-                                   (32, 4096, 4096), (32, 4112, 4096), (32, 32768, 2560), (32, 32784, 2560)])
+                                   (32, 4096, 4096), (32, 4112, 4096), (32, 32768, 2560), (32, 32784, 2560),
+                                   (33, 4096, 4096), (64, 4096, 4096), (64, 4112, 4096), (48, 2560, 4224),
+                                   (40, 1000, 2560)])
 def test_batched_kernel_choice_boundaries(pkg, dev, m, n, k):
     # 3 <= M <= 64: the LDS-staged kernel up to 16 tokens, and with two token tiles for 17..32 tokens on
-    # rows up to 2560 (outputs up to 32768 rows) or 4096 (outputs up to 4096 rows); else the 32-row tile
+    # rows up to 2560 (outputs up to 32768 rows) or 4096 (outputs up to 4096 rows), with four for 33..64
+    # tokens on rows up to 4096 and outputs up to 4096 rows; else the 32-row tile
     # kernel for M > 16 when N * ceil(M/16) >= 18432 and K <= 8192, else the split-K skinny kernel while
     # N * ceil(M/16) <= 32768 (always for M <= 8), else the whole-K wave-per-rows kernel; these shapes
     # sit on either side of those boundaries

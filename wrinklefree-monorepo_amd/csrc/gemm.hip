@@ -716,7 +716,7 @@ hipError_t launch_skinny_glu(const uint8_t* W, int n, int C, const int8_t* A, in
 hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                                   const Epilogue& e, hipStream_t s) {
   const int C = k / 64;
-  if (m <= 32) {
+  if (m <= 64) {
     const hipError_t st = launch_skinny_lds(W, n, k, A, m, lda, e, 0, s);
     if (st != hipErrorNotSupported) return st;
   }
@@ -756,7 +756,7 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   // 67.1 -> 15.0 us, 13824 x 2560 26.1 -> 10.0, 6144 x 4096 25.8 -> 13.3; M = 24: 13824 x 2560 10.5 -> 9.8),
   // the split-K kernels below that and for longer rows (M = 64, 4096 x 14336: 33.5 vs 37.2 us).
   // operands staged in LDS (skinny_lds.h) where its LDS holds them (17..32 tokens: where measured faster)
-  if (m <= 32 && small_offsets) {
+  if (m <= 64 && small_offsets) {
     const hipError_t st = launch_skinny_lds(W, n, k, A, m, lda, e, 0, s);
     if (st != hipErrorNotSupported) return st;
   }

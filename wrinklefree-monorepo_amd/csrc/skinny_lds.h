@@ -1,11 +1,11 @@
-// Batched-decode linear for M <= 32 tokens with both operands staged in LDS (included by the four
+// Batched-decode linear for M <= 64 tokens with both operands staged in LDS (included by the five
 // skinny_mr*.hip files, one per staged token-row count, so they compile in parallel).
 //
 // Replaces, like the other I2_S GEMM paths, bitnet_gemm_i2_i8 / bitnet_gemm_cpu
 // (SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:814-874, SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:370-406).
 //
-// v_mfma_i32_16x16x64_i8, one 16-token tile (two for 17..32 tokens, MR = 32: each weight fragment read
-// from LDS and unpacked once feeds both tiles' MFMAs).  A workgroup owns NT tiles of 16 weight rows and all of K;
+// v_mfma_i32_16x16x64_i8, one 16-token tile (two for 17..32 tokens, MR = 32, four for 33..64, MR = 64:
+// each weight fragment read from LDS and unpacked once feeds every tile's MFMAs).  A workgroup owns NT tiles of 16 weight rows and all of K;
 // its S waves split K into step pairs of 512 weights (128 packed bytes per row), wave w taking pairs
 // w, w + S, ... (TP of them).  Measured on MI355X, what sets the time of this kernel is how its loads
 // cover cache lines, so both operands are brought in whole lines by 16-byte LDS-DMA loads
@@ -55,9 +55,15 @@ __device__ __forceinline__ void dma16(buf_t r, void* lds, uint32_t voff) {
 
 // The per-wave partial tiles of the K reduction overwrite the wave's own weight staging, and the staged
 // output tile the activation staging, so the LDS is the two operand stagings only.
-constexpr size_t lds_bytes(int S, int NT, int TP, int MR) { return (size_t)S * TP * (NT * 2048 + 2 * MR * 256); }
+// With more than two token tiles per step pair (MT > 2 TP) the partial tiles get their own buffer.
+constexpr size_t red_bytes(int S, int NT, int TP, int MT) { return MT > 2 * TP ? (size_t)S * MT * NT * 1024 : 0; }
+constexpr size_t lds_bytes(int S, int NT, int TP, int MR) {
+  return (size_t)S * TP * (NT * 2048 + 2 * MR * 256) + red_bytes(S, NT, TP, (MR + 15) / 16);
+}
 // with the activations in registers (kAreg): the weight staging and the staged output tile
-constexpr size_t lds_bytes_areg(int S, int NT, int TP, int MT) { return (size_t)S * TP * NT * 2048 + 16 * MT * 16 * NT * 4 + 64; }
+constexpr size_t lds_bytes_areg(int S, int NT, int TP, int MT) {
+  return (size_t)S * TP * NT * 2048 + 16 * MT * 16 * NT * 4 + 64 + red_bytes(S, NT, TP, MT);
+}
 
 // ---- norm prologue helpers ---------------------------------------------------------------------------
 // Storage-type tags of the prologue's x and gamma (kNone: no prologue / no gamma).  Distinct from the
@@ -203,20 +209,22 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
                                                  int64_t lda, int M, int N, int C, Epilogue ep, NormSrc ns) {
   static_assert((GLUE ? NT / 2 : NT) <= S, "one wave per output row tile in the epilogue");
   static_assert(GLUE == 0 || NT % 2 == 0, "gated mode pairs gate and up tiles");
-  static_assert(MR == 4 || MR == 8 || MR == 16 || MR == 32, "staged token rows");
+  static_assert(MR == 4 || MR == 8 || MR == 16 || MR == 32 || MR == 64, "staged token rows");
   constexpr bool NORM = XT == kF32 || XT == kBf16;  // codes formed in the prologue, token scales with them
-  // 16-token tiles: MR = 32 runs two, each weight fragment feeding both
-  constexpr int MT = MR > 16 ? 2 : 1;
+  // 16-token tiles: MR = 32 / 64 run two / four, each weight fragment feeding all of them
+  constexpr int MT = MR > 16 ? MR / 16 : 1;
   static_assert(MT == 1 || !NORM, "the norm prologue serves up to 16 tokens");
-  static_assert(MT <= 2 * TP, "partial tiles fit the wave's weight staging");
+  constexpr bool RED_OWN = MT > 2 * TP;  // partial tiles beyond the wave's weight staging: own buffer
   __shared__ __attribute__((aligned(16))) int8_t wl[S][TP][NT][2048];
   __shared__ __attribute__((aligned(16))) int8_t al[XT == kAreg ? 1 : S][XT == kAreg ? 1 : TP][2][XT == kAreg ? 16 : MR * 256];
   // staged output tile of the register-activation mode (the others use the activation staging)
   __shared__ __attribute__((aligned(16))) float ysb[XT == kAreg && STAGED ? 16 * MT * 16 * NT : 1];
+  __shared__ __attribute__((aligned(16))) int redo[RED_OWN ? S : 1][RED_OWN ? MT * NT * 256 : 1];
   // partial tile (token tile mt, row tile nt, token slot j, lane) of wave w, in wave w's own weight
-  // staging (free once the wave has read it: its LDS reads and writes execute in order)
+  // staging (free once the wave has read it: its LDS reads and writes execute in order) when it fits there
   auto red = [&](int wv, int mt, int nt, int j, int l) -> int& {
-    return reinterpret_cast<int*>(&wl[wv][0][0][0])[((mt * NT + nt) * 4 + j) * 64 + l];
+    int* base = RED_OWN ? &redo[wv][0] : reinterpret_cast<int*>(&wl[wv][0][0][0]);
+    return base[((mt * NT + nt) * 4 + j) * 64 + l];
   };
   // norm prologue: scale of token tok, written by its wave (tok % S) after that wave's partial tiles
   constexpr int RPW = (MR + S - 1) / S;
@@ -735,9 +743,12 @@ inline hipError_t launch_persist(const uint8_t* W, int n, int C, const int8_t* A
   return hipErrorNotSupported;
 }
 
-// Shapes whose two-token-tile form (MR = 32) stays within the registers of its occupancy (more row
-// tiles per wave spill).
-constexpr bool fits_two_tiles(int S, int NT) { return NT * S <= 20; }
+// Shapes whose multi-token-tile forms stay within the registers of their occupancy (more row tiles
+// per wave spill): two tiles (MR = 32) with NT * S <= 20, four (MR = 64, activations in registers) with
+// one row tile and one step pair per wave.
+constexpr bool fits_tiles(int MR, int S, int NT, int TP) {
+  return MR <= 16 || (MR == 32 ? NT * S <= 20 : NT == 1 && TP == 1);
+}
 
 // (S, TP) by the number of 512-weight step pairs T2 = ceil(K / 512): S = T2 waves up to 8 (K = 2560: 5,
 // K = 4096: 8, from sweeps), two pairs per wave up to 16 pairs, then 14 x 2 (K <= 14336, LDS permitting).
@@ -751,7 +762,7 @@ hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_
 #define WFB_SL_GO(S, NT, TP)                                                                                   \
   do {                                                                                                         \
     if constexpr ((XT == kAreg ? lds_bytes_areg(S, NT, TP, (MR + 15) / 16) : lds_bytes(S, NT, TP, MR)) <= 163840 && \
-                  (GLUE ? NT / 2 : NT) <= S && (MR <= 16 || fits_two_tiles(S, NT))) {         \
+                  (GLUE ? NT / 2 : NT) <= S && fits_tiles(MR, S, NT, TP)) {                    \
       const dim3 grid(GLUE ? (n / 2 + 8 * NT - 1) / (8 * NT) : (n + 16 * NT - 1) / (16 * NT));                 \
       if (GLUE == 0 && staged)                                                                                 \
         hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, GLUE == 0, XT>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, \
@@ -774,13 +785,14 @@ hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_
     }                                                            \
     return hipErrorNotSupported;                                 \
   } while (0)
-  if constexpr (XT != kAreg) {  // the register-activation mode only serves the long rows below
+  // the register-activation mode serves the long rows below, and 64 tokens on rows up to 4096
+  if constexpr (XT != kAreg || MR == 64) {
     if (T2 <= 2) WFB_SL_NT(2, 1);
     if (T2 <= 4) WFB_SL_NT(4, 1);
     if (T2 <= 5) WFB_SL_NT(5, 1);
     if (T2 <= 8) WFB_SL_NT(8, 1);
   }
-  if constexpr (XT == kNone || XT == kAreg) {
+  if constexpr ((XT == kNone || XT == kAreg) && MR != 64) {
     if (T2 <= 14) WFB_SL_NT(7, 2);
     if (T2 <= 16) WFB_SL_NT(8, 2);
     if (T2 <= 28) WFB_SL_NT(14, 2);
@@ -821,7 +833,7 @@ hipError_t launch_modes(const uint8_t* W, int n, int C, const int8_t* A, int m, 
       }
     }
     const hipError_t st = launch<MR, GLUE, kNone>(W, n, C, A, m, lda, e, nt_pref, ns, s);
-    if constexpr (GLUE == 0 && MR <= 16) {  // activations too long for the LDS beside the weights: in registers
+    if constexpr (GLUE == 0 && MR != 32) {  // activations too long for the LDS beside the weights: in registers
       if (st == hipErrorNotSupported) return launch<MR, GLUE, kAreg>(W, n, C, A, m, lda, e, nt_pref, ns, s);
     }
     return st;

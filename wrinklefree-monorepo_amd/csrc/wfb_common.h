@@ -537,8 +537,10 @@ hipError_t launch_skinny_lds_mr8(const uint8_t* W, int n, int C, const int8_t* A
                                  const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
 hipError_t launch_skinny_lds_mr16(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
                                   const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
-// 17..32 tokens as two 16-token tiles (no norm prologue)
+// 17..32 tokens as two 16-token tiles, 33..64 as four (no norm prologue; the four-tile form plain only)
 hipError_t launch_skinny_lds_mr32(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
+                                  const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
+hipError_t launch_skinny_lds_mr64(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
                                   const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
 inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
                                     const Epilogue& e, int act, hipStream_t s, const NormSrc& ns = NormSrc{}) {
@@ -569,6 +571,11 @@ inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t
   // held in registers (2560 x 6912) it is slower or even, and those keep the other kernels.
   if (m <= 32 && !ns.x && ((k <= 2560 && n <= 32768) || (k <= 4096 && n <= 4096)))
     return launch_skinny_lds_mr32(W, n, C, A, m, lda, e, act, nt_pref, ns, s);
+  // 33..64 tokens: four token tiles, activations in registers (32 rows or more of 2560 do not fit the
+  // staging), one row tile per workgroup -- ahead only on narrow outputs (M = 64: 2560 x 2560 10.1 ->
+  // 9.1 us, 4096 x 4096 13.5 -> 12.6; 6144 x 4096 15.7 -> 23.3, 13824 x 2560 12.9 -> 34.1)
+  if (m > 32 && m <= 64 && !ns.x && k <= 4096 && n <= 4096)
+    return launch_skinny_lds_mr64(W, n, C, A, m, lda, e, act, 1, ns, s);
   return hipErrorNotSupported;
 }
 // 3 <= M <= 64 through the split-K skinny kernel (16, 32 or 64 rows per workgroup); needs
