@@ -57,8 +57,10 @@ __device__ __forceinline__ void dma16(buf_t r, void* lds, uint32_t voff) {
 // output tile the activation staging, so the LDS is the two operand stagings only.
 // With more than two token tiles per step pair (MT > 2 TP) the partial tiles get their own buffer.
 constexpr size_t red_bytes(int S, int NT, int TP, int MT) { return MT > 2 * TP ? (size_t)S * MT * NT * 1024 : 0; }
+// (codes path with several token tiles and step pairs: one activation slot per wave, restaged per pair)
 constexpr size_t lds_bytes(int S, int NT, int TP, int MR) {
-  return (size_t)S * TP * (NT * 2048 + 2 * MR * 256) + red_bytes(S, NT, TP, (MR + 15) / 16);
+  return (size_t)S * TP * NT * 2048 + (size_t)S * (MR > 16 && TP > 1 ? 1 : TP) * 2 * MR * 256 +
+         red_bytes(S, NT, TP, (MR + 15) / 16);
 }
 // with the activations in registers (kAreg): the weight staging and the staged output tile
 constexpr size_t lds_bytes_areg(int S, int NT, int TP, int MT) {
@@ -215,8 +217,12 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   constexpr int MT = MR > 16 ? MR / 16 : 1;
   static_assert(MT == 1 || !NORM, "the norm prologue serves up to 16 tokens");
   constexpr bool RED_OWN = MT > 2 * TP;  // partial tiles beyond the wave's weight staging: own buffer
+  // several token tiles and step pairs (codes path): the activations of one step pair at a time, each
+  // wave restaging its slot for its next pair (the weights of all pairs are staged up front)
+  constexpr bool RS = XT == kNone && MT > 1 && TP > 1;
+  constexpr int TPA = RS ? 1 : TP;
   __shared__ __attribute__((aligned(16))) int8_t wl[S][TP][NT][2048];
-  __shared__ __attribute__((aligned(16))) int8_t al[XT == kAreg ? 1 : S][XT == kAreg ? 1 : TP][2][XT == kAreg ? 16 : MR * 256];
+  __shared__ __attribute__((aligned(16))) int8_t al[XT == kAreg ? 1 : S][XT == kAreg ? 1 : TPA][2][XT == kAreg ? 16 : MR * 256];
   // staged output tile of the register-activation mode (the others use the activation staging)
   __shared__ __attribute__((aligned(16))) float ysb[XT == kAreg && STAGED ? 16 * MT * 16 * NT : 1];
   __shared__ __attribute__((aligned(16))) int redo[RED_OWN ? S : 1][RED_OWN ? MT * NT * 256 : 1];
@@ -261,6 +267,22 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
         }
     }
   };
+  // activations of the wave's step pair u (MR token rows x 256 bytes per step, 4 rows per instruction)
+  // into its staging slot
+  auto dma_act = [&](int u) {
+    const int p = w + S * u;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int i = 0; i < MR / 4; ++i) {
+        const int t = 2 * p + st;
+        const int tok = 4 * i + (lane >> 4);
+        const int q = (lane & 15) ^ (tok & 15);
+        const uint32_t kb = 256u * t + 16u * q;
+        const bool ok = p < T2 && t < T && tok < M && kb < (uint32_t)(64 * C);
+        dma16(ab, al[w][RS ? 0 : u][st] + 1024 * i, ok ? (uint32_t)((int64_t)tok * lda) + kb : a_end);
+      }
+  };
   // epilogue operands of the column this lane owns in the MFMA layout (row n, tokens 16 mt + 4g + j at
   // slot 4 mt + j)
   constexpr int JT = 4 * MT;
@@ -301,20 +323,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   } else if constexpr (XT == kNone) {
     dma_weights();
 #pragma unroll
-    for (int u = 0; u < TP; ++u) {
-      const int p = w + S * u;
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int i = 0; i < MR / 4; ++i) {
-          const int t = 2 * p + st;
-          const int tok = 4 * i + (lane >> 4);
-          const int q = (lane & 15) ^ (tok & 15);
-          const uint32_t kb = 256u * t + 16u * q;
-          const bool ok = p < T2 && t < T && tok < M && kb < (uint32_t)(64 * C);
-          dma16(ab, al[w][u][st] + 1024 * i, ok ? (uint32_t)((int64_t)tok * lda) + kb : a_end);
-        }
-    }
+    for (int u = 0; u < TPA; ++u) dma_act(u);
     col_loads();
   } else {
     // 8 codes of token row r at k = e0 .. e0 + 7 into the staging: step t = e0 / 256 of pair t / 2, which
@@ -354,6 +363,14 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   const int hh = nl >> 3, rr = nl & 7;
 #pragma unroll
   for (int u = 0; u < TP; ++u) {
+    if constexpr (RS) {
+      if (u > 0) {
+        // the slot's previous pair has been read (its fragments are in registers) before it is refilled
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        dma_act(u);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      }
+    }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       v4i av[MT][4];
@@ -365,7 +382,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
         } else {
           // token row 16 mt + nl (its slots swizzled by nl); rows >= M hold zeros or unused codes
           const int tr = 16 * mt + nl;
-          const int8_t* arow = al[w][u][st] + 256 * (tr < MR ? tr : MR - 1);
+          const int8_t* arow = al[w][RS ? 0 : u][st] + 256 * (tr < MR ? tr : MR - 1);
 #pragma unroll
           for (int f = 0; f < 4; ++f) {
             const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;  // step bytes 128 (g / 2) + 16 (g % 2) + 32 f

@@ -569,7 +569,7 @@ inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t
   // 5.1-6.4 -> 4.4, gated 13824 x 2560 8.9-11.8 -> 8.1-9.0, 4096 x 4096 6.3-8.0 -> 5.5-5.8; with 4096-long
   // rows on taller outputs (6144 x 4096: 7.4 -> 9.4 at M = 17, 28672 x 4096: 17.4 -> 29.8) and rows
   // held in registers (2560 x 6912) it is slower or even, and those keep the other kernels.
-  if (m <= 32 && !ns.x && ((k <= 2560 && n <= 32768) || (k <= 4096 && n <= 4096)))
+  if (m <= 32 && !ns.x && ((k <= 2560 && n <= 32768) || (k <= 7168 && n <= 4096)))
     return launch_skinny_lds_mr32(W, n, C, A, m, lda, e, act, nt_pref, ns, s);
   // 33..64 tokens: four token tiles, activations in registers (32 rows or more of 2560 do not fit the
   // staging), one row tile per workgroup -- ahead only on narrow outputs (M = 64: 2560 x 2560 10.1 ->
