@@ -57,10 +57,11 @@ __device__ __forceinline__ void dma16(buf_t r, void* lds, uint32_t voff) {
 // output tile the activation staging, so the LDS is the two operand stagings only.
 // With more than two token tiles per step pair (MT > 2 TP) the partial tiles get their own buffer.
 constexpr size_t red_bytes(int S, int NT, int TP, int MT) { return MT > 2 * TP ? (size_t)S * MT * NT * 1024 : 0; }
-// (codes path with several token tiles and step pairs: one activation slot per wave, restaged per pair)
+// Activation staging of the codes path, in steps per wave: every step of the wave's pairs, or -- with
+// several token tiles -- one slot restaged per pair (two tiles, several pairs) or per step (four tiles).
+constexpr int act_steps(int TP, int MR) { return MR > 32 ? 1 : MR > 16 && TP > 1 ? 2 : 2 * TP; }
 constexpr size_t lds_bytes(int S, int NT, int TP, int MR) {
-  return (size_t)S * TP * NT * 2048 + (size_t)S * (MR > 16 && TP > 1 ? 1 : TP) * 2 * MR * 256 +
-         red_bytes(S, NT, TP, (MR + 15) / 16);
+  return (size_t)S * TP * NT * 2048 + (size_t)S * act_steps(TP, MR) * MR * 256 + red_bytes(S, NT, TP, (MR + 15) / 16);
 }
 // with the activations in registers (kAreg): the weight staging and the staged output tile
 constexpr size_t lds_bytes_areg(int S, int NT, int TP, int MT) {
@@ -217,12 +218,15 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   constexpr int MT = MR > 16 ? MR / 16 : 1;
   static_assert(MT == 1 || !NORM, "the norm prologue serves up to 16 tokens");
   constexpr bool RED_OWN = MT > 2 * TP;  // partial tiles beyond the wave's weight staging: own buffer
-  // several token tiles and step pairs (codes path): the activations of one step pair at a time, each
-  // wave restaging its slot for its next pair (the weights of all pairs are staged up front)
-  constexpr bool RS = XT == kNone && MT > 1 && TP > 1;
-  constexpr int TPA = RS ? 1 : TP;
+  // several token tiles (codes path): the activations of one step pair (two tiles, several pairs) or one
+  // step (four tiles) at a time, each wave restaging its slot for its next unit (the weights of all its
+  // pairs are staged up front); otherwise every step of the wave's pairs at once
+  constexpr int STA = XT == kNone && MT > 2 ? 1 : 2;              // steps per slot
+  constexpr bool RS = XT == kNone && MT > 1 && (TP > 1 || STA == 1);
+  constexpr int TPA = RS ? 1 : TP;                                 // slots per wave
+  static_assert(XT == kAreg || TPA * STA == act_steps(TP, MR), "staging size as the launch counts it");
   __shared__ __attribute__((aligned(16))) int8_t wl[S][TP][NT][2048];
-  __shared__ __attribute__((aligned(16))) int8_t al[XT == kAreg ? 1 : S][XT == kAreg ? 1 : TPA][2][XT == kAreg ? 16 : MR * 256];
+  __shared__ __attribute__((aligned(16))) int8_t al[XT == kAreg ? 1 : S][XT == kAreg ? 1 : TPA][STA][XT == kAreg ? 16 : MR * 256];
   // staged output tile of the register-activation mode (the others use the activation staging)
   __shared__ __attribute__((aligned(16))) float ysb[XT == kAreg && STAGED ? 16 * MT * 16 * NT : 1];
   __shared__ __attribute__((aligned(16))) int redo[RED_OWN ? S : 1][RED_OWN ? MT * NT * 256 : 1];
@@ -267,12 +271,14 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
         }
     }
   };
-  // activations of the wave's step pair u (MR token rows x 256 bytes per step, 4 rows per instruction)
-  // into its staging slot
-  auto dma_act = [&](int u) {
+  // staging slot of step st of the wave's pair u
+  auto aslot = [&](int u, int st) -> int8_t* { return al[w][TPA == 1 ? 0 : u][STA == 1 ? 0 : st]; };
+  // activations of steps st0 .. st1 - 1 of the wave's step pair u (MR token rows x 256 bytes per step,
+  // 4 rows per instruction) into their slots
+  auto dma_act = [&](int u, int st0, int st1) {
     const int p = w + S * u;
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int st = st0; st < st1; ++st)
 #pragma unroll
       for (int i = 0; i < MR / 4; ++i) {
         const int t = 2 * p + st;
@@ -280,7 +286,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
         const int q = (lane & 15) ^ (tok & 15);
         const uint32_t kb = 256u * t + 16u * q;
         const bool ok = p < T2 && t < T && tok < M && kb < (uint32_t)(64 * C);
-        dma16(ab, al[w][RS ? 0 : u][st] + 1024 * i, ok ? (uint32_t)((int64_t)tok * lda) + kb : a_end);
+        dma16(ab, aslot(u, st) + 1024 * i, ok ? (uint32_t)((int64_t)tok * lda) + kb : a_end);
       }
   };
   // epilogue operands of the column this lane owns in the MFMA layout (row n, tokens 16 mt + 4g + j at
@@ -323,7 +329,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   } else if constexpr (XT == kNone) {
     dma_weights();
 #pragma unroll
-    for (int u = 0; u < TPA; ++u) dma_act(u);
+    for (int u = 0; u < TPA; ++u) dma_act(u, 0, STA);
     col_loads();
   } else {
     // 8 codes of token row r at k = e0 .. e0 + 7 into the staging: step t = e0 / 256 of pair t / 2, which
@@ -363,16 +369,16 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   const int hh = nl >> 3, rr = nl & 7;
 #pragma unroll
   for (int u = 0; u < TP; ++u) {
-    if constexpr (RS) {
-      if (u > 0) {
-        // the slot's previous pair has been read (its fragments are in registers) before it is refilled
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-        dma_act(u);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      }
-    }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
+      if constexpr (RS) {
+        if ((u > 0 || st > 0) && st % STA == 0) {
+          // the slot's previous unit has been read (its fragments are in registers) before it is refilled
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+          dma_act(u, st, st + STA);
+          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        }
+      }
       v4i av[MT][4];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -382,7 +388,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
         } else {
           // token row 16 mt + nl (its slots swizzled by nl); rows >= M hold zeros or unused codes
           const int tr = 16 * mt + nl;
-          const int8_t* arow = al[w][RS ? 0 : u][st] + 256 * (tr < MR ? tr : MR - 1);
+          const int8_t* arow = aslot(u, st) + 256 * (tr < MR ? tr : MR - 1);
 #pragma unroll
           for (int f = 0; f < 4; ++f) {
             const int qg = 8 * (g >> 1) + (g & 1) + 2 * f;  // step bytes 128 (g / 2) + 16 (g % 2) + 32 f
@@ -760,12 +766,10 @@ inline hipError_t launch_persist(const uint8_t* W, int n, int C, const int8_t* A
   return hipErrorNotSupported;
 }
 
-// Shapes whose multi-token-tile forms stay within the registers of their occupancy (more row tiles
-// per wave spill): two tiles (MR = 32) with NT * S <= 20, four (MR = 64, activations in registers) with
-// one row tile and one step pair per wave.
-constexpr bool fits_tiles(int MR, int S, int NT, int TP) {
-  return MR <= 16 || (MR == 32 ? NT * S <= 20 : NT == 1 && TP == 1);
-}
+// Shapes whose multi-token-tile forms stay within the registers of their occupancy (more row tiles or
+// step pairs per wave spill): two tiles (MR = 32) with NT * S <= 20, four (MR = 64) with one row tile
+// and one step pair per wave.
+constexpr bool fits_tiles(int MR, int S, int NT, int TP) { return MR <= 16 || (MR == 32 ? NT * S <= 20 : NT == 1 && TP == 1); }
 
 // (S, TP) by the number of 512-weight step pairs T2 = ceil(K / 512): S = T2 waves up to 8 (K = 2560: 5,
 // K = 4096: 8, from sweeps), two pairs per wave up to 16 pairs, then 14 x 2 (K <= 14336, LDS permitting).
@@ -802,7 +806,7 @@ hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_
     }                                                            \
     return hipErrorNotSupported;                                 \
   } while (0)
-  // the register-activation mode serves the long rows below, and 64 tokens on rows up to 4096
+  // the register-activation mode serves the long rows below, and 64 tokens on rows past the staging
   if constexpr (XT != kAreg || MR == 64) {
     if (T2 <= 2) WFB_SL_NT(2, 1);
     if (T2 <= 4) WFB_SL_NT(4, 1);

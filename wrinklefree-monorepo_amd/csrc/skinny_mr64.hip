@@ -1,5 +1,6 @@
 // Batched-decode linear with LDS-staged operands (skinny_lds.h) for 33..64 tokens: four 16-token tiles
-// per weight fragment (plain linear, codes path; activations in registers beyond the shortest rows).
+// per weight fragment (plain linear, codes path; activations staged one step at a time where the LDS
+// holds them, else in registers).
 #include "skinny_lds.h"
 
 namespace wfb {

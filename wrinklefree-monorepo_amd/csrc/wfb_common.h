@@ -571,9 +571,10 @@ inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t
   // held in registers (2560 x 6912) it is slower or even, and those keep the other kernels.
   if (m <= 32 && !ns.x && ((k <= 2560 && n <= 32768) || (k <= 7168 && n <= 4096)))
     return launch_skinny_lds_mr32(W, n, C, A, m, lda, e, act, nt_pref, ns, s);
-  // 33..64 tokens: four token tiles, activations in registers (32 rows or more of 2560 do not fit the
-  // staging), one row tile per workgroup -- ahead only on narrow outputs (M = 64: 2560 x 2560 10.1 ->
-  // 9.1 us, 4096 x 4096 13.5 -> 12.6; 6144 x 4096 15.7 -> 23.3, 13824 x 2560 12.9 -> 34.1)
+  // 33..64 tokens: four token tiles, one row tile per workgroup, activations staged one step at a time
+  // (rows up to 2560) or held in registers (up to 4096) -- ahead only on narrow outputs (M = 64:
+  // 2560 x 2560 10.1 -> 6.4 us, 3200 x 2560 10.2 -> 6.5, 4096 x 4096 13.5 -> 12.5; 13824 x 2560 12.9 ->
+  // 23.2 and 6144 x 4096 15.7 -> 23.3 keep the 32-row tile kernel)
   if (m > 32 && m <= 64 && !ns.x && k <= 4096 && n <= 4096)
     return launch_skinny_lds_mr64(W, n, C, A, m, lda, e, act, 1, ns, s);
   return hipErrorNotSupported;
