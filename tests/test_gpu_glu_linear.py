@@ -18,7 +18,8 @@ CASES = [
     (17, 2048, 1024, torch.bfloat16),   # two token tiles
     (32, 6912, 2560, torch.bfloat16),   # BitNet-2B gate|up at 32 tokens (LDS-staged, two token tiles)
     (24, 2048, 4096, torch.float32),    # 4096-long rows, one round of workgroups
-    (64, 4096, 512, torch.float32),     # four token tiles
+    (64, 4096, 512, torch.float32),     # two launches of two token tiles
+    (40, 6912, 2560, torch.bfloat16),   # BitNet-2B gate|up at 40 tokens (32 + 8)
 ]
 
 

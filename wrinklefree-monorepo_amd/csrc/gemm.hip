@@ -700,6 +700,24 @@ hipError_t launch_mt(const uint8_t* W, int n, int C, const int8_t* A, int m, int
 
 }  // namespace
 
+// 33..64 tokens as two launches of the staged kernel over token rows 0..31 and 32..M-1 (per-lane or
+// whole-line epilogues and the gated product, act != 0; not the greedy-argmax keys, which are laid out by
+// the launch's M).  Returns hipErrorNotSupported, before launching anything, where the staged kernel does
+// not take 32 tokens of this shape.
+static hipError_t launch_token_halves(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
+                                      const Epilogue& e, int act, hipStream_t s) {
+  const hipError_t st = launch_skinny_lds(W, n, k, A, 32, lda, e, act, s);
+  if (st != hipSuccess) return st;
+  Epilogue e2 = e;
+  if (e2.a_scale) e2.a_scale += 32;
+  // the gated product is stored fp32
+  if (e2.out) e2.out = static_cast<char*>(e2.out) + 32 * e2.ldo * (act || e2.out_dtype == WFB_F32 ? 4 : 2);
+  if (e2.acc_out) e2.acc_out += 32 * e2.ldo;
+  if (e2.res) e2.res = static_cast<const char*>(e2.res) + 32 * e2.ldr * (e2.res_dtype == WFB_F32 ? 4 : 2);
+  const hipError_t st2 = launch_skinny_lds(W, n, k, A + 32 * lda, m - 32, lda, e2, act, s);
+  return st2 == hipErrorNotSupported ? hipErrorInvalidValue : st2;  // the second half must not fall back
+}
+
 template <int MT, int GLUE>
 hipError_t launch_skinny_glu(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
                              hipStream_t s) {
@@ -733,6 +751,13 @@ hipError_t launch_gemm_i2s_glu(const uint8_t* W, int n, int k, const int8_t* A, 
     const hipError_t st = launch_skinny_lds(W, n, k, A, m, lda, e, act, s);
     if (st != hipErrorNotSupported) return st;
   }
+  // 33..64 tokens: two launches of the staged two-tile form where it takes 32 tokens of the shape
+  // (gated 13824 x 2560: M = 64 26.5 -> 17.0 us, M = 33 19.8 -> 13.9, measured on MI355X against the
+  // split-K kernel)
+  if (m > 32 && m <= 64) {
+    const hipError_t st = launch_token_halves(W, n, k, A, m, lda, e, act, s);
+    if (st != hipErrorNotSupported) return st;
+  }
 #define WFB_GLU(MT)                                                                              \
   return act == WFB_ACT_SILU ? launch_skinny_glu<MT, WFB_ACT_SILU>(W, n, C, A, m, lda, e, s) \
                              : launch_skinny_glu<MT, WFB_ACT_RELU2>(W, n, C, A, m, lda, e, s)
@@ -758,6 +783,13 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   // operands staged in LDS (skinny_lds.h) where its LDS holds them (17..32 tokens: where measured faster)
   if (m <= 64 && small_offsets) {
     const hipError_t st = launch_skinny_lds(W, n, k, A, m, lda, e, 0, s);
+    if (st != hipErrorNotSupported) return st;
+  }
+  // 33..64 tokens on rows from 4096 to 7168 of narrow outputs (the four-tile form stages neither them nor
+  // their registers): two launches of the two-tile form, measured on MI355X against the split-K kernel
+  // (2560 x 6912: M = 64 18.8 -> 12.7 us, M = 33 13.5 -> 10.4)
+  if (m > 32 && m <= 64 && small_offsets && !e.amax && k > 4096 && k <= 7168 && n <= 4096) {
+    const hipError_t st = launch_token_halves(W, n, k, A, m, lda, e, 0, s);
     if (st != hipErrorNotSupported) return st;
   }
   if (m > 16 && m <= 64 && small_offsets && (int64_t)n * mt >= 18432 && k <= 8192)
