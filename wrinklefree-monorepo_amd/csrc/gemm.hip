@@ -355,11 +355,12 @@ __device__ __forceinline__ void lds_load16(buf_t r, void* lds_base, uint32_t vof
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_base, 16, voff, 0, 0, 0);
 }
 
-template <int TM, int KB, int OCC, int EPI>
+template <int TM, int KB, int OCC, int EPI, int TN>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_i2s_tile_kernel(
     const uint8_t* __restrict__ W, const int8_t* __restrict__ A, int64_t lda, int M, int N, int K, int tiles_m,
     int tiles_n, int ntiles, bool vec_out, Epilogue ep) {
-  constexpr int BM = 32 * TM, BN = 256, TN = 2;
+  // TN 32-column MFMA tiles per wave: 256-column tiles, or 128 where 256 leave most of the chip idle
+  constexpr int BM = 32 * TM, BN = 128 * TN;
   constexpr int AROW = 128 * KB;  // bytes of an activation row per stage
   constexpr int CH = 8 * KB;      // 16-byte chunks per activation row
   constexpr int BROW = 32 * KB;   // bytes of a weight row per stage
@@ -532,8 +533,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 #pragma unroll
     for (int q = 0; q < 4; ++q) wsg[tn][q] = epi_wscale(ep, n0 + (wn * TN + tn) * 32 + 8 * q + 4 * g);
   if constexpr (EPI == 1) {
-    // per 32-row MFMA tile: convert in registers, stage 32 rows x 64 bf16 (128-byte rows, 16-byte
-    // chunks XOR-swizzled by row) in this wave's own LDS buffer, store 8 rows x 128 B per instruction
+    // per 32-row MFMA tile: convert in registers, stage 32 rows x 32 TN bf16 (64 TN-byte rows, 16-byte
+    // chunks XOR-swizzled by row) in this wave's own LDS buffer, store whole rows (8 rows x 128 B or
+    // 16 rows x 64 B per instruction)
+    constexpr int CPR = 4 * TN, RPI = 64 / CPR;  // 16-byte chunks per staged row, rows per instruction
     uint8_t* st = wn == 0 ? reinterpret_cast<uint8_t*>(lds_a0)
                 : wn == 1 ? reinterpret_cast<uint8_t*>(lds_a1)
                 : wn == 2 ? lds_b0 : lds_b1;
@@ -551,14 +554,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
           const bf16x2_t lo = __builtin_convertvector((f32x2_t){y[0], y[1]}, bf16x2_t);
           const bf16x2_t hi = __builtin_convertvector((f32x2_t){y[2], y[3]}, bf16x2_t);
           const int c = tn * 4 + q;
-          *reinterpret_cast<uint2*>(st + i * 128 + ((c ^ (i & 7)) * 16) + 8 * g) =
+          *reinterpret_cast<uint2*>(st + i * 16 * CPR + ((c ^ (i & (CPR - 1))) * 16) + 8 * g) =
               make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
         }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 8 * j + (l >> 3), c = l & 7;
-        const v4i v = *reinterpret_cast<const v4i*>(st + r * 128 + ((c ^ (r & 7)) * 16));
-        const int m = m0 + tm * 32 + r, n = n0 + wn * 64 + c * 8;
+      for (int j = 0; j < 32 / RPI; ++j) {
+        const int r = RPI * j + l / CPR, c = l % CPR;
+        const v4i v = *reinterpret_cast<const v4i*>(st + r * 16 * CPR + ((c ^ (r & (CPR - 1))) * 16));
+        const int m = m0 + tm * 32 + r, n = n0 + wn * 32 * TN + c * 8;
         if (m < M) {
           uint16_t* o = reinterpret_cast<uint16_t*>(ep.out) + (int64_t)m * ep.ldo + n;
           if (n + 7 < N) {
@@ -572,10 +575,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
       }
     }
   } else if constexpr (EPI == 2) {
-    // per 32-row MFMA tile: stage the fp32 outputs (32 rows x 64 columns, 256-byte rows, 16-byte chunks
-    // XOR-swizzled by row) in this wave's own LDS buffer; each lane then takes 8 consecutive outputs of
-    // a row, adds the residual read with one coalesced load (fp32 add, as epi_store), and stores them in
-    // the output type with one or two 16-byte stores -- whole lines, like EPI = 1
+    // per 32-row MFMA tile: stage the fp32 outputs (32 rows x 32 TN columns, 128 TN-byte rows, 16-byte
+    // chunks XOR-swizzled by row) in this wave's own LDS buffer; each lane then takes 8 consecutive
+    // outputs of a row, adds the residual read with one coalesced load (fp32 add, as epi_store), and
+    // stores them in the output type with one or two 16-byte stores -- whole lines, like EPI = 1
+    constexpr int CPR = 8 * TN, LPR8 = CPR / 2, RPI = 64 / LPR8;  // chunks per row, lanes per row, rows
     float* st = wn == 0 ? reinterpret_cast<float*>(lds_a0)
               : wn == 1 ? reinterpret_cast<float*>(lds_a1)
               : wn == 2 ? reinterpret_cast<float*>(lds_b0) : reinterpret_cast<float*>(lds_b1);
@@ -593,15 +597,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
           y.z = __fmul_rn(__fmul_rn((float)(acc[tn][tm][4 * q + 2] - rs), wsg[tn][q]), as);
           y.w = __fmul_rn(__fmul_rn((float)(acc[tn][tm][4 * q + 3] - rs), wsg[tn][q]), as);
           const int c = tn * 8 + 2 * q + g;  // 16-byte chunk of the row: columns 4c .. 4c + 3
-          *reinterpret_cast<float4*>(st + i * 64 + ((c ^ (i & 15)) * 4)) = y;
+          *reinterpret_cast<float4*>(st + i * 4 * CPR + ((c ^ (i & (CPR - 1))) * 4)) = y;
         }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 8 * j + (l >> 3), c8 = l & 7;
-        const float4 ya = *reinterpret_cast<const float4*>(st + r * 64 + (((2 * c8) ^ (r & 15)) * 4));
-        const float4 yb = *reinterpret_cast<const float4*>(st + r * 64 + (((2 * c8 + 1) ^ (r & 15)) * 4));
+      for (int j = 0; j < 32 / RPI; ++j) {
+        const int r = RPI * j + l / LPR8, c8 = l % LPR8;
+        const float4 ya = *reinterpret_cast<const float4*>(st + r * 4 * CPR + (((2 * c8) ^ (r & (CPR - 1))) * 4));
+        const float4 yb = *reinterpret_cast<const float4*>(st + r * 4 * CPR + (((2 * c8 + 1) ^ (r & (CPR - 1))) * 4));
         float y[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
-        const int m = m0 + tm * 32 + r, n = n0 + wn * 64 + c8 * 8;
+        const int m = m0 + tm * 32 + r, n = n0 + wn * 32 * TN + c8 * 8;
         if (m >= M) continue;
         const bool full = n + 7 < N;
         if (ep.res) {
@@ -663,10 +667,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
   }
 }
 
-template <int TM, int KB, int OCC>
+template <int TM, int KB, int OCC, int TN = 2>
 hipError_t launch_tile(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, const Epilogue& e,
                        hipStream_t s) {
-  const int tiles_n = (n + 255) / 256, tiles_m = (m + 32 * TM - 1) / (32 * TM);
+  const int tiles_n = (n + 128 * TN - 1) / (128 * TN), tiles_m = (m + 32 * TM - 1) / (32 * TM);
   const int nwg = tiles_n * tiles_m;
   const int grid = ((nwg + 7) / 8) * 8;
   const bool vec_out = e.ldo % 4 == 0 && (uintptr_t)e.out % 16 == 0 && (uintptr_t)e.acc_out % 16 == 0;
@@ -677,13 +681,13 @@ hipError_t launch_tile(const uint8_t* W, int n, int k, const int8_t* A, int m, i
   const bool staged = e.out && !e.bias && !e.acc_out && (e.ldo * osz) % 16 == 0 && (uintptr_t)e.out % 16 == 0 &&
                       (!e.res || ((e.ldr * rsz) % 16 == 0 && (uintptr_t)e.res % 16 == 0));
   if (bf16_only)
-    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 1>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 1, TN>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
                        tiles_m, tiles_n, nwg, vec_out, e);
   else if (staged)
-    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 2>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 2, TN>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
                        tiles_m, tiles_n, nwg, vec_out, e);
   else
-    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 0>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 0, TN>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
                        tiles_m, tiles_n, nwg, vec_out, e);
   return hipGetLastError();
 }
@@ -774,6 +778,10 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   // the weight stream (measured on MI355X over the Llama-3-8B / BitNet-2B decode shapes: always for
   // M <= 8, for larger M while N * (16-token tiles) <= 32768); it addresses through 32-bit offsets.
   const int mt = (m + 15) / 16;
+  // 32-row tiles of 256 columns that leave CUs idle (fewer than 256): 128-column tiles, four waves of 32
+  // columns, measured on MI355X (13824 x 2560 at M = 64: 12.9 -> 9.6 us; M = 128: 2560 x 2560 10.3 ->
+  // 7.7, 4096 x 14336 45.2 -> 35.5; 2560 x 6912 at M = 512 24.3 -> 22.3)
+  const bool few_tiles = (int64_t)((n + 255) / 256) * ((m + 31) / 32) < 256;
   const bool small_offsets = (int64_t)n * (k / 4) <= INT32_MAX && (int64_t)(m - 1) * lda + k <= INT32_MAX;
   // 17 <= M <= 64 on wide outputs: the 32-row tile kernel (one or two tile rows, its time nearly flat
   // in M), measured on MI355X against the skinny and whole-K kernels over M = 9..64 and the BitNet-2B /
@@ -793,7 +801,7 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
     if (st != hipErrorNotSupported) return st;
   }
   if (m > 16 && m <= 64 && small_offsets && (int64_t)n * mt >= 18432 && k <= 8192)
-    return launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
+    return few_tiles ? launch_tile<1, 2, 3, 1>(W, n, k, A, m, lda, e, s) : launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
   if (m <= 64 && small_offsets && (m <= 8 || (int64_t)n * (mt == 3 ? 4 : mt) <= 32768)) {
     if (m <= 16) return launch_skinny<1>(W, n, C, A, m, lda, e, s);
     if (m <= 32) return launch_skinny<2>(W, n, C, A, m, lda, e, s);
@@ -810,7 +818,7 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   const int64_t tn = (n + 255) / 256, t128 = tn * ((m + 127) / 128), t64 = tn * ((m + 63) / 64);
   if (t128 >= 320) return launch_tile<4, 1, 2>(W, n, k, A, m, lda, e, s);
   if (t64 >= 160) return launch_tile<2, 2, 2>(W, n, k, A, m, lda, e, s);
-  return launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
+  return few_tiles ? launch_tile<1, 2, 3, 1>(W, n, k, A, m, lda, e, s) : launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
 }
 
 }  // namespace wfb
