@@ -22,11 +22,13 @@ def _first_argmax(x):
 # 2048 workgroups); (8, 128256, 4096), (3, 40000, 2560), (5, 33000, 1024), (12, 65543, 2560), (16, 49152, 4096):
 # the persistent head kernel
 # (>= 32768 rows, up to 16 tokens), one-shot elsewhere; (17, 3000, 512), (32, 20000, 2560), (24, 4096, 4096):
-# two token tiles per weight fragment
+# two token tiles per weight fragment; (40, 40000, 2560), (64, 33000, 1024), (17, 32768, 512): more than 16
+# tokens on 32768+ rows, in chunks of 16 tokens through the persistent kernel
 @pytest.mark.parametrize("m,n,k", [(1, 1000, 256), (2, 5000, 640), (1, 70000, 4096), (2, 40000, 2560),
                                    (3, 4099, 2560), (8, 128256, 4096),
                                    (3, 40000, 2560), (5, 33000, 1024), (12, 65543, 2560), (16, 49152, 4096),
-                                   (17, 3000, 512), (32, 20000, 2560), (24, 4096, 4096), (64, 2048, 384)])
+                                   (17, 3000, 512), (32, 20000, 2560), (24, 4096, 4096), (64, 2048, 384),
+                                   (40, 40000, 2560), (64, 33000, 1024), (17, 32768, 512)])
 @pytest.mark.parametrize("ldt", [torch.float32, torch.bfloat16])
 def test_ternary_head_argmax_matches_oracle(pkg, dev, m, n, k, ldt):
     rng = np.random.default_rng(m * 1000 + n + k)

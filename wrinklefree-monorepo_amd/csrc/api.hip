@@ -4,6 +4,7 @@
 // SGB/sgl-kernel/csrc/cpu/torch_extension_cpu.cpp:336-346, 375-386, 410 and the K % 128 check of
 // SGB/sgl-kernel/csrc/bitnet/bitnet_gemv.cpp:331-336, 824-829) and adds the alignment the 128-bit
 // loads need.  Every check runs on the host before anything touches the GPU.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -98,6 +99,7 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
   e.acc_out = acc_out;
   e.amax = amax;
   e.amax_dt = amax_dt;
+  e.amax_ld = 0;
   e.res = res;
   e.res_dtype = res_dtype;
   e.ldr = ldr;
@@ -105,8 +107,25 @@ int linear_impl(Kernel kind, const char* name, const uint8_t* qweight, int64_t n
 
   const bool gemv = kind == Kernel::Gemv || (kind == Kernel::Auto && use_gemv(m, n, k, lda));
   if (amax) {  // greedy argmax: GEMV (M <= 2) or the skinny MFMA kernel, then the cross-workgroup maximum
-    hipError_t st = gemv ? wfb::launch_gemv_i2s(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream))
-                         : wfb::launch_gemm_i2s_skinny(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream));
+    hipError_t st = hipSuccess;
+    if (!gemv && m > 16 && n >= wfb::kHeadChunkMinRows) {
+      // more than 16 tokens on a head of many rows: chunks of 16 tokens through the persistent form,
+      // each writing its tokens' keys into the full [slots, M] layout (measured on MI355X, 128256 x 4096:
+      // M = 64 453 -> 140 us, M = 48 386 -> 109, M = 32 127 -> 79, M = 17 94 -> 77)
+      for (int64_t c0 = 0; c0 < m && st == hipSuccess; c0 += 16) {
+        wfb::Epilogue ec = e;
+        ec.amax = amax + c0;
+        ec.amax_ld = (int)m;
+        if (ec.a_scale) ec.a_scale += c0;
+        if (ec.out) ec.out = static_cast<char*>(ec.out) + c0 * ldo * (out_dtype == WFB_F32 ? 4 : 2);
+        if (ec.acc_out) ec.acc_out += c0 * ldo;
+        st = wfb::launch_gemm_i2s_skinny(qweight, (int)n, (int)k, act + c0 * lda, (int)std::min<int64_t>(16, m - c0), lda,
+                                         ec, as_stream(stream));
+      }
+    } else {
+      st = gemv ? wfb::launch_gemv_i2s(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream))
+                : wfb::launch_gemm_i2s_skinny(qweight, (int)n, (int)k, act, (int)m, lda, e, as_stream(stream));
+    }
     if (st == hipSuccess) st = wfb::launch_argmax_finalize(amax, (n + 15) / 16, m, tokens, as_stream(stream));
     return hip_status(st, name);
   }

@@ -269,7 +269,7 @@ __global__ __launch_bounds__(64 * S) void gemm_i2s_skinny_kernel(const uint8_t* 
           key = epi_store_key(ep, ws, valid ? asl[4 * mt + j] : 0.0f, bias, tok, n, tot, valid);
         key = group_max_u64<16>(key);
         const int slot = blockIdx.x * NT + nt;  // one slot per 16 rows
-        if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
+        if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * (ep.amax_ld ? ep.amax_ld : M) + tok] = key;
       }
     return;
   }

@@ -406,7 +406,7 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
       key = group_max_u64<64>(key);
       // slots are per 16 rows: the workgroup's first slot takes its maximum, the others key 0
       const int slot = row0 / 16 + t;
-      if (t < RB / 16 && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + m] = t == 0 ? key : 0;
+      if (t < RB / 16 && slot < (N + 15) / 16) ep.amax[(int64_t)slot * (ep.amax_ld ? ep.amax_ld : M) + m] = t == 0 ? key : 0;
     }
     return;
   }

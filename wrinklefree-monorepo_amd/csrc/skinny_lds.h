@@ -493,7 +493,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
         uint64_t key = epi_store_key_r(ep, col.ws, col.as[jj], col.bias, col.res[jj], tok, n, tot, valid);
         key = group_max_u64<16>(key);
         const int slot = blockIdx.x * NT + nt;
-        if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
+        if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * (ep.amax_ld ? ep.amax_ld : M) + tok] = key;
       }
       return;
     }
@@ -734,7 +734,7 @@ __global__ __launch_bounds__(64 * S) void kernel_persist(const uint8_t* __restri
         uint64_t key = epi_store_key_r(ep, ws, a, 0.0f, 0.0f, tok, n, tot, valid);
         key = group_max_u64<16>(key);
         const int slot = tile * NT + nt;
-        if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * M + tok] = key;
+        if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * (ep.amax_ld ? ep.amax_ld : M) + tok] = key;
       } else if (n < N && tok < M) {
         epi_store_r(ep, ws, a, 0.0f, 0.0f, tok, n, tot);
       }

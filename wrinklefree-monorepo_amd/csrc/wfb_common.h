@@ -182,10 +182,12 @@ struct Epilogue {
   int nseg;
   int seg_end[WFB_MAX_SEGMENTS - 1];
   // Greedy-argmax epilogue (GEMV and skinny kernels only): when set, workgroup b writes, for each
-  // token m, the largest argmax key of its rows to amax[b * M + m] (see amax_key); the value compared
-  // is y rounded to amax_dt (WFB_F32 or WFB_BF16), i.e. the logit as stored.
+  // token m, the largest argmax key of its rows to amax[b * ld + m], ld = amax_ld or, if that is 0, M
+  // (see amax_key); the value compared is y rounded to amax_dt (WFB_F32 or WFB_BF16), i.e. the logit as
+  // stored.  (A launch over a chunk of the tokens sets amax_ld to the full count and offsets amax.)
   uint64_t* amax;
   int amax_dt;
+  int amax_ld;
   // Residual added to every output before it is stored (y = ... + res[m, n]), or null.
   const void* res;
   int res_dtype;
@@ -579,6 +581,8 @@ inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t
     return launch_skinny_lds_mr64(W, n, C, A, m, lda, e, act, 1, ns, s);
   return hipErrorNotSupported;
 }
+// Rows from which a greedy head of more than 16 tokens runs in chunks of 16 (the persistent form's rows).
+constexpr int kHeadChunkMinRows = 32768;
 // 3 <= M <= 64 through the split-K skinny kernel (16, 32 or 64 rows per workgroup); needs
 // N*K/4 and (M-1)*lda + K below 2^31
 hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda,
