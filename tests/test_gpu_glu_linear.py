@@ -20,6 +20,7 @@ CASES = [
     (24, 2048, 4096, torch.float32),    # 4096-long rows, one round of workgroups
     (64, 4096, 512, torch.float32),     # two launches of two token tiles
     (40, 6912, 2560, torch.bfloat16),   # BitNet-2B gate|up at 40 tokens (32 + 8)
+    (37, 14336, 4096, torch.bfloat16),  # Llama-3-8B gate|up at 37 tokens (chunks of 16, 16, 5)
 ]
 
 
