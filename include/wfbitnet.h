@@ -288,7 +288,9 @@ int wfb_gqa_decode_attention(const void* q, int64_t ldq, const void* k_new, int6
  * batch * num_heads * (head_dim + 2) * splits, at most WFB_ATTN_WS(...)).  Same arguments, checks and
  * results as wfb_gqa_decode_attention with a workspace.  Every call on one GPU shares that GPU's
  * scratch: calls that overlap on one GPU (other streams, other threads) race; calls ordered on one
- * stream do not.  Nothing in it needs clearing between calls (each split writes all it is read for). */
+ * stream do not.  Nothing in it needs clearing between calls (each split writes all it is read for).
+ * The scratch used is that of the stream's device (the current device for the null stream), whichever
+ * device is current. */
 #define WFB_ATTN_SCRATCH_FLOATS (8 * 1024 * 1024)
 int wfb_gqa_decode_attention_noalloc(const void* q, int64_t ldq, const void* k_new, int64_t ldk,
                                      const void* v_new, int64_t ldv, int dtype,

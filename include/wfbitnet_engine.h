@@ -130,6 +130,13 @@ void bitnet_free_result(GenerationResult* result);
 int wfb_engine_sample_top_p(const float* logits, int64_t n, float temperature, float top_p, uint32_t seed,
                             int32_t draws, int32_t* out);
 
+/* Test hook, no counterpart in the reference's ABI: after `n` more successful allocations the engine's
+ * allocator (device buffers and the prompt's pinned id buffer) reports one failure, then allocates normally
+ * again; n < 0 (the default) never fails.  Process-wide.  Lets tests reach the out-of-memory paths, e.g. a
+ * prompt longer than any before it whose buffer growth fails: that call returns -1 and leaves no buffers,
+ * and the next prompt allocates again.  Returns 0. */
+int wfb_engine_fail_alloc_after(int64_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -194,3 +194,52 @@ def test_engine_errors_on_the_device(pkg, dev, tmp_path):
         with pytest.raises(RuntimeError, match="no prompt has been run"):
             eng.decode_step(3)
         assert eng.generate([4, 5], max_tokens=0) == []
+
+
+@pytest.mark.parametrize("after", [0, 3, 7])
+def test_failed_prompt_buffer_growth_leaves_no_state(pkg, dev, tmp_path, after):
+    """A prompt longer than every earlier one grows the prompt buffers (7 device buffers, then the pinned id
+    buffer).  When one of those allocations fails (the first, a middle one, the pinned one) the call returns -1
+    with the allocator's message and keeps no buffers, so later prompts, shorter or longer, allocate again and
+    give a fresh engine's tokens."""
+    M = pkg.model
+    cfg = M.BitNetConfig(**SMALL, hidden_act="relu2")
+    model = _model(M, dev, cfg, seed=2)
+    path = tmp_path / "m.bin"
+    model.save_sglbitnt(path)
+    short = _prompt(cfg, 6, 4)[0].tolist()
+    longp = _prompt(cfg, 50, 5)[0].tolist()
+    with pkg.NativeEngine(str(path), max_seq_len=96) as ref:
+        want_long = ref.generate(longp, max_tokens=12)
+    with pkg.NativeEngine(str(path), max_seq_len=96) as ref:
+        want_short = ref.generate(short, max_tokens=12)
+    with pkg.NativeEngine(str(path), max_seq_len=96) as eng:
+        assert eng.generate(short, max_tokens=12) == want_short
+        pkg.engine.fail_alloc_after(after)
+        try:
+            with pytest.raises(RuntimeError, match="allocation failure injected"):
+                eng.generate(longp, max_tokens=12)
+        finally:
+            pkg.engine.fail_alloc_after(-1)
+        with pytest.raises(RuntimeError, match="no prompt has been run"):
+            eng.decode_step(len(longp))
+        assert eng.generate(short, max_tokens=12) == want_short
+        assert eng.generate(longp, max_tokens=12) == want_long
+
+
+def test_engine_calls_keep_the_callers_device(pkg, dev, tmp_path):
+    """Every engine entry point runs on the engine's device and leaves the calling thread's current device as
+    it found it (with one GPU: the same device before and after each call, also after a failed call)."""
+    M = pkg.model
+    cfg = M.BitNetConfig(**SMALL)
+    model = _model(M, dev, cfg, seed=1)
+    path = tmp_path / "m.bin"
+    model.save_sglbitnt(path)
+    before = torch.cuda.current_device()
+    with pkg.NativeEngine(str(path), max_seq_len=32) as eng:
+        eng.generate([1, 2, 3], max_tokens=4)
+        assert torch.cuda.current_device() == before
+        with pytest.raises(RuntimeError):
+            eng.decode_step(40)
+        assert torch.cuda.current_device() == before
+    assert torch.cuda.current_device() == before

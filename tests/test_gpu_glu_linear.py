@@ -21,6 +21,8 @@ CASES = [
     (64, 4096, 512, torch.float32),     # two launches of two token tiles
     (40, 6912, 2560, torch.bfloat16),   # BitNet-2B gate|up at 40 tokens (32 + 8)
     (37, 14336, 4096, torch.bfloat16),  # Llama-3-8B gate|up at 37 tokens (chunks of 16, 16, 5)
+    (33, 14336, 4096, torch.bfloat16),  # chunks of 16, 16 and a 1-token tail
+    (49, 14336, 4096, torch.bfloat16),  # chunks of 16, 16, 16 and a 1-token tail
 ]
 
 

@@ -412,7 +412,7 @@ int wfb_gqa_decode_attention_noalloc(const void* q, int64_t ldq, const void* k_n
                 (long long)wfb::kAttnScratchFloats);
   float* part = nullptr;
   if (need > 0) {
-    const hipError_t e = wfb::gqa_decode_scratch(&part);
+    const hipError_t e = wfb::gqa_decode_scratch(as_stream(stream), &part);
     if (e != hipSuccess) return hip_status(e, name);
   }
   return hip_status(wfb::launch_gqa_decode(dtype, (int)head_dim, g, q, ldq, k_new, ldk, v_new, ldv, rope_cos,

@@ -541,15 +541,25 @@ std::mutex g_scratch_mu;
 float* g_scratch_dev[kScratchDevices];  // device address of `scratch` on each GPU, looked up once
 }  // namespace
 
-hipError_t gqa_decode_scratch(float** ptr) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+hipError_t gqa_decode_scratch(hipStream_t stream, float** ptr) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) return e;
+  int dev = cur;
+  if (stream) {  // the scratch of the GPU the work runs on (the null stream is the current device's)
+    e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) return e;
+  }
   if (dev < 0 || dev >= kScratchDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_dev[dev]) {  // first call on this device, with it current: its own copy's address
+  if (!g_scratch_dev[dev]) {  // first call on this device: its own copy's address, looked up with it current
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return e;
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
     if (e != hipSuccess) return e;
     g_scratch_dev[dev] = static_cast<float*>(p);
   }

@@ -24,6 +24,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -230,7 +231,7 @@ struct BitNetEngine {
   int32_t* last_tok = nullptr;     // device [1]
   uint16_t* ring = nullptr;        // device [kRing, H]
   uint16_t* x_start = nullptr;     // device [H] hidden state before the first generated token
-  void* logits = nullptr;          // device [V] (bf16 for the ternary head, fp32 for the dense head)
+  void* logits = nullptr;          // device [V] fp32
   void* logits_h = nullptr;        // pinned host copy
   int64_t* ids_h = nullptr;        // pinned host prompt ids (pre.cap)
   int32_t* tokens_h = nullptr;     // pinned host [kChunk]
@@ -275,8 +276,21 @@ int wcheck(int st, const char* what) {
     if (e_ != hipSuccess) return hipfail(e_, what); \
   } while (0)
 
+// Allocations left before the engine's allocator reports a failure; negative = never (the default).
+// Set only through wfb_engine_fail_alloc_after, which tests use to reach the out-of-memory paths.
+std::atomic<int64_t> g_fail_alloc_after{-1};
+
+int alloc_gate(const char* what) {
+  int64_t n = g_fail_alloc_after.load();
+  while (n > 0 && !g_fail_alloc_after.compare_exchange_weak(n, n - 1)) {
+  }
+  if (n == 0) return efail(std::string(what) + ": allocation failure injected (wfb_engine_fail_alloc_after)");
+  return 0;
+}
+
 template <typename T>
 int dalloc(Engine& e, T*& p, size_t count) {
+  ECHECK(alloc_gate("hipMalloc"));
   void* q = nullptr;
   const hipError_t st = hipMalloc(&q, std::max<size_t>(count * sizeof(T), 256));
   if (st != hipSuccess) return hipfail(st, "hipMalloc");
@@ -399,25 +413,34 @@ int load_floats(Engine& e, Uploader& up, const ModelFile& f, const std::string& 
   return 0;
 }
 
-int alloc_acts(Engine& e, Acts& a, int64_t cap) {
-  const Cfg& c = e.c;
-  a.cap = cap;
-  ECHECK(dalloc(e, a.x, cap * c.hidden));
-  ECHECK(dalloc(e, a.qkv, cap * c.nqkv()));
-  ECHECK(dalloc(e, a.att, cap * c.qd()));
-  ECHECK(dalloc(e, a.codes, cap * e.kmax));
-  ECHECK(dalloc(e, a.ascale, cap));
-  ECHECK(dalloc(e, a.mid, std::min<int64_t>(cap, 64) * c.inter));
-  if (cap > 64 || c.inter % 32 != 0) ECHECK(dalloc(e, a.gu, cap * 2 * c.inter));
-  ECHECK(dalloc(e, a.ids, cap));
-  return 0;
-}
-
 void free_acts(Engine& e, Acts& a) {
   for (void* p : {(void*)a.x, (void*)a.qkv, (void*)a.att, (void*)a.codes, (void*)a.ascale, (void*)a.mid, (void*)a.gu,
                   (void*)a.ids})
     dfree(e, p);
   a = Acts{};
+}
+
+// All buffers of `a` for `cap` rows; on failure the ones already made are freed and `a` is left empty
+// (cap 0), so the next call that needs them allocates again.
+int alloc_acts(Engine& e, Acts& a, int64_t cap) {
+  const Cfg& c = e.c;
+  Acts n;
+  int st = dalloc(e, n.x, cap * c.hidden);
+  if (st == 0) st = dalloc(e, n.qkv, cap * c.nqkv());
+  if (st == 0) st = dalloc(e, n.att, cap * c.qd());
+  if (st == 0) st = dalloc(e, n.codes, cap * e.kmax);
+  if (st == 0) st = dalloc(e, n.ascale, cap);
+  if (st == 0) st = dalloc(e, n.mid, std::min<int64_t>(cap, 64) * c.inter);
+  if (st == 0 && (cap > 64 || c.inter % 32 != 0)) st = dalloc(e, n.gu, cap * 2 * c.inter);
+  if (st == 0) st = dalloc(e, n.ids, cap);
+  if (st != 0) {
+    free_acts(e, n);
+    a = Acts{};
+    return st;
+  }
+  n.cap = cap;
+  a = n;
+  return 0;
 }
 
 // The fused norm + linear launches take these sizes (the Python backend's rmsnorm_linear_supported and
@@ -521,8 +544,8 @@ int layer(Engine& e, const Layer& Ly, Acts& a, int64_t m, bool prompt) {
                 "linear_residual (down)");
 }
 
-// Final RMSNorm + LM head on the pending hidden state dec.x[0]: first-max token into ctl[0], logits
-// stored when `logits` (bf16 for the ternary head, fp32 for the dense head).
+// Final RMSNorm + LM head on the pending hidden state dec.x[0]: first-max token into ctl[0] over the fp32
+// logits (as the reference's std::max_element, bitnet_engine.cpp:774-779), logits stored (fp32) when `logits`.
 int head(Engine& e, bool logits) {
   const Cfg& c = e.c;
   Acts& a = e.dec;
@@ -531,7 +554,7 @@ int head(Engine& e, bool logits) {
                                        e.kpad_h, e.kpad_h, a.ascale, e.s),
                   "rmsnorm_quant (head)"));
     return wcheck(wfb_linear_i2s_argmax(e.head_q, c.vocab, e.kpad_h, a.codes, 1, e.kpad_h, a.ascale, e.head_scale, 0.0f,
-                                        logits ? e.logits : nullptr, WFB_BF16, c.vocab, e.argmax_ws, e.ctl, e.s),
+                                        logits ? e.logits : nullptr, WFB_F32, c.vocab, e.argmax_ws, e.ctl, e.s),
                   "LM head");
   }
   return wcheck(wfb_lm_head_argmax(a.x, WFB_BF16, c.hidden, e.final_norm, WFB_BF16, c.rms_eps, e.head_dense, WFB_BF16,
@@ -595,13 +618,28 @@ int prefill(Engine& e, const int32_t* ids, int64_t n) {
   e.have_hidden = false;
   e.seq_len = 0;
   if (n > e.pre.cap) {
+    // Grow the prompt buffers. The old set is released first (no peak of both); the new set and its pinned
+    // id buffer are committed only when every allocation succeeded, so a failure leaves no buffers (cap 0,
+    // ids_h NULL) and a later prompt of any length allocates again.
     ECHECK(sync(e, "prefill"));
+    const int64_t cap = std::min<int64_t>(c.max_len, std::max<int64_t>(n, 2 * e.pre.cap));
     free_acts(e, e.pre);
     if (e.ids_h) (void)hipHostFree(e.ids_h);
     e.ids_h = nullptr;
-    const int64_t cap = std::min<int64_t>(c.max_len, std::max<int64_t>(n, 2 * e.pre.cap));
-    ECHECK(alloc_acts(e, e.pre, cap));
-    HCHECK(hipHostMalloc((void**)&e.ids_h, cap * sizeof(int64_t), hipHostMallocDefault), "hipHostMalloc");
+    Acts grown;
+    ECHECK(alloc_acts(e, grown, cap));
+    int64_t* ids_h = nullptr;
+    int st = alloc_gate("hipHostMalloc");
+    if (st == 0) {
+      const hipError_t he = hipHostMalloc((void**)&ids_h, cap * sizeof(int64_t), hipHostMallocDefault);
+      if (he != hipSuccess) st = hipfail(he, "hipHostMalloc");
+    }
+    if (st != 0) {
+      free_acts(e, grown);
+      return st;
+    }
+    e.pre = grown;
+    e.ids_h = ids_h;
   }
   Acts& a = e.pre;
   for (int64_t i = 0; i < n; ++i) e.ids_h[i] = ids[i];
@@ -659,28 +697,14 @@ int32_t sample_top_p(const float* logits, int64_t n, float temperature, float to
 }
 
 // Host float logits of the last head replay.
-const float* host_logits(Engine& e, std::vector<float>& buf) {
-  if (e.head_q) {
-    buf.resize((size_t)e.c.vocab);
-    const uint16_t* b = static_cast<const uint16_t*>(e.logits_h);
-    for (int64_t v = 0; v < e.c.vocab; ++v) {
-      const uint32_t u = (uint32_t)b[v] << 16;
-      std::memcpy(&buf[v], &u, 4);
-    }
-    return buf.data();
-  }
-  return static_cast<const float*>(e.logits_h);
-}
-
-// Head with logits, host sample: the picked token (not yet run through the model).
+// Head with logits (fp32 for either head), host sample: the picked token (not yet run through the model).
 int pick_sampled(Engine& e, float temperature, float top_p, int32_t* tok) {
   HCHECK(hipGraphLaunch(e.g_head, e.s), "graph launch");
-  const size_t lb = (size_t)e.c.vocab * (e.head_q ? 2 : 4);
-  HCHECK(hipMemcpyAsync(e.logits_h, e.logits, lb, hipMemcpyDeviceToHost, e.s), "logits download");
+  HCHECK(hipMemcpyAsync(e.logits_h, e.logits, (size_t)e.c.vocab * 4, hipMemcpyDeviceToHost, e.s), "logits download");
   ECHECK(sync(e, "head"));
-  std::vector<float> buf, probs;
+  std::vector<float> probs;
   std::vector<std::pair<float, int32_t>> order;
-  *tok = sample_top_p(host_logits(e, buf), e.c.vocab, temperature, top_p, e.rng, probs, order);
+  *tok = sample_top_p(static_cast<const float*>(e.logits_h), e.c.vocab, temperature, top_p, e.rng, probs, order);
   return 0;
 }
 
@@ -949,12 +973,26 @@ int decode_step(Engine& e, int32_t position, const SamplingParams* p, int32_t* o
   return 0;
 }
 
-// Every entry point runs on the engine's device.
-int enter(Engine* e) {
-  if (!e) return efail("Engine not initialized");
-  HCHECK(hipSetDevice(e->device), "hipSetDevice");
-  return 0;
-}
+// Every entry point runs on the engine's device and gives the calling thread its own current device back.
+class DeviceScope {
+ public:
+  int enter(const Engine* e) {
+    if (!e) return efail("Engine not initialized");
+    HCHECK(hipGetDevice(&prev_), "hipGetDevice");
+    if (prev_ != e->device) {
+      HCHECK(hipSetDevice(e->device), "hipSetDevice");
+      restore_ = true;
+    }
+    return 0;
+  }
+  ~DeviceScope() {
+    if (restore_) (void)hipSetDevice(prev_);
+  }
+
+ private:
+  int prev_ = 0;
+  bool restore_ = false;
+};
 
 }  // namespace
 
@@ -975,7 +1013,8 @@ BitNetEngine* bitnet_engine_create(const char* model_path, const BitNetConfig* c
 
 void bitnet_engine_destroy(BitNetEngine* engine) {
   if (!engine) return;
-  (void)hipSetDevice(engine->device);
+  DeviceScope dev;
+  (void)dev.enter(engine);
   delete engine;
 }
 
@@ -983,17 +1022,20 @@ const char* bitnet_get_error(void) { return g_eng_err.c_str(); }
 
 int bitnet_generate(BitNetEngine* engine, const int32_t* input_ids, int32_t num_input_tokens,
                     const SamplingParams* params, GenerationResult* result) {
-  if (enter(engine) != 0) return -1;
+  DeviceScope dev;
+  if (dev.enter(engine) != 0) return -1;
   return generate(*engine, input_ids, num_input_tokens, params, result) == 0 ? 0 : -1;
 }
 
 int bitnet_prefill(BitNetEngine* engine, const int32_t* input_ids, int32_t num_tokens) {
-  if (enter(engine) != 0) return -1;
+  DeviceScope dev;
+  if (dev.enter(engine) != 0) return -1;
   return prefill(*engine, input_ids, num_tokens) == 0 ? 0 : -1;
 }
 
 int bitnet_decode_step(BitNetEngine* engine, int32_t position, const SamplingParams* params, int32_t* output_id) {
-  if (enter(engine) != 0) return -1;
+  DeviceScope dev;
+  if (dev.enter(engine) != 0) return -1;
   return decode_step(*engine, position, params, output_id) == 0 ? 0 : -1;
 }
 
@@ -1015,6 +1057,11 @@ void bitnet_free_result(GenerationResult* result) {
   std::free(result->logits);
   result->output_ids = nullptr;
   result->logits = nullptr;
+}
+
+int wfb_engine_fail_alloc_after(int64_t n) {
+  g_fail_alloc_after.store(n < 0 ? -1 : n);
+  return 0;
 }
 
 int wfb_engine_sample_top_p(const float* logits, int64_t n, float temperature, float top_p, uint32_t seed,

@@ -492,8 +492,8 @@ constexpr int64_t kAttnScratchFloats = int64_t(8) << 20;
 static_assert(kAttnScratchFloats == WFB_ATTN_SCRATCH_FLOATS, "scratch size stated in the header");
 // floats of split partials launch_gqa_decode uses for these sizes (0: one split, no workspace pass)
 int64_t gqa_decode_workspace_floats(int64_t max_len, int g, int64_t batch, int64_t hkv, int d);
-// device address of this GPU's scratch array (looked up on the first call per device)
-hipError_t gqa_decode_scratch(float** ptr);
+// device address of the scratch array on the stream's GPU (looked up on the first call per device)
+hipError_t gqa_decode_scratch(hipStream_t stream, float** ptr);
 hipError_t launch_gqa_decode(int dt, int d, int g, const void* q, int64_t ldq, const void* kn, int64_t ldk,
                              const void* vn, int64_t ldv, const float* rc, const float* rs, void* kc, void* vc,
                              int64_t max_len, const int64_t* pos, int b, int hkv, float scale, void* out, int64_t ldo,

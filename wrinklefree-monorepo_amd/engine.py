@@ -48,6 +48,7 @@ SIGNATURES = {
     "bitnet_free_result": (None, [ctypes.POINTER(GenerationResult)]),
     "wfb_engine_sample_top_p": (ctypes.c_int, [_vp, ctypes.c_int64, ctypes.c_float, ctypes.c_float, ctypes.c_uint32,
                                                ctypes.c_int32, _i32p]),
+    "wfb_engine_fail_alloc_after": (ctypes.c_int, [ctypes.c_int64]),
 }
 
 _bound = None
@@ -167,3 +168,8 @@ def sample_top_p(logits: Sequence[float], temperature: float, top_p: float, seed
     if st != 0:
         raise RuntimeError(f"wfb_engine_sample_top_p failed: {last_error()}")
     return list(out[:draws])
+
+
+def fail_alloc_after(n: int) -> None:
+    """Test hook: after `n` more successful engine allocations the next one fails (n < 0: never)."""
+    lib().wfb_engine_fail_alloc_after(int(n))

@@ -172,11 +172,11 @@ class HipBackend:
     def norm_linear_argmax(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor], eps: float,
                            linear: PackedLinear) -> torch.Tensor:
         """Greedy next tokens int64 [M] of a ternary LM head: norm + quantise, then the linear with the argmax
-        fused in (logits compared as rounded to out_dtype, never stored)."""
+        fused in (fp32 logits compared, as the reference engine's std::max_element, never stored)."""
         q, a_scale = rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=linear.k_pad)
         if self.keep_acc:
             self._linears(q, a_scale, [linear])
-        return bitnet_linear_argmax(linear.qweight, q, linear.scale, a_scale=a_scale, logits_dtype=self.out_dtype)
+        return bitnet_linear_argmax(linear.qweight, q, linear.scale, a_scale=a_scale, logits_dtype=torch.float32)
 
     def _linear_residual(self, q: torch.Tensor, a_scale: torch.Tensor, linear: PackedLinear,
                          residual: torch.Tensor) -> torch.Tensor:
