@@ -367,7 +367,8 @@ def e2e_bench(pkg, torch, dev, cpu: bool = True):
     """Greedy decoding on the fused HIP backend (BitLinears on libwfbitnet, float glue in torch).
     Llama-3-8B shape, every linear ternary, random init on the device; prefill of 8
     prompts x 256 tokens (2048 tokens, one M = 2048 GEMM per projection), then 256 decode steps at
-    batch 8.  configs[0]: SmolLM2-135M shape, 32-token prompt, 128 new tokens at batch 1.
+    batch 8; and the same with 8 prompts x 2048 tokens (16384 prompt tokens, decode attention over
+    2048..2303 keys per sequence).  configs[0]: SmolLM2-135M shape, 32-token prompt, 128 new tokens at batch 1.
     Wall-clock times around synchronised regions (host launch overhead included); the prefill is the
     mean of 3 prompt forwards after one at the same size (fresh caches each time); decode is timed
     both with eager launches and replayed from one HIP graph capture of the decode step.  ``cpu``: also
@@ -423,6 +424,8 @@ def e2e_bench(pkg, torch, dev, cpu: bool = True):
         torch.cuda.empty_cache()
 
     run(M.LLAMA3_8B, 8, 256, 256, torch.bfloat16, "llama3_8b")
+    # configs[4] read as a 2048-token prompt per sequence: decode attention over 2048..2303 keys
+    run(M.LLAMA3_8B, 8, 2048, 256, torch.bfloat16, "llama3_8b_8x2048")
     run(M.SMOLLM2_135M, 1, 32, 128, torch.float32, "smollm2_135m")
     return res
 
@@ -490,28 +493,30 @@ def engine_bench(pkg, torch, dev):
     return res
 
 
-def e2e_cpu_baseline(M, model, prompt, torch, new_tokens: int = 12):
-    """The same model decoded on the host: float glue as torch CPU ops, quantised groups on the numpy
-    oracle (oracle/model_backend.py).  Bounded sample: the prompt plus ``new_tokens`` greedy tokens."""
-    from oracle.model_backend import OracleBackend
-    host = model.on_host(OracleBackend(M.quantised_linears(model).values(), "cpu"))
-    p = prompt.cpu()
+def e2e_cpu_baseline(M, model, prompt, torch, new_tokens: int = 128):
+    """The same model decoded greedily on the host CPU: oracle/c/cpu_decode.c, a C restatement of the
+    reference native engine's per-token loop (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:490-554,
+    742-823) over this model, every BitLinear on the AVX2 port of the reference I2_S GEMV op with OpenMP
+    over its output rows, the fp32 attention and LM head on OpenMP loops, OMP_NUM_THREADS threads.
+    Batch 1: the prompt's first row, then ``new_tokens`` greedy tokens (the configs[0] workload)."""
+    from oracle.model_backend import cpu_decoder
+    p = prompt[0].cpu().numpy()
+    dec = cpu_decoder(model, p.size + new_tokens)
     t = time.perf_counter()
-    with torch.no_grad():
-        host.reset(p.shape[0], p.shape[1] + new_tokens)
-        host.forward(p, 0, tokens=True)
-    t_prefill = time.perf_counter() - t
+    dec.greedy(p, 1)
+    t_prompt = time.perf_counter() - t
     t = time.perf_counter()
-    with torch.no_grad():
-        host.generate(p, new_tokens)
+    toks, _ = dec.greedy(p, new_tokens)
     t_all = time.perf_counter() - t
     steps = new_tokens - 1
-    decode_s = max(t_all - t_prefill, 1e-9)
+    decode_s = max(t_all - t_prompt, 1e-9)
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(p.shape[0] * steps / decode_s, 2), "unit": "tok/s", "cores": cores,
-            "kind": "port", "ms_per_token": round(decode_s / steps * 1e3, 1),
-            "sample": f"SmolLM2-135M shape, batch {p.shape[0]}, {p.shape[1]}-token prompt + {new_tokens} greedy "
-                      f"tokens on the host (torch CPU float glue, numpy-oracle BitLinears, BLAS threads = cores)"}
+    return {"value": round(steps / decode_s, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+            "ms_per_token": round(decode_s / steps * 1e3, 3), "prompt_ms": round(t_prompt * 1e3, 2),
+            "distinct_tokens": int(len(set(toks.tolist()))),
+            "sample": f"SmolLM2-135M shape, batch 1, {p.size}-token prompt + {new_tokens} greedy tokens on the host "
+                      f"(C restatement of the reference engine loop, BitLinears on the AVX2 port of the reference "
+                      f"I2_S GEMV, OpenMP {cores} threads)"}
 
 
 def device_copy_gbs(torch, dev, nbytes: int = 1 << 30) -> float:

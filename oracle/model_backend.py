@@ -64,3 +64,40 @@ class OracleBackend:
         q, s = orc.glu_rmsnorm_quant(gate.float().cpu().numpy(), up.float().cpu().numpy(), code, g, eps,
                                      k_pad=linears[0].k_pad)
         return self._apply(q, s, linears)
+
+
+def cpu_decoder(model, max_len: int):
+    """The model's weights as oracle/c/cpu_decode.c's host decoder (refbind.CpuDecoder): the end-to-end
+    CPU baseline.  Packed linears keep their I2_S bytes and scales; the embedding, norms and the fp32
+    LM head (dense or tied; a ternary head is not supported here) are copied to host fp32."""
+    from . import refbind
+
+    cfg = model.cfg
+    if model.lm_head is not None:
+        raise ValueError("cpu_decoder: ternary LM heads are not supported")
+
+    def host(t):
+        return t.detach().float().cpu().numpy()
+
+    def stack(attr):
+        return np.stack([getattr(L, attr).qweight.cpu().numpy() for L in model.layers])
+
+    L0 = model.layers[0]
+    dims = dict(layers=cfg.num_layers, hidden=cfg.hidden_size, inter=cfg.intermediate_size, heads=cfg.num_heads,
+                kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, vocab=cfg.vocab_size, max_len=max_len,
+                kpad_h=L0.q.k_pad, kpad_qd=L0.o.k_pad, kpad_f=L0.down.k_pad,
+                act=2 if cfg.hidden_act == "relu2" else 1, rms_eps=cfg.rms_eps, subln_eps=cfg.subln_eps)
+    import sys
+
+    cos, sin = sys.modules[type(model).__module__]._rope_tables_cpu(cfg.rope_theta, cfg.head_dim, max_len)
+    arrays = dict(
+        embed=host(model.embed), head=host(model.head_weight), final_norm=host(model.final_norm),
+        in_norm=np.stack([host(L.input_norm) for L in model.layers]),
+        post_norm=np.stack([host(L.post_attn_norm) for L in model.layers]),
+        attn_sub=np.stack([host(L.attn_sub_norm) for L in model.layers]),
+        ffn_sub=np.stack([host(L.ffn_sub_norm) for L in model.layers]),
+        scales=np.stack([[float(getattr(L, n).scale.item()) for n in ("q", "k", "v", "o", "gate", "up", "down")]
+                         for L in model.layers]).astype(np.float32),
+        wq=stack("q"), wk=stack("k"), wv=stack("v"), wo=stack("o"), wg=stack("gate"), wu=stack("up"),
+        wd=stack("down"), rope_cos=cos.numpy(), rope_sin=sin.numpy())
+    return refbind.CpuDecoder(dims, arrays)

@@ -109,6 +109,45 @@ class OracleC:
         return q, s[0]
 
 
+class CpuModel(ctypes.Structure):
+    """oracle/c/cpu_decode.c's cpu_model."""
+    _fields_ = [(n, ctypes.c_int32) for n in ("layers", "hidden", "inter", "heads", "kv_heads", "head_dim", "vocab",
+                                               "max_len", "kpad_h", "kpad_qd", "kpad_f", "act")] + \
+               [("rms_eps", ctypes.c_float), ("subln_eps", ctypes.c_float)] + \
+               [(n, _vp) for n in ("embed", "head", "final_norm", "in_norm", "post_norm", "attn_sub", "ffn_sub",
+                                   "scales", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "rope_cos", "rope_sin")]
+
+
+class CpuDecoder:
+    """Greedy decoding of a BitNet Llama model on the host (oracle/c/cpu_decode.c): the end-to-end CPU
+    baseline.  ``arrays``: numpy arrays named as cpu_model's pointer fields (contiguous, fp32 / uint8);
+    ``dims``: its integer and float fields."""
+
+    def __init__(self, dims: dict, arrays: dict, path: Path = ORACLE_C):
+        self.lib = ctypes.CDLL(str(path))
+        self.lib.cpu_decode_greedy.restype = _int
+        self.lib.cpu_decode_greedy.argtypes = [ctypes.POINTER(CpuModel), _vp, _int, _int, _vp, _vp]
+        self._keep = {}
+        m = CpuModel()
+        for k, v in dims.items():
+            setattr(m, k, v)
+        for k, v in arrays.items():
+            want = np.uint8 if k.startswith("w") else np.float32
+            a = np.ascontiguousarray(v, want)
+            self._keep[k] = a
+            setattr(m, k, a.ctypes.data)
+        self.m = m
+
+    def greedy(self, prompt, n_new: int):
+        """(n_new generated token ids, logits [vocab] after the prompt)."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(n_new, 1), np.int32)
+        logits = np.zeros(self.m.vocab, np.float32)
+        if self.lib.cpu_decode_greedy(ctypes.byref(self.m), _ptr(p), p.size, n_new, _ptr(out), _ptr(logits)) != 0:
+            raise ValueError("cpu_decode_greedy: bad sizes or out of memory")
+        return out[:n_new], logits
+
+
 class RefLib:
     """The reference's compiled kernels (bitnet_gemv.cpp) behind oracle/c/ref_shim.cpp."""
 

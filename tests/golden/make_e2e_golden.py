@@ -52,7 +52,9 @@ def load_stage1():
     return mod
 
 
-def main() -> None:
+def build_reference_model():
+    """The reference's stage-1 BitNet model at the SmolLM2-135M shape from random_float_state(cfg, SEED):
+    returns (model, cfg, model.py module)."""
     import transformers
 
     sys.path.insert(0, str(ROOT))
@@ -76,6 +78,13 @@ def main() -> None:
     model = stage1.convert_model_to_bitnet(model, cfg.hidden_size, cfg.intermediate_size)
     n_bitlinear = sum(type(m).__name__ == "BitLinear" for m in model.modules())
     assert n_bitlinear == 7 * cfg.num_layers, n_bitlinear
+    return model, cfg, M
+
+
+def main() -> None:
+    import transformers
+
+    model, cfg, M = build_reference_model()
 
     prompt = torch.randint(0, cfg.vocab_size, (1, PROMPT_LEN), generator=torch.Generator().manual_seed(PROMPT_SEED))
     noise = 1e-7 * torch.randn((1, PROMPT_LEN + NEW, cfg.hidden_size), generator=torch.Generator().manual_seed(11))

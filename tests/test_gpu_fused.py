@@ -167,7 +167,7 @@ def test_tile_epilogue_out_types_match_oracle(pkg, dev, m, n, k, odt):
     assert torch.equal(got.cpu(), want)
 
 
-@pytest.mark.parametrize("h,f,qn,kvn", [(2560, 6912, 2560, 640), (1024, 2816, 1024, 256)])
+@pytest.mark.parametrize("h,f,qn,kvn", [(2560, 6912, 2560, 640), (1024, 2816, 1024, 256), (512, 1024, 512, 100)])
 def test_reference_fused_mlp_and_qkv_ops(pkg, dev, h, f, qn, kvn):
     """bitnet_mlp_forward / bitnet_qkv_forward (the reference's batch-1 fused ops,
     SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:150-375, schemas torch_extension_cpu.cpp:921-926) equal the
@@ -186,6 +186,13 @@ def test_reference_fused_mlp_and_qkv_ops(pkg, dev, h, f, qn, kvn):
         assert o.dtype == torch.float32 and np.array_equal(o.cpu().numpy(), want)
     outs2 = torch.ops.wfbitnet.bitnet_qkv_forward(xt[None, :], *[torch.from_numpy(w).to(dev) for w in ws], *sc)
     assert all(torch.equal(a, b) for a, b in zip(outs, outs2))
+    # the q|k|v concatenation is rebuilt after an in-place update of a weight (same tensor, new version)
+    wt = [torch.from_numpy(w).to(dev) for w in ws]
+    pkg.bitnet_qkv_forward(xt, *wt, *sc)
+    w_new = orc.pack_i2s(orc.random_ternary(rng, kvn, h))
+    wt[1].copy_(torch.from_numpy(w_new))
+    o_new = pkg.bitnet_qkv_forward(xt, *wt, *sc)[1]
+    assert np.array_equal(o_new.cpu().numpy(), orc.rescale(orc.accumulate(w_new, q_ref), sc[1], s_ref)[0])
     # mlp
     gw, uw = (orc.pack_i2s(orc.random_ternary(rng, f, h)) for _ in range(2))
     dw = orc.pack_i2s(orc.random_ternary(rng, h, f))

@@ -114,8 +114,7 @@ class _SampledChecks:
             q, a_scale = self.pkg.rmsnorm_quantize_i8(x, norm_weight, eps=eps, k_pad=linear.k_pad)
             w = self._unpacked(linear).astype(np.float32)
             acc = (q.cpu().numpy().astype(np.float32) @ w.T).astype(np.int64)
-            logits = orc.rescale(acc, np.float32(linear.scale.item()), a_scale.cpu().numpy())
-            logits = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(logits))  # compared as stored (bf16)
+            logits = orc.rescale(acc, np.float32(linear.scale.item()), a_scale.cpu().numpy())  # fp32, as compared
             assert np.array_equal(tok.cpu().numpy(), logits.argmax(axis=1)), "LM head token != oracle argmax"
             self.done.append(("lm_head", x.shape[0]))
         return tok
@@ -160,3 +159,44 @@ def test_llama3_8b_full_depth_prefill_and_decode(pkg, dev):
     assert len(be.done) == 2 * 7 + 1 + 7 + 1
     assert torch.equal(unfused, eager), "unfused launches give different tokens from the fused path"
     assert len(set(eager.flatten().tolist())) > 16
+
+
+def test_llama3_8b_full_depth_2048_token_prompts(pkg, dev):
+    """configs[4] at its other reading: 8 prompts of 2048 tokens each (16384 prompt tokens, one M = 16384 GEMM
+    per projection), then decode steps over 2048+ keys per sequence.  Eager and graph-replayed decoding give
+    the same tokens; on an unfused run every projection of layer 0 at M = 16384, every projection of layer 31
+    at the second decode step (M = 8) and the LM head are checked against the oracle as above."""
+    M = pkg.model
+    cfg = M.LLAMA3_8B
+    t0 = 2048
+    model = M.BitNetDecoder(cfg, seed=1, device=dev, dtype=torch.bfloat16, init_on_device=True,
+                            backend=M.HipBackend(out_dtype=torch.bfloat16, fused=True))
+    prompt = torch.randint(0, cfg.vocab_size, (BATCH, t0), generator=torch.Generator().manual_seed(9)).to(dev)
+    new = 4
+    eager = model.generate(prompt, new).cpu()
+    graph = model.generate(prompt, new, graph=True).cpu()
+    print("llama3-8b 8 x 2048: fused eager / graph done", flush=True)
+    assert torch.equal(eager, graph), "graph replays diverge from eager decoding"
+
+    Sampled = type("Sampled", (_SampledChecks, M.HipBackend), {})
+    be = Sampled(out_dtype=torch.bfloat16, fused=False)
+    be.setup(pkg, {id(l): n for n, l in M.quantised_linears(model).items()}, np.random.default_rng(1))
+    model.backend = be
+    projs = ("q", "k", "v", "o", "gate", "up", "down")
+    with torch.no_grad():
+        model.reset(BATCH, t0 + new)
+        be.sample = {f"layers.0.{p}" for p in projs} | {"lm_head"}
+        nxt = model.forward(prompt, 0, tokens=True)
+        print(f"llama3-8b 8 x 2048: prefill checks {len(be.done)}", flush=True)
+        toks = [nxt]
+        ids = nxt[:, None].clone()
+        pos = torch.full((BATCH,), t0, dtype=torch.long, device=dev)
+        for s in range(new - 1):
+            be.sample = ({f"layers.31.{p}" for p in projs} | {"lm_head"}) if s == 1 else set()
+            nxt = model.decode_step(ids, pos, tokens=True)
+            toks.append(nxt)
+            ids = nxt[:, None].clone()
+            pos += 1
+    unfused = torch.stack(toks, dim=1).cpu()
+    assert set(be.done) == {(p, BATCH * t0) for p in projs} | {(p, BATCH) for p in projs} | {("lm_head", BATCH)}
+    assert torch.equal(unfused, eager), "unfused launches give different tokens from the fused path"

@@ -831,7 +831,15 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   // of the chip idle (M = 512, N = 2560, K = 6912: 21.7 vs 30.8 us).
   const int64_t tn = (n + 255) / 256, t128 = tn * ((m + 127) / 128), t64 = tn * ((m + 63) / 64);
   if (t128 >= 320) return launch_tile<4, 1, 2>(W, n, k, A, m, lda, e, s);
-  if (t64 >= 160) return launch_tile<2, 2, 2>(W, n, k, A, m, lda, e, s);
+  // 64-row tiles: 256 columns, or 128 columns at three workgroups per CU where those fill the last round of
+  // workgroup slots better (2560 x 6912 at M = 2048: 320 tiles on 512 slots, or 640 on 768: 47.3 -> 42.5 us;
+  // 13824 x 2560 at M = 512 keeps 256 columns, 23.1 against 27.3 us; interleaved medians on MI355X)
+  auto fill = [](int64_t t, int64_t slots) { return (double)t / (double)(((t + slots - 1) / slots) * slots); };
+  if (t64 >= 160) {
+    const int64_t t64n = ((n + 127) / 128) * ((m + 63) / 64);
+    if (fill(t64n, 768) > fill(t64, 512) + 0.1) return launch_tile<2, 2, 3, 1>(W, n, k, A, m, lda, e, s);
+    return launch_tile<2, 2, 2>(W, n, k, A, m, lda, e, s);
+  }
   return few_tiles ? launch_tile<1, 2, 3, 1>(W, n, k, A, m, lda, e, s) : launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
 }
 

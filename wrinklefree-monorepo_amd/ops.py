@@ -14,8 +14,10 @@ The ops are also registered as ``torch.ops.wfbitnet.*`` with the reference schem
 
 from __future__ import annotations
 
+import collections
 import ctypes
-from typing import Optional, Tuple, Union
+import weakref
+from typing import Optional, Sequence, Tuple, Union
 
 import torch
 
@@ -897,16 +899,46 @@ def _fused_input(name: str, x: torch.Tensor, packed: torch.Tensor) -> torch.Tens
     return x if x.dtype in (torch.float32, torch.bfloat16, torch.float16) else x.float()
 
 
+# Row concatenations of the packed weights the fused ops launch over, with their scales on the device: built
+# once per set of weight tensors and reused while those tensors are alive and unmodified (identity, storage
+# and version counter all match).  A model that keeps its projections concatenated (model.py) never needs it.
+_CONCAT_CACHE: "collections.OrderedDict" = collections.OrderedDict()
+_CONCAT_CACHE_MAX = 64
+
+
+def _concat_weights(ws: Sequence[torch.Tensor], scales: Sequence[float]) -> Tuple[torch.Tensor, torch.Tensor]:
+    key = tuple((id(w), w.data_ptr(), w._version, tuple(w.shape)) for w in ws) + (tuple(float(x) for x in scales),)
+    hit = _CONCAT_CACHE.get(key)
+    if hit is not None and all(r() is w for r, w in zip(hit[0], ws)):
+        _CONCAT_CACHE.move_to_end(key)
+        return hit[1], hit[2]
+    cat = torch.cat([w.contiguous() for w in ws], dim=0)
+    sc = torch.tensor([float(x) for x in scales], dtype=torch.float32, device=ws[0].device)
+    _CONCAT_CACHE[key] = ([weakref.ref(w) for w in ws], cat, sc)
+    while len(_CONCAT_CACHE) > _CONCAT_CACHE_MAX:
+        _CONCAT_CACHE.popitem(last=False)
+    return cat, sc
+
+
 def bitnet_qkv_forward(input: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor, v_weight: torch.Tensor,
                        q_scale: float, k_scale: float, v_scale: float
                        ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Fused QKV of one token: the input quantised once (per-token absmax int8), then q / k / v = acc * a_scale *
     w_scale, fp32 1-D outputs.  The op of SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:289-375 (schema
     torch_extension_cpu.cpp:924-926) without its double sum(a) subtraction (anomaly ii): q = acc(q_weight) *
-    a_scale * q_scale exactly as bitnet_linear gives it."""
+    a_scale * q_scale exactly as bitnet_linear gives it.  Two launches: the quantiser and one segmented linear
+    over q|k|v (rows concatenated once per weight set); separate linears where a projection's rows are not a
+    multiple of 8."""
     name = "bitnet_qkv_forward"
     x = _fused_input(name, input, q_weight)
+    ws = (q_weight, k_weight, v_weight)
     q8, a_s = quantize_activations_i8_per_token(x)
+    if all(w.dtype == torch.uint8 and w.dim() == 2 and w.shape[1] == q_weight.shape[1] and w.shape[0] % 8 == 0
+           for w in ws) and q_weight.is_cuda:
+        cat, sc = _concat_weights(ws, (q_scale, k_scale, v_scale))
+        rows = [w.shape[0] for w in ws]
+        y = bitnet_linear_segmented(cat, rows, sc, q8, a_scale=a_s, out_dtype=torch.float32).reshape(-1)
+        return tuple(torch.split(y, rows))
     return tuple(bitnet_linear(w, q8, float(sc), a_scale=a_s, out_dtype=torch.float32).reshape(-1)
                  for w, sc in ((q_weight, q_scale), (k_weight, k_scale), (v_weight, v_scale)))
 
@@ -917,7 +949,10 @@ def bitnet_mlp_forward(input: torch.Tensor, gate_weight: torch.Tensor, up_weight
     """Fused BitNet MLP of one token: quantise the input once, gate / up = acc * a_scale * w_scale (fp32),
     relu(gate)^2 * up, SubLN (ffn_sub_norm, eps), re-quantise, down = acc * h_scale * down_scale; fp32 [hidden].
     The op of SGB/sgl-kernel/csrc/cpu/bitnet_fused_layer.cpp:150-287 (schema torch_extension_cpu.cpp:921-923)
-    with every projection scaled by its weight scale and sum(a) removed once (anomaly ii not copied)."""
+    with every projection scaled by its weight scale and sum(a) removed once (anomaly ii not copied).
+    Three launches: the quantiser, gate|up with relu(gate)^2 * up in its epilogue (rows concatenated once per
+    weight set), SubLN + quantisation in the down projection's prologue -- bit-identical to the five separate
+    calls, which are kept for sizes those kernels do not take."""
     name = "bitnet_mlp_forward"
     x = _fused_input(name, input, gate_weight)
     f = gate_weight.shape[0]
@@ -926,9 +961,17 @@ def bitnet_mlp_forward(input: torch.Tensor, gate_weight: torch.Tensor, up_weight
     if ffn_sub_norm.numel() != f:
         raise ValueError(f"{name}: ffn_sub_norm must have {f} elements")
     q8, a_s = quantize_activations_i8_per_token(x)
+    norm_w = ffn_sub_norm.to(torch.float32).contiguous()
+    fused = (gate_weight.dtype == torch.uint8 and up_weight.dtype == torch.uint8 and gate_weight.is_cuda
+             and f % 32 == 0 and rmsnorm_linear_supported(1, f, f))
+    if fused:
+        cat, sc = _concat_weights((gate_weight, up_weight), (gate_scale, up_scale))
+        hid = bitnet_linear_glu(cat, sc, q8, "relu2", a_scale=a_s, mid_dtype=torch.float32)
+        _, dsc = _concat_weights((down_weight,), (down_scale,))
+        return rmsnorm_linear(hid, norm_w, down_weight, dsc, eps=float(eps), out_dtype=torch.float32).reshape(-1)
     gate = bitnet_linear(gate_weight, q8, float(gate_scale), a_scale=a_s, out_dtype=torch.float32)
     up = bitnet_linear(up_weight, q8, float(up_scale), a_scale=a_s, out_dtype=torch.float32)
-    h8, h_s = glu_rmsnorm_quantize_i8(gate, up, "relu2", ffn_sub_norm.to(torch.float32).contiguous(), eps=float(eps))
+    h8, h_s = glu_rmsnorm_quantize_i8(gate, up, "relu2", norm_w, eps=float(eps))
     return bitnet_linear(down_weight, h8, float(down_scale), a_scale=h_s, out_dtype=torch.float32).reshape(-1)
 
 
