@@ -432,7 +432,8 @@ def e2e_bench(pkg, torch, dev, cpu: bool = True):
 
 def engine_bench(pkg, torch, dev):
     """The native engine (include/wfbitnet_engine.h, the reference engine's C ABI) on SGLBITNT files of the
-    configs[0] / BitNet-2B / configs[4] shapes (bf16 glue, random init on the device, written to /dev/shm): load time,
+    configs[0] / BitNet-2B / configs[4] shapes (bf16 glue, and configs[0] also with the fp32 glue of the reference
+    engine; random init on the device, written to /dev/shm): load time,
     the prompt as one batched pass (mean of 3), greedy decoding in bitnet_generate (graph replays, one host
     synchronisation per 32 tokens; generate's time minus the prompt's), and the latency of one
     bitnet_decode_step call (one replay plus the token's copy to the host); for BitNet-2B also the whole
@@ -443,10 +444,12 @@ def engine_bench(pkg, torch, dev):
     M = pkg.model
     res = {}
     tmpdir = "/dev/shm" if os.path.isdir("/dev/shm") else None
-    for name, cfg, t0, new in (("smollm2_135m", M.SMOLLM2_135M, 32, 128), ("bitnet_2b", M.BITNET_2B, 64, 64),
-                               ("llama3_8b", M.LLAMA3_8B, 256, 256)):
+    for name, cfg, t0, new, dt in (("smollm2_135m", M.SMOLLM2_135M, 32, 128, torch.bfloat16),
+                                   ("smollm2_135m_fp32", M.SMOLLM2_135M, 32, 128, torch.float32),
+                                   ("bitnet_2b", M.BITNET_2B, 64, 64, torch.bfloat16),
+                                   ("llama3_8b", M.LLAMA3_8B, 256, 256, torch.bfloat16)):
         print(f"[engine] {name}: writing the model file", file=sys.stderr, flush=True)
-        model = M.BitNetDecoder(cfg, seed=0, device=dev, dtype=torch.bfloat16, init_on_device=True)
+        model = M.BitNetDecoder(cfg, seed=0, device=dev, dtype=dt, init_on_device=True)
         max_len = 576 if name == "bitnet_2b" else t0 + new
         with tempfile.NamedTemporaryFile(dir=tmpdir, suffix=".sglbitnt") as f:
             model.save_sglbitnt(f.name)

@@ -243,3 +243,32 @@ def test_engine_calls_keep_the_callers_device(pkg, dev, tmp_path):
             eng.decode_step(40)
         assert torch.cuda.current_device() == before
     assert torch.cuda.current_device() == before
+
+
+@pytest.mark.parametrize("case,plen", [("smollm2", 40), ("relu2_ternary_head", 5), ("relu2_ternary_head", 100),
+                                       ("dense_head", 40)])
+def test_engine_fp32_glue_matches_the_fp32_model(pkg, dev, tmp_path, case, plen):
+    """A file whose config says torch_dtype float32 runs the engine's float glue in fp32 -- embedding, norms,
+    residual stream, KV cache, attention and a dense head, as the reference engine computes
+    (bitnet_engine.cpp:107, 146-150, 289, 490-554) -- with the prompt's attention as one decode attention per
+    position.  Its greedy tokens equal the fp32 Python model's (HipBackend fp32, fused, prompt attention by
+    steps), id for id; the same weights in a bf16 file give the bf16 model's tokens."""
+    M = pkg.model
+    cfg, dense = _cases(M)[case]
+    be = M.HipBackend(out_dtype=torch.float32, fused=True)
+    if dense:
+        model = M.BitNetDecoder.from_float_state(M.random_float_state(cfg, 11), cfg, device=dev, dtype=torch.float32,
+                                                 backend=be, prefill_attention="steps")
+    else:
+        model = M.BitNetDecoder(cfg, seed=11, device=dev, dtype=torch.float32, backend=be, prefill_attention="steps")
+    path = tmp_path / "m32.bin"
+    model.save_sglbitnt(path)
+    max_len, new = 192, 40
+    prompt = _prompt(cfg, plen, 3)
+    want = model.generate(prompt, new, max_len=max_len)[0].tolist()
+    with pkg.NativeEngine(str(path), max_seq_len=max_len) as eng:
+        got = eng.generate(prompt[0].tolist(), max_tokens=new)
+        assert got == want, f"first divergence at {next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)}"
+        eng.prefill(prompt[0].tolist())
+        assert [eng.decode_step(plen + i) for i in range(8)] == want[:8]
+    assert len(set(want)) > 4

@@ -3,10 +3,15 @@
 //
 // The reference runs one token at a time on the CPU, prompt included
 // (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:490-554, 742-823).  Here:
-//  * the weights, the bf16 KV cache and every work buffer live in HBM from bitnet_engine_create on;
+//  * the weights, the KV cache and every work buffer live in HBM from bitnet_engine_create on;
 //    q|k|v and gate|up are concatenated at load time into one segmented weight each;
-//  * a prompt is one batched pass: the layer sequence at M = prompt length (prefill GEMMs, matrix-core
-//    prefill attention with the cache append), its last row kept as the pending hidden state;
+//  * the float glue (embedding, norms, residual stream, KV cache, attention, dense LM head) is fp32 for a
+//    file whose config says torch_dtype float32 (or, without that key, stores its embedding in float32), as
+//    the reference engine computes; otherwise bf16 (half the bytes of the residual stream, the cache and a
+//    dense head);
+//  * a prompt is one batched pass: the layer sequence at M = prompt length (prefill GEMMs; bf16: matrix-core
+//    prefill attention with the cache append, fp32: one decode attention per position), its last row kept as
+//    the pending hidden state;
 //  * a generated token is one replay of a HIP graph captured once per engine:
 //      LM head (final RMSNorm + head + first-max argmax)  -> token on the device
 //      embedding row of that token -> the layer sequence at M = 1 (decode attention at the device
@@ -15,9 +20,9 @@
 //  * sampling (temperature > 0) replays the head alone with the logits stored, samples on the host
 //    with the reference's algorithm (bitnet_engine.cpp:208-253, 782-788) and replays the rest.
 // Every layer step issues exactly the calls the Python model's fused HIP backend issues for the same
-// rows (wrinklefree-monorepo_amd/model.py, HipBackend(fused=True) with bf16 glue), so both produce the
-// same tokens bit for bit.  This file is host code only; the engine's own small kernels (embedding rows,
-// bf16 conversion at load, the decode step's commit, the hidden-state restore) are in engine_kernels.hip.
+// rows (wrinklefree-monorepo_amd/model.py, HipBackend(fused=True) with bf16 glue, or fp32 glue with
+// prefill_attention="steps"), so both produce the same tokens bit for bit.  This file is host code only; the engine's own small kernels (embedding rows,
+// float conversion at load, the decode step's commit, the hidden-state restore) are in engine_kernels.hip.
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -189,20 +194,21 @@ struct Cfg {
 struct Layer {
   uint8_t *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
   float* scales = nullptr;  // device [7]: q, k, v, o, gate, up, down
-  uint16_t *in_norm = nullptr, *post_norm = nullptr, *attn_sub = nullptr, *ffn_sub = nullptr;
-  uint16_t *kc = nullptr, *vc = nullptr;  // [kv_heads, max_len, head_dim] bf16
+  // float vectors in the engine's glue dtype (bf16 or fp32, Engine::gdt)
+  void *in_norm = nullptr, *post_norm = nullptr, *attn_sub = nullptr, *ffn_sub = nullptr;
+  void *kc = nullptr, *vc = nullptr;  // [kv_heads, max_len, head_dim]
 };
 
 // Work buffers of one row count (the decode set holds 1 row, the prompt set grows with the prompt).
 struct Acts {
   int64_t cap = 0;
-  uint16_t* x = nullptr;     // [cap, H] residual stream
-  uint16_t* qkv = nullptr;   // [cap, Nqkv]
-  uint16_t* att = nullptr;   // [cap, qd]
+  void* x = nullptr;         // [cap, H] residual stream (glue dtype)
+  void* qkv = nullptr;       // [cap, Nqkv] (glue dtype)
+  void* att = nullptr;       // [cap, qd] (glue dtype)
   int8_t* codes = nullptr;   // [cap, kmax]
   float* ascale = nullptr;   // [cap]
   float* mid = nullptr;      // [min(cap, 64), F] gated product of the M <= 64 path
-  uint16_t* gu = nullptr;    // [cap, 2F] gate|up outputs of the M > 64 path (and of every M when F % 32 != 0)
+  void* gu = nullptr;        // [cap, 2F] gate|up outputs (glue dtype) of the M > 64 path (and of every M when F % 32 != 0)
   int64_t* ids = nullptr;    // [cap] token ids of the embedding gather
 };
 
@@ -215,12 +221,18 @@ struct BitNetEngine {
   std::vector<void*> allocs;  // every device allocation, freed at destroy
   int64_t kpad_h = 0, kpad_qd = 0, kpad_f = 0, kmax = 0;
   int64_t seg_qkv[3] = {0, 0, 0};
-  uint16_t* embed = nullptr;
+  // Glue dtype: WFB_BF16, or WFB_F32 for a file whose config says torch_dtype float32 (or, without that key,
+  // whose embedding is stored in float32) -- the reference engine's arithmetic (bitnet_engine.cpp:107,
+  // 146-150, 289, 541-553): embedding, norms, residual stream, KV cache, attention and a dense head in fp32.
+  int gdt = WFB_BF16;
+  int64_t es = 2;                 // its element size
+  int64_t* iota = nullptr;        // device [max_len] = 0, 1, ... (fp32 prompts: one decode attention per position)
+  void* embed = nullptr;
   std::vector<Layer> L;
-  uint16_t* final_norm = nullptr;
+  void* final_norm = nullptr;
   uint8_t* head_q = nullptr;      // ternary head [V, kpad_h/4]
   float* head_scale = nullptr;    // device [1]
-  uint16_t* head_dense = nullptr; // dense head [V, H] (the embedding when tied)
+  void* head_dense = nullptr;     // dense head [V, H] (the embedding when tied)
   float *rope_cos = nullptr, *rope_sin = nullptr;
   Acts dec, pre;
   float* attn_ws = nullptr;
@@ -229,8 +241,8 @@ struct BitNetEngine {
   int64_t* ctl_h = nullptr;        // pinned host mirror
   int32_t* tokens = nullptr;       // device [max_len] tokens of a greedy generation
   int32_t* last_tok = nullptr;     // device [1]
-  uint16_t* ring = nullptr;        // device [kRing, H]
-  uint16_t* x_start = nullptr;     // device [H] hidden state before the first generated token
+  void* ring = nullptr;            // device [kRing, H]
+  void* x_start = nullptr;         // device [H] hidden state before the first generated token
   void* logits = nullptr;          // device [V] fp32
   void* logits_h = nullptr;        // pinned host copy
   int64_t* ids_h = nullptr;        // pinned host prompt ids (pre.cap)
@@ -312,6 +324,13 @@ void dfree(Engine& e, void* p) {
   e.allocs.erase(std::remove(e.allocs.begin(), e.allocs.end(), p), e.allocs.end());
 }
 
+// n elements of the glue dtype
+int galloc(Engine& e, void*& p, int64_t n) { return dalloc_bytes(e, p, (size_t)n * (size_t)e.es); }
+
+// element i of a glue-dtype buffer
+void* at(const Engine& e, void* p, int64_t i) { return static_cast<char*>(p) + i * e.es; }
+const void* at(const Engine& e, const void* p, int64_t i) { return static_cast<const char*>(p) + i * e.es; }
+
 int check_packed(const ModelFile& f, const std::string& name, int64_t out_rows, int64_t in_features) {
   const TensorRec* t = f.find(name);
   if (!t) return efail("Tensor not found: " + name);
@@ -391,12 +410,16 @@ int load_packed(Uploader& up, const ModelFile& f, const std::string& name, int64
   return 0;
 }
 
-// A float tensor of `numel` elements as bf16 on the device; absent (optional) -> ones.
-int load_floats(Engine& e, Uploader& up, const ModelFile& f, const std::string& name, int64_t numel, uint16_t* dst,
+// A float tensor of `numel` elements in the glue dtype on the device; absent (optional) -> ones.
+int load_floats(Engine& e, Uploader& up, const ModelFile& f, const std::string& name, int64_t numel, void* dst,
                 bool optional, void* scratch, size_t scratch_bytes) {
   const TensorRec* t = f.find(name);
   if (!t) {
     if (!optional) return efail("Tensor not found: " + name);
+    if (e.gdt == WFB_F32) {
+      std::vector<float> ones((size_t)numel, 1.0f);
+      return up.put(dst, reinterpret_cast<const uint8_t*>(ones.data()), (size_t)numel * 4);
+    }
     std::vector<uint16_t> ones((size_t)numel, 0x3F80);
     return up.put(dst, reinterpret_cast<const uint8_t*>(ones.data()), (size_t)numel * 2);
   }
@@ -408,7 +431,7 @@ int load_floats(Engine& e, Uploader& up, const ModelFile& f, const std::string& 
   for (int64_t off = 0; off < numel; off += per) {
     const int64_t len = std::min(per, numel - off);
     ECHECK(up.put(scratch, f.base + t->offset + off * esize, (size_t)(len * esize)));
-    HCHECK(wfb::launch_to_bf16(scratch, (int)t->dtype, len, dst + off, e.s), "to_bf16");
+    HCHECK(wfb::launch_to_float(scratch, (int)t->dtype, len, at(e, dst, off), e.gdt, e.s), "float conversion");
   }
   return 0;
 }
@@ -425,13 +448,13 @@ void free_acts(Engine& e, Acts& a) {
 int alloc_acts(Engine& e, Acts& a, int64_t cap) {
   const Cfg& c = e.c;
   Acts n;
-  int st = dalloc(e, n.x, cap * c.hidden);
-  if (st == 0) st = dalloc(e, n.qkv, cap * c.nqkv());
-  if (st == 0) st = dalloc(e, n.att, cap * c.qd());
+  int st = galloc(e, n.x, cap * c.hidden);
+  if (st == 0) st = galloc(e, n.qkv, cap * c.nqkv());
+  if (st == 0) st = galloc(e, n.att, cap * c.qd());
   if (st == 0) st = dalloc(e, n.codes, cap * e.kmax);
   if (st == 0) st = dalloc(e, n.ascale, cap);
   if (st == 0) st = dalloc(e, n.mid, std::min<int64_t>(cap, 64) * c.inter);
-  if (st == 0 && (cap > 64 || c.inter % 32 != 0)) st = dalloc(e, n.gu, cap * 2 * c.inter);
+  if (st == 0 && (cap > 64 || c.inter % 32 != 0)) st = galloc(e, n.gu, cap * 2 * c.inter);
   if (st == 0) st = dalloc(e, n.ids, cap);
   if (st != 0) {
     free_acts(e, n);
@@ -455,92 +478,104 @@ bool fused_norm_ok(int64_t m, int64_t h, int64_t k) {
 }
 
 // residual + linear(quantise(norm(x))) into the residual stream x (in place), one projection.
-int norm_linear_residual(Engine& e, Acts& a, int64_t m, const void* x, int xdt, int64_t h, const uint16_t* gamma,
+int norm_linear_residual(Engine& e, Acts& a, int64_t m, const void* x, int xdt, int64_t h, const void* gamma,
                          float eps, const uint8_t* w, int64_t kpad, const float* scale) {
   const Cfg& c = e.c;
   void* st = e.s;
+  const int g = e.gdt;
   if (fused_norm_ok(m, h, kpad)) {
     const int64_t rows = c.hidden;
-    return wcheck(wfb_rmsnorm_linear_i2s(x, xdt, h, gamma, WFB_BF16, eps, m, h, w, c.hidden, kpad, 1, &rows, scale,
-                                         a.x, WFB_BF16, c.hidden, a.x, WFB_BF16, c.hidden, st),
+    return wcheck(wfb_rmsnorm_linear_i2s(x, xdt, h, gamma, g, eps, m, h, w, c.hidden, kpad, 1, &rows, scale, a.x, g,
+                                         c.hidden, a.x, g, c.hidden, st),
                   "rmsnorm_linear (residual)");
   }
-  ECHECK(wcheck(wfb_rmsnorm_quant_i8(x, xdt, h, gamma, WFB_BF16, eps, m, h, a.codes, kpad, kpad, a.ascale, st),
+  ECHECK(wcheck(wfb_rmsnorm_quant_i8(x, xdt, h, gamma, g, eps, m, h, a.codes, kpad, kpad, a.ascale, st),
                 "rmsnorm_quant"));
-  return wcheck(wfb_linear_i2s_residual(w, c.hidden, kpad, a.codes, m, kpad, a.ascale, scale, 0.0f, a.x, WFB_BF16,
-                                        c.hidden, a.x, WFB_BF16, c.hidden, st),
+  return wcheck(wfb_linear_i2s_residual(w, c.hidden, kpad, a.codes, m, kpad, a.ascale, scale, 0.0f, a.x, g, c.hidden,
+                                        a.x, g, c.hidden, st),
                 "linear_residual");
 }
 
-// One decoder layer over the m rows of a.x.  prompt: rows are positions 0..m-1 (prefill attention);
-// else one row at the device position ctl[1] (decode attention).
+// One decoder layer over the m rows of a.x.  prompt: rows are positions 0..m-1 (prefill attention; in fp32,
+// which the matrix-core prefill kernel does not take, one decode attention per position, as the reference
+// engine runs every prompt token through its attention, bitnet_engine.cpp:381-441); else one row at the device
+// position ctl[1] (decode attention).
 int layer(Engine& e, const Layer& Ly, Acts& a, int64_t m, bool prompt) {
   const Cfg& c = e.c;
   void* st = e.s;
+  const int g = e.gdt;
   const int64_t H = c.hidden, F = c.inter, qd = c.qd(), kvd = c.kvd(), nqkv = c.nqkv();
   const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
   // RMSNorm -> q|k|v
   if (fused_norm_ok(m, H, e.kpad_h)) {
-    ECHECK(wcheck(wfb_rmsnorm_linear_i2s(a.x, WFB_BF16, H, Ly.in_norm, WFB_BF16, c.rms_eps, m, H, Ly.qkv, nqkv, e.kpad_h,
-                                         3, e.seg_qkv, Ly.scales, nullptr, WFB_F32, nqkv, a.qkv, WFB_BF16, nqkv, st),
+    ECHECK(wcheck(wfb_rmsnorm_linear_i2s(a.x, g, H, Ly.in_norm, g, c.rms_eps, m, H, Ly.qkv, nqkv, e.kpad_h, 3,
+                                         e.seg_qkv, Ly.scales, nullptr, WFB_F32, nqkv, a.qkv, g, nqkv, st),
                   "rmsnorm_linear (q|k|v)"));
   } else {
-    ECHECK(wcheck(wfb_rmsnorm_quant_i8(a.x, WFB_BF16, H, Ly.in_norm, WFB_BF16, c.rms_eps, m, H, a.codes, e.kpad_h,
-                                       e.kpad_h, a.ascale, st),
+    ECHECK(wcheck(wfb_rmsnorm_quant_i8(a.x, g, H, Ly.in_norm, g, c.rms_eps, m, H, a.codes, e.kpad_h, e.kpad_h,
+                                       a.ascale, st),
                   "rmsnorm_quant"));
     ECHECK(wcheck(wfb_linear_i2s_segmented(Ly.qkv, nqkv, e.kpad_h, 3, e.seg_qkv, Ly.scales, a.codes, m, e.kpad_h,
-                                           a.ascale, nullptr, WFB_F32, a.qkv, WFB_BF16, nqkv, nullptr, st),
+                                           a.ascale, nullptr, WFB_F32, a.qkv, g, nqkv, nullptr, st),
                   "linear_segmented (q|k|v)"));
   }
   // rotary embedding + cache append + attention
-  if (prompt) {
-    ECHECK(wcheck(wfb_gqa_prefill_attention(a.qkv, nqkv, a.qkv + qd, nqkv, a.qkv + qd + kvd, nqkv, WFB_BF16, e.rope_cos,
-                                            e.rope_sin, Ly.kc, Ly.vc, c.max_len, 0, 1, m, c.heads, c.kv_heads,
-                                            c.head_dim, scale, a.att, qd, st),
+  if (prompt && g == WFB_BF16) {
+    ECHECK(wcheck(wfb_gqa_prefill_attention(a.qkv, nqkv, at(e, a.qkv, qd), nqkv, at(e, a.qkv, qd + kvd), nqkv, g,
+                                            e.rope_cos, e.rope_sin, Ly.kc, Ly.vc, c.max_len, 0, 1, m, c.heads,
+                                            c.kv_heads, c.head_dim, scale, a.att, qd, st),
                   "prefill attention"));
+  } else if (prompt) {
+    for (int64_t i = 0; i < m; ++i) {
+      const int64_t r = i * nqkv;
+      ECHECK(wcheck(wfb_gqa_decode_attention(at(e, a.qkv, r), nqkv, at(e, a.qkv, r + qd), nqkv,
+                                             at(e, a.qkv, r + qd + kvd), nqkv, g, e.rope_cos, e.rope_sin, Ly.kc, Ly.vc,
+                                             c.max_len, e.iota + i, 1, c.heads, c.kv_heads, c.head_dim, scale,
+                                             at(e, a.att, i * qd), qd, e.attn_ws, st),
+                    "decode attention (prompt)"));
+    }
   } else {
-    ECHECK(wcheck(wfb_gqa_decode_attention(a.qkv, nqkv, a.qkv + qd, nqkv, a.qkv + qd + kvd, nqkv, WFB_BF16, e.rope_cos,
-                                           e.rope_sin, Ly.kc, Ly.vc, c.max_len, e.ctl + 1, 1, c.heads, c.kv_heads,
-                                           c.head_dim, scale, a.att, qd, e.attn_ws, st),
+    ECHECK(wcheck(wfb_gqa_decode_attention(a.qkv, nqkv, at(e, a.qkv, qd), nqkv, at(e, a.qkv, qd + kvd), nqkv, g,
+                                           e.rope_cos, e.rope_sin, Ly.kc, Ly.vc, c.max_len, e.ctl + 1, 1, c.heads,
+                                           c.kv_heads, c.head_dim, scale, a.att, qd, e.attn_ws, st),
                   "decode attention"));
   }
   // SubLN -> o + residual
-  ECHECK(norm_linear_residual(e, a, m, a.att, WFB_BF16, qd, Ly.attn_sub, c.subln_eps, Ly.o, e.kpad_qd, Ly.scales + 3));
+  ECHECK(norm_linear_residual(e, a, m, a.att, g, qd, Ly.attn_sub, c.subln_eps, Ly.o, e.kpad_qd, Ly.scales + 3));
   // RMSNorm -> gate|up -> act(gate) * up -> SubLN -> down + residual
   if (m <= 64 && F % 32 == 0) {
     if (fused_glu_ok(m, H, e.kpad_h)) {
-      ECHECK(wcheck(wfb_rmsnorm_linear_i2s_glu(a.x, WFB_BF16, H, Ly.post_norm, WFB_BF16, c.rms_eps, m, H, Ly.gu, 2 * F,
-                                               e.kpad_h, Ly.scales + 4, c.act, WFB_BF16, a.mid, F, st),
+      ECHECK(wcheck(wfb_rmsnorm_linear_i2s_glu(a.x, g, H, Ly.post_norm, g, c.rms_eps, m, H, Ly.gu, 2 * F, e.kpad_h,
+                                               Ly.scales + 4, c.act, g, a.mid, F, st),
                     "rmsnorm_linear_glu"));
     } else {
-      ECHECK(wcheck(wfb_rmsnorm_quant_i8(a.x, WFB_BF16, H, Ly.post_norm, WFB_BF16, c.rms_eps, m, H, a.codes, e.kpad_h,
-                                         e.kpad_h, a.ascale, st),
+      ECHECK(wcheck(wfb_rmsnorm_quant_i8(a.x, g, H, Ly.post_norm, g, c.rms_eps, m, H, a.codes, e.kpad_h, e.kpad_h,
+                                         a.ascale, st),
                     "rmsnorm_quant"));
-      ECHECK(wcheck(wfb_linear_i2s_glu(Ly.gu, 2 * F, e.kpad_h, a.codes, m, e.kpad_h, a.ascale, Ly.scales + 4, c.act,
-                                       WFB_BF16, a.mid, F, st),
+      ECHECK(wcheck(wfb_linear_i2s_glu(Ly.gu, 2 * F, e.kpad_h, a.codes, m, e.kpad_h, a.ascale, Ly.scales + 4, c.act, g,
+                                       a.mid, F, st),
                     "linear_glu"));
     }
     return norm_linear_residual(e, a, m, a.mid, WFB_F32, F, Ly.ffn_sub, c.subln_eps, Ly.down, e.kpad_f, Ly.scales + 6);
   }
   const int64_t seg_gu[2] = {F, F};
   if (fused_norm_ok(m, H, e.kpad_h)) {
-    ECHECK(wcheck(wfb_rmsnorm_linear_i2s(a.x, WFB_BF16, H, Ly.post_norm, WFB_BF16, c.rms_eps, m, H, Ly.gu, 2 * F,
-                                         e.kpad_h, 2, seg_gu, Ly.scales + 4, nullptr, WFB_F32, 2 * F, a.gu, WFB_BF16,
-                                         2 * F, st),
+    ECHECK(wcheck(wfb_rmsnorm_linear_i2s(a.x, g, H, Ly.post_norm, g, c.rms_eps, m, H, Ly.gu, 2 * F, e.kpad_h, 2, seg_gu,
+                                         Ly.scales + 4, nullptr, WFB_F32, 2 * F, a.gu, g, 2 * F, st),
                   "rmsnorm_linear (gate|up)"));
   } else {
-    ECHECK(wcheck(wfb_rmsnorm_quant_i8(a.x, WFB_BF16, H, Ly.post_norm, WFB_BF16, c.rms_eps, m, H, a.codes, e.kpad_h,
-                                       e.kpad_h, a.ascale, st),
+    ECHECK(wcheck(wfb_rmsnorm_quant_i8(a.x, g, H, Ly.post_norm, g, c.rms_eps, m, H, a.codes, e.kpad_h, e.kpad_h,
+                                       a.ascale, st),
                   "rmsnorm_quant"));
     ECHECK(wcheck(wfb_linear_i2s_segmented(Ly.gu, 2 * F, e.kpad_h, 2, seg_gu, Ly.scales + 4, a.codes, m, e.kpad_h,
-                                           a.ascale, nullptr, WFB_F32, a.gu, WFB_BF16, 2 * F, nullptr, st),
+                                           a.ascale, nullptr, WFB_F32, a.gu, g, 2 * F, nullptr, st),
                   "linear_segmented (gate|up)"));
   }
-  ECHECK(wcheck(wfb_glu_rmsnorm_quant_i8(a.gu, a.gu + F, WFB_BF16, 2 * F, c.act, Ly.ffn_sub, WFB_BF16, c.subln_eps, m,
-                                         F, a.codes, e.kpad_f, e.kpad_f, a.ascale, st),
+  ECHECK(wcheck(wfb_glu_rmsnorm_quant_i8(a.gu, at(e, a.gu, F), g, 2 * F, c.act, Ly.ffn_sub, g, c.subln_eps, m, F,
+                                         a.codes, e.kpad_f, e.kpad_f, a.ascale, st),
                 "glu_rmsnorm_quant"));
   return wcheck(wfb_linear_i2s_residual(Ly.down, H, e.kpad_f, a.codes, m, e.kpad_f, a.ascale, Ly.scales + 6, 0.0f, a.x,
-                                        WFB_BF16, H, a.x, WFB_BF16, H, st),
+                                        g, H, a.x, g, H, st),
                 "linear_residual (down)");
 }
 
@@ -549,17 +584,18 @@ int layer(Engine& e, const Layer& Ly, Acts& a, int64_t m, bool prompt) {
 int head(Engine& e, bool logits) {
   const Cfg& c = e.c;
   Acts& a = e.dec;
+  const int g = e.gdt;
   if (e.head_q) {
-    ECHECK(wcheck(wfb_rmsnorm_quant_i8(a.x, WFB_BF16, c.hidden, e.final_norm, WFB_BF16, c.rms_eps, 1, c.hidden, a.codes,
-                                       e.kpad_h, e.kpad_h, a.ascale, e.s),
+    ECHECK(wcheck(wfb_rmsnorm_quant_i8(a.x, g, c.hidden, e.final_norm, g, c.rms_eps, 1, c.hidden, a.codes, e.kpad_h,
+                                       e.kpad_h, a.ascale, e.s),
                   "rmsnorm_quant (head)"));
     return wcheck(wfb_linear_i2s_argmax(e.head_q, c.vocab, e.kpad_h, a.codes, 1, e.kpad_h, a.ascale, e.head_scale, 0.0f,
                                         logits ? e.logits : nullptr, WFB_F32, c.vocab, e.argmax_ws, e.ctl, e.s),
                   "LM head");
   }
-  return wcheck(wfb_lm_head_argmax(a.x, WFB_BF16, c.hidden, e.final_norm, WFB_BF16, c.rms_eps, e.head_dense, WFB_BF16,
-                                   c.hidden, 1, c.vocab, c.hidden, logits ? static_cast<float*>(e.logits) : nullptr,
-                                   c.vocab, e.argmax_ws, e.ctl, e.s),
+  return wcheck(wfb_lm_head_argmax(a.x, g, c.hidden, e.final_norm, g, c.rms_eps, e.head_dense, g, c.hidden, 1, c.vocab,
+                                   c.hidden, logits ? static_cast<float*>(e.logits) : nullptr, c.vocab, e.argmax_ws,
+                                   e.ctl, e.s),
                 "LM head");
 }
 
@@ -567,9 +603,10 @@ int head(Engine& e, bool logits) {
 int body(Engine& e) {
   const Cfg& c = e.c;
   Acts& a = e.dec;
-  HCHECK(wfb::launch_embed_rows(e.embed, c.vocab, (int)c.hidden, e.ctl, 1, a.x, e.s), "embedding");
+  HCHECK(wfb::launch_embed_rows(e.embed, c.vocab, (int)c.hidden, (int)e.es, e.ctl, 1, a.x, e.s), "embedding");
   for (const Layer& Ly : e.L) ECHECK(layer(e, Ly, a, 1, false));
-  HCHECK(wfb::launch_commit(e.ctl, e.tokens, c.max_len, e.last_tok, a.x, e.ring, kRing, (int)c.hidden, e.s), "commit");
+  HCHECK(wfb::launch_commit(e.ctl, e.tokens, c.max_len, e.last_tok, a.x, e.ring, kRing, (int)c.hidden, (int)e.es, e.s),
+         "commit");
   return 0;
 }
 
@@ -644,9 +681,10 @@ int prefill(Engine& e, const int32_t* ids, int64_t n) {
   Acts& a = e.pre;
   for (int64_t i = 0; i < n; ++i) e.ids_h[i] = ids[i];
   HCHECK(hipMemcpyAsync(a.ids, e.ids_h, n * sizeof(int64_t), hipMemcpyHostToDevice, e.s), "prompt upload");
-  HCHECK(wfb::launch_embed_rows(e.embed, c.vocab, (int)c.hidden, a.ids, n, a.x, e.s), "embedding");
+  HCHECK(wfb::launch_embed_rows(e.embed, c.vocab, (int)c.hidden, (int)e.es, a.ids, n, a.x, e.s), "embedding");
   for (const Layer& Ly : e.L) ECHECK(layer(e, Ly, a, n, true));
-  HCHECK(hipMemcpyAsync(e.dec.x, a.x + (n - 1) * c.hidden, c.hidden * 2, hipMemcpyDeviceToDevice, e.s), "hidden copy");
+  HCHECK(hipMemcpyAsync(e.dec.x, at(e, a.x, (n - 1) * c.hidden), c.hidden * e.es, hipMemcpyDeviceToDevice, e.s),
+         "hidden copy");
   ECHECK(sync(e, "prefill"));
   e.seq_len = n;
   e.have_hidden = true;
@@ -786,6 +824,13 @@ int create(Engine& e, const char* path, const BitNetConfig* user) {
   e.seg_qkv[0] = c.qd();
   e.seg_qkv[1] = e.seg_qkv[2] = c.kvd();
   ECHECK(check_tensors(f, c));  // the whole file, before anything touches the GPU
+  {
+    const std::string td = json_raw(js, "torch_dtype");
+    const TensorRec* emb = f.find("model.embed_tokens.weight");
+    const bool fp32 = td.empty() ? emb->dtype == 1 : td == "\"float32\"";
+    e.gdt = fp32 ? WFB_F32 : WFB_BF16;
+    e.es = fp32 ? 4 : 2;
+  }
 
   HCHECK(hipGetDevice(&e.device), "hipGetDevice");
   HCHECK(hipStreamCreateWithFlags(&e.s, hipStreamNonBlocking), "hipStreamCreate");
@@ -795,7 +840,7 @@ int create(Engine& e, const char* path, const BitNetConfig* user) {
   ECHECK(dalloc_bytes(e, scratch, scratch_bytes));
 
   const int64_t H = c.hidden, F = c.inter, qd = c.qd(), kvd = c.kvd(), V = c.vocab;
-  ECHECK(dalloc(e, e.embed, V * H));
+  ECHECK(galloc(e, e.embed, V * H));
   ECHECK(load_floats(e, up, f, "model.embed_tokens.weight", V * H, e.embed, false, scratch, scratch_bytes));
   e.L.resize((size_t)c.layers);
   for (int64_t i = 0; i < c.layers; ++i) {
@@ -816,22 +861,22 @@ int create(Engine& e, const char* path, const BitNetConfig* user) {
     ECHECK(load_packed(up, f, pre + "mlp.up_proj.weight", F, H, Ly.gu + F * e.kpad_h / 4, sc, 5));
     ECHECK(load_packed(up, f, pre + "mlp.down_proj.weight", H, F, Ly.down, sc, 6));
     ECHECK(up.put(Ly.scales, reinterpret_cast<const uint8_t*>(sc.data()), 7 * sizeof(float)));
-    ECHECK(dalloc(e, Ly.in_norm, H));
-    ECHECK(dalloc(e, Ly.post_norm, H));
-    ECHECK(dalloc(e, Ly.attn_sub, qd));
-    ECHECK(dalloc(e, Ly.ffn_sub, F));
+    ECHECK(galloc(e, Ly.in_norm, H));
+    ECHECK(galloc(e, Ly.post_norm, H));
+    ECHECK(galloc(e, Ly.attn_sub, qd));
+    ECHECK(galloc(e, Ly.ffn_sub, F));
     ECHECK(load_floats(e, up, f, pre + "input_layernorm.weight", H, Ly.in_norm, false, scratch, scratch_bytes));
     ECHECK(load_floats(e, up, f, pre + "post_attention_layernorm.weight", H, Ly.post_norm, false, scratch,
                        scratch_bytes));
     ECHECK(load_floats(e, up, f, pre + "self_attn.attn_sub_norm.weight", qd, Ly.attn_sub, true, scratch, scratch_bytes));
     ECHECK(load_floats(e, up, f, pre + "mlp.ffn_sub_norm.weight", F, Ly.ffn_sub, true, scratch, scratch_bytes));
     const int64_t cache = c.kv_heads * c.max_len * c.head_dim;
-    ECHECK(dalloc(e, Ly.kc, cache));
-    ECHECK(dalloc(e, Ly.vc, cache));
-    HCHECK(hipMemsetAsync(Ly.kc, 0, cache * 2, e.s), "cache clear");
-    HCHECK(hipMemsetAsync(Ly.vc, 0, cache * 2, e.s), "cache clear");
+    ECHECK(galloc(e, Ly.kc, cache));
+    ECHECK(galloc(e, Ly.vc, cache));
+    HCHECK(hipMemsetAsync(Ly.kc, 0, cache * e.es, e.s), "cache clear");
+    HCHECK(hipMemsetAsync(Ly.vc, 0, cache * e.es, e.s), "cache clear");
   }
-  ECHECK(dalloc(e, e.final_norm, H));
+  ECHECK(galloc(e, e.final_norm, H));
   ECHECK(load_floats(e, up, f, "model.norm.weight", H, e.final_norm, false, scratch, scratch_bytes));
   if (const TensorRec* t = f.find("lm_head.weight")) {
     if (t->dtype == 0) {
@@ -841,7 +886,7 @@ int create(Engine& e, const char* path, const BitNetConfig* user) {
       ECHECK(load_packed(up, f, "lm_head.weight", V, H, e.head_q, sc, 0));
       ECHECK(up.put(e.head_scale, reinterpret_cast<const uint8_t*>(sc.data()), sizeof(float)));
     } else {
-      ECHECK(dalloc(e, e.head_dense, V * H));
+      ECHECK(galloc(e, e.head_dense, V * H));
       ECHECK(load_floats(e, up, f, "lm_head.weight", V * H, e.head_dense, false, scratch, scratch_bytes));
     }
   } else {
@@ -864,13 +909,19 @@ int create(Engine& e, const char* path, const BitNetConfig* user) {
   ECHECK(dalloc(e, e.ctl, 4));
   ECHECK(dalloc(e, e.tokens, c.max_len));
   ECHECK(dalloc(e, e.last_tok, 1));
-  ECHECK(dalloc(e, e.ring, kRing * H));
-  ECHECK(dalloc(e, e.x_start, H));
+  ECHECK(galloc(e, e.ring, kRing * H));
+  ECHECK(galloc(e, e.x_start, H));
+  if (e.gdt == WFB_F32) {
+    std::vector<int64_t> iota((size_t)c.max_len);
+    for (int64_t i = 0; i < c.max_len; ++i) iota[(size_t)i] = i;
+    ECHECK(dalloc(e, e.iota, c.max_len));
+    HCHECK(hipMemcpy(e.iota, iota.data(), iota.size() * sizeof(int64_t), hipMemcpyHostToDevice), "positions upload");
+  }
   ECHECK(dalloc_bytes(e, e.logits, V * 4));
   HCHECK(hipHostMalloc((void**)&e.ctl_h, 4 * sizeof(int64_t), hipHostMallocDefault), "hipHostMalloc");
   HCHECK(hipHostMalloc(&e.logits_h, V * 4, hipHostMallocDefault), "hipHostMalloc");
   HCHECK(hipHostMalloc((void**)&e.tokens_h, kChunk * sizeof(int32_t), hipHostMallocDefault), "hipHostMalloc");
-  HCHECK(hipMemsetAsync(e.dec.x, 0, H * 2, e.s), "clear");
+  HCHECK(hipMemsetAsync(e.dec.x, 0, H * e.es, e.s), "clear");
   for (int i = 0; i < 3; ++i) ECHECK(set_ctl(e, i, 0));
   // one eager step (position 0 of every cache, rewritten by the first prompt) before the captures
   ECHECK(head(e, true));
@@ -903,7 +954,7 @@ int generate(Engine& e, const int32_t* ids, int32_t n, const SamplingParams* p, 
   if (p->temperature <= 0.0f) {
     ECHECK(set_ctl(e, 1, n));
     ECHECK(set_ctl(e, 2, 0));
-    HCHECK(hipMemcpyAsync(e.x_start, e.dec.x, e.c.hidden * 2, hipMemcpyDeviceToDevice, e.s), "hidden copy");
+    HCHECK(hipMemcpyAsync(e.x_start, e.dec.x, e.c.hidden * e.es, hipMemcpyDeviceToDevice, e.s), "hidden copy");
     int64_t eos_at = -1;
     while ((int64_t)out.size() < max_new && eos_at < 0) {
       const int64_t c0 = (int64_t)out.size();
@@ -922,8 +973,8 @@ int generate(Engine& e, const int32_t* ids, int32_t n, const SamplingParams* p, 
     }
     if (eos_at >= 0) {
       // the reference stops before running the EOS token: state after token eos_at - 1
-      const uint16_t* src = eos_at == 0 ? e.x_start : e.ring + ((eos_at - 1) % kRing) * e.c.hidden;
-      HCHECK(wfb::launch_copy_row(src, e.dec.x, (int)e.c.hidden, e.s), "hidden restore");
+      const void* src = eos_at == 0 ? e.x_start : at(e, e.ring, ((eos_at - 1) % kRing) * e.c.hidden);
+      HCHECK(wfb::launch_copy_row(src, e.dec.x, (int)e.c.hidden, (int)e.es, e.s), "hidden restore");
       ECHECK(sync(e, "decode"));
       e.seq_len = n + eos_at;
     } else {

@@ -261,7 +261,8 @@ class BitNetDecoder:
         as one libwfbitnet kernel; "torch" runs them as torch ops.  ``prefill_attention``: "hip" runs a
         prompt's rotary embedding, cache append and causal attention on libwfbitnet's matrix-core kernel
         (bf16 models with head_dim 64/128 and at most 8 query heads per kv head; other models use torch);
-        "torch" always uses torch ops."""
+        "steps" runs it as one decode-attention launch per prompt position (any model dtype; the native
+        engine's fp32 prompt path); "torch" always uses torch ops."""
         self._setup(cfg, device, dtype, backend, decode_attention, prefill_attention)
         gen = torch.Generator(device=self.device if init_on_device else "cpu").manual_seed(seed)
         self.embed = (torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen, device=gen.device) * 0.02).to(
@@ -278,8 +279,8 @@ class BitNetDecoder:
 
     def _setup(self, cfg: BitNetConfig, device, dtype: torch.dtype, backend, decode_attention: str,
                prefill_attention: str = "hip") -> None:
-        if decode_attention not in ("hip", "torch") or prefill_attention not in ("hip", "torch"):
-            raise ValueError("decode_attention and prefill_attention must be 'hip' or 'torch'")
+        if decode_attention not in ("hip", "torch") or prefill_attention not in ("hip", "torch", "steps"):
+            raise ValueError("decode_attention must be 'hip' or 'torch', prefill_attention 'hip', 'steps' or 'torch'")
         self.decode_attention = decode_attention
         self.prefill_attention = prefill_attention
         self.fuse_residual = True  # residual adds in the o / down epilogues when the backend offers it
@@ -303,15 +304,17 @@ class BitNetDecoder:
         """Write the model as an SGLBITNT file with the tensor names the reference engine loads
         (SGB/sgl-kernel/csrc/inference/bitnet_engine.cpp:622-668): packed linears uint8 [out, k_pad/4] with
         their scale, embedding and norms as float32, a ternary LM head (uint8) or an untied dense head
-        (float32) as lm_head.weight, none for a head tied to the embedding.  ``config_overrides``: extra or
-        replaced keys of the config JSON (e.g. ``eos_token_id``)."""
+        (float32) as lm_head.weight, none for a head tied to the embedding.  The config's ``torch_dtype`` is the
+        model's glue dtype ("float32" or "bfloat16"), which the native engine computes in.
+        ``config_overrides``: extra or replaced keys of the config JSON (e.g. ``eos_token_id``)."""
         cfg = self.cfg
         config = {"vocab_size": cfg.vocab_size, "hidden_size": cfg.hidden_size,
                   "intermediate_size": cfg.intermediate_size, "num_hidden_layers": cfg.num_layers,
                   "num_attention_heads": cfg.num_heads, "num_key_value_heads": cfg.num_kv_heads,
                   "head_dim": cfg.head_dim, "rope_theta": cfg.rope_theta, "rms_norm_eps": cfg.rms_eps,
                   "subln_eps": cfg.subln_eps, "tie_word_embeddings": self.lm_head is None,
-                  "hidden_act": cfg.hidden_act, "max_position_embeddings": 4096}
+                  "hidden_act": cfg.hidden_act, "max_position_embeddings": 4096,
+                  "torch_dtype": "float32" if self.dtype == torch.float32 else "bfloat16"}
         t = {"model.embed_tokens.weight": (self.embed.float(), None)}
         for i, L in enumerate(self.layers):
             pre = f"model.layers.{i}."
@@ -599,11 +602,30 @@ class BitNetDecoder:
                 kc, vc = self._cache(li, b)
                 return gqa_prefill_attention(q, k, v, kc, vc, start, t, self._rope_cos, self._rope_sin,
                                              scale=1.0 / math.sqrt(cfg.head_dim))
+            if self.prefill_attention == "steps" and self.device.type == "cuda":
+                return self._prefill_by_steps(li, q, k, v, b, t, start)
             q = self._rope(q.reshape(b, t, cfg.num_heads, cfg.head_dim), pos)
             k = self._rope(k.reshape(b, t, cfg.num_kv_heads, cfg.head_dim), pos)
             return self._attention(li, q, k, v.reshape(b, t, cfg.num_kv_heads, cfg.head_dim), start)
 
         return attend
+
+    def _prefill_by_steps(self, li: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, b: int, t: int,
+                          start: int) -> torch.Tensor:
+        """The prompt's attention as one decode-attention launch per position (the native engine's fp32 prompt
+        path, and the reference engine's token-by-token loop, bitnet_engine.cpp:381-441): token i of every
+        sequence ropes and appends its key and value at start + i and attends over keys 0..start + i.
+        q/k/v are [B*T, width] rows (possibly column slices of one q|k|v output)."""
+        cfg = self.cfg
+        kc, vc = self._cache(li, b)
+        qd = cfg.num_heads * cfg.head_dim
+        q3, k3, v3 = q.unflatten(0, (b, t)), k.unflatten(0, (b, t)), v.unflatten(0, (b, t))
+        pos = (torch.arange(start, start + t, device=self.device)[:, None]).expand(t, b).contiguous()
+        out = torch.empty((b, t, qd), dtype=q.dtype, device=self.device)
+        for i in range(t):
+            gqa_decode_attention(q3[:, i], k3[:, i], v3[:, i], kc, vc, pos[i], self._rope_cos, self._rope_sin,
+                                 scale=1.0 / math.sqrt(cfg.head_dim), out=out[:, i])
+        return out.reshape(b * t, qd)
 
     def forward(self, ids: torch.Tensor, start: int, tokens: bool = False) -> torch.Tensor:
         """ids [B, T] at positions start..start+T-1; returns fp32 logits of the last position [B, vocab], or
