@@ -711,6 +711,8 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(shapes[dom]["bytes"] / (d["us"] * 1e-6) / 1e9, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(d["frac_hbm_peak"], 4),
                 "traffic": measured_traffic(d["N"], d["K"]),
+                "traffic_source": "read from profiles/gemv_i2s_decode_bitnet2b.txt (two rocprofv3 --pmc runs, "
+                                  "FETCH_SIZE then WRITE_SIZE, calibrated against a plain copy), not measured here",
                 "kernel": f"gemv_i2s M=1 N={d['N']} K={d['K']}",
                 "bytes_per_launch": shapes[dom]["bytes"]}
     launch = launch_context(torch, dev, L, args.steps, args.warmup, shapes[dom]["bytes"])

@@ -127,7 +127,8 @@ def test_bitnet_linear_native_module(pkg, dev):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 2560, 2560), (8, 4096, 14336), (3, 640, 1024), (200, 2560, 6912), (64, 520, 512),
-                                   (300, 1016, 640), (1024, 6144, 512), (2048, 6144, 256)])
+                                   (300, 1016, 640), (1024, 6144, 512), (2048, 6144, 256), (64, 4096, 4096),
+                                   (37, 1024, 4096), (57, 2560, 6912)])
 @pytest.mark.parametrize("rdt", [torch.float32, torch.bfloat16])
 def test_linear_residual_matches_oracle(pkg, dev, m, n, k, rdt):
     """out = residual + acc * w_scale * a_scale in one launch (GEMV, skinny and tile kernels): the fp32

@@ -255,11 +255,13 @@ def test_batched_long_rows_register_activations(pkg, dev, m, n, k):
                                    (32, 4096, 4096), (32, 4112, 4096), (32, 32768, 2560), (32, 32784, 2560),
                                    (33, 4096, 4096), (64, 4096, 4096), (64, 4112, 4096), (48, 2560, 4224),
                                    (40, 1000, 2560), (32, 4096, 7168), (17, 4112, 6912), (24, 2560, 7296),
-                                   (33, 2560, 6912), (64, 4096, 7168), (64, 4112, 6912)])
+                                   (33, 2560, 6912), (64, 4096, 7168), (64, 4112, 6912), (48, 2560, 6912),
+                                   (49, 2560, 6912), (37, 4096, 4096), (49, 4000, 4096), (64, 2560, 4096)])
 def test_batched_kernel_choice_boundaries(pkg, dev, m, n, k):
     # 3 <= M <= 64: the LDS-staged kernel up to 16 tokens, and with two token tiles for 17..32 tokens on
     # rows up to 2560 (outputs up to 32768 rows) or 7168 (outputs up to 4096 rows), with four for 33..64
-    # tokens on rows up to 4096 and outputs up to 4096 rows (two launches of two tiles for rows up to 7168);
+    # tokens on rows up to 4096 and outputs up to 4096 rows (two token blocks of two-tile workgroups for rows
+    # of 4096, and for rows up to 7168 from 49 tokens; two launches of two tiles below that);
     # else the 32-row tile
     # kernel for M > 16 when N * ceil(M/16) >= 18432 and K <= 8192, else the split-K skinny kernel while
     # N * ceil(M/16) <= 32768 (always for M <= 8), else the whole-K wave-per-rows kernel; these shapes

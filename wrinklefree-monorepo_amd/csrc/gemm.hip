@@ -811,6 +811,12 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   // their registers): two launches of the two-tile form, measured on MI355X against the split-K kernel
   // (2560 x 6912: M = 64 18.8 -> 12.7 us, M = 33 13.5 -> 10.4)
   if (m > 32 && m <= 64 && small_offsets && !e.amax && k > 4096 && k <= 7168 && n <= 4096) {
+    // from 49 tokens one launch with two token blocks of workgroups (2560 x 6912 at M = 64: 12.4 -> 11.2 us;
+    // at M = 33..48 the two launches stay ahead, 10.3-11.0 against 11.0-11.1)
+    if (m > 48) {
+      const hipError_t st = launch_skinny_lds_mr32(W, n, C, A, m, lda, e, 0, 1, NormSrc{}, s);
+      if (st != hipErrorNotSupported) return st;
+    }
     const hipError_t st = launch_token_halves(W, n, k, A, m, lda, e, 0, s);
     if (st != hipErrorNotSupported) return st;
   }

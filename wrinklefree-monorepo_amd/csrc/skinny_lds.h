@@ -245,6 +245,19 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   const int nl = lane & 15, g = lane >> 4;
   const int half = N / 2;
   const int n0 = GLUE ? blockIdx.x * 16 * (NT / 2) : blockIdx.x * 16 * NT;
+  if constexpr (MR == 32 && !NORM) {
+    // launch over more than MR tokens: workgroups (x, y) take token rows MR y .. MR y + MR - 1 (the host
+    // leaves the greedy-argmax keys out of this form)
+    if (gridDim.y > 1) {
+      const int t0 = MR * (int)blockIdx.y;
+      A += (int64_t)t0 * lda;
+      M = min(MR, M - t0);
+      if (ep.a_scale) ep.a_scale += t0;
+      if (ep.out) ep.out = static_cast<char*>(ep.out) + (int64_t)t0 * ep.ldo * (GLUE || ep.out_dtype == WFB_F32 ? 4 : 2);
+      if (ep.acc_out) ep.acc_out += (int64_t)t0 * ep.ldo;
+      if (ep.res) ep.res = static_cast<const char*>(ep.res) + (int64_t)t0 * ep.ldr * (ep.res_dtype == WFB_F32 ? 4 : 2);
+    }
+  }
   const uint32_t row_bytes = (uint32_t)C * 16;
   const uint32_t w_end = (uint32_t)N * row_bytes, a_end = (uint32_t)((int64_t)(M - 1) * lda + (int64_t)C * 64);
   const buf_t wb = make_buf(W, w_end);
@@ -780,11 +793,14 @@ hipError_t launch(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_
                   const NormSrc& ns, hipStream_t s) {
   const int T2 = (C + 7) / 8;
   const bool staged = GLUE == 0 && e.out && !e.acc_out && !e.amax;
+  // two-tile form over more than 32 tokens: one grid row of workgroups per 32 tokens (no argmax keys)
+  const unsigned tblocks = MR == 32 && XT == kNone && m > 32 ? (unsigned)((m + 31) / 32) : 1u;
+  if (tblocks > 1 && e.amax) return hipErrorNotSupported;
 #define WFB_SL_GO(S, NT, TP)                                                                                   \
   do {                                                                                                         \
     if constexpr ((XT == kAreg ? lds_bytes_areg(S, NT, TP, (MR + 15) / 16) : lds_bytes(S, NT, TP, MR)) <= 163840 && \
                   (GLUE ? NT / 2 : NT) <= S && fits_tiles(MR, S, NT, TP)) {                    \
-      const dim3 grid(GLUE ? (n / 2 + 8 * NT - 1) / (8 * NT) : (n + 16 * NT - 1) / (16 * NT));                 \
+      const dim3 grid(GLUE ? (n / 2 + 8 * NT - 1) / (8 * NT) : (n + 16 * NT - 1) / (16 * NT), tblocks);        \
       if (GLUE == 0 && staged)                                                                                 \
         hipLaunchKernelGGL((kernel<S, NT, TP, MR, GLUE, GLUE == 0, XT>), grid, dim3(64 * S), 0, s, W, A, lda, m, n, \
                            C, e, ns);                                                                          \

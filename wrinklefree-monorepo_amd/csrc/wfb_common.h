@@ -539,7 +539,8 @@ hipError_t launch_skinny_lds_mr8(const uint8_t* W, int n, int C, const int8_t* A
                                  const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
 hipError_t launch_skinny_lds_mr16(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
                                   const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
-// 17..32 tokens as two 16-token tiles, 33..64 as four (no norm prologue; the four-tile form plain only)
+// 17..32 tokens as two 16-token tiles (33..64 as two token blocks of such workgroups, one grid row each),
+// 33..64 as four (no norm prologue; the four-tile form plain only)
 hipError_t launch_skinny_lds_mr32(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
                                   const Epilogue& e, int act, int nt_pref, const NormSrc& ns, hipStream_t s);
 hipError_t launch_skinny_lds_mr64(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda,
@@ -577,8 +578,16 @@ inline hipError_t launch_skinny_lds(const uint8_t* W, int n, int k, const int8_t
   // (rows up to 2560) or held in registers (up to 4096) -- ahead only on narrow outputs (M = 64:
   // 2560 x 2560 10.1 -> 6.4 us, 3200 x 2560 10.2 -> 6.5, 4096 x 4096 13.5 -> 12.5; 13824 x 2560 12.9 ->
   // 23.2 and 6144 x 4096 15.7 -> 23.3 keep the 32-row tile kernel)
-  if (m > 32 && m <= 64 && !ns.x && k <= 4096 && n <= 4096)
+  if (m > 32 && m <= 64 && !ns.x && k <= 4096 && n <= 4096) {
+    // rows of 4096 (the four-tile form holds their activations in registers): the two-tile form over two
+    // token blocks of one launch instead, measured on MI355X (4096 x 4096: M = 40 10.2 -> 9.4 us, M = 64
+    // 11.8 -> 10.0; on 2560-long rows it is slower, 6.2 -> 7.7 us at 2560 x 2560)
+    if (k == 4096 && !e.amax) {
+      const hipError_t st = launch_skinny_lds_mr32(W, n, C, A, m, lda, e, act, 1, ns, s);
+      if (st != hipErrorNotSupported) return st;
+    }
     return launch_skinny_lds_mr64(W, n, C, A, m, lda, e, act, 1, ns, s);
+  }
   return hipErrorNotSupported;
 }
 // Rows from which a greedy head of more than 16 tokens runs in chunks of 16 (the persistent form's rows).
