@@ -103,6 +103,9 @@ CASES = [
     # while a bf16 chunk stays 256 keys: a chunk of a split that does not own pos reaches key pos
     (4, 8, 1, 64, 32832, [200, 127, 128, 32831], torch.bfloat16, True),
     (2, 8, 1, 128, 32832, [383, 32700], torch.float32, True),                           # fp32, 128-key splits
+    # 64 sequence-heads: split length from each sequence's position (64 .. 512 keys, 1 .. 8 prefetched
+    # chunks, partial last splits)
+    (8, 32, 8, 128, 4100, [4099, 3000, 2047, 2048, 1023, 767, 768, 5], torch.bfloat16, True),
 ]
 
 
@@ -110,8 +113,9 @@ CASES = [
 @pytest.mark.parametrize("case", CASES, ids=[f"b{c[0]}_h{c[1]}x{c[2]}_d{c[3]}_L{c[4]}_{str(c[6])[6:]}" for c in CASES])
 def test_decode_attention_matches_torch(pkg, dev, case, split):
     """Both forms: key splits on separate workgroups merged by the combine kernel (split; 64-key splits,
-    doubled only while splits x query heads would pass the combine's 4096), and one workgroup per
-    (kv head, sequence) over all keys (single)."""
+    doubled while splits x query heads would pass the combine's 4096, and with the position once the
+    batch's sequence-heads would hold more than 768 splits), and one workgroup per (kv head, sequence)
+    over all keys (single)."""
     b, hq, hkv, d, max_len, pos, dtype, rope = case
     _run_case(pkg, dev, b, hq, hkv, d, max_len, pos, dtype, rope, seed=hq * 7 + max_len, split=split)
 

@@ -17,13 +17,14 @@
 // own global store).  The G = heads / kv_heads query heads of the group share every K/V load.
 //
 // Split context (flash decoding).  With few sequences and kv heads a workgroup per (kv head, sequence)
-// leaves most of the GPU idle, so the keys are cut into ceil(max_len / KS) splits of KS keys, one
-// workgroup each (grid z); split s covers keys [s*KS, min(pos+1, (s+1)*KS)) and writes its unnormalised
-// output with its running max m and sum l to a workspace, and gqa_combine_kernel merges the splits that
-// hold keys (out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), M = max_s m_s).  The split holding pos
-// appends the new key and value.  KS (64 keys unless the combine's staging would outgrow its LDS) is
-// chosen from max_len, not from pos, which lives on the device, so a captured HIP graph stays valid as
-// pos advances; splits past pos exit at once.
+// leaves most of the GPU idle, so the keys are cut into splits of KS keys, one workgroup each (grid z);
+// split s covers keys [s*KS, min(pos+1, (s+1)*KS)) and writes its unnormalised output with its running
+// max m and sum l to a workspace, and gqa_combine_kernel merges the splits that hold keys
+// (out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), M = max_s m_s).  The split holding pos appends
+// the new key and value.  The grid holds ceil(max_len / KS_MIN) splits (KS_MIN = 64 keys unless the
+// combine's staging would outgrow its LDS), fixed by max_len; KS itself is read from pos on the device
+// (KS_MIN doubled while the sequence would need more splits than its share of the GPU), so a captured
+// HIP graph stays valid as pos advances; splits past pos exit at once.
 //
 // Work mapping (4 waves).  A key is read by LPK = D/8 lanes, 8 elements each (one 16-byte load for
 // 16-bit caches), so one wave instruction covers 64/LPK whole keys and a wave's loads are contiguous.
@@ -133,12 +134,21 @@ __device__ __forceinline__ float sum_across_keys(float v) {
   return v;
 }
 
-template <int DT, int D, int G, int CH>
+// Keys per split of a sequence at position pos: ks doubled while the keys 0..pos would need more than spt
+// splits (spt = 0: ks as given).  Read from the device-side position by the split and combine kernels
+// alike, so a captured launch adapts to the position it is replayed at.
+__device__ inline int split_len(int64_t pos, int ks, int spt) {
+  if (spt > 0)
+    while ((pos + ks) / ks > spt) ks *= 2;  // ceil((pos + 1) / ks) splits
+  return ks;
+}
+
+template <int DT, int D, int G, int CH, bool PF = false>
 __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
     const void* __restrict__ q, int64_t ldq, const void* __restrict__ kn, int64_t ldk, const void* __restrict__ vn,
     int64_t ldv, const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, void* __restrict__ kc,
     void* __restrict__ vc, int64_t max_len, const int64_t* __restrict__ pos_arr, int hkv, float scale,
-    void* __restrict__ out, int64_t ldo, int ks, float* __restrict__ part) {
+    void* __restrict__ out, int64_t ldo, int ks_min, int spt, float* __restrict__ part) {
   constexpr int LPK = D / 8;           // lanes per key
   constexpr int KPW = 64 / LPK;        // keys per wave instruction
   constexpr int KW = CH / 4;           // keys per wave per chunk (CH keys per chunk)
@@ -164,8 +174,9 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
       for (int i = t; i < G * D; i += kAttnThreads) store_elem<DT>(out, obase + i, __builtin_nanf(""));
     return;  // (split mode: the combine kernel flags the rows)
   }
+  const int ks = split_len(pos, ks_min, spt);
+  if ((int64_t)split * ks > pos) return;  // no keys in this split (the combine kernel skips it)
   const int k0 = split * ks;
-  if (k0 > pos) return;  // no keys in this split (the combine kernel skips it)
   const int k1 = (int)(pos + 1 < (int64_t)k0 + ks ? pos + 1 : (int64_t)k0 + ks);
   const bool owns_new = pos < k1;  // the split holding key pos appends the new key and value
   const int64_t cbase = ((int64_t)b * hkv + kvh) * max_len * D;  // element offset of this cache slice
@@ -179,13 +190,17 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   const uint32_t kbytes = (uint32_t)((int64_t)kend * D * ESZ);
   const buf_t kb = make_buf(reinterpret_cast<const char*>(kc) + cbase * ESZ, kbytes);
   const buf_t vb = make_buf(reinterpret_cast<const char*>(vc) + cbase * ESZ, kbytes);
-  Raw8<DT> kr[R], vr[R];
-  auto load_chunk = [&](int c0) {
+  // PF: two register sets of K, the next chunk's keys requested before the current chunk is used and
+  // its values right after the current chunk's values are consumed
+  Raw8<DT> kr[PF ? 2 : 1][R], vr[R];
+  auto load_k = [&](int c0, int set) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int key = c0 + w * KW + r * KPW + kl;
-      kr[r] = load_raw8<DT>(kb, (uint32_t)(key * D + d0) * ESZ);
+      kr[set][r] = load_raw8<DT>(kb, (uint32_t)(key * D + d0) * ESZ);
     }
+  };
+  auto load_v = [&](int c0) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int key = c0 + w * KW + r * KPW + kl;
@@ -215,7 +230,8 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   const float kx1 = load_elem<DT>(kn, ko + tk), kx2 = load_elem<DT>(kn, ko + tk + HD);
   const float kcs = cs ? cs[tk] : 1.0f, ksn = cs ? sn[tk] : 0.0f;
   const float vx = load_elem<DT>(vn, (int64_t)b * ldv + (int64_t)kvh * D + tv);
-  load_chunk(k0);
+  load_k(k0, 0);
+  load_v(k0);
 
 #pragma unroll
   for (int it = 0; it < NQ; ++it) {
@@ -252,11 +268,22 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   }
   __syncthreads();
 
-  float qf[G][8];
+  // the lane's 8 query elements per head; for 16-bit caches as bf16 pairs (the rotated query was rounded
+  // to the storage type, so the pairs hold it exactly) to leave registers for the prefetched keys
+  constexpr bool QP = DT != WFB_F32;
+  float qf[QP ? 1 : G][8];
+  uint32_t qp[QP ? G : 1][4];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qf[g][e] = qs[g][d0 + e];
+    for (int e = 0; e < 8; e += 2) {
+      if constexpr (QP)
+        qp[g][e / 2] = (__float_as_uint(qs[g][d0 + e]) >> 16) | (__float_as_uint(qs[g][d0 + e + 1]) & 0xffff0000u);
+      else {
+        qf[g][e] = qs[g][d0 + e];
+        qf[g][e + 1] = qs[g][d0 + e + 1];
+      }
+    }
   float acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -269,14 +296,20 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
     l_run[h] = 0.0f;
   }
 
-  for (int c0 = k0; c0 < k1; c0 += CH) {
-    if (c0 != k0) load_chunk(c0);
-    // scores
+  // one chunk of CH keys from register set `set`: scores, online softmax, weighted sum of values
+  auto chunk = [&](int c0, int set) {
+    // scores (the empty asm keeps the query pairs packed across chunks: without it the compiler
+    // widens them once, ahead of the loop, into twice the registers)
+    if constexpr (QP)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(qp[g][i]));
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int key = c0 + w * KW + r * KPW + kl;
       float kf[8];
-      widen8<DT>(kr[r], kf);
+      widen8<DT>(kr[set][r], kf);
       // only the split that owns pos wrote knew / vnew; a chunk longer than the split (CH > ks) can
       // reach key pos in a split that does not own it, where the key is masked and must stay finite
       if (owns_new && key == pos) {
@@ -287,7 +320,14 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
       for (int g = 0; g < G; ++g) {
         float s = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s += qf[g][e] * kf[e];
+        for (int e = 0; e < 8; ++e) {
+          float qe;
+          if constexpr (QP)
+            qe = __uint_as_float(e % 2 ? qp[g][e / 2] & 0xffff0000u : qp[g][e / 2] << 16);
+          else
+            qe = qf[g][e];
+          s += qe * kf[e];
+        }
         s = group_sum_f32<LPK>(s);
         if (lane % LPK == 0) sc[g][key - c0] = key < k1 ? s * scale : -__builtin_inff();
       }
@@ -344,6 +384,27 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
       }
     }
     __syncthreads();  // sc and alpha_s are rewritten by the next chunk
+  };
+  if constexpr (PF) {
+    // software pipelined: chunk c + 1's keys are in flight while chunk c is used, its values from the
+    // end of chunk c's weighted sum (loads complete in issue order, so each use waits only for its own)
+    for (int c0 = k0; c0 < k1; c0 += 2 * CH) {
+      if (c0 + CH < k1) load_k(c0 + CH, 1);
+      chunk(c0, 0);
+      if (c0 + CH >= k1) break;
+      load_v(c0 + CH);
+      if (c0 + 2 * CH < k1) load_k(c0 + 2 * CH, 0);
+      chunk(c0 + CH, 1);
+      if (c0 + 2 * CH < k1) load_v(c0 + 2 * CH);
+    }
+  } else {
+    for (int c0 = k0; c0 < k1; c0 += CH) {
+      if (c0 != k0) {
+        load_k(c0, 0);
+        load_v(c0);
+      }
+      chunk(c0, 0);
+    }
   }
 
   if (lane == 0) {
@@ -381,12 +442,13 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   }
 }
 
-// Merges the splits of one (kv head, sequence) that hold keys: splits 0 .. pos / KS.
+// Merges the splits of one (kv head, sequence) that hold keys: splits 0 .. pos / KS, KS the sequence's
+// split length (split_len).
 template <int DT, int D, int G>
 __global__ __launch_bounds__(kAttnThreads) void gqa_combine_kernel(const float* __restrict__ part,
                                                                    const int64_t* __restrict__ pos_arr,
-                                                                   int64_t max_len, int hkv, int ks, int nsplit,
-                                                                   void* __restrict__ out, int64_t ldo) {
+                                                                   int64_t max_len, int hkv, int ks_min, int spt,
+                                                                   int nsplit, void* __restrict__ out, int64_t ldo) {
   // LDS: the running max m and sum l of every (split, head), then the per-head denominators.  The
   // partials are read with independent loads (m and l once per workgroup, the accumulators unrolled
   // over the splits) rather than as a chain of dependent loops per output element.
@@ -398,7 +460,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_combine_kernel(const float* 
     for (int i = t; i < G * D; i += kAttnThreads) store_elem<DT>(out, obase + i, __builtin_nanf(""));
     return;
   }
-  const int ns = (int)(pos / ks) + 1;
+  const int ns = (int)(pos / split_len(pos, ks_min, spt)) + 1;  // <= nsplit
   const float* pp = part + (((int64_t)b * hkv + kvh) * nsplit) * G * (D + 2);
   float* sm = cw;                // [ns * G]: m, then the split weights e^(m_s - M)
   float* sl = cw + nsplit * G;   // [ns * G]: l
@@ -457,39 +519,65 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_combine_kernel(const float* 
   }
 }
 
+// Split attention and the combine.  spt = 0: splits of ks_min keys, ceil(max_len / ks_min) of them per
+// (kv head, sequence).  spt > 0: a sequence at position pos uses ceil((pos + 1) / KS) <= spt splits of
+// KS = split_len(pos, ks_min, spt) keys, so the grid holds min(spt, ceil(max_len / ks_min)) splits and no
+// workgroups that would only find their split empty; the split kernel walks its keys in chunks of 64 with
+// the next chunk's K and V loads in flight.
+template <int DT, int D, int G>
+hipError_t launch_attn_split(const void* q, int64_t ldq, const void* kn, int64_t ldk, const void* vn, int64_t ldv,
+                             const float* rc, const float* rs, void* kc, void* vc, int64_t max_len, const int64_t* pos,
+                             int b, int hkv, float scale, void* out, int64_t ldo, float* part, int64_t ks_min, int spt,
+                             hipStream_t s) {
+  const int64_t nsplit_max = (max_len + ks_min - 1) / ks_min;
+  const int64_t nsplit = spt > 0 && spt < nsplit_max ? spt : nsplit_max;
+  if (spt > 0)
+    hipLaunchKernelGGL((gqa_decode_kernel<DT, D, G, 64, true>), dim3(hkv, b, nsplit), dim3(kAttnThreads), 0, s, q,
+                       ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, hkv, scale, out, ldo, (int)ks_min, spt, part);
+  else
+    hipLaunchKernelGGL((gqa_decode_kernel<DT, D, G, 64>), dim3(hkv, b, nsplit), dim3(kAttnThreads), 0, s, q, ldq, kn,
+                       ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, hkv, scale, out, ldo, (int)ks_min, 0, part);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t lds = (size_t)(2 * nsplit * G + G) * sizeof(float);  // nsplit * G <= kAttnMaxSplitHeads
+  hipLaunchKernelGGL((gqa_combine_kernel<DT, D, G>), dim3(hkv, b), dim3(kAttnThreads), lds, s, part, pos, max_len,
+                     hkv, (int)ks_min, spt, (int)nsplit, out, ldo);
+  return hipGetLastError();
+}
+
+// Target of live workgroups for the split kernel: the split length grows with the position until a
+// sequence's keys take at most ceil(kAttnLiveSplits / (b * hkv)) splits.
+constexpr int kAttnLiveSplits = 768;
+
 template <int DT, int D, int G>
 hipError_t launch_attn_g(const void* q, int64_t ldq, const void* kn, int64_t ldk, const void* vn, int64_t ldv,
                          const float* rc, const float* rs, void* kc, void* vc, int64_t max_len, const int64_t* pos,
                          int b, int hkv, float scale, void* out, int64_t ldo, float* part, hipStream_t s) {
-  // keys per split: 64 (doubled only while the combine's LDS staging of the split weights would pass
-  // 32 KB); one split (no workspace pass) when a single split covers max_len or no workspace is given.
-  // The choice depends on max_len, not on the device-side positions, so a captured graph stays valid:
-  // splits past a sequence's position exit at once and the combine reads only those holding keys.
-  // Measured at the Llama-3-8B batch-8 shape (split + combine, eager): 64-key splits are the fastest
-  // or within 2% at every position of a 4096-slot cache (12.6 us at position 300, 20.7 at 1000,
-  // 60.1 at 4000), where a grid-size target of 512 workgroups (512-key splits) gave 26.8 / 28.8 / 59.1.
+  // Split length: at least ks_min = 64 keys (doubled only while the combine's LDS staging of the split
+  // weights would pass 32 KB).  When the batch's sequences x kv heads would otherwise hold more than
+  // kAttnLiveSplits splits at max_len, the length grows with the position instead, so the live splits
+  // stay near kAttnLiveSplits: short contexts get many small splits to fill the GPU, long ones fewer and
+  // longer splits whose chunk loads overlap.  The grid and workspace depend on max_len only and the
+  // kernels read the positions on the device, so a captured graph stays valid at every position.
+  // Measured at the Llama-3-8B batch-8 shape (64 sequence-heads, 4096 slots, split + combine, eager):
+  // 14.5 / 15.7 / 24.7 / 31.6 / 37.5 us at positions 700 / 1000 / 2047 / 3000 / 4095 against 14.3 /
+  // 17.8 / 29.0 / 42.3 / 49.3 with fixed 64-key splits; targets of 384 / 512 / 1024 live splits were
+  // slower somewhere in that range.  One split (no workspace pass) when a single split covers max_len
+  // or no workspace is given.
   const int64_t ks = split_keys(max_len, G);
   const int64_t nsplit = (max_len + ks - 1) / ks;
   if (nsplit == 1 || part == nullptr) {
     constexpr int CH = DT == WFB_F32 ? 128 : 256;
     hipLaunchKernelGGL((gqa_decode_kernel<DT, D, G, CH>), dim3(hkv, b, 1), dim3(kAttnThreads), 0, s, q, ldq, kn, ldk,
-                       vn, ldv, rc, rs, kc, vc, max_len, pos, hkv, scale, out, ldo, (int)(max_len + 1),
+                       vn, ldv, rc, rs, kc, vc, max_len, pos, hkv, scale, out, ldo, (int)(max_len + 1), 0,
                        (float*)nullptr);
     return hipGetLastError();
   }
-  if (ks == 64)
-    hipLaunchKernelGGL((gqa_decode_kernel<DT, D, G, 64>), dim3(hkv, b, nsplit), dim3(kAttnThreads), 0, s, q, ldq, kn,
-                       ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, hkv, scale, out, ldo, (int)ks, part);
-  else
-    hipLaunchKernelGGL((gqa_decode_kernel<DT, D, G, DT == WFB_F32 ? 128 : 256>), dim3(hkv, b, nsplit),
-                       dim3(kAttnThreads), 0, s, q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, hkv, scale, out,
-                       ldo, (int)ks, part);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const size_t lds = (size_t)(2 * nsplit * G + G) * sizeof(float);  // nsplit * G <= kAttnMaxSplitHeads
-  hipLaunchKernelGGL((gqa_combine_kernel<DT, D, G>), dim3(hkv, b), dim3(kAttnThreads), lds, s, part, pos, max_len,
-                     hkv, (int)ks, (int)nsplit, out, ldo);
-  return hipGetLastError();
+  const int64_t seq_heads = (int64_t)b * hkv;
+  const int64_t spt = (kAttnLiveSplits + seq_heads - 1) / seq_heads;
+  const int dyn = spt < nsplit ? (int)spt : 0;
+  return launch_attn_split<DT, D, G>(q, ldq, kn, ldk, vn, ldv, rc, rs, kc, vc, max_len, pos, b, hkv, scale, out, ldo,
+                                     part, ks, dyn, s);
 }
 
 template <int DT, int D>
