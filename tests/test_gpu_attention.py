@@ -106,6 +106,8 @@ CASES = [
     # 64 sequence-heads: split length from each sequence's position (64 .. 512 keys, 1 .. 8 prefetched
     # chunks, partial last splits)
     (8, 32, 8, 128, 4100, [4099, 3000, 2047, 2048, 1023, 767, 768, 5], torch.bfloat16, True),
+    # 776 sequence-heads (more than the 768 live-split target): one split per sequence, all its keys
+    (97, 16, 8, 64, 200, [(37 * i + 11) % 200 for i in range(97)], torch.bfloat16, True),
 ]
 
 
