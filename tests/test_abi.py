@@ -307,3 +307,21 @@ def test_linear_glu_argument_errors(pkg):
     assert st(lda=200) == -1 and "row stride" in pkg._lib.last_error()
     assert st(ldo=32) == -1 and "N/2" in pkg._lib.last_error()
     assert st(m=0) == 0
+
+
+def test_fused_op_weight_cache(pkg):
+    """The fused reference ops' weight concatenations (host logic, CPU tensors): a single weight is used as it
+    is (no copy), a set is concatenated once and reused until a weight changes in place, and the cache holds
+    the q|k|v and gate|up sets of a 128-layer model."""
+    ops = pkg.ops
+    w = torch.arange(64, dtype=torch.uint8).reshape(8, 8)
+    same, sc = ops._concat_weights((w,), (0.5,))
+    assert same is w and sc.tolist() == [0.5]
+    a, b = torch.zeros(8, 8, dtype=torch.uint8), torch.ones(16, 8, dtype=torch.uint8)
+    cat1, s1 = ops._concat_weights((a, b), (0.25, 2.0))
+    cat2, _ = ops._concat_weights((a, b), (0.25, 2.0))
+    assert cat2 is cat1 and cat1.shape == (24, 8) and s1.tolist() == [0.25, 2.0]
+    b.fill_(3)  # in place: new version counter
+    cat3, _ = ops._concat_weights((a, b), (0.25, 2.0))
+    assert cat3 is not cat1 and int(cat3[8:].min()) == 3
+    assert ops._CONCAT_CACHE_MAX >= 2 * 128

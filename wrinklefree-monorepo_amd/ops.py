@@ -901,12 +901,30 @@ def _fused_input(name: str, x: torch.Tensor, packed: torch.Tensor) -> torch.Tens
 
 # Row concatenations of the packed weights the fused ops launch over, with their scales on the device: built
 # once per set of weight tensors and reused while those tensors are alive and unmodified (identity, storage
-# and version counter all match).  A model that keeps its projections concatenated (model.py) never needs it.
+# and version counter all match); room for the q|k|v and gate|up sets of a 128-layer model.  A single weight
+# is used as it is (only its scale is cached).  A model that keeps its projections concatenated (model.py)
+# never needs it.
 _CONCAT_CACHE: "collections.OrderedDict" = collections.OrderedDict()
-_CONCAT_CACHE_MAX = 64
+_CONCAT_CACHE_MAX = 256
+_SCALE_CACHE: "collections.OrderedDict" = collections.OrderedDict()
+
+
+def _scale_tensor(scales: Sequence[float], device: torch.device) -> torch.Tensor:
+    key = (tuple(float(x) for x in scales), str(device))
+    sc = _SCALE_CACHE.get(key)
+    if sc is None:
+        sc = torch.tensor(list(key[0]), dtype=torch.float32, device=device)
+        _SCALE_CACHE[key] = sc
+        while len(_SCALE_CACHE) > _CONCAT_CACHE_MAX:
+            _SCALE_CACHE.popitem(last=False)
+    else:
+        _SCALE_CACHE.move_to_end(key)
+    return sc
 
 
 def _concat_weights(ws: Sequence[torch.Tensor], scales: Sequence[float]) -> Tuple[torch.Tensor, torch.Tensor]:
+    if len(ws) == 1:
+        return ws[0].contiguous(), _scale_tensor(scales, ws[0].device)
     key = tuple((id(w), w.data_ptr(), w._version, tuple(w.shape)) for w in ws) + (tuple(float(x) for x in scales),)
     hit = _CONCAT_CACHE.get(key)
     if hit is not None and all(r() is w for r, w in zip(hit[0], ws)):
@@ -967,8 +985,8 @@ def bitnet_mlp_forward(input: torch.Tensor, gate_weight: torch.Tensor, up_weight
     if fused:
         cat, sc = _concat_weights((gate_weight, up_weight), (gate_scale, up_scale))
         hid = bitnet_linear_glu(cat, sc, q8, "relu2", a_scale=a_s, mid_dtype=torch.float32)
-        _, dsc = _concat_weights((down_weight,), (down_scale,))
-        return rmsnorm_linear(hid, norm_w, down_weight, dsc, eps=float(eps), out_dtype=torch.float32).reshape(-1)
+        dw, dsc = _concat_weights((down_weight,), (down_scale,))
+        return rmsnorm_linear(hid, norm_w, dw, dsc, eps=float(eps), out_dtype=torch.float32).reshape(-1)
     gate = bitnet_linear(gate_weight, q8, float(gate_scale), a_scale=a_s, out_dtype=torch.float32)
     up = bitnet_linear(up_weight, q8, float(up_scale), a_scale=a_s, out_dtype=torch.float32)
     h8, h_s = glu_rmsnorm_quantize_i8(gate, up, "relu2", norm_w, eps=float(eps))
