@@ -1,5 +1,5 @@
-"""Host-side AddressSanitizer run of the C ABI (the sanitizer pass SURVEY-planned for the host code; the
-reference builds -O3 -DNDEBUG with none, SGB/sgl-kernel/csrc/bitnet/CMakeLists.txt:45).
+"""Host-side AddressSanitizer run of the C ABI (a sanitizer pass over the host code; the reference builds
+-O3 -DNDEBUG with none, SGB/sgl-kernel/csrc/bitnet/CMakeLists.txt:45).
 
 tests/asan/abi_driver.cpp, linked against the library whose host-only sources (entry-point validation
 and dispatch, the native engine) are compiled with ASan (wrinklefree-monorepo_amd/_build.py build_asan,
