@@ -357,8 +357,8 @@ __device__ __forceinline__ void lds_load16(buf_t r, void* lds_base, uint32_t vof
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_base, 16, voff, 0, 0, 0);
 }
 
-template <int TM, int KB, int OCC, int EPI, int TN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_i2s_tile_kernel(
+template <int TM, int KB, int OCC, int EPI, int TN, int KSPL = 1>
+__global__ __launch_bounds__(256 * KSPL) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_i2s_tile_kernel(
     const uint8_t* __restrict__ W, const int8_t* __restrict__ A, int64_t lda, int M, int N, int K, int tiles_m,
     int tiles_n, int ntiles, bool vec_out, Epilogue ep) {
   // TN 32-column MFMA tiles per wave: 256-column tiles, or 128 where 256 leave most of the chip idle
@@ -373,12 +373,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
   constexpr int X = 4 * KB;                        // (block, field) MFMA steps per stage
   constexpr int LPR = 256 / BM, SCH = CH / LPR;    // sum(a): lanes per row, chunks per lane
   static_assert(AI >= 1 && BI >= 1 && ASZ >= 8192 && BSZ >= 8192 && SCH >= 1 && SCH <= X && LPR <= 8, "tile shape");
-  __shared__ __attribute__((aligned(16))) int8_t lds_a0[ASZ];
-  __shared__ __attribute__((aligned(16))) int8_t lds_a1[ASZ];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_b0[BSZ];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_b1[BSZ];
-  __shared__ int rowsum[BM];
-  const int tid = threadIdx.x, l = tid & 63, wn = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // KSPL > 1: KSPL groups of four waves split the stages of K (group kh takes stages kh*KSH ..), each with
+  // its own operand buffers and sum(a); their integer tile partials are added in LDS at the end (exact, in
+  // any order) and group 0 runs the epilogue -- more waves on one tile where few tiles leave CUs idle.
+  static_assert(KSPL == 1 || KSPL == 2, "one or two K groups");
+  __shared__ __attribute__((aligned(16))) int8_t lds_a0s[KSPL][ASZ];
+  __shared__ __attribute__((aligned(16))) int8_t lds_a1s[KSPL][ASZ];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b0s[KSPL][BSZ];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b1s[KSPL][BSZ];
+  __shared__ int rowsum_s[KSPL][BM];
+  const int tid = threadIdx.x, l = tid & 63, wq = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = KSPL > 1 ? wq >> 2 : 0, wn = KSPL > 1 ? wq & 3 : wq;  // K group, wave within it
+  int8_t* const lds_a0 = lds_a0s[kh];
+  int8_t* const lds_a1 = lds_a1s[kh];
+  uint8_t* const lds_b0 = lds_b0s[kh];
+  uint8_t* const lds_b1 = lds_b1s[kh];
+  int* const rowsum = rowsum_s[kh];
   const int i = l & 31, g = l >> 5;
 
   const int per = gridDim.x / 8;  // the grid is a multiple of 8
@@ -507,17 +517,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
     }
   };
 
-  issue(0, lds_a0, lds_b0);
-  for (int kb = 0; kb < KS; kb += 2) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of stage kb are in LDS
-    __syncthreads();                      // everyone's; and everyone is done with stage kb - 1
-    if (kb + 1 < KS) issue(kb + 1, lds_a1, lds_b1);
-    compute(lds_a0, lds_b0);
-    if (kb + 1 < KS) {
+  if constexpr (KSPL == 1) {
+    issue(0, lds_a0, lds_b0);
+    for (int kb = 0; kb < KS; kb += 2) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of stage kb are in LDS
+      __syncthreads();                      // everyone's; and everyone is done with stage kb - 1
+      if (kb + 1 < KS) issue(kb + 1, lds_a1, lds_b1);
+      compute(lds_a0, lds_b0);
+      if (kb + 1 < KS) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        if (kb + 2 < KS) issue(kb + 2, lds_a0, lds_b0);
+        compute(lds_a1, lds_b1);
+      }
+    }
+  } else {
+    // group kh: stages k0s .. k0s + ksn - 1; both groups step through KSH stages so that every wave of the
+    // workgroup meets the same barriers (the shorter group skips its missing last stage's loads and work)
+    const int KSH = (KS + KSPL - 1) / KSPL, k0s = kh * KSH, ksn = min(KS - k0s, KSH);
+    if (ksn > 0) issue(k0s, lds_a0, lds_b0);
+    for (int kb = 0; kb < KSH; kb += 2) {
       __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
-      if (kb + 2 < KS) issue(kb + 2, lds_a0, lds_b0);
-      compute(lds_a1, lds_b1);
+      if (kb + 1 < ksn) issue(k0s + kb + 1, lds_a1, lds_b1);
+      if (kb < ksn) compute(lds_a0, lds_b0);
+      if (kb + 1 < KSH) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        if (kb + 2 < ksn) issue(k0s + kb + 2, lds_a0, lds_b0);
+        if (kb + 1 < ksn) compute(lds_a1, lds_b1);
+      }
     }
   }
 
@@ -527,6 +556,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
   if constexpr (LPR >= 8) ssum += __shfl_xor(ssum, 4);
   if ((l % LPR) == 0) rowsum[srow] = ssum;
   __syncthreads();  // also: every wave is done reading the operand buffers
+  if constexpr (KSPL > 1) {
+    // group 1's partial tiles into group 0's accumulators, wave wn through group 1's buffer number wn (free
+    // now); sum(a) of a row is the sum of the two groups' row sums (rsum)
+    static_assert(64 * TM * TN * 16 * 4 <= (ASZ < BSZ ? ASZ : BSZ), "a wave's partial tiles fit one buffer");
+    int* xr = reinterpret_cast<int*>(wn == 0 ? (void*)lds_a0s[1] : wn == 1 ? (void*)lds_a1s[1]
+                                     : wn == 2 ? (void*)lds_b0s[1] : (void*)lds_b1s[1]);
+    if (kh == 1) {
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) xr[((tn * TM + tm) * 16 + q) * 64 + l] = acc[tn][tm][q];
+    }
+    __syncthreads();
+    if (kh == 1) return;  // (no barrier follows)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[tn][tm][q] += xr[((tn * TM + tm) * 16 + q) * 64 + l];
+  }
+  auto rsum = [&](int r) { return KSPL > 1 ? rowsum_s[0][r] + rowsum_s[KSPL - 1][r] : rowsum_s[0][r]; };
 
   // weight scale per 4-column output group (segments are multiples of 8 rows, so a group has one)
   float wsg[TN][4];
@@ -544,7 +597,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
                 : wn == 2 ? lds_b0 : lds_b1;
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
-      const int rs = rowsum[tm * 32 + i];
+      const int rs = rsum(tm * 32 + i);
       const float as = epi_ascale(ep, min(m0 + tm * 32 + i, M - 1));
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn)
@@ -587,7 +640,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
               : wn == 2 ? reinterpret_cast<float*>(lds_b0) : reinterpret_cast<float*>(lds_b1);
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
-      const int rs = rowsum[tm * 32 + i];
+      const int rs = rsum(tm * 32 + i);
       const float as = epi_ascale(ep, min(m0 + tm * 32 + i, M - 1));
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn)
@@ -654,7 +707,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
       const int m = m0 + tm * 32 + i;
       if (m >= M) continue;
       const float as = epi_ascale(ep, m);
-      const int rs = rowsum[tm * 32 + i];
+      const int rs = rsum(tm * 32 + i);
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
@@ -669,7 +722,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
   }
 }
 
-template <int TM, int KB, int OCC, int TN = 2>
+template <int TM, int KB, int OCC, int TN = 2, int KSPL = 1>
 hipError_t launch_tile(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, const Epilogue& e,
                        hipStream_t s) {
   const int tiles_n = (n + 128 * TN - 1) / (128 * TN), tiles_m = (m + 32 * TM - 1) / (32 * TM);
@@ -683,13 +736,13 @@ hipError_t launch_tile(const uint8_t* W, int n, int k, const int8_t* A, int m, i
   const bool staged = e.out && !e.bias && !e.acc_out && (e.ldo * osz) % 16 == 0 && (uintptr_t)e.out % 16 == 0 &&
                       (!e.res || ((e.ldr * rsz) % 16 == 0 && (uintptr_t)e.res % 16 == 0));
   if (bf16_only)
-    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 1, TN>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 1, TN, KSPL>), dim3(grid), dim3(256 * KSPL), 0, s, W, A, lda, m, n, k,
                        tiles_m, tiles_n, nwg, vec_out, e);
   else if (staged)
-    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 2, TN>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 2, TN, KSPL>), dim3(grid), dim3(256 * KSPL), 0, s, W, A, lda, m, n, k,
                        tiles_m, tiles_n, nwg, vec_out, e);
   else
-    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 0, TN>), dim3(grid), dim3(256), 0, s, W, A, lda, m, n, k,
+    hipLaunchKernelGGL((gemm_i2s_tile_kernel<TM, KB, OCC, 0, TN, KSPL>), dim3(grid), dim3(256 * KSPL), 0, s, W, A, lda, m, n, k,
                        tiles_m, tiles_n, nwg, vec_out, e);
   return hipGetLastError();
 }
@@ -794,7 +847,10 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   const int mt = (m + 15) / 16;
   // 32-row tiles of 256 columns that leave CUs idle (fewer than 256): 128-column tiles, four waves of 32
   // columns, measured on MI355X (13824 x 2560 at M = 64: 12.9 -> 9.6 us; M = 128: 2560 x 2560 10.3 ->
-  // 7.7, 4096 x 14336 45.2 -> 35.5; 2560 x 6912 at M = 512 24.3 -> 22.3)
+  // 7.7, 4096 x 14336 45.2 -> 35.5; 2560 x 6912 at M = 512 24.3 -> 22.3), and two groups of four waves
+  // splitting K on each tile, two workgroups per CU (interleaved medians: 13824 x 2560 at M = 64 8.1 ->
+  // 7.2 us, 6144 x 4096 at M = 64 10.1 -> 8.5, 2560 x 6912 at M = 256 15.7 -> 12.3, at M = 512 20.1 ->
+  // 18.9; 28672 x 4096 at M = 64 unchanged)
   const bool few_tiles = (int64_t)((n + 255) / 256) * ((m + 31) / 32) < 256;
   const bool small_offsets = (int64_t)n * (k / 4) <= INT32_MAX && (int64_t)(m - 1) * lda + k <= INT32_MAX;
   // 17 <= M <= 64 on wide outputs: the 32-row tile kernel (one or two tile rows, its time nearly flat
@@ -821,7 +877,7 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
     if (st != hipErrorNotSupported) return st;
   }
   if (m > 16 && m <= 64 && small_offsets && (int64_t)n * mt >= 18432 && k <= 8192)
-    return few_tiles ? launch_tile<1, 2, 3, 1>(W, n, k, A, m, lda, e, s) : launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
+    return few_tiles ? launch_tile<1, 2, 4, 1, 2>(W, n, k, A, m, lda, e, s) : launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
   if (m <= 64 && small_offsets && (m <= 8 || (int64_t)n * (mt == 3 ? 4 : mt) <= 32768)) {
     if (m <= 16) return launch_skinny<1>(W, n, C, A, m, lda, e, s);
     if (m <= 32) return launch_skinny<2>(W, n, C, A, m, lda, e, s);
@@ -846,7 +902,7 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
     if (fill(t64n, 768) > fill(t64, 512) + 0.1) return launch_tile<2, 2, 3, 1>(W, n, k, A, m, lda, e, s);
     return launch_tile<2, 2, 2>(W, n, k, A, m, lda, e, s);
   }
-  return few_tiles ? launch_tile<1, 2, 3, 1>(W, n, k, A, m, lda, e, s) : launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
+  return few_tiles ? launch_tile<1, 2, 4, 1, 2>(W, n, k, A, m, lda, e, s) : launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
 }
 
 }  // namespace wfb
