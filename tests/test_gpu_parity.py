@@ -256,13 +256,14 @@ def test_batched_long_rows_register_activations(pkg, dev, m, n, k):
                                    (33, 4096, 4096), (64, 4096, 4096), (64, 4112, 4096), (48, 2560, 4224),
                                    (40, 1000, 2560), (32, 4096, 7168), (17, 4112, 6912), (24, 2560, 7296),
                                    (33, 2560, 6912), (64, 4096, 7168), (64, 4112, 6912), (48, 2560, 6912),
-                                   (49, 2560, 6912), (37, 4096, 4096), (49, 4000, 4096), (64, 2560, 4096)])
+                                   (49, 2560, 6912), (37, 4096, 4096), (49, 4000, 4096), (64, 2560, 4096),
+                                   (33, 4096, 14336), (64, 4104, 14336), (48, 4096, 16384), (64, 4088, 4096)])
 def test_batched_kernel_choice_boundaries(pkg, dev, m, n, k):
     # 3 <= M <= 64: the LDS-staged kernel up to 16 tokens, and with two token tiles for 17..32 tokens on
     # rows up to 2560 (outputs up to 32768 rows) or 7168 (outputs up to 4096 rows), with four for 33..64
     # tokens on rows up to 4096 and outputs up to 4096 rows (two token blocks of two-tile workgroups for rows
-    # of 4096, and for rows up to 7168 from 49 tokens; two launches of two tiles below that);
-    # else the 32-row tile
+    # of 4096, and for rows up to 7168 from 49 tokens; two launches of two tiles below that); 33..64 tokens
+    # on rows and outputs of 4096 or more: the 32-row tile kernel with its K split; else the 32-row tile
     # kernel for M > 16 when N * ceil(M/16) >= 18432 and K <= 8192, else the split-K skinny kernel while
     # N * ceil(M/16) <= 32768 (always for M <= 8), else the whole-K wave-per-rows kernel; these shapes
     # sit on either side of those boundaries

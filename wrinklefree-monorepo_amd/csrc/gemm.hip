@@ -858,6 +858,12 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   // Llama-3-8B shapes: faster from N * ceil(M/16) >= 18432 with K <= 8192 (M = 64: 28672 x 4096
   // 67.1 -> 15.0 us, 13824 x 2560 26.1 -> 10.0, 6144 x 4096 25.8 -> 13.3; M = 24: 13824 x 2560 10.5 -> 9.8),
   // the split-K kernels below that and for longer rows (M = 64, 4096 x 14336: 33.5 vs 37.2 us).
+  // 33..64 tokens on rows of 4096 or more and 4096 or more outputs: the tile kernel with its K split
+  // (interleaved medians on MI355X: 4096 x 4096 at M = 40..64 9.5-10.4 -> 8.4 us, 4096 x 14336 24.7-31.5
+  // -> 21.5; 6144 x 4096 and 28672 x 4096 within 1%; at 17..32 tokens, and on 2560-long or 2560-row
+  // shapes, the kernels below stay ahead)
+  if (m > 32 && m <= 64 && small_offsets && !e.amax && k >= 4096 && n >= 4096)
+    return launch_tile<1, 2, 4, 1, 2>(W, n, k, A, m, lda, e, s);
   // operands staged in LDS (skinny_lds.h) where its LDS holds them (17..32 tokens: where measured faster)
   if (m <= 64 && small_offsets) {
     const hipError_t st = launch_skinny_lds(W, n, k, A, m, lda, e, 0, s);
