@@ -52,6 +52,16 @@ def _check_linear(pkg, dev, packed, a, w_scale, a_scale, kernel="auto", bias=Non
     if check_fp32:
         y32 = pkg.bitnet_linear(pw, pa, float(w_scale), a_scale=ps, bias=pb, out_dtype=torch.float32, kernel=kernel)
         assert np.array_equal(y32.cpu().numpy(), y_ref)
+    if bias is None:
+        # the production forms: bf16 out alone (whole-line bf16 epilogue), and with a bf16 residual added
+        y1 = pkg.bitnet_linear(pw, pa, float(w_scale), a_scale=ps, kernel=kernel)
+        assert np.array_equal(y1.view(torch.int16).cpu().numpy().view(np.uint16), orc.f32_to_bf16_bits(y_ref)), \
+            "bf16-only output bits differ"
+        m = a.shape[0]
+        res = torch.linspace(-2.0, 2.0, m * n, dtype=torch.float32).reshape(m, n).to(torch.bfloat16)
+        want = torch.from_numpy(y_ref.astype(np.float32) + res.float().numpy()).to(torch.bfloat16)
+        got = pkg.bitnet_linear_residual(pw, pa, float(w_scale), res.to(dev), a_scale=ps)
+        assert torch.equal(got.cpu(), want), "residual output differs"
 
 
 # ---- a1: pack -------------------------------------------------------------------------------------
