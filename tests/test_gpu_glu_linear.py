@@ -12,17 +12,23 @@ pytestmark = pytest.mark.gpu
 
 CASES = [
     # m, half, k, mid dtype
-    (8, 14336, 4096, torch.bfloat16),   # Llama-3-8B gate|up (4 row tiles x 4 waves)
+    (8, 14336, 4096, torch.bfloat16),   # Llama-3-8B gate|up (LDS-staged, 4 row tiles x 4 waves)
     (1, 6912, 2560, torch.bfloat16),    # BitNet-2B
     (3, 1536, 640, torch.float32),      # SmolLM2 (fp32 model), K padded
+    (16, 14336, 4096, torch.bfloat16),  # LDS-staged at 16 tokens on long rows
     (17, 2048, 1024, torch.bfloat16),   # two token tiles
     (32, 6912, 2560, torch.bfloat16),   # BitNet-2B gate|up at 32 tokens (LDS-staged, two token tiles)
     (24, 2048, 4096, torch.float32),    # 4096-long rows, one round of workgroups
-    (64, 4096, 512, torch.float32),     # two launches of two token tiles
+    # K-split tile kernel with the gated epilogue (32 tokens x 64 outputs per tile):
+    (24, 14336, 4096, torch.bfloat16),  # 17..32 tokens on long rows of a wide gate|up
+    (17, 4096, 4096, torch.float32),    # (its smallest N and K)
+    (64, 4096, 512, torch.float32),     # two full token tiles
     (40, 6912, 2560, torch.bfloat16),   # BitNet-2B gate|up at 40 tokens (32 + 8)
-    (37, 14336, 4096, torch.bfloat16),  # Llama-3-8B gate|up at 37 tokens (chunks of 16, 16, 5)
-    (33, 14336, 4096, torch.bfloat16),  # chunks of 16, 16 and a 1-token tail
-    (49, 14336, 4096, torch.bfloat16),  # chunks of 16, 16, 16 and a 1-token tail
+    (37, 14336, 4096, torch.bfloat16),  # Llama-3-8B gate|up at 37 tokens
+    (33, 14336, 4096, torch.bfloat16),  # a 1-token second tile row
+    (49, 14336, 4096, torch.bfloat16),
+    (45, 1056, 1152, torch.float32),    # half not a multiple of 64 (a half-full last tile), 9 K blocks
+    (64, 96, 128, torch.bfloat16),      # one K block, two tiles per row
 ]
 
 

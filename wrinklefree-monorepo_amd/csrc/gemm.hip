@@ -357,7 +357,7 @@ __device__ __forceinline__ void lds_load16(buf_t r, void* lds_base, uint32_t vof
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_base, 16, voff, 0, 0, 0);
 }
 
-template <int TM, int KB, int OCC, int EPI, int TN, int KSPL = 1>
+template <int TM, int KB, int OCC, int EPI, int TN, int KSPL = 1, int GL = 0>
 __global__ __launch_bounds__(256 * KSPL) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_i2s_tile_kernel(
     const uint8_t* __restrict__ W, const int8_t* __restrict__ A, int64_t lda, int M, int N, int K, int tiles_m,
     int tiles_n, int ntiles, bool vec_out, Epilogue ep) {
@@ -377,6 +377,10 @@ __global__ __launch_bounds__(256 * KSPL) __attribute__((amdgpu_waves_per_eu(OCC,
   // its own operand buffers and sum(a); their integer tile partials are added in LDS at the end (exact, in
   // any order) and group 0 runs the epilogue -- more waves on one tile where few tiles leave CUs idle.
   static_assert(KSPL == 1 || KSPL == 2, "one or two K groups");
+  // GL (1 SiLU, 2 relu^2): W is gate|up (N = 2 * half); a tile's 128 weight rows are 64 gate rows n0 .. and
+  // their up rows half + n0 .., loaded and multiplied by waves 0-1 and 2-3 (one wave's load instructions
+  // cover the 32 rows it multiplies), and the epilogue stores act(gate) * up fp32 for 64 output columns
+  static_assert(GL == 0 || (TN == 1 && EPI == 0 && BI * (64 / BLPR) == 32), "gated tiles: 128 rows, 32 loaded per wave");
   __shared__ __attribute__((aligned(16))) int8_t lds_a0s[KSPL][ASZ];
   __shared__ __attribute__((aligned(16))) int8_t lds_a1s[KSPL][ASZ];
   __shared__ __attribute__((aligned(16))) uint8_t lds_b0s[KSPL][BSZ];
@@ -397,17 +401,19 @@ __global__ __launch_bounds__(256 * KSPL) __attribute__((amdgpu_waves_per_eu(OCC,
   const int gsz = kGroupM * tiles_n;
   const int grp = t / gsz, rr = t - grp * gsz;
   const int gm = min(kGroupM, tiles_m - grp * kGroupM);
-  const int m0 = (grp * kGroupM + rr % gm) * BM, n0 = (rr / gm) * BN;
+  const int m0 = (grp * kGroupM + rr % gm) * BM, n0 = (rr / gm) * (GL ? BN / 2 : BN);
+  const int half = N / 2;  // (gated mode)
 
   // The buffer descriptors start at the tile's first activation row and first weight row (64-bit
   // pointer arithmetic), so the 32-bit offsets inside them stay below (BM - 1) * lda + K and
   // 256 * K / 4 whatever M, N and the row stride (the host checks (BM - 1) * lda + K < 2^31).
   const int KS = (K + AROW - 1) / AROW;
   const uint32_t row_bytes = (uint32_t)K / 4;
-  const int mrows = min(BM, M - m0), nrows = min(BN, N - n0);
+  const int mrows = min(BM, M - m0), nrows = GL ? min(BN / 2, half - n0) : min(BN, N - n0);
   const uint32_t a_end = (uint32_t)((int64_t)(mrows - 1) * lda + K), b_end = (uint32_t)nrows * row_bytes;
   const buf_t ab = make_buf(A + (int64_t)m0 * lda, a_end);
-  const buf_t wb = make_buf(W + (int64_t)n0 * row_bytes, b_end);
+  const int wrow0 = GL && wn >= 2 ? half + n0 : n0;  // first weight row this wave loads from (gated: up rows)
+  const buf_t wb = make_buf(W + (int64_t)wrow0 * row_bytes, b_end);
 
   // LDS position p of activation row r holds chunk p ^ aswz(r); position q of weight row R holds
   // 16-byte piece q ^ bswz(R).  (16 consecutive rows then fall on 16 distinct 16-byte bank groups.)
@@ -427,7 +433,8 @@ __global__ __launch_bounds__(256 * KSPL) __attribute__((amdgpu_waves_per_eu(OCC,
 #pragma unroll
   for (int jj = 0; jj < BI; ++jj) {
     const int R = (64 / BLPR) * (BI * wn + jj) + l / BLPR;
-    b_row[jj] = (uint32_t)min(R, nrows - 1) * row_bytes;
+    const int Rl = GL && wn >= 2 ? R - BN / 2 : R;  // row within the block this wave loads from
+    b_row[jj] = (uint32_t)min(Rl, nrows - 1) * row_bytes;
     b_col[jj] = 16 * ((l % BLPR) ^ bswz(R));
   }
   auto issue = [&](int kt, int8_t* la, uint8_t* lb) {
@@ -580,6 +587,60 @@ __global__ __launch_bounds__(256 * KSPL) __attribute__((amdgpu_waves_per_eu(OCC,
         for (int q = 0; q < 16; ++q) acc[tn][tm][q] += xr[((tn * TM + tm) * 16 + q) * 64 + l];
   }
   auto rsum = [&](int r) { return KSPL > 1 ? rowsum_s[0][r] + rowsum_s[KSPL - 1][r] : rowsum_s[0][r]; };
+
+  if constexpr (GL != 0) {
+    // up waves 2, 3 hand their rescaled products (rounded to ep.mid_dtype, as a plain linear stores them)
+    // to gate waves 0, 1 through LDS; the gate waves store act(gate) * up (fp32) -- the skinny kernels'
+    // gated epilogue, element for element
+    static_assert(64 * TM * 16 * 4 <= ASZ, "a wave's products fit one activation buffer");
+    float* xf = reinterpret_cast<float*>((wn & 1) ? lds_a1 : lds_a0);
+    const int c0 = 32 * (wn & 1);  // the wave pair's 32 of the tile's 64 output columns
+    auto mid = [&](float y) { return ep.mid_dtype == WFB_BF16 ? bf16_bits_to_f32(f32_to_bf16_rne(y)) : y; };
+    if (wn >= 2) {
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+        const int rs = rsum(tm * 32 + i);
+        const float as = epi_ascale(ep, min(m0 + tm * 32 + i, M - 1));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float wsu = epi_wscale(ep, half + n0 + c0 + 8 * q + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            xf[((tm * 4 + q) * 4 + e) * 64 + l] = mid(__fmul_rn(__fmul_rn((float)(acc[0][tm][4 * q + e] - rs), wsu), as));
+        }
+      }
+    }
+    __syncthreads();  // (the waves of this K group only: the other one has ended)
+    if (wn >= 2) return;
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      const int m = m0 + tm * 32 + i;
+      if (m >= M) continue;
+      const int rs = rsum(tm * 32 + i);
+      const float as = epi_ascale(ep, m);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + c0 + 8 * q + 4 * g;
+        if (n >= half) continue;
+        const float wsg = epi_wscale(ep, n);
+        float o4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float yg = mid(__fmul_rn(__fmul_rn((float)(acc[0][tm][4 * q + e] - rs), wsg), as));
+          o4[e] = glu<GL>(yg, xf[((tm * 4 + q) * 4 + e) * 64 + l]);
+        }
+        float* o = reinterpret_cast<float*>(ep.out) + (int64_t)m * ep.ldo + n;
+        if (vec_out && n + 3 < half) {
+          *reinterpret_cast<float4*>(o) = make_float4(o4[0], o4[1], o4[2], o4[3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < half) o[e] = o4[e];
+        }
+      }
+    }
+    return;
+  }
 
   // weight scale per 4-column output group (segments are multiples of 8 rows, so a group has one)
   float wsg[TN][4];
@@ -747,6 +808,21 @@ hipError_t launch_tile(const uint8_t* W, int n, int k, const int8_t* A, int m, i
   return hipGetLastError();
 }
 
+// Gated gate|up (N = 2 * half rows) as 32 x 64-output tiles of the K-split tile kernel: out [m, half] fp32 =
+// act(gate) * up.
+template <int GL>
+hipError_t launch_tile_glu(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, const Epilogue& e,
+                           hipStream_t s) {
+  const int half = n / 2;
+  const int tiles_n = (half + 63) / 64, tiles_m = (m + 31) / 32;
+  const int nwg = tiles_n * tiles_m;
+  const int grid = ((nwg + 7) / 8) * 8;
+  const bool vec_out = e.ldo % 4 == 0 && (uintptr_t)e.out % 16 == 0;
+  hipLaunchKernelGGL((gemm_i2s_tile_kernel<1, 2, 4, 0, 1, 2, GL>), dim3(grid), dim3(512), 0, s, W, A, lda, m, n, k,
+                     tiles_m, tiles_n, nwg, vec_out, e);
+  return hipGetLastError();
+}
+
 template <int MT>
 hipError_t launch_mt(const uint8_t* W, int n, int C, const int8_t* A, int m, int64_t lda, const Epilogue& e,
                      hipStream_t s) {
@@ -806,35 +882,24 @@ hipError_t launch_gemm_i2s_skinny(const uint8_t* W, int n, int k, const int8_t* 
 hipError_t launch_gemm_i2s_glu(const uint8_t* W, int n, int k, const int8_t* A, int m, int64_t lda, int act,
                                const Epilogue& e, hipStream_t s) {
   const int C = k / 64;
-  if (m <= 32) {
-    const hipError_t st = launch_skinny_lds(W, n, k, A, m, lda, e, act, s);
-    if (st != hipErrorNotSupported) return st;
-  }
-  // 33..64 tokens: two launches of the staged two-tile form where it takes 32 tokens of the shape
-  // (gated 13824 x 2560: M = 64 26.5 -> 17.0 us, M = 33 19.8 -> 13.9, measured on MI355X against the
-  // split-K kernel)
-  if (m > 32 && m <= 64) {
-    const hipError_t st = launch_token_halves(W, n, k, A, m, lda, e, act, s);
-    if (st != hipErrorNotSupported) return st;
-    // else chunks of 16 tokens through the one-tile form where it takes the shape (gated 28672 x 4096,
-    // measured on MI355X against the split-K kernel: M = 64 64.7 -> 45.0 us, M = 48 55.0 -> 34.5,
-    // M = 33 46.5 -> 30.2)
-    for (int c0 = 0; c0 < m; c0 += 16) {
-      Epilogue ec = e;
-      if (ec.a_scale) ec.a_scale += c0;
-      ec.out = static_cast<char*>(ec.out) + (int64_t)c0 * ec.ldo * 4;  // the gated product is fp32
-      const hipError_t sc = launch_skinny_lds(W, n, k, A + (int64_t)c0 * lda, std::min(16, m - c0), lda, ec, act, s);
-      if (sc == hipErrorNotSupported && c0 == 0) break;  // nothing launched: the split-K kernel below
-      if (sc != hipSuccess) return sc == hipErrorNotSupported ? hipErrorInvalidValue : sc;
-      if (c0 + 16 >= m) return hipSuccess;
-    }
-  }
+  // 33..64 tokens, and 17..32 on long rows of a wide gate|up: the K-split tile kernel with the gated
+  // epilogue, 32 tokens x 64 outputs per tile (interleaved medians on MI355X against the staged kernel
+  // below, SiLU, bf16 products: gated 28672 x 4096 at M = 64 43.8 -> 19.0 us, M = 33 28.6 -> 19.6, M = 24
+  // 24.4 -> 14.6; 13824 x 2560 at M = 64 15.8 -> 10.9, M = 33 13.3 -> 12.4; 3072 x 4096 at M = 64 13.2 ->
+  // 12.1; slower at M <= 32 on 13824 x 2560 (8.2 -> 10.7, half the CUs without a tile) and 3072 x 4096,
+  // and at M <= 16)
+  const bool small_offsets = (int64_t)n * (k / 4) <= INT32_MAX && (int64_t)(m - 1) * lda + k <= INT32_MAX;
+  if (m > 64 || n % 2 != 0 || !small_offsets) return hipErrorInvalidValue;  // (the C ABI checks these first)
+  if (m > 32 || (m > 16 && k >= 4096 && n >= 8192))
+    return act == WFB_ACT_SILU ? launch_tile_glu<WFB_ACT_SILU>(W, n, k, A, m, lda, e, s)
+                               : launch_tile_glu<WFB_ACT_RELU2>(W, n, k, A, m, lda, e, s);
+  const hipError_t st = launch_skinny_lds(W, n, k, A, m, lda, e, act, s);
+  if (st != hipErrorNotSupported) return st;
 #define WFB_GLU(MT)                                                                              \
   return act == WFB_ACT_SILU ? launch_skinny_glu<MT, WFB_ACT_SILU>(W, n, C, A, m, lda, e, s) \
                              : launch_skinny_glu<MT, WFB_ACT_RELU2>(W, n, C, A, m, lda, e, s)
   if (m <= 16) WFB_GLU(1);
-  if (m <= 32) WFB_GLU(2);
-  WFB_GLU(4);
+  WFB_GLU(2);
 #undef WFB_GLU
 }
 
