@@ -28,9 +28,14 @@
 //
 // Work mapping (4 waves).  A key is read by LPK = D/8 lanes, 8 elements each (one 16-byte load for
 // 16-bit caches), so one wave instruction covers 64/LPK whole keys and a wave's loads are contiguous.
-// Keys are processed in chunks of CH; per chunk each wave loads its CH/4 keys of K and V up front,
-// forms the G partial dot products per lane against its 8 query elements (held in registers), sums them
-// over the key's LPK lanes with DPP, and parks the scores in LDS.  A running (online) softmax per head
+// Keys are processed in chunks of CH; per chunk each wave loads its CH/4 keys of K and V up front.
+// bf16 caches: the scores go through the matrix cores, S[head, key] = Q K^T per 16 keys of a wave
+// (v_mfma_f32_16x16x32_bf16: A = the group's query heads as rows, zero past G; B = the 16 keys as
+// columns, a lane's fragment being 16 contiguous bytes of its key's row; k = 32 head dimensions per
+// step), the products of bf16 operands exact in fp32 and summed in fp32.  The appended key pos is not
+// among the cache reads; its G scores are computed once per workgroup from the LDS copy of the key.
+// fp32 caches: each lane forms the G partial dot products against its 8 query elements (held in
+// registers) and they are summed over the key's LPK lanes with DPP.  The scores are parked in LDS.  A running (online) softmax per head
 // -- chunk max, rescale factor exp(m_old - m_new), exp(s - m_new), running sum -- is kept by the wave
 // that owns the head; then each lane accumulates p * v for its keys and 8 elements.  At the end the
 // per-lane partial outputs are summed over the lanes of a wave sharing the same elements (xor
@@ -143,8 +148,13 @@ __device__ inline int split_len(int64_t pos, int ks, int spt) {
   return ks;
 }
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// (PF, bf16: three workgroups per CU -- at most 168 registers -- where the register budget allows it)
 template <int DT, int D, int G, int CH, bool PF = false>
-__global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(PF && DT == WFB_BF16 && G <= 4 ? 3 : 1)))
+void gqa_decode_kernel(
     const void* __restrict__ q, int64_t ldq, const void* __restrict__ kn, int64_t ldk, const void* __restrict__ vn,
     int64_t ldv, const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, void* __restrict__ kc,
     void* __restrict__ vc, int64_t max_len, const int64_t* __restrict__ pos_arr, int hkv, float scale,
@@ -157,11 +167,15 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   constexpr int HD = D / 2;
   constexpr int HPW = (G + 3) / 4;     // heads per wave in the softmax step
   static_assert(R * KPW * 4 == CH, "chunk must tile the waves");
+  constexpr bool MQ = DT == WFB_BF16;  // scores on the matrix cores
+  constexpr int NTL = KW / 16;         // (MQ) 16-key MFMA tiles per wave and chunk
+  static_assert(!MQ || (KW % 16 == 0 && D % 32 == 0 && G <= 16 && R == NTL * (D / 32)), "matrix-core score tiles");
 
   __shared__ float qs[G][D];
   __shared__ float knew[D], vnew[D];
   __shared__ float sc[G][CH];
   __shared__ float alpha_s[G], lsum_s[G];
+  __shared__ float snew_s[G];  // (MQ) scores of the appended key
   __shared__ float red[4][G][D];
 
   const int kvh = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
@@ -196,8 +210,14 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   auto load_k = [&](int c0, int set) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int key = c0 + w * KW + r * KPW + kl;
-      kr[set][r] = load_raw8<DT>(kb, (uint32_t)(key * D + d0) * ESZ);
+      if constexpr (MQ) {  // B fragment j of tile tl: key 16 tl + lane % 16, dimensions 32 j + 8 (lane / 16) ..
+        const int tl = r / (D / 32), j = r % (D / 32);
+        const int key = c0 + w * KW + 16 * tl + (lane & 15);
+        kr[set][r] = load_raw8<DT>(kb, (uint32_t)(key * D + 32 * j + 8 * (lane >> 4)) * ESZ);
+      } else {
+        const int key = c0 + w * KW + r * KPW + kl;
+        kr[set][r] = load_raw8<DT>(kb, (uint32_t)(key * D + d0) * ESZ);
+      }
     }
   };
   auto load_v = [&](int c0) {
@@ -272,18 +292,45 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   // to the storage type, so the pairs hold it exactly) to leave registers for the prefetched keys
   constexpr bool QP = DT != WFB_F32;
   float qf[QP ? 1 : G][8];
-  uint32_t qp[QP ? G : 1][4];
+  uint32_t qp[QP && !MQ ? G : 1][4];
+  v4i qa[MQ ? D / 32 : 1];  // (MQ) A fragments: row = head lane % 16, dimensions 32 j + 8 (lane / 16) ..
+  if constexpr (MQ) {
+    const int h = lane & 15;
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+    for (int j = 0; j < D / 32; ++j)
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      if constexpr (QP)
-        qp[g][e / 2] = (__float_as_uint(qs[g][d0 + e]) >> 16) | (__float_as_uint(qs[g][d0 + e + 1]) & 0xffff0000u);
-      else {
-        qf[g][e] = qs[g][d0 + e];
-        qf[g][e + 1] = qs[g][d0 + e + 1];
+      for (int e = 0; e < 8; e += 2) {
+        const int dd = 32 * j + 8 * (lane >> 4) + e;
+        qa[j][e / 2] =
+            h < G ? (int)((__float_as_uint(qs[h][dd]) >> 16) | (__float_as_uint(qs[h][dd + 1]) & 0xffff0000u)) : 0;
+      }
+    if (owns_new) {  // the appended key's scores: wave w takes heads w, w + 4, ..
+#pragma unroll
+      for (int hh = 0; hh < HPW; ++hh) {
+        const int g = w + 4 * hh;
+        if (g < G) {
+          float p = 0.0f;
+#pragma unroll
+          for (int e = 0; e < D / 64; ++e) p += qs[g][lane + 64 * e] * knew[lane + 64 * e];
+          p = wave_sum_f32(p);
+          if (lane == 0) snew_s[g] = p;
+        }
       }
     }
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        if constexpr (QP)
+          qp[g][e / 2] = (__float_as_uint(qs[g][d0 + e]) >> 16) | (__float_as_uint(qs[g][d0 + e + 1]) & 0xffff0000u);
+        else {
+          qf[g][e] = qs[g][d0 + e];
+          qf[g][e + 1] = qs[g][d0 + e + 1];
+        }
+      }
+  }
   float acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -300,13 +347,34 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(
   auto chunk = [&](int c0, int set) {
     // scores (the empty asm keeps the query pairs packed across chunks: without it the compiler
     // widens them once, ahead of the loop, into twice the registers)
-    if constexpr (QP)
+    if constexpr (QP && !MQ)
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(qp[g][i]));
+    if constexpr (MQ) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+      for (int tl = 0; tl < NTL; ++tl) {
+        f32x4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < D / 32; ++j)
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[j]),
+                                                       __builtin_bit_cast(bf16x8_t, kr[set][tl * (D / 32) + j].r[0]), c,
+                                                       0, 0, 0);
+        // lane l holds S[head 4 (l / 16) + i, key 16 tl + l % 16]
+        const int key = c0 + w * KW + 16 * tl + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int g = 4 * (lane >> 4) + i;
+          if (g < G) {
+            const float sv = owns_new && key == pos ? snew_s[g] : c[i];
+            sc[g][key - c0] = key < k1 ? sv * scale : -__builtin_inff();
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < (MQ ? 0 : R); ++r) {
       const int key = c0 + w * KW + r * KPW + kl;
       float kf[8];
       widen8<DT>(kr[set][r], kf);
