@@ -350,6 +350,9 @@ hipError_t launch_skinny(const uint8_t* W, int n, int C, const int8_t* A, int m,
 //    output with an optional residual, aligned rows): fp32 outputs staged through LDS, the residual
 //    added after a coalesced 16-byte load, whole-line stores.  EPI = 0: any output type, bias,
 //    accumulator copy, stored from registers.
+//  * KSPL = 2: two groups of four waves split the tile's K stages, their int32 partials added in LDS.
+//  * GL (gated gate|up, with KSPL = 2): 64 gate rows and their 64 up rows per tile; the fp32 output is
+//    act(gate) * up, the up products handed to the gate waves through LDS.
 constexpr int kGroupM = 8;
 
 typedef __attribute__((address_space(3))) void lds_void;
