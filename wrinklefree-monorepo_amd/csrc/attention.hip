@@ -37,9 +37,9 @@
 // fp32 caches: each lane forms the G partial dot products against its 8 query elements (held in
 // registers) and they are summed over the key's LPK lanes with DPP.  The scores are parked in LDS.  A
 // running (online) softmax per head -- chunk max, rescale factor exp(m_old - m_new), exp(s - m_new),
-// running sum -- is kept by the wave that owns the head; then each lane accumulates p * v for its keys and 8 elements.  At the end the
-// per-lane partial outputs are summed over the lanes of a wave sharing the same elements (xor
-// shuffles), then over the 4 waves in LDS, and divided by the softmax sum.
+// running sum -- is kept by the wave that owns the head; then each lane accumulates p * v for its keys
+// and 8 elements.  At the end the per-lane partial outputs are summed over the lanes of a wave sharing
+// the same elements (xor shuffles), then over the 4 waves in LDS, and divided by the softmax sum.
 #include <mutex>
 
 #include "wfb_common.h"
