@@ -53,6 +53,23 @@ def test_glu_linear_matches_oracle_and_unfused(pkg, dev, case, act):
     assert torch.equal(q1, q2) and torch.equal(s1, s2)
 
 
+@pytest.mark.parametrize("m,half,k", [(40, 1056, 1152), (20, 4096, 4096), (64, 96, 128), (8, 2048, 1024)])
+def test_glu_linear_strided_out_no_token_scales(pkg, dev, m, half, k):
+    """Without token scales and into a strided fp32 view (odd row stride, base 4 bytes past a 16-byte
+    boundary: the per-element stores), equal to the unfused path, every kernel form."""
+    rng = np.random.default_rng(m * 3 + half)
+    packed = torch.from_numpy(orc.pack_i2s(orc.random_ternary(rng, 2 * half, k))).to(dev)
+    a = torch.from_numpy(orc.random_int8(rng, m, k)).to(dev)
+    scales = torch.from_numpy(orc.log_uniform(rng, 2).astype(np.float32) * 4e-3).to(dev)
+    big = torch.full((m, half + 5), float("nan"), dtype=torch.float32, device=dev)
+    out = big[:, 1:half + 1]
+    x = pkg.bitnet_linear_glu(packed, scales, a, "silu", mid_dtype=torch.bfloat16, out=out)
+    assert x.data_ptr() == out.data_ptr()
+    y = pkg.bitnet_linear_segmented(packed, [half, half], scales, a, out_dtype=torch.bfloat16).float().cpu().numpy()
+    assert np.array_equal(out.cpu().numpy(), orc.glu(y[:, :half], y[:, half:], orc.ACT_SILU))
+    assert torch.isnan(big[:, 0]).all() and torch.isnan(big[:, half + 1:]).all()  # nothing outside the view
+
+
 def test_glu_linear_errors(pkg, dev):
     packed = torch.zeros((96, 32), dtype=torch.uint8, device=dev)
     a = torch.zeros((2, 128), dtype=torch.int8, device=dev)
