@@ -108,6 +108,11 @@ CASES = [
     (8, 32, 8, 128, 4100, [4099, 3000, 2047, 2048, 1023, 767, 768, 5], torch.bfloat16, True),
     # 776 sequence-heads (more than the 768 live-split target): one split per sequence, all its keys
     (97, 16, 8, 64, 200, [(37 * i + 11) % 200 for i in range(97)], torch.bfloat16, True),
+    # position-scaled splits with G = 8 (the matrix-core scores' heads 4..7 in the second lane group) and
+    # with G = 3 at head_dim 64 (two 32-dimension steps per score tile)
+    (16, 64, 8, 128, 2100, [2099, 1500, 640, 64, 63, 0, 1000, 2047, 1, 700, 1999, 128, 129, 300, 1700, 900],
+     torch.bfloat16, True),
+    (64, 9, 3, 64, 600, [(53 * i + 7) % 600 for i in range(64)], torch.bfloat16, True),
 ]
 
 
