@@ -273,7 +273,8 @@ def test_batched_kernel_choice_boundaries(pkg, dev, m, n, k):
     # rows up to 2560 (outputs up to 32768 rows) or 7168 (outputs up to 4096 rows), with four for 33..64
     # tokens on rows up to 4096 and outputs up to 4096 rows (two token blocks of two-tile workgroups for rows
     # of 4096, and for rows up to 7168 from 49 tokens; two launches of two tiles below that); 33..64 tokens
-    # on rows and outputs of 4096 or more: the 32-row tile kernel with its K split; else the 32-row tile
+    # on rows and outputs of 4096 or more: the 32-row tile kernel with its K split (four groups on rows of
+    # 8192 or more, two below); else the 32-row tile
     # kernel for M > 16 when N * ceil(M/16) >= 18432 and K <= 8192, else the split-K skinny kernel while
     # N * ceil(M/16) <= 32768 (always for M <= 8), else the whole-K wave-per-rows kernel; these shapes
     # sit on either side of those boundaries
@@ -281,6 +282,18 @@ def test_batched_kernel_choice_boundaries(pkg, dev, m, n, k):
     packed = _packed(rng, n, k)
     a = orc.random_int8(rng, m, k)
     _check_linear(pkg, dev, packed, a, orc.log_uniform(rng), orc.log_uniform(rng, m), kernel="gemm")
+
+
+@pytest.mark.parametrize("m,n,k", [(96, 2560, 6912), (256, 2560, 6912), (100, 2560, 7040), (384, 2560, 6912),
+                                   (256, 4096, 14336), (512, 4096, 14336), (320, 4096, 8192), (512, 2560, 2560),
+                                   (512, 2600, 6912), (480, 4096, 8320)])
+def test_gemm_k_groups(pkg, dev, m, n, k):
+    # M > 64 on few 32-row tiles: three groups of four waves splitting K on 32 x 256 tiles (160..256 of
+    # them), four groups on 32 x 128 tiles for rows of 6912 or more below that; ragged N and K included
+    rng = np.random.default_rng(3500 + m + n + k)
+    packed = _packed(rng, n, k)
+    a = orc.random_int8(rng, m, k)
+    _check_linear(pkg, dev, packed, a, orc.log_uniform(rng), orc.log_uniform(rng, m), check_fp32=False)
 
 
 @pytest.mark.parametrize("n,k", [(13824, 2560), (2560, 6912)])

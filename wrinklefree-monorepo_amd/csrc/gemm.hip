@@ -350,7 +350,7 @@ hipError_t launch_skinny(const uint8_t* W, int n, int C, const int8_t* A, int m,
 //    output with an optional residual, aligned rows): fp32 outputs staged through LDS, the residual
 //    added after a coalesced 16-byte load, whole-line stores.  EPI = 0: any output type, bias,
 //    accumulator copy, stored from registers.
-//  * KSPL = 2: two groups of four waves split the tile's K stages, their int32 partials added in LDS.
+//  * KSPL = 2..4: groups of four waves split the tile's K stages, their int32 partials added in LDS.
 //  * GL (gated gate|up, with KSPL = 2): 64 gate rows and their 64 up rows per tile; the fp32 output is
 //    act(gate) * up, the up products handed to the gate waves through LDS.
 constexpr int kGroupM = 8;
@@ -379,7 +379,7 @@ __global__ __launch_bounds__(256 * KSPL) __attribute__((amdgpu_waves_per_eu(OCC,
   // KSPL > 1: KSPL groups of four waves split the stages of K (group kh takes stages kh*KSH ..), each with
   // its own operand buffers and sum(a); their integer tile partials are added in LDS at the end (exact, in
   // any order) and group 0 runs the epilogue -- more waves on one tile where few tiles leave CUs idle.
-  static_assert(KSPL == 1 || KSPL == 2, "one or two K groups");
+  static_assert(KSPL >= 1 && KSPL <= 4, "one to four K groups");
   // GL (1 SiLU, 2 relu^2): W is gate|up (N = 2 * half); a tile's 128 weight rows are 64 gate rows n0 .. and
   // their up rows half + n0 .., loaded and multiplied by waves 0-1 and 2-3 (one wave's load instructions
   // cover the 32 rows it multiplies), and the epilogue stores act(gate) * up fp32 for 64 output columns
@@ -566,7 +566,7 @@ __global__ __launch_bounds__(256 * KSPL) __attribute__((amdgpu_waves_per_eu(OCC,
   if constexpr (LPR >= 8) ssum += __shfl_xor(ssum, 4);
   if ((l % LPR) == 0) rowsum[srow] = ssum;
   __syncthreads();  // also: every wave is done reading the operand buffers
-  if constexpr (KSPL > 1) {
+  if constexpr (KSPL == 2) {
     // group 1's partial tiles into group 0's accumulators, wave wn through group 1's buffer number wn (free
     // now); sum(a) of a row is the sum of the two groups' row sums (rsum)
     static_assert(64 * TM * TN * 16 * 4 <= (ASZ < BSZ ? ASZ : BSZ), "a wave's partial tiles fit one buffer");
@@ -588,8 +588,45 @@ __global__ __launch_bounds__(256 * KSPL) __attribute__((amdgpu_waves_per_eu(OCC,
       for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
         for (int q = 0; q < 16; ++q) acc[tn][tm][q] += xr[((tn * TM + tm) * 16 + q) * 64 + l];
+  } else if constexpr (KSPL > 2) {
+    // the same with groups 1 .. KSPL - 1, each through its own buffers, added into group 0 in order
+    static_assert(64 * TM * TN * 16 * 4 <= (ASZ < BSZ ? ASZ : BSZ), "a wave's partial tiles fit one buffer");
+    auto xbuf = [&](int gk) {
+      return reinterpret_cast<int*>(wn == 0 ? (void*)lds_a0s[gk] : wn == 1 ? (void*)lds_a1s[gk]
+                                    : wn == 2 ? (void*)lds_b0s[gk] : (void*)lds_b1s[gk]);
+    };
+    if (kh >= 1) {
+      int* xr = xbuf(kh);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) xr[((tn * TM + tm) * 16 + q) * 64 + l] = acc[tn][tm][q];
+    }
+    __syncthreads();
+    if (kh >= 1) return;  // (no barrier follows)
+#pragma unroll
+    for (int gk = 1; gk < KSPL; ++gk) {
+      const int* xr = xbuf(gk);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) acc[tn][tm][q] += xr[((tn * TM + tm) * 16 + q) * 64 + l];
+    }
   }
-  auto rsum = [&](int r) { return KSPL > 1 ? rowsum_s[0][r] + rowsum_s[KSPL - 1][r] : rowsum_s[0][r]; };
+  auto rsum = [&](int r) {
+    if constexpr (KSPL <= 2) {
+      return KSPL > 1 ? rowsum_s[0][r] + rowsum_s[KSPL - 1][r] : rowsum_s[0][r];
+    } else {
+      int v = rowsum_s[0][r];
+#pragma unroll
+      for (int gk = 1; gk < KSPL; ++gk) v += rowsum_s[gk][r];
+      return v;
+    }
+  };
 
   if constexpr (GL != 0) {
     // up waves 2, 3 hand their rescaled products (rounded to ep.mid_dtype, as a plain linear stores them)
@@ -930,8 +967,10 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
   // (interleaved medians on MI355X: 4096 x 4096 at M = 40..64 9.5-10.4 -> 8.4 us, 4096 x 14336 24.7-31.5
   // -> 21.5; 6144 x 4096 and 28672 x 4096 within 1%; at 17..32 tokens, and on 2560-long or 2560-row
   // shapes, the kernels below stay ahead)
+  // (rows of 8192 or more: four groups of four waves splitting K, 4096 x 14336 at M = 64 22.2 -> 18.2 us)
   if (m > 32 && m <= 64 && small_offsets && !e.amax && k >= 4096 && n >= 4096)
-    return launch_tile<1, 2, 4, 1, 2>(W, n, k, A, m, lda, e, s);
+    return k >= 8192 ? launch_tile<1, 2, 4, 1, 4>(W, n, k, A, m, lda, e, s)
+                     : launch_tile<1, 2, 4, 1, 2>(W, n, k, A, m, lda, e, s);
   // operands staged in LDS (skinny_lds.h) where its LDS holds them (17..32 tokens: where measured faster)
   if (m <= 64 && small_offsets) {
     const hipError_t st = launch_skinny_lds(W, n, k, A, m, lda, e, 0, s);
@@ -976,6 +1015,14 @@ hipError_t launch_gemm_i2s(const uint8_t* W, int n, int k, const int8_t* A, int 
     if (fill(t64n, 768) > fill(t64, 512) + 0.1) return launch_tile<2, 2, 3, 1>(W, n, k, A, m, lda, e, s);
     return launch_tile<2, 2, 2>(W, n, k, A, m, lda, e, s);
   }
+  // 160..256 tiles of 32 x 256: three groups of four waves splitting K on each, one workgroup per CU
+  // (interleaved medians on MI355X against the two-group 32 x 128 and the one-group 32 x 256 forms: 2560 x
+  // 6912 at M = 512 20.5 -> 17.7 us, 4096 x 14336 at M = 512 49.6 -> 37.4, 2560 x 2560 at M = 512 9.9 ->
+  // 9.5); fewer tiles on rows of 6912 or more: 32 x 128 tiles with four groups (2560 x 6912 at M = 256 12.9
+  // -> 11.6)
+  const int64_t t256 = tn * ((m + 31) / 32);
+  if (t256 >= 160 && t256 <= 256) return launch_tile<1, 2, 3, 2, 3>(W, n, k, A, m, lda, e, s);
+  if (few_tiles && k >= 6912) return launch_tile<1, 2, 4, 1, 4>(W, n, k, A, m, lda, e, s);
   return few_tiles ? launch_tile<1, 2, 4, 1, 2>(W, n, k, A, m, lda, e, s) : launch_tile<1, 2, 3>(W, n, k, A, m, lda, e, s);
 }
 
