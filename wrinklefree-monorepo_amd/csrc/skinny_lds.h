@@ -596,9 +596,15 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
 // activation fragments and token scales are loaded once into registers (they are the same for every
 // tile), so the LDS holds only weights: a ring of DEPTH tile buffers, DEPTH - 1 tiles' weight DMA in
 // flight while one tile is multiplied, reduced and stored -- about 128 KB per CU at K = 4096, what the M = 1
-// GEMV keeps in flight to stream at ~6.4 TB/s.  A tile's wait is vmcnt(ops of the tiles issued after it)
-// (loads complete in issue order; the epilogue's stores sit between those tiles, so the wait can only be
-// longer, never short).  TP = 1 (K <= 4096).  Same operand layouts and arithmetic as the one-shot kernel.
+// GEMV keeps in flight to stream at ~6.4 TB/s.  TP = 1 (K <= 4096).  Same operand layouts and arithmetic
+// as the one-shot kernel.
+// Waits: a tile's DMA is waited for with vmcnt(DMA instructions issued after it).  Loads complete in issue
+// order, so that count is exact for them; stores may complete before earlier loads on this part, so the
+// epilogue's stores are left out of the count (counting them let a wait pass with the tile's DMA still
+// in flight) -- a store still outstanding can only make the wait longer.
+// Every LDS access of the loop is inline asm (with its own lgkmcnt wait): the compiler, which cannot tell
+// the ring slots from the other LDS, otherwise waits for every outstanding LDS DMA (vmcnt(0)) before each
+// LDS read, which drains the ring on every tile (measured: 35.0 -> 26.5 us for the Llama-3-8B head at M = 8).
 template <int OPS>
 __device__ __forceinline__ void wait_tiles_after(int later) {
   // vmcnt(n) with expcnt / lgkmcnt at their maxima (gfx9: vmcnt bits 3:0 and 15:14)
@@ -616,16 +622,63 @@ __device__ __forceinline__ void wait_tiles_after(int later) {
 #undef WFB_VMCNT
 }
 
-template <int S, int NT, int DEPTH>
+// LDS offset of a pointer into __shared__ memory (the low 32 bits of its flat address)
+__device__ __forceinline__ uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)p; }
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Sum of the S int32 partial tiles 2048 bytes apart from LDS offset a (one wait; integer sums, so the
+// order is immaterial).
+template <int S>
+__device__ __forceinline__ int lds_sum_parts(uint32_t a) {
+  int t[8];
+  if constexpr (S == 8) {
+    asm volatile(
+        "ds_read_b32 %0, %8\n\tds_read_b32 %1, %8 offset:2048\n\tds_read_b32 %2, %8 offset:4096\n\t"
+        "ds_read_b32 %3, %8 offset:6144\n\tds_read_b32 %4, %8 offset:8192\n\tds_read_b32 %5, %8 offset:10240\n\t"
+        "ds_read_b32 %6, %8 offset:12288\n\tds_read_b32 %7, %8 offset:14336\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7])
+        : "v"(a)
+        : "memory");
+    return t[0] + t[1] + t[2] + t[3] + t[4] + t[5] + t[6] + t[7];
+  } else if constexpr (S == 5) {
+    asm volatile(
+        "ds_read_b32 %0, %5\n\tds_read_b32 %1, %5 offset:2048\n\tds_read_b32 %2, %5 offset:4096\n\t"
+        "ds_read_b32 %3, %5 offset:6144\n\tds_read_b32 %4, %5 offset:8192\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4])
+        : "v"(a)
+        : "memory");
+    return t[0] + t[1] + t[2] + t[3] + t[4];
+  } else if constexpr (S == 4) {
+    asm volatile(
+        "ds_read_b32 %0, %4\n\tds_read_b32 %1, %4 offset:2048\n\tds_read_b32 %2, %4 offset:4096\n\t"
+        "ds_read_b32 %3, %4 offset:6144\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3])
+        : "v"(a)
+        : "memory");
+    return t[0] + t[1] + t[2] + t[3];
+  } else {
+    static_assert(S == 2, "S in {2, 4, 5, 8}");
+    asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %2 offset:2048\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(t[0]), "=&v"(t[1])
+                 : "v"(a)
+                 : "memory");
+    return t[0] + t[1];
+  }
+}
+
+// KO (keys only: greedy-argmax keys and no other output): each lane's key goes out as one buffer store,
+// lanes with nothing to store pointing past the key buffer (which drops the store).
+template <int S, int NT, int DEPTH, bool KO>
 __global__ __launch_bounds__(64 * S) void kernel_persist(const uint8_t* __restrict__ W, const int8_t* __restrict__ A,
                                                          int64_t lda, int M, int N, int C, int ntiles, Epilogue ep) {
   static_assert(DEPTH >= 2 && DEPTH <= 8 && 7 * 2 * NT < 64, "ring depth and vmcnt range");
+  static_assert(NT == 2, "partial tiles 2048 bytes apart, four fragment reads per tile");
   constexpr int OPS = 2 * NT;  // LDS-DMA instructions of one tile's weights (per wave)
   __shared__ __attribute__((aligned(16))) int8_t wl[DEPTH][S][NT][2048];
   // partial tiles, double-buffered by tile parity: a wave only ever refills its own weight slot (program
   // order protects it), and a parity buffer is rewritten two tiles later, after a barrier every wave
   // passes only once done with the epilogue that read it -- one barrier per tile
-  __shared__ int redb[2][S][NT * 4][64];
+  __shared__ __attribute__((aligned(16))) int redb[2][S][NT * 4][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nl = lane & 15, g = lane >> 4;
   const uint32_t row_bytes = (uint32_t)C * 16;
@@ -653,6 +706,12 @@ __global__ __launch_bounds__(64 * S) void kernel_persist(const uint8_t* __restri
 #pragma unroll
   for (int j = 0; j < 4; ++j) as[j] = 4 * g + j < M ? epi_ascale(ep, 4 * g + j) : 0.0f;
   const float ws = ep.ws_dev ? ep.ws_dev[0] : ep.ws;
+  // (keys only) the key buffer: slots of 16 rows x ld tokens
+  const int nslots = (N + 15) / 16;
+  const int ldk = ep.amax_ld ? ep.amax_ld : M;
+  const uint32_t kbytes = (uint32_t)(nslots * ldk) * 8u;
+  const buf_t kbuf = make_buf(ep.amax, KO ? kbytes : 0u);
+  const bool key_bf16 = ep.amax_dt == WFB_BF16;
 
   auto dma = [&](int tile, int buf) {
 #pragma unroll
@@ -694,23 +753,34 @@ __global__ __launch_bounds__(64 * S) void kernel_persist(const uint8_t* __restri
     if (tile >= ntiles) break;
     const int buf = it % DEPTH;
     const int ahead = blockIdx.x + (it + DEPTH - 1) * gridDim.x;
-    if (ahead < ntiles) dma(ahead, (it + DEPTH - 1) % DEPTH);  // buffer freed by the previous tile's last barrier
+    if (ahead < ntiles) dma(ahead, (it + DEPTH - 1) % DEPTH);  // slot last read by this wave, for tile it - 1
     const int later = min(DEPTH - 1, (ntiles - 1 - tile) / (int)gridDim.x);
     wait_tiles_after<OPS>(later);
 
+    // the wave's four weight fragments (steps 0 / 1 x row tiles 0 / 1), one wait
+    v4i wv[2][NT];
+    {
+      const int8_t* base = &wl[buf][w][0][0] + 1024 * hh + 128 * rr;
+      const int s0 = g ^ (rr ^ hh), s1 = (4 + g) ^ (rr ^ hh);
+      asm volatile(
+          "ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(wv[0][0]), "=&v"(wv[0][1]), "=&v"(wv[1][0]), "=&v"(wv[1][1])
+          : "v"(lds_off(base + 16 * s0)), "v"(lds_off(base + 2048 + 16 * s0)), "v"(lds_off(base + 16 * s1)),
+            "v"(lds_off(base + 2048 + 16 * s1))
+          : "memory");
+    }
     v4i acc1[NT], acc4[NT], acc16[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc1[nt] = acc4[nt] = acc16[nt] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      const int slot = (4 * st + g) ^ (rr ^ hh);
+    for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const v4i wv = *reinterpret_cast<const v4i*>(wl[buf][w][nt] + 1024 * hh + 128 * rr + 16 * slot);
         v4i b0, b1, b2, b3;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int d = wv[e];
+          const int d = wv[st][nt][e];
           b0[e] = (d >> 2) & 0x30303030;
           b1[e] = d & 0x30303030;
           b2[e] = d & 0x0C0C0C0C;
@@ -721,38 +791,56 @@ __global__ __launch_bounds__(64 * S) void kernel_persist(const uint8_t* __restri
         acc4[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[st][2], b2, acc4[nt], 0, 0, 0);
         acc1[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[st][3], b3, acc1[nt], 0, 0, 0);
       }
-    }
     const int par = it & 1;
+    {
+      // partial (nt, j) of this wave at redb[par][w][nt * 4 + j][lane] (256 bytes apart), then the barrier
+      int v[NT * 4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        redb[par][w][nt * 4 + j][lane] = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj[j];
-    __syncthreads();
+        for (int nt = 0; nt < NT; ++nt)
+          v[nt * 4 + j] = acc1[nt][j] + (acc4[nt][j] >> 2) + (acc16[nt][j] >> 4) - sj[j];
+      asm volatile(
+          "ds_write_b32 %0, %1\n\tds_write_b32 %0, %2 offset:256\n\tds_write_b32 %0, %3 offset:512\n\t"
+          "ds_write_b32 %0, %4 offset:768\n\tds_write_b32 %0, %5 offset:1024\n\tds_write_b32 %0, %6 offset:1280\n\t"
+          "ds_write_b32 %0, %7 offset:1536\n\tds_write_b32 %0, %8 offset:1792\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier"
+          :
+          : "v"(lds_off(&redb[par][w][0][lane])), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]),
+            "v"(v[6]), "v"(v[7])
+          : "memory");
+    }
     // epilogue spread over the waves: (row tile nt, token slot j) pairs c = w, w + S, ...; lane (nl, g)
     // finishes row 16 nt + nl of token 4g + j
     for (int c = w; c < NT * 4; c += S) {
       const int nt = c >> 2, j = c & 3;
       const int tok = 4 * g + j;
       const int n = tile * 16 * NT + 16 * nt + nl;
-      int tot = redb[par][0][c][lane];
-#pragma unroll
-      for (int k = 1; k < S; ++k) tot += redb[par][k][c][lane];
-      float a = as[0];
-#pragma unroll
-      for (int jj = 1; jj < 4; ++jj)
-        if (j == jj) a = as[jj];
-      if (ep.amax) {  // greedy-argmax keys: the maximum over the 16 rows of each token, one slot per 16 rows
+      const int tot = lds_sum_parts<S>(lds_off(&redb[par][0][c][lane]));
+      // (selects, not an indexed array: the compiler would place that in LDS, where each read would wait for
+      // the ring's DMA)
+      const float a = (j & 2) ? ((j & 1) ? as[3] : as[2]) : ((j & 1) ? as[1] : as[0]);
+      if constexpr (KO) {
+        const bool valid = tok < M && n < N;
+        const float y = epi_y(ep, ws, a, 0.0f, tot);
+        const float yk = key_bf16 ? bf16_bits_to_f32(f32_to_bf16_rne(y)) : y;
+        uint64_t key = valid ? amax_key(yk, n) : 0;
+        key = group_max_u64<16>(key);
+        const int slot = tile * NT + nt;
+        const bool st = nl == 0 && tok < M && slot < nslots;
+        const u32x2 kv = {(uint32_t)key, (uint32_t)(key >> 32)};
+        __builtin_amdgcn_raw_buffer_store_b64(kv, kbuf, st ? (uint32_t)(slot * ldk + tok) * 8u : kbytes, 0, 0);
+      } else if (ep.amax) {  // greedy-argmax keys with other outputs: the maximum over the 16 rows of each token
         const bool valid = tok < M && n < N;
         uint64_t key = epi_store_key_r(ep, ws, a, 0.0f, 0.0f, tok, n, tot, valid);
         key = group_max_u64<16>(key);
         const int slot = tile * NT + nt;
-        if (nl == 0 && tok < M && slot < (N + 15) / 16) ep.amax[(int64_t)slot * (ep.amax_ld ? ep.amax_ld : M) + tok] = key;
+        if (nl == 0 && tok < M && slot < nslots) ep.amax[(int64_t)slot * ldk + tok] = key;
       } else if (n < N && tok < M) {
         epi_store_r(ep, ws, a, 0.0f, 0.0f, tok, n, tot);
       }
     }
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): nothing of this wave in flight at exit
 }
 
 // Persistent launch for grids of many tiles: two 16-row tiles per workgroup step, the ring as deep as the
@@ -768,7 +856,10 @@ inline hipError_t launch_persist(const uint8_t* W, int n, int C, const int8_t* A
   do {                                                                                                 \
     constexpr int D = (163840 - 2 * S * NT * 1024) / (S * NT * 2048) > 8 ? 8                          \
                                                                         : (163840 - 2 * S * NT * 1024) / (S * NT * 2048); \
-    hipLaunchKernelGGL((kernel_persist<S, NT, D>), dim3(grid), dim3(64 * S), 0, s, W, A, lda, m, n, C, ntiles, e); \
+    if (e.amax && !e.out && !e.acc_out)                                                                \
+      hipLaunchKernelGGL((kernel_persist<S, NT, D, true>), dim3(grid), dim3(64 * S), 0, s, W, A, lda, m, n, C, ntiles, e); \
+    else                                                                                               \
+      hipLaunchKernelGGL((kernel_persist<S, NT, D, false>), dim3(grid), dim3(64 * S), 0, s, W, A, lda, m, n, C, ntiles, e); \
     return hipGetLastError();                                                                          \
   } while (0)
   if (T2 <= 2) WFB_SL_P(2);
