@@ -91,6 +91,30 @@ __device__ __forceinline__ void load8_buf(buf_t b, int e0, float (&v)[kVec]) {
   }
 }
 
+// 8 elements from the raw 16-byte words of load8_buf (fp32: two words, 16-bit types: one)
+template <int DT>
+__device__ __forceinline__ void widen_raw8(const v4i (&a)[DT == WFB_F32 ? 2 : 1], float (&v)[kVec]) {
+  if constexpr (DT == WFB_F32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = __int_as_float(a[0][e]);
+      v[4 + e] = __int_as_float(a[1][e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = (uint32_t)a[0][e];
+      if constexpr (DT == WFB_BF16) {
+        v[2 * e] = __uint_as_float(w << 16);
+        v[2 * e + 1] = __uint_as_float(w & 0xffff0000u);
+      } else {
+        v[2 * e] = f16_bits_to_f32((uint16_t)(w & 0xffffu));
+        v[2 * e + 1] = f16_bits_to_f32((uint16_t)(w >> 16));
+      }
+    }
+  }
+}
+
 template <int DT, int GLU>
 __device__ __forceinline__ void load_row8_full(buf_t xb, buf_t ub, int e0, float (&v)[kVec]) {
   load8_buf<DT>(xb, e0, v);
@@ -123,6 +147,12 @@ __global__ __launch_bounds__(kTPB) void quant_rows_kernel(const void* __restrict
 
   float v[kMaxIt][kVec];
   const bool full = vec && h % kVec == 0;  // uniform
+  // (whole-vector rows with gamma) gamma's 8 elements per iteration as raw 16-byte words, requested right
+  // after the row's: issued after the reduction inside the per-iteration loop below, each load was
+  // followed by a wait of its own, one cache round trip per iteration
+  constexpr int GW = GDT == WFB_F32 ? 2 : 1;
+  v4i graw[NORM ? kMaxIt : 1][GW];
+  const bool gpre = NORM && full && gamma != nullptr;  // uniform
   if (full) {
     const buf_t xb = row_buf<DT>(xr, h), ub = GLU != 0 ? row_buf<DT>(ur, h) : xb;
 #pragma unroll
@@ -132,6 +162,17 @@ __global__ __launch_bounds__(kTPB) void quant_rows_kernel(const void* __restrict
         for (int e = 0; e < kVec; ++e) v[it][e] = 0.0f;
       } else {
         load_row8_full<DT, GLU>(xb, ub, (it * kTPB + t) * kVec, v[it]);
+      }
+    }
+    if constexpr (NORM) {
+      if (gpre) {
+        // every iteration's words, without branches (vectors past the row read zeros through the range)
+        const buf_t gb = row_buf<GDT>(gamma, h);
+#pragma unroll
+        for (int it = 0; it < kMaxIt; ++it)
+#pragma unroll
+          for (int q = 0; q < GW; ++q)
+            graw[it][q] = buf_load16(gb, (uint32_t)((it * kTPB + t) * kVec) * (GDT == WFB_F32 ? 4u : 2u) + 16u * q);
       }
     }
   } else {
@@ -170,8 +211,8 @@ __global__ __launch_bounds__(kTPB) void quant_rows_kernel(const void* __restrict
       if (gamma == nullptr) {
 #pragma unroll
         for (int e = 0; e < kVec; ++e) g[e] = 1.0f;
-      } else if (full) {
-        load8_buf<GDT>(row_buf<GDT>(gamma, h), e0, g);
+      } else if (gpre) {
+        widen_raw8<GDT>(graw[it], g);
       } else if (vec && e0 + kVec <= h) {
         load8<GDT>(gamma, e0, g);
       } else {
@@ -332,10 +373,24 @@ __global__ __launch_bounds__(kWideThreads) void quant_rows_wide_kernel(
 
   float v[VPT][kVec];
   const bool full = vec && h % kVec == 0;  // uniform
+  // (whole-vector rows with gamma) gamma's words requested with the row's, as in quant_rows_kernel
+  constexpr int GW = GDT == WFB_F32 ? 2 : 1;
+  v4i graw[NORM ? VPT : 1][GW];
+  const bool gpre = NORM && full && gamma != nullptr;  // uniform
   if (full) {  // every load in flight before the first wait (vectors past the row read as zeros)
     const buf_t xb = row_buf<DT>(xr, h), ub = GLU != 0 ? row_buf<DT>(ur, h) : xb;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) load_row8_full<DT, GLU>(xb, ub, (t + kWideThreads * i) * kVec, v[i]);
+    if constexpr (NORM) {
+      if (gpre) {
+        const buf_t gb = row_buf<GDT>(gamma, h);
+#pragma unroll
+        for (int i = 0; i < VPT; ++i)
+#pragma unroll
+          for (int q = 0; q < GW; ++q)
+            graw[i][q] = buf_load16(gb, (uint32_t)((t + kWideThreads * i) * kVec) * (GDT == WFB_F32 ? 4u : 2u) + 16u * q);
+      }
+    }
   }
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
@@ -409,8 +464,8 @@ __global__ __launch_bounds__(kWideThreads) void quant_rows_wide_kernel(
       if (gamma == nullptr) {
 #pragma unroll
         for (int e = 0; e < kVec; ++e) g[e] = 1.0f;
-      } else if (full) {
-        load8_buf<GDT>(row_buf<GDT>(gamma, h), e0, g);
+      } else if (gpre) {
+        widen_raw8<GDT>(graw[i], g);
       } else if (vec && e0 + kVec <= h) {
         load8<GDT>(gamma, e0, g);
       } else {
