@@ -28,19 +28,31 @@ __device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
 }
 
 // One workgroup per token; each thread keeps kFinLoads independent slot loads in flight per round (a
-// 128256-row head has 8016 slots: one round), then a wave and a workgroup maximum.
+// 128256-row head has 8016 slots: one round), then a wave and a workgroup maximum.  BUF: the loads go
+// through a buffer descriptor bounded at the workspace's end (workspaces under 4 GiB), so slots past it
+// read 0 without a branch -- guarded loads compiled to one wait per load.
 constexpr int kFinThreads = 1024, kFinLoads = 8;
+typedef uint32_t u32x2_fin __attribute__((ext_vector_type(2)));
+template <bool BUF>
 __global__ __launch_bounds__(kFinThreads) void argmax_finalize_kernel(const uint64_t* __restrict__ parts, int64_t np,
                                                                       int m, int64_t* __restrict__ tokens) {
   __shared__ uint64_t sb[kFinThreads / 64];
   const int mm = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const uint32_t pbytes = BUF ? (uint32_t)(np * m) * 8u : 0u;
+  const buf_t pb = make_buf(parts, pbytes);
   uint64_t best = 0;
   for (int64_t p0 = 0; p0 < np; p0 += (int64_t)kFinThreads * kFinLoads) {
     uint64_t v[kFinLoads];
 #pragma unroll
     for (int i = 0; i < kFinLoads; ++i) {
       const int64_t p = p0 + t + (int64_t)kFinThreads * i;
-      v[i] = p < np ? parts[p * m + mm] : 0;
+      if constexpr (BUF) {
+        const u32x2_fin a =
+            __builtin_amdgcn_raw_buffer_load_b64(pb, p < np ? (uint32_t)(p * m + mm) * 8u : pbytes, 0, 0);
+        v[i] = ((uint64_t)a[1] << 32) | a[0];
+      } else {
+        v[i] = p < np ? parts[p * m + mm] : 0;
+      }
     }
 #pragma unroll
     for (int i = 0; i < kFinLoads; ++i) best = v[i] > best ? v[i] : best;
@@ -244,7 +256,12 @@ hipError_t launch_head_t(const void* x, int64_t ldx, const void* gamma, int gdt,
 }  // namespace
 
 hipError_t launch_argmax_finalize(const uint64_t* parts, int64_t n_parts, int64_t m, int64_t* tokens, hipStream_t s) {
-  hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)m), dim3(kFinThreads), 0, s, parts, n_parts, (int)m, tokens);
+  if (n_parts * m * 8 < ((int64_t)1 << 32))
+    hipLaunchKernelGGL((argmax_finalize_kernel<true>), dim3((unsigned)m), dim3(kFinThreads), 0, s, parts, n_parts, (int)m,
+                       tokens);
+  else
+    hipLaunchKernelGGL((argmax_finalize_kernel<false>), dim3((unsigned)m), dim3(kFinThreads), 0, s, parts, n_parts, (int)m,
+                       tokens);
   return hipGetLastError();
 }
 
