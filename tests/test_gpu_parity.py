@@ -162,6 +162,25 @@ def test_rmsnorm_quant_fp32_input_eps(pkg, dev):
     assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
 
 
+@pytest.mark.parametrize("gdtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("m,h", [(8, 14336), (3, 6912), (8, 10000), (2, 16384)])
+def test_rmsnorm_quant_long_fp32_rows_gamma(pkg, dev, gdtype, m, h):
+    """fp32 rows longer than 4096 (the decode layer's gated row: 256 threads per row, gamma's words
+    requested with the row's, rows past the last full iteration included) and, gated, the 1024-thread
+    form (rows up to 15360): codes and scales equal the oracle's for bf16 and fp32 gamma."""
+    rng = np.random.default_rng(h * 3 + m)
+    x = orc.outlier_hidden(rng, m, h).astype(np.float32)
+    g = torch.from_numpy((1 + 0.1 * rng.standard_normal(h)).astype(np.float32)).to(gdtype)
+    q, s = pkg.rmsnorm_quantize_i8(_t(x, dev), g.to(dev), eps=1e-6)
+    q_ref, s_ref = orc.rmsnorm_quant(x, g.float().numpy(), 1e-6)
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+    up = orc.outlier_hidden(rng, m, h).astype(np.float32)
+    for act in ("silu", "relu2"):
+        qg, sg = pkg.glu_rmsnorm_quantize_i8(_t(x, dev), _t(up, dev), act, g.to(dev), eps=1e-6)
+        qg_ref, sg_ref = orc.glu_rmsnorm_quant(x, up, 1 if act == "silu" else 2, g.float().numpy(), 1e-6)
+        assert np.array_equal(qg.cpu().numpy(), qg_ref) and np.array_equal(sg.cpu().numpy(), sg_ref)
+
+
 # ---- a4 / a5 / a6: GEMV, batched sweep, prefill GEMM ---------------------------------------------
 
 
