@@ -49,6 +49,7 @@ namespace wfb {
 namespace skinny_lds {
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void dma16(buf_t r, void* lds, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, 0, 0, 0);
 }
@@ -309,12 +310,43 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
 #pragma unroll
   for (int jj = 0; jj < JT; ++jj) toks[jj] = 16 * (jj >> 2) + 4 * g + (jj & 3);
   EpiCol<JT> col;
+  // staged epilogue: thread i of the workgroup finishes 4 consecutive outputs (token i / (RW / 4), rows
+  // n0 + 4 (i % (RW / 4)) ..) for i = threadIdx.x, + 64 S, ...; its residual values are requested here,
+  // with the other epilogue operands, instead of after the final barrier (where each was a round trip of
+  // its own at the end of the kernel).  Whole 4-element groups of aligned residuals only, as raw words
+  // through a buffer range (groups past the tile read zeros, no branches); the others load late.
+  constexpr int RW = 16 * NT;
+  constexpr int RI = STAGED ? (16 * MT * (RW / 4) + 64 * S - 1) / (64 * S) : 1;  // items per thread
+  v4i rraw[RI];
+  const bool rpre = STAGED && ep.res && ep.ldr % 4 == 0 &&
+                    (uintptr_t)ep.res % (ep.res_dtype == WFB_F32 ? 16 : 8) == 0;  // uniform
+  auto res_loads = [&]() {
+    if constexpr (STAGED) {
+      if (!rpre) return;
+      const uint32_t esz = ep.res_dtype == WFB_F32 ? 4u : 2u;
+      const uint32_t rbytes = (uint32_t)((int64_t)(M - 1) * ep.ldr + N) * esz;
+      const buf_t rb = make_buf(ep.res, rbytes);
+#pragma unroll
+      for (int r = 0; r < RI; ++r) {
+        const int i = threadIdx.x + 64 * S * r;
+        const int tok = i / (RW / 4), n = n0 + 4 * (i % (RW / 4));
+        const uint32_t off = tok < M && n + 3 < N ? (uint32_t)((int64_t)tok * ep.ldr + n) * esz : rbytes;
+        if (esz == 4) {
+          rraw[r] = buf_load16(rb, off);
+        } else {
+          const u32x2 h2 = __builtin_amdgcn_raw_buffer_load_b64(rb, off, 0, 0);
+          rraw[r] = v4i{(int)h2[0], (int)h2[1], 0, 0};
+        }
+      }
+    }
+  };
   auto col_loads = [&]() {
     if (!GLUE && w < NT) {
       Epilogue e1 = ep;
       if (STAGED) e1.res = nullptr;  // the staged path adds the residual with whole-line loads
       col.load(e1, tile_row(w) + nl, N, toks, M);
     }
+    res_loads();
   };
   float my_scale[RPW];
   // register-activation mode: lane (nl, g)'s 16 activation bytes of token tile mt, step pair u, step st,
@@ -522,7 +554,6 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   } else {
     // y (fp32, before the residual) of the [M tokens x 16 NT rows] tile into LDS (the activation staging),
     // rows rotated by 4 per token to spread the banks
-    constexpr int RW = 16 * NT;
     float* ys = XT == kAreg ? ysb : reinterpret_cast<float*>(&al[0][0][0][0]);  // free after the barrier above
     static_assert(XT == kAreg || sizeof(al) >= 16 * MT * RW * 4, "staging space");
     if (w < NT) {
@@ -538,26 +569,26 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     }
     __syncthreads();
     const bool out_vec = ep.ldo % 4 == 0 && (uintptr_t)ep.out % (ep.out_dtype == WFB_F32 ? 16 : 8) == 0;
-    const bool res_vec = !ep.res || (ep.ldr % 4 == 0 && (uintptr_t)ep.res % (ep.res_dtype == WFB_F32 ? 16 : 8) == 0);
-    for (int i = threadIdx.x; i < M * (RW / 4); i += 64 * S) {
+#pragma unroll
+    for (int r = 0; r < RI; ++r) {
+      const int i = threadIdx.x + 64 * S * r;
       const int tok = i / (RW / 4), q = i % (RW / 4);
       const int n = n0 + 4 * q;
-      if (n >= N) continue;
+      if (tok >= M || n >= N) continue;
       const bool full = n + 3 < N;
       float y[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) y[e] = ys[tok * RW + ((4 * q + e + 4 * tok) & (RW - 1))];
       if (ep.res) {
         float rv[4];
-        const int64_t ro = (int64_t)tok * ep.ldr + n;
-        if (full && res_vec) {
+        if (rpre && full) {  // requested at kernel entry
           if (ep.res_dtype == WFB_F32) {
-            const float4 r4 = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ep.res) + ro);
-            rv[0] = r4.x; rv[1] = r4.y; rv[2] = r4.z; rv[3] = r4.w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rv[e] = __int_as_float(rraw[r][e]);
           } else {
-            const uint2 r2 = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(ep.res) + ro);
-            rv[0] = __uint_as_float(r2.x << 16); rv[1] = __uint_as_float(r2.x & 0xffff0000u);
-            rv[2] = __uint_as_float(r2.y << 16); rv[3] = __uint_as_float(r2.y & 0xffff0000u);
+            const uint32_t x0 = (uint32_t)rraw[r][0], x1 = (uint32_t)rraw[r][1];
+            rv[0] = __uint_as_float(x0 << 16); rv[1] = __uint_as_float(x0 & 0xffff0000u);
+            rv[2] = __uint_as_float(x1 << 16); rv[3] = __uint_as_float(x1 & 0xffff0000u);
           }
         } else {
 #pragma unroll
@@ -624,7 +655,6 @@ __device__ __forceinline__ void wait_tiles_after(int later) {
 
 // LDS offset of a pointer into __shared__ memory (the low 32 bits of its flat address)
 __device__ __forceinline__ uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)p; }
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Sum of the S int32 partial tiles 2048 bytes apart from LDS offset a (one wait; integer sums, so the
 // order is immaterial).
