@@ -340,12 +340,30 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
       }
     }
   };
+  // gated epilogue operands (the gate and up rows' weight scales, and the token scales of the codes path),
+  // requested with the others at entry rather than after the final barrier
+  float gws[2] = {0.0f, 0.0f}, gas[GLUE != 0 && !NORM ? JT : 1];
+  auto glu_loads = [&]() {
+    if constexpr (GLUE != 0) {
+      if (w < NT / 2) {
+        const int n = n0 + 16 * w + nl;
+        const int nc = n < half ? n : half - 1;  // (a column past the outputs stores nothing)
+        gws[0] = epi_wscale(ep, nc);
+        gws[1] = epi_wscale(ep, half + nc);
+        if constexpr (!NORM) {
+#pragma unroll
+          for (int jj = 0; jj < JT; ++jj) gas[jj] = toks[jj] < M ? epi_ascale(ep, toks[jj]) : 0.0f;
+        }
+      }
+    }
+  };
   auto col_loads = [&]() {
     if (!GLUE && w < NT) {
       Epilogue e1 = ep;
       if (STAGED) e1.res = nullptr;  // the staged path adds the residual with whole-line loads
       col.load(e1, tile_row(w) + nl, N, toks, M);
     }
+    glu_loads();
     res_loads();
   };
   float my_scale[RPW];
@@ -503,7 +521,7 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
     if (w >= NT / 2) return;
     const int n = n0 + 16 * w + nl;  // output column = gate row; its up row is half + n
     if (n >= half) return;
-    const float wsg = epi_wscale(ep, n), wsu = epi_wscale(ep, half + n);
+    const float wsg = gws[0], wsu = gws[1];
 #pragma unroll
     for (int jj = 0; jj < JT; ++jj) {
       const int tok = toks[jj], mt = jj >> 2, j = jj & 3;
@@ -514,7 +532,9 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
         tg += red(k, mt, w, j, lane);
         tu += red(k, mt, w + NT / 2, j, lane);
       }
-      const float as = NORM ? col.as[jj] : epi_ascale(ep, tok);
+      float as;
+      if constexpr (NORM) as = col.as[jj];
+      else as = gas[jj];
       float yg = __fmul_rn(__fmul_rn((float)tg, wsg), as), yu = __fmul_rn(__fmul_rn((float)tu, wsu), as);
       if (ep.mid_dtype == WFB_BF16) {
         yg = bf16_bits_to_f32(f32_to_bf16_rne(yg));
