@@ -319,7 +319,8 @@ __global__ __launch_bounds__(64 * S) void kernel(const uint8_t* __restrict__ W, 
   constexpr int RI = STAGED ? (16 * MT * (RW / 4) + 64 * S - 1) / (64 * S) : 1;  // items per thread
   v4i rraw[RI];
   const bool rpre = STAGED && ep.res && ep.ldr % 4 == 0 &&
-                    (uintptr_t)ep.res % (ep.res_dtype == WFB_F32 ? 16 : 8) == 0;  // uniform
+                    (uintptr_t)ep.res % (ep.res_dtype == WFB_F32 ? 16 : 8) == 0 &&
+                    ((int64_t)(M - 1) * ep.ldr + N) * 4 < ((int64_t)1 << 32);  // uniform; range within 32 bits
   auto res_loads = [&]() {
     if constexpr (STAGED) {
       if (!rpre) return;
@@ -906,7 +907,8 @@ inline hipError_t launch_persist(const uint8_t* W, int n, int C, const int8_t* A
   do {                                                                                                 \
     constexpr int D = (163840 - 2 * S * NT * 1024) / (S * NT * 2048) > 8 ? 8                          \
                                                                         : (163840 - 2 * S * NT * 1024) / (S * NT * 2048); \
-    if (e.amax && !e.out && !e.acc_out)                                                                \
+    if (e.amax && !e.out && !e.acc_out &&                                                              \
+        (int64_t)((n + 15) / 16) * (e.amax_ld ? e.amax_ld : m) * 8 < ((int64_t)1 << 32))                 \
       hipLaunchKernelGGL((kernel_persist<S, NT, D, true>), dim3(grid), dim3(64 * S), 0, s, W, A, lda, m, n, C, ntiles, e); \
     else                                                                                               \
       hipLaunchKernelGGL((kernel_persist<S, NT, D, false>), dim3(grid), dim3(64 * S), 0, s, W, A, lda, m, n, C, ntiles, e); \
