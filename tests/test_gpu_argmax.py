@@ -19,15 +19,15 @@ def _first_argmax(x):
 
 
 # (1, 70000, 4096), (2, 40000, 2560): the GEMV with activation fragments from global memory (grids above
-# 2048 workgroups); (8, 128256, 4096), (3, 40000, 2560), (5, 33000, 1024), (12, 65543, 2560), (16, 49152, 4096):
-# the persistent head kernel
+# 2048 workgroups); (8, 128256, 4096), (3, 40000, 2560), (5, 33000, 1024), (12, 65543, 2560), (16, 49152, 4096),
+# (6, 34000, 2048), (9, 33100, 1536): the persistent head kernel (8, 5, 2, 4 and 4 waves per workgroup)
 # (>= 32768 rows, up to 16 tokens), one-shot elsewhere; (17, 3000, 512), (32, 20000, 2560), (24, 4096, 4096):
 # two token tiles per weight fragment; (40, 40000, 2560), (64, 33000, 1024), (17, 32768, 512): more than 16
 # tokens on 32768+ rows, in chunks of 16 tokens through the persistent kernel
 @pytest.mark.parametrize("m,n,k", [(1, 1000, 256), (2, 5000, 640), (1, 70000, 4096), (2, 40000, 2560),
                                    (3, 4099, 2560), (8, 128256, 4096),
                                    (3, 40000, 2560), (5, 33000, 1024), (12, 65543, 2560), (16, 49152, 4096),
-                                   (17, 3000, 512), (32, 20000, 2560), (24, 4096, 4096), (64, 2048, 384),
+                                   (6, 34000, 2048), (9, 33100, 1536), (17, 3000, 512), (32, 20000, 2560), (24, 4096, 4096), (64, 2048, 384),
                                    (40, 40000, 2560), (64, 33000, 1024), (17, 32768, 512)])
 @pytest.mark.parametrize("ldt", [torch.float32, torch.bfloat16])
 def test_ternary_head_argmax_matches_oracle(pkg, dev, m, n, k, ldt):
@@ -51,7 +51,7 @@ def test_ternary_head_argmax_matches_oracle(pkg, dev, m, n, k, ldt):
     assert torch.equal(pkg.bitnet_linear_argmax(pw, at, float(ws), a_scale=st, logits_dtype=ldt), tok)
 
 
-@pytest.mark.parametrize("m,n,k", [(4, 36000, 4096), (8, 33011, 2560), (16, 40000, 1024)])
+@pytest.mark.parametrize("m,n,k", [(4, 36000, 4096), (8, 33011, 2560), (16, 40000, 1024), (7, 33000, 2048)])
 def test_persistent_head_accumulators(pkg, dev, m, n, k):
     """The persistent form of the batched-decode kernel with an accumulator copy (>= 32768 rows): every
     int32 accumulator and fp32 output equal the oracle's."""
