@@ -291,10 +291,8 @@ __global__ __launch_bounds__(64 * S) void gemv_i2s_kernel(const uint8_t* __restr
       if (e0 < kpad) {
         uint32_t lo = 0, hi = 0;  // zeros past h
         if (e0 < h) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) lo |= (uint32_t)(quant_i8(xv[j][e], inv) & 0xff) << (8 * e);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) hi |= (uint32_t)(quant_i8(xv[j][4 + e], inv) & 0xff) << (8 * e);
+          lo = quant4_i8(&xv[j][0], inv);
+          hi = quant4_i8(&xv[j][4], inv);
         }
         *reinterpret_cast<uint2*>(&codes[0][e0]) = make_uint2(lo, hi);
       }

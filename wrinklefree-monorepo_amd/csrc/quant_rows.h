@@ -245,11 +245,7 @@ __global__ __launch_bounds__(kTPB) void quant_rows_kernel(const void* __restrict
     const int e0 = (it * kTPB + t) * kVec;
     if (e0 >= h) break;
     if (e0 + kVec <= h) {
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) lo |= (uint32_t)(quant_i8(v[it][e], inv) & 0xff) << (8 * e);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) hi |= (uint32_t)(quant_i8(v[it][4 + e], inv) & 0xff) << (8 * e);
+      const uint32_t lo = quant4_i8(&v[it][0], inv), hi = quant4_i8(&v[it][4], inv);
       *reinterpret_cast<uint2*>(qr + e0) = make_uint2(lo, hi);
     } else {
 #pragma unroll
@@ -331,11 +327,7 @@ __global__ __launch_bounds__(256) void quant_rows_wave_kernel(const void* __rest
   for (int j = 0; j < VPL; ++j) {
     const int e0 = (lane + 64 * j) * kVec;
     if (e0 + kVec <= h) {
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) lo |= (uint32_t)(quant_i8(v[j][e], inv) & 0xff) << (8 * e);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) hi |= (uint32_t)(quant_i8(v[j][4 + e], inv) & 0xff) << (8 * e);
+      const uint32_t lo = quant4_i8(&v[j][0], inv), hi = quant4_i8(&v[j][4], inv);
       *reinterpret_cast<uint2*>(qr + e0) = make_uint2(lo, hi);
     } else if (e0 < h) {
 #pragma unroll
@@ -499,11 +491,7 @@ __global__ __launch_bounds__(kWideThreads) void quant_rows_wide_kernel(
     const int e0 = (t + kWideThreads * i) * kVec;
     if (e0 >= h) break;
     if (e0 + kVec <= h) {
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) lo |= (uint32_t)(quant_i8(v[i][e], inv) & 0xff) << (8 * e);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) hi |= (uint32_t)(quant_i8(v[i][4 + e], inv) & 0xff) << (8 * e);
+      const uint32_t lo = quant4_i8(&v[i][0], inv), hi = quant4_i8(&v[i][4], inv);
       *reinterpret_cast<uint2*>(qr + e0) = make_uint2(lo, hi);
     } else {
 #pragma unroll
