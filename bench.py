@@ -795,8 +795,8 @@ def main():
                 ws = torch.ones(1, dtype=torch.float32, device=dev)
                 out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
                 calls = [[L.linear_args("wfb_linear_i2s", c, n, k, a, m, a_scale, ws, out)] for c in copies]
-                # 30 warm-up launches: with 5, the first timed run after another kernel read 0.1-0.2 us
-                # slow on the short shapes (M = 4 measured after the M = 2 GEMV above the M = 8 time)
+                # 30 warm-up launches: with 5, the first timed run after another kernel (here M = 4, after
+                # the M = 2 GEMV) read 0.1-0.2 us slow on the short shapes
                 ms = timed(torch, calls, args.steps, 30)
                 gbs = gemv_bytes(m, n, k) / (ms * 1e-3) / 1e9
                 sweep.append({"M": m, "N": n, "K": k, "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
